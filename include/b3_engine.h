@@ -1,0 +1,107 @@
+/*
+ * b3_engine.h - C ABI of the MI355X batched stepping engine.
+ *
+ * The reference exposes its GPU path as header-only functions over a
+ * strided B3Batch of AoS worlds (b3_batch.cuh:12-99).  This library keeps
+ * the same names and semantics, but the worlds live on the device inside an
+ * engine handle, in a structure-of-arrays layout, so each entry point takes
+ * a B3Engine* where the reference takes a B3Batch.  Scenes are still built
+ * on the host with the reference's creation API (b3_setup.h) and handed
+ * over once.
+ *
+ * Conventions (docs/API.md:58-63, b3_batch.cuh:19-99):
+ *   - functions return hipSuccess or a hipError_t and never abort;
+ *   - invalid arguments give hipErrorInvalidValue with no mutation and no
+ *     launch; an empty batch or dt == 0 is a successful no-op;
+ *   - the *_gpu functions enqueue on `stream` without allocating or
+ *     synchronising; execution errors surface at the caller's
+ *     synchronisation point;
+ *   - masks are one byte per world in device memory, nonzero selects.
+ *     NULL selects every world, except the reset mask of
+ *     b3_batch_step_gpu, where NULL resets none;
+ *   - b3_engine_create is the only call that allocates device memory, and
+ *     b3_engine_destroy the only one that frees it.
+ */
+#ifndef PUFFYSICS_AMD_B3_ENGINE_H
+#define PUFFYSICS_AMD_B3_ENGINE_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+
+#include "b3_types.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct B3Engine B3Engine;
+
+/* Create an engine on the current HIP device holding copies of the host
+ * worlds viewed by `worlds` (a B3Batch exactly as b3_batch_valid accepts,
+ * b3_batch.cuh:21-27), whose B3World capacities are `config_signature`
+ * (B3_CONFIG_SIGNATURE of the caller's build, 01_config.inl:70-74).  The
+ * worlds are checked for in-range counts and body/shape indices.  Blocks
+ * until the upload is complete. */
+hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long config_signature);
+
+/* Free everything the engine allocated.  NULL is a no-op. */
+hipError_t b3_engine_destroy(B3Engine* engine);
+
+/* Number of worlds, or -1 for NULL. */
+int b3_engine_count(const B3Engine* engine);
+
+/* Register `count` contiguous host B3World snapshots used by the reset
+ * paths (b3_batch_restore's `initial`, b3_batch.cuh:50-60).  Blocks until
+ * the copy is complete. */
+hipError_t b3_engine_set_snapshots(B3Engine* engine, const void* initial);
+
+/* Replace the device worlds with the host worlds of `worlds` (same count
+ * and signature as at creation).  Blocks until complete. */
+hipError_t b3_engine_upload(B3Engine* engine, B3Batch worlds);
+
+/* Copy the device worlds out into the host worlds viewed by `worlds`.
+ * Every field the step reads or writes is exact; contact points at or
+ * beyond a contact's point_count and contact slots at or beyond
+ * contact_count hold whatever the device last wrote there.  Blocks until
+ * complete. */
+hipError_t b3_engine_download(B3Engine* engine, B3Batch worlds);
+
+/* Restore the worlds selected by `reset` from the registered snapshots
+ * (b3_batch_restore_gpu, b3_batch.cuh:91-99).  Restores every persistent
+ * field: header, bodies, shapes, joints and the snapshot's live contacts. */
+hipError_t b3_batch_restore_gpu(B3Engine* engine, const unsigned char* reset, hipStream_t stream);
+
+/* Masked restore then masked step, fused in one launch: equal to
+ * b3_batch_restore(reset_mask) followed by b3_batch_step(step_mask)
+ * (b3_batch.cuh:39-60).  step_mask NULL steps every world, reset_mask NULL
+ * restores none.  dt must be finite and >= 0, substeps >= 1
+ * (b3_batch_step_gpu, b3_batch.cuh:81-89). */
+hipError_t b3_batch_step_gpu(B3Engine* engine, float dt, int substeps, const unsigned char* step_mask,
+    const unsigned char* reset_mask, hipStream_t stream);
+
+/* Accumulate per-body forces and torques, and apply linear impulses, from
+ * dense device arrays laid out [world][body][xyz] over the engine's
+ * body capacity (max_bodies of the signature).  Each selected world gets,
+ * for every body b < body_count, in this order:
+ *   force += force[w][b]                       (b3_apply_force, 09_step.inl:132-134)
+ *   torque += torque[w][b]                     (b3_apply_torque, 09_step.inl:136-138)
+ *   lin_vel += inv_mass * impulse[w][b] if the body is dynamic
+ *                                              (b3_apply_linear_impulse, 09_step.inl:140-146)
+ * Any of the three arrays may be NULL to skip that input; `mask` NULL
+ * selects every world. */
+hipError_t b3_batch_apply_gpu(B3Engine* engine, const float* force, const float* torque,
+    const float* linear_impulse, const unsigned char* mask, hipStream_t stream);
+
+/* Per-world B3StepStats (02_types.inl:336-346, b3_step_stats in
+ * 04_world.inl:59-77) into a device array of `count` records. */
+hipError_t b3_batch_stats_gpu(B3Engine* engine, B3StepStats* out, hipStream_t stream);
+
+/* Device view of the live worlds for fused observation kernels: word k of
+ * world w is ((uint32_t*)tiles)[((w / 64) * world_words + k) * 64 + w % 64],
+ * where world_words = sizeof(B3World) / 4 of the engine's signature. */
+hipError_t b3_engine_device_view(const B3Engine* engine, void** tiles, size_t* world_words);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

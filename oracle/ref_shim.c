@@ -45,3 +45,8 @@ long long ref_run(int scene, void* worlds, const void* initial, int count, unsig
     return b3w_run(scene, (B3World*)worlds, (const B3World*)initial, count, seed, t0, nsteps, dt,
         substeps, nthreads, cpus);
 }
+int ref_build_batch(int scene, void* worlds, int count, unsigned long long seed, int first) {
+    for (int i = 0; i < count; i++)
+        if (!b3s_build(scene, (B3World*)worlds + i, seed, first + i)) return 0;
+    return 1;
+}

@@ -1,0 +1,432 @@
+/*
+ * b3_engine.hip - MI355X kernels and C ABI of the batched stepping engine.
+ *
+ * Launch geometry: every batch is split into tiles of 64 worlds, one
+ * wave64 workgroup per tile, so each lane owns one world.  The grid is the
+ * tile count (1024 workgroups at 65,536 worlds).  Worlds are stored as
+ * word-transposed tiles (b3d_lane.h), which makes every per-field access of
+ * a wave a single 256-byte row.
+ *
+ * Kernels:
+ *   b3k_upload / b3k_download  AoS <-> tiles, transposed through LDS in
+ *                              64 x 64 word blocks (both sides coalesced)
+ *   b3k_restore                masked snapshot restore; the wave copies one
+ *                              resetting world at a time with all 64 lanes
+ *   b3k_step                   optional fused restore, then one b3_step per
+ *                              selected lane with body velocities in LDS
+ *   b3k_apply                  dense force / torque / impulse inputs
+ *   b3k_stats                  per-world B3StepStats
+ */
+#include <hip/hip_runtime.h>
+
+#include <stdlib.h>
+#include <string.h>
+
+#include "b3_engine.h"
+#include "b3_engine_internal.h"
+#include "b3d_lane.h"
+
+using namespace b3d;
+
+namespace {
+
+constexpr int kXposeThreads = 256;
+
+/* ---- AoS <-> tile transposes ---- */
+
+/* One workgroup per (tile, 64-word block): reads 64 worlds x 64 words with
+ * each world's block contiguous, writes 64 rows of 64 lanes. */
+__global__ __launch_bounds__(kXposeThreads) void b3k_upload(const uint32_t* __restrict__ aos,
+        uint32_t* __restrict__ tiles, int count, int world_words) {
+    __shared__ uint32_t blk[64][65];
+    int tile = blockIdx.y;
+    int k0 = blockIdx.x * 64;
+    for (int e = threadIdx.x; e < 64 * 64; e += kXposeThreads) {
+        int l = e >> 6, kk = e & 63;
+        int w = tile * 64 + l;
+        uint32_t v = 0;
+        if (w < count && k0 + kk < world_words) v = aos[(size_t)w * world_words + k0 + kk];
+        blk[l][kk] = v;
+    }
+    __syncthreads();
+    size_t base = (size_t)tile * world_words * 64;
+    for (int e = threadIdx.x; e < 64 * 64; e += kXposeThreads) {
+        int kk = e >> 6, l = e & 63;
+        if (k0 + kk < world_words) tiles[base + (size_t)(k0 + kk) * 64 + l] = blk[l][kk];
+    }
+}
+
+__global__ __launch_bounds__(kXposeThreads) void b3k_download(const uint32_t* __restrict__ tiles,
+        uint32_t* __restrict__ aos, int count, int world_words) {
+    __shared__ uint32_t blk[64][65];
+    int tile = blockIdx.y;
+    int k0 = blockIdx.x * 64;
+    size_t base = (size_t)tile * world_words * 64;
+    for (int e = threadIdx.x; e < 64 * 64; e += kXposeThreads) {
+        int kk = e >> 6, l = e & 63;
+        blk[l][kk] = k0 + kk < world_words ? tiles[base + (size_t)(k0 + kk) * 64 + l] : 0u;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < 64 * 64; e += kXposeThreads) {
+        int l = e >> 6, kk = e & 63;
+        int w = tile * 64 + l;
+        if (w < count && k0 + kk < world_words) aos[(size_t)w * world_words + k0 + kk] = blk[l][kk];
+    }
+}
+
+/* ---- masked restore ---- */
+
+/* Copy words [k0, k1) of the world in lane `l` from snapshot to live, one
+ * word per lane of the wave. */
+__device__ __forceinline__ void copy_words(uint32_t* __restrict__ live, const uint32_t* __restrict__ snap,
+        int l, int k0, int k1) {
+    for (int k = k0 + (int)threadIdx.x; k < k1; k += 64) live[(size_t)k * 64 + l] = snap[(size_t)k * 64 + l];
+}
+
+/* Restore the resetting worlds of this workgroup's tile, one world at a
+ * time with all 64 lanes. */
+__device__ void restore_tile(uint32_t* live, const uint32_t* snap, const Geometry& g, int count,
+        const unsigned char* reset) {
+    int tile = blockIdx.x;
+    int w = tile * 64 + (int)threadIdx.x;
+    int want = w < count && reset[w] != 0;
+    uint64_t bits = __ballot(want);
+    size_t base = (size_t)tile * g.world_words * 64;
+    uint32_t* lt = live + base;
+    const uint32_t* st = snap + base;
+    while (bits) {
+        int l = __builtin_ctzll(bits);
+        bits &= bits - 1;
+        int lo[3], hi[3];
+        restore_ranges(g, (int)st[(size_t)H_CONTACT_COUNT * 64 + l], lo, hi);
+        for (int r = 0; r < 3; r++) copy_words(lt, st, l, lo[r], hi[r]);
+    }
+}
+
+__global__ __launch_bounds__(64) void b3k_restore(uint32_t* live, const uint32_t* snap, Geometry g, int count,
+        const unsigned char* reset) {
+    restore_tile(live, snap, g, count, reset);
+}
+
+/* ---- the step ---- */
+
+__global__ __launch_bounds__(64) void b3k_step(uint32_t* live, const uint32_t* snap, uint32_t* scratch,
+        Geometry g, int count, float dt, int substeps, const unsigned char* step_mask,
+        const unsigned char* reset_mask) {
+    extern __shared__ float vel_rows[];
+    if (reset_mask) {
+        restore_tile(live, snap, g, count, reset_mask);
+        __syncthreads();
+    }
+    int tile = blockIdx.x;
+    int lane = threadIdx.x;
+    int w = tile * 64 + lane;
+    if (w >= count || (step_mask && !step_mask[w])) return;
+    Lane L;
+    L.w = live + (size_t)tile * g.world_words * 64 + lane;
+    L.scr = scratch + (size_t)tile * g.scr_words * 64 + lane;
+    L.vel = vel_rows + lane;
+    L.g = g;
+    vel_load(L);
+    step_world(L, dt, substeps);
+    vel_store(L);
+}
+
+/* ---- inputs and stats ---- */
+
+__global__ __launch_bounds__(64) void b3k_apply(uint32_t* live, Geometry g, int count, const float* force,
+        const float* torque, const float* impulse, const unsigned char* mask) {
+    int tile = blockIdx.x;
+    int lane = threadIdx.x;
+    int w = tile * 64 + lane;
+    if (w >= count || (mask && !mask[w])) return;
+    Lane L;
+    L.w = live + (size_t)tile * g.world_words * 64 + lane;
+    L.g = g;
+    int nb = body_count(L);
+    for (int b = 0; b < nb; b++) {
+        size_t in = ((size_t)w * g.max_b + b) * 3;
+        if (force) {
+            V3 f = v3(force[in], force[in + 1], force[in + 2]);
+            st3(L.w, bw(L, b, B_FORCE), add(ld3(L.w, bw(L, b, B_FORCE)), f));
+        }
+        if (torque) {
+            V3 t = v3(torque[in], torque[in + 1], torque[in + 2]);
+            st3(L.w, bw(L, b, B_TORQUE), add(ld3(L.w, bw(L, b, B_TORQUE)), t));
+        }
+        if (impulse && ldi(L.w, bw(L, b, B_TYPE)) == kDynamic) {
+            V3 p = v3(impulse[in], impulse[in + 1], impulse[in + 2]);
+            st3(L.w, bw(L, b, B_LIN_VEL), madd(ld3(L.w, bw(L, b, B_LIN_VEL)), ldf(L.w, bw(L, b, B_INV_MASS)), p));
+        }
+    }
+}
+
+__global__ __launch_bounds__(64) void b3k_stats(const uint32_t* live, Geometry g, int count, B3StepStats* out) {
+    int tile = blockIdx.x;
+    int lane = threadIdx.x;
+    int w = tile * 64 + lane;
+    if (w >= count) return;
+    const uint32_t* p = live + (size_t)tile * g.world_words * 64 + lane;
+    B3StepStats s;
+    s.body_count = ldi(p, H_BODY_COUNT);
+    s.shape_count = ldi(p, H_SHAPE_COUNT);
+    s.contact_count = ldi(p, H_CONTACT_COUNT);
+    s.joint_count = ldi(p, H_JOINT_COUNT);
+    s.body_overflow = ldi(p, B3D_W(B3WorldHeader, body_overflow));
+    s.shape_overflow = ldi(p, B3D_W(B3WorldHeader, shape_overflow));
+    s.joint_overflow = ldi(p, B3D_W(B3WorldHeader, joint_overflow));
+    s.contact_overflow = ldi(p, H_CONTACT_OVERFLOW);
+    s.contacts_dropped = ldi(p, H_CONTACTS_DROPPED);
+    out[w] = s;
+}
+
+/* ---- host helpers ---- */
+
+bool batch_valid(const B3Batch& b, size_t world_bytes) {
+    if (b.count < 0) return false;
+    if (b.count == 0) return true;
+    return b.data != NULL && b.stride >= world_bytes && b.world_offset <= b.stride - world_bytes
+        && (size_t)b.count <= SIZE_MAX / b.stride;
+}
+
+int host_word(const unsigned char* world, int k) {
+    int v;
+    memcpy(&v, world + (size_t)k * 4, 4);
+    return v;
+}
+
+/* Structural checks that keep every index the kernels follow in range. */
+bool world_valid(const unsigned char* wp, const Geometry& g) {
+    int nb = host_word(wp, H_BODY_COUNT), ns = host_word(wp, H_SHAPE_COUNT);
+    int nc = host_word(wp, H_CONTACT_COUNT), nj = host_word(wp, H_JOINT_COUNT);
+    if (nb < 0 || nb > g.max_b || ns < 0 || ns > g.max_s || nc < 0 || nc > g.max_c || nj < 0 || nj > g.max_j)
+        return false;
+    for (int s = 0; s < ns; s++) {
+        int b = host_word(wp, g.so + s * kShapeWords + S_BODY);
+        if (b < 0 || b >= nb) return false;
+    }
+    for (int j = 0; j < nj; j++) {
+        int a = host_word(wp, g.jo + j * kJointWords + J_BODY_A);
+        int b = host_word(wp, g.jo + j * kJointWords + J_BODY_B);
+        if (a < 0 || a >= nb || b < 0 || b >= nb) return false;
+    }
+    for (int c = 0; c < nc; c++) {
+        int base = g.co + c * kContactWords;
+        int sa = host_word(wp, base + C_SHAPE_A), sb = host_word(wp, base + C_SHAPE_B);
+        int ba = host_word(wp, base + C_BODY_A), bb = host_word(wp, base + C_BODY_B);
+        int pc = host_word(wp, base + C_POINT_COUNT);
+        if (sa < 0 || sa >= ns || sb < 0 || sb >= ns || ba < 0 || ba >= nb || bb < 0 || bb >= nb || pc < 0
+                || pc > kMaxManifold)
+            return false;
+    }
+    return true;
+}
+
+/* Gather the batch's worlds into one contiguous host buffer. */
+unsigned char* gather(const B3Batch& b, size_t world_bytes) {
+    unsigned char* buf = (unsigned char*)malloc((size_t)b.count * world_bytes + 1);
+    if (!buf) return NULL;
+    for (int i = 0; i < b.count; i++)
+        memcpy(buf + (size_t)i * world_bytes,
+            (const unsigned char*)b.data + (size_t)i * b.stride + b.world_offset, world_bytes);
+    return buf;
+}
+
+hipError_t on_device(const B3Engine* e) {
+    int dev = -1;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    return dev == e->device ? hipSuccess : hipErrorInvalidDevice;
+}
+
+/* Host AoS buffer -> staging -> tiles (dst). */
+hipError_t put_worlds(B3Engine* e, const unsigned char* host, uint32_t* dst) {
+    if (e->count == 0) return hipSuccess;
+    size_t bytes = (size_t)e->count * e->world_bytes;
+    hipError_t err = hipMemcpy(e->staging, host, bytes, hipMemcpyHostToDevice);
+    if (err != hipSuccess) return err;
+    dim3 grid((unsigned)((e->g.world_words + 63) / 64), (unsigned)e->tiles);
+    b3k_upload<<<grid, kXposeThreads>>>((const uint32_t*)e->staging, dst, e->count, e->g.world_words);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    return hipDeviceSynchronize();
+}
+
+}  // namespace
+
+extern "C" {
+
+hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long config_signature) {
+    if (!out) return hipErrorInvalidValue;
+    *out = NULL;
+    Geometry g;
+    size_t world_bytes;
+    if (!geometry_of(config_signature, &g, &world_bytes)) return hipErrorInvalidValue;
+    if (!batch_valid(worlds, world_bytes)) return hipErrorInvalidValue;
+    size_t lds = (size_t)g.max_b * kVelWords * kLanes * sizeof(float);
+    if (lds > 160u * 1024u) return hipErrorInvalidValue;
+    for (int i = 0; i < worlds.count; i++) {
+        const unsigned char* wp = (const unsigned char*)worlds.data + (size_t)i * worlds.stride + worlds.world_offset;
+        if (!world_valid(wp, g)) return hipErrorInvalidValue;
+    }
+    B3Engine* e = (B3Engine*)calloc(1, sizeof(B3Engine));
+    if (!e) return hipErrorOutOfMemory;
+    hipError_t err = hipGetDevice(&e->device);
+    if (err != hipSuccess) {
+        free(e);
+        return err;
+    }
+    e->count = worlds.count;
+    e->tiles = (worlds.count + 63) / 64;
+    e->sig = config_signature;
+    e->g = g;
+    e->world_bytes = world_bytes;
+    e->tile_words = (size_t)g.world_words * 64;
+    e->lds_bytes = lds;
+    if (lds > 64u * 1024u) {
+        err = hipFuncSetAttribute((const void*)b3k_step, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (err != hipSuccess) {
+            free(e);
+            return err;
+        }
+    }
+    if (e->tiles > 0) {
+        size_t tiles_bytes = (size_t)e->tiles * e->tile_words * 4;
+        if ((err = hipMalloc((void**)&e->live, tiles_bytes)) != hipSuccess
+                || (err = hipMalloc((void**)&e->snap, tiles_bytes)) != hipSuccess
+                || (err = hipMalloc((void**)&e->scratch, (size_t)e->tiles * g.scr_words * 64 * 4)) != hipSuccess
+                || (err = hipMalloc((void**)&e->staging, (size_t)e->count * world_bytes)) != hipSuccess) {
+            (void)b3_engine_destroy(e);
+            return err;
+        }
+        unsigned char* host = gather(worlds, world_bytes);
+        if (!host) {
+            (void)b3_engine_destroy(e);
+            return hipErrorOutOfMemory;
+        }
+        /* Snapshots default to the initial worlds. */
+        err = put_worlds(e, host, e->live);
+        if (err == hipSuccess) err = put_worlds(e, host, e->snap);
+        free(host);
+        if (err != hipSuccess) {
+            (void)b3_engine_destroy(e);
+            return err;
+        }
+    }
+    *out = e;
+    return hipSuccess;
+}
+
+hipError_t b3_engine_destroy(B3Engine* e) {
+    if (!e) return hipSuccess;
+    hipError_t first = hipSuccess;
+    void* bufs[4] = {e->live, e->snap, e->scratch, e->staging};
+    for (void* p : bufs) {
+        if (!p) continue;
+        hipError_t err = hipFree(p);
+        if (first == hipSuccess) first = err;
+    }
+    free(e);
+    return first;
+}
+
+int b3_engine_count(const B3Engine* e) { return e ? e->count : -1; }
+
+hipError_t b3_engine_set_snapshots(B3Engine* e, const void* initial) {
+    if (!e || (e->count && !initial)) return hipErrorInvalidValue;
+    hipError_t err = on_device(e);
+    if (err != hipSuccess) return err;
+    for (int i = 0; i < e->count; i++)
+        if (!world_valid((const unsigned char*)initial + (size_t)i * e->world_bytes, e->g)) return hipErrorInvalidValue;
+    return put_worlds(e, (const unsigned char*)initial, e->snap);
+}
+
+hipError_t b3_engine_upload(B3Engine* e, B3Batch worlds) {
+    if (!e || !batch_valid(worlds, e->world_bytes) || worlds.count != e->count) return hipErrorInvalidValue;
+    hipError_t err = on_device(e);
+    if (err != hipSuccess) return err;
+    for (int i = 0; i < worlds.count; i++) {
+        const unsigned char* wp = (const unsigned char*)worlds.data + (size_t)i * worlds.stride + worlds.world_offset;
+        if (!world_valid(wp, e->g)) return hipErrorInvalidValue;
+    }
+    if (e->count == 0) return hipSuccess;
+    unsigned char* host = gather(worlds, e->world_bytes);
+    if (!host) return hipErrorOutOfMemory;
+    err = put_worlds(e, host, e->live);
+    free(host);
+    return err;
+}
+
+hipError_t b3_engine_download(B3Engine* e, B3Batch worlds) {
+    if (!e || !batch_valid(worlds, e->world_bytes) || worlds.count != e->count) return hipErrorInvalidValue;
+    hipError_t err = on_device(e);
+    if (err != hipSuccess) return err;
+    if (e->count == 0) return hipSuccess;
+    dim3 grid((unsigned)((e->g.world_words + 63) / 64), (unsigned)e->tiles);
+    b3k_download<<<grid, kXposeThreads>>>(e->live, (uint32_t*)e->staging, e->count, e->g.world_words);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    unsigned char* host = (unsigned char*)malloc((size_t)e->count * e->world_bytes);
+    if (!host) return hipErrorOutOfMemory;
+    err = hipMemcpy(host, e->staging, (size_t)e->count * e->world_bytes, hipMemcpyDeviceToHost);
+    if (err == hipSuccess) {
+        for (int i = 0; i < e->count; i++)
+            memcpy((unsigned char*)worlds.data + (size_t)i * worlds.stride + worlds.world_offset,
+                host + (size_t)i * e->world_bytes, e->world_bytes);
+    }
+    free(host);
+    return err;
+}
+
+hipError_t b3_batch_restore_gpu(B3Engine* e, const unsigned char* reset, hipStream_t stream) {
+    if (!e) return hipErrorInvalidValue;
+    if (e->count == 0) return hipSuccess;
+    hipError_t err = on_device(e);
+    if (err != hipSuccess) return err;
+    if (!reset) {
+        /* NULL restores every world: one device-to-device copy. */
+        err = hipMemcpyAsync(e->live, e->snap, (size_t)e->tiles * e->tile_words * 4, hipMemcpyDeviceToDevice, stream);
+        return err;
+    }
+    b3k_restore<<<e->tiles, 64, 0, stream>>>(e->live, e->snap, e->g, e->count, reset);
+    return hipGetLastError();
+}
+
+hipError_t b3_batch_step_gpu(B3Engine* e, float dt, int substeps, const unsigned char* step_mask,
+        const unsigned char* reset_mask, hipStream_t stream) {
+    if (!e || !isfinite(dt) || dt < 0.0f || substeps < 1) return hipErrorInvalidValue;
+    if (e->count == 0) return hipSuccess;
+    hipError_t err = on_device(e);
+    if (err != hipSuccess) return err;
+    if (dt == 0.0f) return reset_mask ? b3_batch_restore_gpu(e, reset_mask, stream) : hipSuccess;
+    b3k_step<<<e->tiles, 64, e->lds_bytes, stream>>>(e->live, e->snap, e->scratch, e->g, e->count, dt, substeps,
+        step_mask, reset_mask);
+    return hipGetLastError();
+}
+
+hipError_t b3_batch_apply_gpu(B3Engine* e, const float* force, const float* torque, const float* linear_impulse,
+        const unsigned char* mask, hipStream_t stream) {
+    if (!e) return hipErrorInvalidValue;
+    if (e->count == 0 || (!force && !torque && !linear_impulse)) return hipSuccess;
+    hipError_t err = on_device(e);
+    if (err != hipSuccess) return err;
+    b3k_apply<<<e->tiles, 64, 0, stream>>>(e->live, e->g, e->count, force, torque, linear_impulse, mask);
+    return hipGetLastError();
+}
+
+hipError_t b3_batch_stats_gpu(B3Engine* e, B3StepStats* out, hipStream_t stream) {
+    if (!e || (e->count && !out)) return hipErrorInvalidValue;
+    if (e->count == 0) return hipSuccess;
+    hipError_t err = on_device(e);
+    if (err != hipSuccess) return err;
+    b3k_stats<<<e->tiles, 64, 0, stream>>>(e->live, e->g, e->count, out);
+    return hipGetLastError();
+}
+
+hipError_t b3_engine_device_view(const B3Engine* e, void** tiles, size_t* world_words) {
+    if (!e || !tiles || !world_words) return hipErrorInvalidValue;
+    *tiles = e->live;
+    *world_words = (size_t)e->g.world_words;
+    return hipSuccess;
+}
+
+}  // extern "C"

@@ -1,0 +1,146 @@
+"""Python binding of the engine's C ABI (include/b3_engine.h).
+
+Mirrors the reference's batch interface (b3_batch.cuh:12-99): the
+module-level b3_batch_* functions take the same arguments with the same
+meaning and return the hipError_t code (0 = hipSuccess), never raising;
+`B3Engine` wraps them for Python callers and raises `B3Error` instead.
+Masks and input arrays are torch tensors on the engine's device (or raw
+device pointers); `stream` is a torch.cuda.Stream, a raw hipStream_t, or
+None for the current torch stream.  PyTorch only supplies device memory
+and streams: every physics operation runs in libb3engine.so.
+"""
+import ctypes as C
+
+import numpy as np
+
+from . import _native
+from .b3types import B3StepStats, batch_of, world_dtype
+
+HIP_SUCCESS = 0
+HIP_ERROR_INVALID_VALUE = 1
+
+
+class B3Error(RuntimeError):
+    def __init__(self, call, code):
+        super().__init__("%s failed with hipError_t %d" % (call, code))
+        self.code = code
+
+
+def _ptr(x):
+    """Device pointer of a tensor / integer / None."""
+    if x is None:
+        return None
+    if isinstance(x, int):
+        return x
+    return x.data_ptr()
+
+
+def _stream(s):
+    if s is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(s, int):
+        return s
+    return s.cuda_stream
+
+
+def b3_engine_create(worlds, sig):
+    """(code, handle) for a contiguous numpy array of host worlds."""
+    h = C.c_void_p()
+    code = _native.engine_lib().b3_engine_create(C.byref(h), batch_of(worlds), sig)
+    return code, h
+
+
+def b3_batch_step_gpu(engine, dt, substeps, step_mask=None, reset_mask=None, stream=None):
+    """Fused masked restore + masked step (b3_batch_step_gpu, b3_batch.cuh:81-89)."""
+    return _native.engine_lib().b3_batch_step_gpu(engine, dt, substeps, _ptr(step_mask), _ptr(reset_mask),
+                                                  _stream(stream))
+
+
+def b3_batch_restore_gpu(engine, reset=None, stream=None):
+    """Masked snapshot restore (b3_batch_restore_gpu, b3_batch.cuh:91-99)."""
+    return _native.engine_lib().b3_batch_restore_gpu(engine, _ptr(reset), _stream(stream))
+
+
+def b3_batch_apply_gpu(engine, force=None, torque=None, linear_impulse=None, mask=None, stream=None):
+    """Dense b3_apply_force / b3_apply_torque / b3_apply_linear_impulse (09_step.inl:132-146)."""
+    return _native.engine_lib().b3_batch_apply_gpu(engine, _ptr(force), _ptr(torque), _ptr(linear_impulse),
+                                                   _ptr(mask), _stream(stream))
+
+
+class B3Engine:
+    """A batch of worlds resident on the current HIP device."""
+
+    def __init__(self, worlds, sig):
+        worlds = np.ascontiguousarray(worlds)
+        if worlds.dtype != world_dtype(sig):
+            raise ValueError("worlds do not have the B3World layout of signature %#x" % sig)
+        self.sig = sig
+        self.dtype = worlds.dtype
+        self.count = len(worlds)
+        code, self._h = b3_engine_create(worlds, sig)
+        if code != HIP_SUCCESS:
+            raise B3Error("b3_engine_create", code)
+        self._lib = _native.engine_lib()
+
+    @property
+    def handle(self):
+        return self._h
+
+    def _check(self, name, code):
+        if code != HIP_SUCCESS:
+            raise B3Error(name, code)
+
+    def close(self):
+        if self._h:
+            code = self._lib.b3_engine_destroy(self._h)
+            self._h = C.c_void_p()
+            self._check("b3_engine_destroy", code)
+
+    def __del__(self):
+        try:
+            if getattr(self, "_h", None):
+                self._lib.b3_engine_destroy(self._h)
+                self._h = C.c_void_p()
+        except Exception:
+            pass
+
+    def set_snapshots(self, worlds):
+        worlds = np.ascontiguousarray(worlds, dtype=self.dtype)
+        if len(worlds) != self.count:
+            raise ValueError("need %d snapshots" % self.count)
+        self._check("b3_engine_set_snapshots", self._lib.b3_engine_set_snapshots(self._h, worlds.ctypes.data))
+
+    def upload(self, worlds):
+        worlds = np.ascontiguousarray(worlds, dtype=self.dtype)
+        self._check("b3_engine_upload", self._lib.b3_engine_upload(self._h, batch_of(worlds)))
+
+    def download(self):
+        out = np.zeros(self.count, dtype=self.dtype)
+        self._check("b3_engine_download", self._lib.b3_engine_download(self._h, batch_of(out)))
+        return out
+
+    def step(self, dt, substeps, step_mask=None, reset_mask=None, stream=None):
+        self._check("b3_batch_step_gpu", b3_batch_step_gpu(self._h, dt, substeps, step_mask, reset_mask, stream))
+
+    def restore(self, reset=None, stream=None):
+        self._check("b3_batch_restore_gpu", b3_batch_restore_gpu(self._h, reset, stream))
+
+    def apply(self, force=None, torque=None, linear_impulse=None, mask=None, stream=None):
+        self._check("b3_batch_apply_gpu", b3_batch_apply_gpu(self._h, force, torque, linear_impulse, mask, stream))
+
+    def stats(self, stream=None):
+        """Per-world B3StepStats as a numpy structured array (synchronises)."""
+        import torch
+        out = torch.zeros(self.count * C.sizeof(B3StepStats), dtype=torch.uint8, device="cuda")
+        self._check("b3_batch_stats_gpu", self._lib.b3_batch_stats_gpu(self._h, out.data_ptr(), _stream(stream)))
+        torch.cuda.synchronize()
+        return out.cpu().numpy().view(np.dtype(B3StepStats))
+
+    def scene_masks(self, scene, seed, step, reset_out, step_out, stream=None):
+        self._check("b3w_masks_gpu", self._lib.b3w_masks_gpu(scene, seed, step, self.count, _ptr(reset_out),
+                                                             _ptr(step_out), _stream(stream)))
+
+    def scene_inputs(self, scene, seed, step, step_mask=None, stream=None):
+        self._check("b3w_inputs_gpu", self._lib.b3w_inputs_gpu(self._h, scene, seed, step, _ptr(step_mask),
+                                                               _stream(stream)))

@@ -1,0 +1,109 @@
+/*
+ * b3emu.cpp - host build of the engine's per-lane step, for logic tests.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Compiles the same per-lane code the gfx950
+ * kernels run (puffysics_amd/csrc/b3d_lane.h, b3d_inputs.h) with g++ and
+ * drives it over word-transposed tiles one lane at a time, with a plain
+ * array standing in for the LDS velocity rows.  Built with
+ * -ffp-contract=off and glibc's atan2f it must match the oracle bit for
+ * bit, which pins the tile layout, the restore ranges and every index the
+ * kernels compute, on a machine without a GPU.  The engine library never
+ * links this file.
+ */
+#include <stdlib.h>
+#include <string.h>
+#include <vector>
+
+#include "b3d_inputs.h"
+#include "b3d_lane.h"
+
+using namespace b3d;
+
+extern "C" {
+
+/* words per world and per tile of scratch, or 0 for a bad signature */
+int emu_world_words(unsigned long long sig) {
+    Geometry g;
+    size_t wb;
+    return geometry_of(sig, &g, &wb) ? g.world_words : 0;
+}
+int emu_scratch_words(unsigned long long sig) {
+    Geometry g;
+    size_t wb;
+    return geometry_of(sig, &g, &wb) ? g.scr_words : 0;
+}
+
+void emu_upload(const uint32_t* aos, int count, unsigned long long sig, uint32_t* tiles) {
+    Geometry g;
+    size_t wb;
+    if (!geometry_of(sig, &g, &wb)) return;
+    int ntiles = (count + kLanes - 1) / kLanes;
+    memset(tiles, 0, (size_t)ntiles * g.world_words * kLanes * 4);
+    for (int w = 0; w < count; w++)
+        for (int k = 0; k < g.world_words; k++)
+            tiles[((size_t)(w / kLanes) * g.world_words + k) * kLanes + w % kLanes] = aos[(size_t)w * g.world_words + k];
+}
+
+void emu_download(const uint32_t* tiles, int count, unsigned long long sig, uint32_t* aos) {
+    Geometry g;
+    size_t wb;
+    if (!geometry_of(sig, &g, &wb)) return;
+    for (int w = 0; w < count; w++)
+        for (int k = 0; k < g.world_words; k++)
+            aos[(size_t)w * g.world_words + k] = tiles[((size_t)(w / kLanes) * g.world_words + k) * kLanes + w % kLanes];
+}
+
+void emu_restore(uint32_t* tiles, const uint32_t* snap, int count, unsigned long long sig, const unsigned char* reset) {
+    Geometry g;
+    size_t wb;
+    if (!geometry_of(sig, &g, &wb)) return;
+    for (int w = 0; w < count; w++) {
+        if (reset && !reset[w]) continue;
+        size_t base = (size_t)(w / kLanes) * g.world_words * kLanes + w % kLanes;
+        int lo[3], hi[3];
+        restore_ranges(g, (int)snap[base + (size_t)H_CONTACT_COUNT * kLanes], lo, hi);
+        for (int r = 0; r < 3; r++)
+            for (int k = lo[r]; k < hi[r]; k++) tiles[base + (size_t)k * kLanes] = snap[base + (size_t)k * kLanes];
+    }
+}
+
+static Lane lane_of(uint32_t* tiles, uint32_t* scratch, float* vel, const Geometry& g, int w) {
+    Lane L;
+    int t = w / kLanes, l = w % kLanes;
+    L.w = tiles + (size_t)t * g.world_words * kLanes + l;
+    L.scr = scratch ? scratch + (size_t)t * g.scr_words * kLanes + l : nullptr;
+    L.vel = vel ? vel + l : nullptr;
+    L.g = g;
+    return L;
+}
+
+void emu_step(uint32_t* tiles, int count, unsigned long long sig, float dt, int substeps,
+        const unsigned char* step_mask) {
+    Geometry g;
+    size_t wb;
+    if (!geometry_of(sig, &g, &wb)) return;
+    int ntiles = (count + kLanes - 1) / kLanes;
+    std::vector<uint32_t> scratch((size_t)ntiles * g.scr_words * kLanes);
+    std::vector<float> vel((size_t)g.max_b * kVelWords * kLanes);
+    for (int w = 0; w < count; w++) {
+        if (step_mask && !step_mask[w]) continue;
+        Lane L = lane_of(tiles, scratch.data(), vel.data(), g, w);
+        vel_load(L);
+        step_world(L, dt, substeps);
+        vel_store(L);
+    }
+}
+
+void emu_inputs(uint32_t* tiles, int count, unsigned long long sig, int scene, unsigned long long seed, int step,
+        const unsigned char* step_mask) {
+    Geometry g;
+    size_t wb;
+    if (!geometry_of(sig, &g, &wb)) return;
+    for (int w = 0; w < count; w++) {
+        if (step_mask && !step_mask[w]) continue;
+        Lane L = lane_of(tiles, nullptr, nullptr, g, w);
+        scene_inputs(L, scene, seed, w, step);
+    }
+}
+
+}  // extern "C"

@@ -1,0 +1,210 @@
+"""GPU engine against the oracle (the reference's b3_step restated on the CPU).
+
+Everything runs through the C ABI of libb3engine.so.  Tolerances are the
+parity contract of the engine:
+  - contact pairs, point counts and feature ids bit-exact;
+  - single-step body state within 1e-4 relative / 1e-5 absolute;
+  - over long runs, batch means of per-world mean height and mean energy
+    within 1%.
+Scenes without hinges do not call atan2f, the only libm function on the
+step path whose device implementation differs from glibc's, so for them
+the device result must be bit-identical to the oracle's.
+"""
+import numpy as np
+import pytest
+
+from b3test import clone, diff_words, oracle_run, words
+from puffysics_amd import scenes
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+def _engine(worlds, scene):
+    from puffysics_amd.engine import B3Engine
+    return B3Engine(worlds, scenes.SCENES[scene].sig)
+
+
+def gpu_run(eng, scene, t0, nsteps, seed=scenes.SEED):
+    """The workload loop on the device: masks, restore, inputs, step."""
+    sc = scenes.SCENES[scene]
+    reset = torch.zeros(eng.count, dtype=torch.uint8, device="cuda")
+    stepm = torch.zeros(eng.count, dtype=torch.uint8, device="cuda")
+    for t in range(t0, t0 + nsteps):
+        eng.scene_masks(scene, seed, t, reset, stepm)
+        eng.restore(reset)
+        eng.scene_inputs(scene, seed, t, stepm)
+        eng.step(sc.dt, sc.substeps, stepm)
+    torch.cuda.synchronize()
+
+
+def describe(bad, got, ref, initial):
+    """First differing words with the device, oracle and initial values."""
+    wg, wr, wi = words(got), words(ref), words(initial)
+    rows = ["world %d word %d: device %08x oracle %08x initial %08x" % (i, k, wg[i, k], wr[i, k], wi[i, k])
+            for i, k in bad[:8]]
+    return "%d differing words in worlds %s\n%s" % (len(bad), np.unique(bad[:, 0])[:20].tolist(), "\n".join(rows))
+
+
+def contact_keys(worlds):
+    """(world, contact, shape_a, shape_b, point_count, features...) rows."""
+    rows = []
+    for i, w in enumerate(worlds):
+        for c in range(int(w["contact_count"])):
+            ct = w["contacts"][c]
+            pc = int(ct["point_count"])
+            feats = tuple(int(ct["points"][p]["feature"]) for p in range(pc))
+            rows.append((i, c, int(ct["shape_a"]), int(ct["shape_b"]), pc) + feats)
+    return rows
+
+
+def body_state(worlds):
+    b = worlds["bodies"]
+    cols = []
+    for f in ("position", "center", "lin_vel", "ang_vel"):
+        cols += [b[f][a] for a in "xyz"]
+    cols += [b["rotation"]["v"][a] for a in "xyz"] + [b["rotation"]["s"]]
+    return np.stack(cols, axis=-1)
+
+
+def assert_close_state(got, ref, rel=1e-4, abs_=1e-5):
+    g, r = body_state(got), body_state(ref)
+    err = np.abs(g - r)
+    ok = err <= abs_ + rel * np.abs(r)
+    assert ok.all(), "max err %g at %s" % (err.max(), np.argwhere(~ok)[:5].tolist())
+
+
+@pytest.mark.parametrize("scene,count,steps", [(1, 200, 120), (2, 200, 130), (4, 130, 60)])
+def test_contact_scenes_bit_exact(scene, count, steps):
+    worlds = scenes.build(scene, count)
+    eng = _engine(worlds, scene)
+    ref = clone(worlds)
+    oracle_run(scene, ref, clone(worlds), 0, steps, threads=8)
+    gpu_run(eng, scene, 0, steps)
+    got = eng.download()
+    bad = diff_words(got, ref, scenes.SCENES[scene].sig)
+    assert len(bad) == 0, describe(bad, got, ref, worlds)
+
+
+@pytest.mark.parametrize("scene,count", [(1, 130), (2, 130), (3, 130), (4, 70), (5, 200)])
+def test_single_step_parity(scene, count):
+    worlds = scenes.build(scene, count)
+    # advance a little on the oracle so contacts and warm starts exist
+    warm = 30 if scene != 4 else 20
+    oracle_run(scene, worlds, clone(worlds), 0, warm, threads=8)
+    fresh = scenes.build(scene, count)
+    eng = _engine(worlds, scene)
+    eng.set_snapshots(fresh)
+    ref = clone(worlds)
+    oracle_run(scene, ref, fresh, warm, 1)
+    gpu_run(eng, scene, warm, 1)
+    got = eng.download()
+    assert contact_keys(got) == contact_keys(ref)
+    assert_close_state(got, ref)
+
+
+def world_stats(worlds, gravity=9.81):
+    """Per-world mean height and mean (kinetic + potential) energy of the
+    dynamic bodies."""
+    b = worlds["bodies"]
+    dyn = b["type"] == 2
+    inv_m = b["inv_mass"]
+    m = np.where(inv_m > 0, 1.0 / np.where(inv_m > 0, inv_m, 1.0), 0.0)
+    v2 = sum(b["lin_vel"][a].astype(np.float64) ** 2 for a in "xyz")
+    y = b["center"]["y"].astype(np.float64)
+    e = 0.5 * m * v2 + m * gravity * y
+    n = np.maximum(dyn.sum(axis=1), 1)
+    return (np.where(dyn, y, 0).sum(axis=1) / n, np.where(dyn, e, 0).sum(axis=1) / n)
+
+
+@pytest.mark.parametrize("scene,count,steps", [(1, 128, 1000), (2, 128, 1000), (3, 128, 1000), (4, 64, 2000),
+                                               (5, 256, 1000)])
+def test_long_run_aggregates(scene, count, steps):
+    worlds = scenes.build(scene, count)
+    eng = _engine(worlds, scene)
+    ref = clone(worlds)
+    initial = clone(worlds)
+    chunk = 100
+    hg, hr, eg, er = [], [], [], []
+    for t0 in range(0, steps, chunk):
+        oracle_run(scene, ref, initial, t0, chunk, threads=8)
+        gpu_run(eng, scene, t0, chunk)
+        got = eng.download()
+        a, b = world_stats(got), world_stats(ref)
+        hg.append(a[0]); eg.append(a[1]); hr.append(b[0]); er.append(b[1])
+    hg, hr, eg, er = (np.mean(x, axis=0) for x in (hg, hr, eg, er))
+    assert abs(hg.mean() - hr.mean()) <= 0.01 * abs(hr.mean())
+    assert abs(eg.mean() - er.mean()) <= 0.01 * abs(er.mean())
+
+
+def test_fused_reset_equals_restore_then_step():
+    scene = 5
+    sc = scenes.SCENES[scene]
+    worlds = scenes.build(scene, 192)
+    a = _engine(worlds, scene)
+    b = _engine(worlds, scene)
+    gpu_run(a, scene, 0, 5)
+    gpu_run(b, scene, 0, 5)
+    reset = torch.zeros(192, dtype=torch.uint8, device="cuda")
+    reset[::7] = 1
+    stepm = torch.ones(192, dtype=torch.uint8, device="cuda")
+    stepm[::3] = 0
+    a.step(sc.dt, sc.substeps, stepm, reset)
+    b.restore(reset)
+    b.step(sc.dt, sc.substeps, stepm)
+    torch.cuda.synchronize()
+    assert len(diff_words(a.download(), b.download(), sc.sig)) == 0
+
+
+def test_apply_matches_host_apply():
+    scene = 2
+    sc = scenes.SCENES[scene]
+    worlds = scenes.build(scene, 96)
+    eng = _engine(worlds, scene)
+    nb = sc.caps[0]
+    g = torch.Generator().manual_seed(3)
+    f = torch.randn(96, nb, 3, generator=g)
+    tq = torch.randn(96, nb, 3, generator=g)
+    imp = torch.randn(96, nb, 3, generator=g)
+    mask = (torch.arange(96) % 4 != 1).to(torch.uint8)
+    eng.apply(f.cuda(), tq.cuda(), imp.cuda(), mask.cuda())
+    torch.cuda.synchronize()
+    got = eng.download()
+    ref = clone(worlds)
+    fn, tn, pn = f.numpy(), tq.numpy(), imp.numpy()
+    live = np.arange(nb)[None, :] < ref["body_count"][:, None]
+    sel = mask.numpy().astype(bool)[:, None] & live
+    dyn = sel & (ref["bodies"]["type"] == 2)
+    for k, a in enumerate("xyz"):
+        F = ref["bodies"]["force"][a]
+        F[sel] = (F + fn[:, :, k])[sel]
+        T = ref["bodies"]["torque"][a]
+        T[sel] = (T + tn[:, :, k])[sel]
+        V = ref["bodies"]["lin_vel"][a]
+        V[dyn] = (V + ref["bodies"]["inv_mass"] * pn[:, :, k])[dyn]
+    assert len(diff_words(got, ref, sc.sig)) == 0
+
+
+def test_stats_match_worlds():
+    scene = 4
+    worlds = scenes.build(scene, 70)
+    eng = _engine(worlds, scene)
+    gpu_run(eng, scene, 0, 30)
+    st = eng.stats()
+    got = eng.download()
+    assert (st["contact_count"] == got["contact_count"]).all()
+    assert (st["body_count"] == got["body_count"]).all()
+    assert (st["contacts_dropped"] == got["contacts_dropped"]).all()
+
+
+def test_invalid_arguments_do_not_launch():
+    from puffysics_amd.engine import b3_batch_step_gpu, HIP_ERROR_INVALID_VALUE
+    scene = 1
+    worlds = scenes.build(scene, 64)
+    eng = _engine(worlds, scene)
+    before = eng.download()
+    for dt, subs in ((float("nan"), 4), (-1.0, 4), (float("inf"), 4), (1.0 / 60, 0)):
+        assert b3_batch_step_gpu(eng.handle, dt, subs) == HIP_ERROR_INVALID_VALUE
+    assert b3_batch_step_gpu(eng.handle, 0.0, 4) == 0
+    torch.cuda.synchronize()
+    assert (eng.download().view(np.uint8) == before.view(np.uint8)).all()
