@@ -13,7 +13,8 @@
  *   b3k_restore                masked snapshot restore; the wave copies one
  *                              resetting world at a time with all 64 lanes
  *   b3k_step                   optional fused restore, then one b3_step per
- *                              selected lane with body velocities in LDS
+ *                              selected lane; LDS holds the lane's clip
+ *                              polygons, then its body velocities
  *   b3k_apply                  dense force / torque / impulse inputs
  *   b3k_stats                  per-world B3StepStats
  */
@@ -127,9 +128,7 @@ __global__ __launch_bounds__(64) void b3k_step(uint32_t* live, const uint32_t* s
     L.scr = scratch + (size_t)tile * g.scr_words * 64 + lane;
     L.vel = vel_rows + lane;
     L.g = g;
-    vel_load(L);
     step_world(L, dt, substeps);
-    vel_store(L);
 }
 
 /* ---- inputs and stats ---- */
@@ -263,7 +262,7 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
     size_t world_bytes;
     if (!geometry_of(config_signature, &g, &world_bytes)) return hipErrorInvalidValue;
     if (!batch_valid(worlds, world_bytes)) return hipErrorInvalidValue;
-    size_t lds = (size_t)g.max_b * kVelWords * kLanes * sizeof(float);
+    size_t lds = (size_t)lds_rows(g) * kLanes * sizeof(float);
     if (lds > 160u * 1024u) return hipErrorInvalidValue;
     for (int i = 0; i < worlds.count; i++) {
         const unsigned char* wp = (const unsigned char*)worlds.data + (size_t)i * worlds.stride + worlds.world_offset;

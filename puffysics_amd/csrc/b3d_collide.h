@@ -10,8 +10,8 @@
  *   capsule-box 5, box-box SAT axis 0..14 (edge axes give one support
  *   point), clipped incident-face points 16+i (reference face on A) or
  *   20+i (reference face on B).
- * All state lives in registers; the clip polygons are two 8-vertex arrays
- * that the compiler keeps in scratch or registers.
+ * The manifold lives in registers; the two 8-vertex clip polygons of the
+ * box-box path live in a caller-provided per-lane buffer (LDS on the GPU).
  */
 #ifndef PUFFYSICS_AMD_B3D_COLLIDE_H
 #define PUFFYSICS_AMD_B3D_COLLIDE_H
@@ -43,13 +43,20 @@ struct Posed {
 };
 
 B3D_FN void mani_clear(Mani* m) { m->count = 0; m->normal = v3(0.0f, 1.0f, 0.0f); }
+/* Append a point.  Slots are selected with constant indices so that the
+ * manifold stays in registers. */
 B3D_FN void mani_push(Mani* m, V3 pa, V3 pb, float sep, uint32_t feat) {
     if (m->count >= kMaxManifold) return;
-    int i = m->count++;
-    m->p_a[i] = pa;
-    m->p_b[i] = pb;
-    m->sep[i] = sep;
-    m->feature[i] = feat;
+#pragma unroll
+    for (int k = 0; k < kMaxManifold; k++) {
+        if (k == m->count) {
+            m->p_a[k] = pa;
+            m->p_b[k] = pb;
+            m->sep[k] = sep;
+            m->feature[k] = feat;
+        }
+    }
+    m->count++;
 }
 
 /* Closest point to p on segment ab (05_collision.inl:5-13). */
@@ -193,44 +200,74 @@ B3D_FN Obb make_obb(V3 c, Q q, V3 h) {
     return o;
 }
 B3D_FN float half_i(V3 h, int i) { return i == 0 ? h.x : (i == 1 ? h.y : h.z); }
+/* Field-wise choice between two boxes (a pointer select would force both
+ * into memory). */
+B3D_FN V3 vsel(bool c, V3 x, V3 y) { return v3(c ? x.x : y.x, c ? x.y : y.y, c ? x.z : y.z); }
+B3D_FN Obb obb_sel(bool c, const Obb* x, const Obb* y) {
+    Obb o;
+    o.c = vsel(c, x->c, y->c);
+    o.ax[0] = vsel(c, x->ax[0], y->ax[0]);
+    o.ax[1] = vsel(c, x->ax[1], y->ax[1]);
+    o.ax[2] = vsel(c, x->ax[2], y->ax[2]);
+    o.h = vsel(c, x->h, y->h);
+    return o;
+}
+/* Axis i of a box, selected without indexing so the box stays in registers. */
+B3D_FN V3 axis_i(const Obb* o, int i) { return i == 0 ? o->ax[0] : (i == 1 ? o->ax[1] : o->ax[2]); }
 B3D_FN V3 support(const Obb* o, V3 dir) {
     float sx = dot(o->ax[0], dir) < 0.0f ? -o->h.x : o->h.x;
     float sy = dot(o->ax[1], dir) < 0.0f ? -o->h.y : o->h.y;
     float sz = dot(o->ax[2], dir) < 0.0f ? -o->h.z : o->h.z;
     return add(o->c, add(scale(o->ax[0], sx), add(scale(o->ax[1], sy), scale(o->ax[2], sz))));
 }
+/* Clip polygons live in a per-lane buffer with a stride of 64 floats
+ * between consecutive words (LDS on the GPU): vertex i of a polygon at
+ * words 3i..3i+2.  Two polygons of kClipVerts vertices are used. */
+constexpr int kClipVerts = 8;
+constexpr int kClipStride = 64;
+constexpr int kClipWords = 2 * 3 * kClipVerts;
+B3D_FN V3 clip_get(const float* poly, int i) {
+    const float* v = poly + 3 * i * kClipStride;
+    return v3(v[0], v[kClipStride], v[2 * kClipStride]);
+}
+B3D_FN void clip_put(float* poly, int i, V3 x) {
+    float* v = poly + 3 * i * kClipStride;
+    v[0] = x.x;
+    v[kClipStride] = x.y;
+    v[2 * kClipStride] = x.z;
+}
 /* Sutherland-Hodgman against one plane, at most 8 output vertices. */
-B3D_FN int clip_plane(const V3* in, int n, V3* out, V3 pn, float po) {
+B3D_FN int clip_plane(const float* in, int n, float* out, V3 pn, float po) {
     if (n <= 0) return 0;
     int c = 0;
-    V3 prev = in[n - 1];
+    V3 prev = clip_get(in, n - 1);
     float pd = dot(prev, pn) - po;
     int pin = pd <= 0.0f;
     for (int i = 0; i < n; i++) {
-        V3 cur = in[i];
+        V3 cur = clip_get(in, i);
         float cd = dot(cur, pn) - po;
         int cin = cd <= 0.0f;
-        if (cin != pin && c < 8) {
+        if (cin != pin && c < kClipVerts) {
             float t = pd / (pd - cd);
-            out[c++] = madd(prev, t, sub(cur, prev));
+            clip_put(out, c++, madd(prev, t, sub(cur, prev)));
         }
-        if (cin && c < 8) out[c++] = cur;
+        if (cin && c < kClipVerts) clip_put(out, c++, cur);
         prev = cur;
         pd = cd;
         pin = cin;
     }
     return c;
 }
-B3D_FN void face_pts(const Obb* o, int axis, float sign, V3 out[4]) {
+B3D_FN void face_pts(const Obb* o, int axis, float sign, float* out) {
     int ta = (axis + 1) % 3;
     int tb = (axis + 2) % 3;
-    V3 c = madd(o->c, sign * half_i(o->h, axis), o->ax[axis]);
-    V3 a = scale(o->ax[ta], half_i(o->h, ta));
-    V3 b = scale(o->ax[tb], half_i(o->h, tb));
-    out[0] = sub(sub(c, a), b);
-    out[1] = add(sub(c, a), b);
-    out[2] = add(add(c, a), b);
-    out[3] = sub(add(c, a), b);
+    V3 c = madd(o->c, sign * half_i(o->h, axis), axis_i(o, axis));
+    V3 a = scale(axis_i(o, ta), half_i(o->h, ta));
+    V3 b = scale(axis_i(o, tb), half_i(o->h, tb));
+    clip_put(out, 0, sub(sub(c, a), b));
+    clip_put(out, 1, add(sub(c, a), b));
+    clip_put(out, 2, add(add(c, a), b));
+    clip_put(out, 3, sub(add(c, a), b));
 }
 B3D_FN int best_axis(const Obb* o, V3 n) {
     float b0 = fabsf(dot(o->ax[0], n));
@@ -271,8 +308,8 @@ B3D_FN int try_edge(float e, float ra, float rb, V3 cr, float* best, V3* n, int 
 }
 
 /* 15-axis SAT, then reference-face clipping or a support-point pair
- * (05_collision.inl:295-461). */
-B3D_FN void collide_boxes(Mani* m, const Obb* a, const Obb* b) {
+ * (05_collision.inl:295-461).  `clip` is the two-polygon buffer. */
+B3D_FN void collide_boxes(Mani* m, const Obb* a, const Obb* b, float* clip) {
     mani_clear(m);
     V3 d = sub(b->c, a->c);
     float t0 = dot(d, a->ax[0]), t1 = dot(d, a->ax[1]), t2 = dot(d, a->ax[2]);
@@ -314,27 +351,31 @@ B3D_FN void collide_boxes(Mani* m, const Obb* a, const Obb* b) {
         mani_support(m, a, b, n, feat);
         return;
     }
-    const Obb* ref = feat < 3 ? a : b;
-    const Obb* inc = feat < 3 ? b : a;
+    Obb ref = obb_sel(feat < 3, a, b);
+    Obb inc = obb_sel(feat < 3, b, a);
     int ref_axis = feat < 3 ? feat : feat - 3;
-    float rd = dot(ref->ax[ref_axis], n);
+    V3 ref_ax = axis_i(&ref, ref_axis);
+    float rd = dot(ref_ax, n);
     float ref_sign = (feat < 3 ? rd < 0.0f : rd > 0.0f) ? -1.0f : 1.0f;
-    V3 rn = scale(ref->ax[ref_axis], ref_sign);
-    int inc_axis = best_axis(inc, rn);
-    float inc_sign = dot(inc->ax[inc_axis], rn) > 0.0f ? -1.0f : 1.0f;
-    V3 poly[8], tmp[8];
-    face_pts(inc, inc_axis, inc_sign, poly);
+    V3 rn = scale(ref_ax, ref_sign);
+    int inc_axis = best_axis(&inc, rn);
+    float inc_sign = dot(axis_i(&inc, inc_axis), rn) > 0.0f ? -1.0f : 1.0f;
+    float* poly = clip;
+    float* tmp = clip + 3 * kClipVerts * kClipStride;
+    face_pts(&inc, inc_axis, inc_sign, poly);
     int count = 4;
     int ta = (ref_axis + 1) % 3;
     int tb = (ref_axis + 2) % 3;
-    V3 face_c = madd(ref->c, ref_sign * half_i(ref->h, ref_axis), ref->ax[ref_axis]);
+    V3 face_c = madd(ref.c, ref_sign * half_i(ref.h, ref_axis), ref_ax);
     for (int i = 0; i < 4; i++) {
         int t = i < 2 ? ta : tb;
         float s = (i & 1) ? 1.0f : -1.0f;
-        V3 cn = scale(ref->ax[t], s);
-        float co = dot(cn, ref->c) + half_i(ref->h, t);
+        V3 cn = scale(axis_i(&ref, t), s);
+        float co = dot(cn, ref.c) + half_i(ref.h, t);
         count = clip_plane(poly, count, tmp, cn, co);
-        for (int k = 0; k < count; k++) poly[k] = tmp[k];
+        float* t2 = poly;
+        poly = tmp;
+        tmp = t2;
         if (count == 0) {
             mani_support(m, a, b, n, feat);
             return;
@@ -342,11 +383,12 @@ B3D_FN void collide_boxes(Mani* m, const Obb* a, const Obb* b) {
     }
     float ro = dot(rn, face_c);
     for (int i = 0; i < count && m->count < kMaxManifold; i++) {
-        float plane_s = dot(poly[i], rn) - ro;
+        V3 pv = clip_get(poly, i);
+        float plane_s = dot(pv, rn) - ro;
         if (plane_s <= kSpeculative) {
-            V3 on_ref = msub(poly[i], plane_s, rn);
-            V3 pa = feat < 3 ? on_ref : poly[i];
-            V3 pb = feat < 3 ? poly[i] : on_ref;
+            V3 on_ref = msub(pv, plane_s, rn);
+            V3 pa = feat < 3 ? on_ref : pv;
+            V3 pb = feat < 3 ? pv : on_ref;
             float sep = dot(sub(pb, pa), n);
             mani_push(m, pa, pb, sep, (feat < 3 ? 16u : 20u) + (uint32_t)i);
         }
@@ -356,16 +398,19 @@ B3D_FN void collide_boxes(Mani* m, const Obb* a, const Obb* b) {
 
 B3D_FN void mani_flip(Mani* m) {
     m->normal = neg(m->normal);
-    for (int i = 0; i < m->count; i++) {
-        V3 t = m->p_a[i];
-        m->p_a[i] = m->p_b[i];
-        m->p_b[i] = t;
+#pragma unroll
+    for (int i = 0; i < kMaxManifold; i++) {
+        if (i < m->count) {
+            V3 t = m->p_a[i];
+            m->p_a[i] = m->p_b[i];
+            m->p_b[i] = t;
+        }
     }
 }
 
 /* Type-ordered dispatch; the manifold comes back oriented A -> B with every
  * separation recomputed along the final normal (05_collision.inl:472-534). */
-B3D_FN void collide_pair(Mani* m, Posed A, Posed B) {
+B3D_FN void collide_pair(Mani* m, Posed A, Posed B, float* clip) {
     V3 center_a = A.p, center_b = B.p;
     int flip = 0;
     if (A.type > B.type) {
@@ -394,12 +439,14 @@ B3D_FN void collide_pair(Mani* m, Posed A, Posed B) {
     } else {
         Obb oa = make_obb(A.p, A.q, A.half);
         Obb ob = make_obb(B.p, B.q, B.half);
-        collide_boxes(m, &oa, &ob);
+        collide_boxes(m, &oa, &ob, clip);
     }
     if (flip && m->count > 0) mani_flip(m);
     if (m->count > 0) {
         if (dot(m->normal, sub(center_b, center_a)) < 0.0f) m->normal = neg(m->normal);
-        for (int i = 0; i < m->count; i++) m->sep[i] = dot(sub(m->p_b[i], m->p_a[i]), m->normal);
+#pragma unroll
+        for (int i = 0; i < kMaxManifold; i++)
+            if (i < m->count) m->sep[i] = dot(sub(m->p_b[i], m->p_a[i]), m->normal);
     }
 }
 

@@ -195,7 +195,24 @@ constexpr int J_SPRING_SOFTNESS = B3D_W(B3Joint, spring_softness);
 /* old warm-cache record in scratch (the reference's B3Warm, 02_types.inl:133-142) */
 constexpr int O_SHAPE_A = 0, O_SHAPE_B = 1, O_POINT_COUNT = 2, O_FEATURE = 3, O_NORMAL_IMPULSE = 7,
               O_FRICTION_IMPULSE = 11, O_TWIST_IMPULSE = 13, O_ROLLING_IMPULSE = 14, kOldWords = 17;
-constexpr int kAabbWords = 6;
+
+/* Per-step shape record in scratch: world pose, size, owning body and
+ * padded bounds, written once per step by the shape pass so that the pair
+ * loop never follows a body index. */
+constexpr int SS_P = 0, SS_Q = 3, SS_RADIUS = 7, SS_HALF = 8, SS_TYPE = 11, SS_BODY = 12, SS_BFLAGS = 13,
+              SS_LO = 14, SS_HI = 17, SS_CENTER = 20, kShapeScr = 23;
+constexpr int kBodyStatic = 1, kBodyDynamic = 2;   /* SS_BFLAGS bits */
+/* Contact point separations for the current delta poses. */
+constexpr int kSepScr = 4;
+/* Joint record in scratch: the joint-connection key and the hinge axis
+ * through each inverse inertia (per step), then everything that depends
+ * only on the bodies' delta poses (recomputed after every position
+ * update): twist angle, hinge perpendicular rows and their 2x2 mass, point
+ * anchors, point separation and the inverted 3x3 point mass, and the weld's
+ * angular error. */
+constexpr int JS_KEY = 0, JS_IA_AX = 1, JS_IB_AX = 4, JS_TW = 7, JS_RELX = 8, JS_RELY = 9, JS_PX = 10,
+              JS_PY = 13, JS_KXX = 16, JS_KYY = 17, JS_KXY = 18, JS_KINV2 = 19, JS_KOK = 20, JS_RA = 21,
+              JS_RB = 24, JS_PSEP = 27, JS_KINV = 30, JS_CV = 39, kJointScr = 42;
 
 constexpr int kStatic = 0, kKinematic = 1, kDynamic = 2;
 constexpr uint32_t kFlagDynamic = 0x00001000u;
@@ -209,7 +226,7 @@ struct Geometry {
     int max_b, max_s, max_c, max_j;
     int bo, so, co, jo;   /* word offsets of bodies, shapes, contacts, joints */
     int world_words;      /* words per world (sizeof(B3World) / 4) */
-    int scr_aabb, scr_old, scr_words;
+    int scr_shape, scr_old, scr_sep, scr_joint, scr_words;
 };
 
 /* Geometry of a capacity signature; false when it is invalid. */
@@ -226,9 +243,11 @@ B3D_FN bool geometry_of(unsigned long long sig, Geometry* g, size_t* world_bytes
     g->co = (int)(L.contacts_off / 4);
     g->jo = (int)(L.joints_off / 4);
     g->world_words = (int)(L.world_size / 4);
-    g->scr_aabb = 0;
-    g->scr_old = g->max_s * kAabbWords;
-    g->scr_words = g->scr_old + g->max_c * kOldWords;
+    g->scr_shape = 0;
+    g->scr_old = g->scr_shape + g->max_s * kShapeScr;
+    g->scr_sep = g->scr_old + g->max_c * kOldWords;
+    g->scr_joint = g->scr_sep + g->max_c * kSepScr;
+    g->scr_words = g->scr_joint + g->max_j * kJointScr;
     *world_bytes = L.world_size;
     return true;
 }
@@ -237,9 +256,16 @@ B3D_FN bool geometry_of(unsigned long long sig, Geometry* g, size_t* world_bytes
 struct Lane {
     uint32_t* w;    /* live tile + lane */
     uint32_t* scr;  /* scratch tile + lane */
-    float* vel;     /* velocity rows + lane */
+    float* vel;     /* velocity rows + lane; before the velocities are
+                       staged the same rows hold the clip polygons */
     Geometry g;
 };
+
+/* Words of LDS rows per lane that one step needs. */
+B3D_FN int lds_rows(const Geometry& g) {
+    int v = g.max_b * kVelWords;
+    return v > kClipWords ? v : kClipWords;
+}
 
 /* Word ranges [lo[i], hi[i]) that a snapshot restore copies: header,
  * bodies and shapes; the snapshot's live contacts; every joint slot.  These
@@ -343,31 +369,53 @@ B3D_FN void shape_aabb(const Posed& P, V3* lo, V3* hi) {
     *hi = add(P.p, e);
 }
 
-/* Is there a joint with collide_connected == 0 between bodies a and b? */
-B3D_FN int joined(const Lane& L, int nj, int a, int b) {
-    for (int i = 0; i < nj; i++) {
-        if (ldi(L.w, jw(L, i, J_COLLIDE_CONNECTED))) continue;
-        int ja = ldi(L.w, jw(L, i, J_BODY_A)), jb = ldi(L.w, jw(L, i, J_BODY_B));
-        if ((ja == a && jb == b) || (ja == b && jb == a)) return 1;
+B3D_FN uint32_t* shape_rec(const Lane& L, int s) { return L.scr + (L.g.scr_shape + s * kShapeScr) * kLanes; }
+B3D_FN uint32_t* old_rec(const Lane& L, int k) { return L.scr + (L.g.scr_old + k * kOldWords) * kLanes; }
+B3D_FN uint32_t* sep_rec(const Lane& L, int c) { return L.scr + (L.g.scr_sep + c * kSepScr) * kLanes; }
+B3D_FN uint32_t* joint_rec(const Lane& L, int j) { return L.scr + (L.g.scr_joint + j * kJointScr) * kLanes; }
+B3D_FN uint32_t pair_key(int a, int b) { return a < b ? ((uint32_t)a << 16) | (uint32_t)b : ((uint32_t)b << 16) | (uint32_t)a; }
+
+/* Shape pass: world pose, padded bounds and owning-body facts of every
+ * shape (b3_shape_aabb plus the 0.02 pad, 08_contacts.inl:109-114). */
+B3D_FN void shape_pass(const Lane& L, int ns) {
+    V3 pad = v3(kSpeculative, kSpeculative, kSpeculative);
+    for (int s = 0; s < ns; s++) {
+        int b = ldi(L.w, sw(L, s, S_BODY));
+        V3 bpos = ld3(L.w, bw(L, b, B_POSITION));
+        Q brot = ldq(L.w, bw(L, b, B_ROTATION));
+        V3 center = ld3(L.w, bw(L, b, B_CENTER));
+        int btype = ldi(L.w, bw(L, b, B_TYPE));
+        Posed P = pose_shape(L, s, bpos, brot);
+        V3 lo, hi;
+        shape_aabb(P, &lo, &hi);
+        uint32_t* r = shape_rec(L, s);
+        st3(r, SS_P, P.p);
+        stq(r, SS_Q, P.q);
+        stf(r, SS_RADIUS, P.radius);
+        st3(r, SS_HALF, P.half);
+        sti(r, SS_TYPE, P.type);
+        sti(r, SS_BODY, b);
+        sti(r, SS_BFLAGS, (btype == kStatic ? kBodyStatic : 0) | (btype == kDynamic ? kBodyDynamic : 0));
+        st3(r, SS_LO, sub(lo, pad));
+        st3(r, SS_HI, add(hi, pad));
+        st3(r, SS_CENTER, center);
     }
-    return 0;
 }
 
-struct BodyLite { V3 center; int type; float inv_mass; M3 inv_i; };
-
-B3D_FN BodyLite body_lite(const Lane& L, int b) {
-    BodyLite r;
-    r.center = ld3(L.w, bw(L, b, B_CENTER));
-    r.type = ldi(L.w, bw(L, b, B_TYPE));
-    r.inv_mass = ldf(L.w, bw(L, b, B_INV_MASS));
-    r.inv_i = ldm3(L.w, bw(L, b, B_INV_I_WORLD));
-    return r;
+B3D_FN Posed posed_from(const uint32_t* r) {
+    Posed P;
+    P.p = ld3(r, SS_P);
+    P.q = ldq(r, SS_Q);
+    P.radius = ldf(r, SS_RADIUS);
+    P.half = ld3(r, SS_HALF);
+    P.type = ldi(r, SS_TYPE);
+    return P;
 }
 
 /* Copy one contact's warm-start data into the old-cache scratch
  * (08_contacts.inl:65-91). */
 B3D_FN void save_old(const Lane& L, int k) {
-    uint32_t* o = L.scr + (L.g.scr_old + k * kOldWords) * kLanes;
+    uint32_t* o = old_rec(L, k);
     int pc = clampi(ldi(L.w, cw(L, k, C_POINT_COUNT)), 0, kMaxManifold);
     sti(o, O_SHAPE_A, ldi(L.w, cw(L, k, C_SHAPE_A)));
     sti(o, O_SHAPE_B, ldi(L.w, cw(L, k, C_SHAPE_B)));
@@ -398,11 +446,15 @@ struct NewContact {
 /* Take the impulses of old record k for the points whose feature matches
  * (08_contacts.inl:154-170; the last matching old point wins). */
 B3D_FN void warm_from_old(const Lane& L, int k, NewContact* nc) {
-    const uint32_t* o = L.scr + (L.g.scr_old + k * kOldWords) * kLanes;
+    const uint32_t* o = old_rec(L, k);
     int opc = ldi(o, O_POINT_COUNT);
-    for (int p = 0; p < nc->count; p++)
-        for (int q = 0; q < opc; q++)
-            if (nc->feature[p] == ldu(o, O_FEATURE + q)) nc->ni[p] = ldf(o, O_NORMAL_IMPULSE + q);
+#pragma unroll
+    for (int p = 0; p < kMaxManifold; p++) {
+        if (p >= nc->count) continue;
+#pragma unroll
+        for (int q = 0; q < kMaxManifold; q++)
+            if (q < opc && nc->feature[p] == ldu(o, O_FEATURE + q)) nc->ni[p] = ldf(o, O_NORMAL_IMPULSE + q);
+    }
     nc->fi.x = ldf(o, O_FRICTION_IMPULSE);
     nc->fi.y = ldf(o, O_FRICTION_IMPULSE + 1);
     nc->twist = ldf(o, O_TWIST_IMPULSE);
@@ -411,11 +463,10 @@ B3D_FN void warm_from_old(const Lane& L, int k, NewContact* nc) {
 
 B3D_FN int pair_less(int a0, int b0, int a1, int b1) { return a0 < a1 || (a0 == a1 && b0 < b1); }
 
-/* Contact generation, warm start and contact preparation for one world:
- * b3_find_contacts (08_contacts.inl:64-173) with b3_contact_from_mani
- * (08:5-39) and b3_prepare_one_contact (08:234-291) applied to each new
- * contact as it is produced. */
-B3D_FN void collide_and_prepare(const Lane& L, Soft cs, Soft ss) {
+/* Contact generation and warm start: b3_find_contacts (08_contacts.inl:
+ * 64-173) with b3_contact_from_mani (08:5-39).  The prepared fields are
+ * filled in by prepare_contacts. */
+B3D_FN void find_contacts(const Lane& L) {
     const Geometry& g = L.g;
     int old_n = clampi(ldi(L.w, H_CONTACT_COUNT), 0, g.max_c);
     int sorted = 1;
@@ -429,47 +480,45 @@ B3D_FN void collide_and_prepare(const Lane& L, Soft cs, Soft ss) {
     }
     int ns = clampi(ldi(L.w, H_SHAPE_COUNT), 0, g.max_s);
     int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, g.max_j);
-    V3 pad = v3(kSpeculative, kSpeculative, kSpeculative);
-    for (int s = 0; s < ns; s++) {
-        int b = ldi(L.w, sw(L, s, S_BODY));
-        Posed P = pose_shape(L, s, ld3(L.w, bw(L, b, B_POSITION)), ldq(L.w, bw(L, b, B_ROTATION)));
-        V3 lo, hi;
-        shape_aabb(P, &lo, &hi);
-        uint32_t* a = L.scr + (g.scr_aabb + s * kAabbWords) * kLanes;
-        st3(a, 0, sub(lo, pad));
-        st3(a, 3, add(hi, pad));
+    shape_pass(L, ns);
+    /* joint-connected body pairs (08:95-108) as sorted-pair keys */
+    for (int j = 0; j < nj; j++) {
+        uint32_t key = 0xffffffffu;
+        if (!ldi(L.w, jw(L, j, J_COLLIDE_CONNECTED)))
+            key = pair_key(ldi(L.w, jw(L, j, J_BODY_A)), ldi(L.w, jw(L, j, J_BODY_B)));
+        sti(joint_rec(L, j), JS_KEY, (int)key);
     }
     int cc = 0;
     int overflow = ldi(L.w, H_CONTACT_OVERFLOW);
     int dropped = ldi(L.w, H_CONTACTS_DROPPED);
     int optr = 0;
-    const float inv_tau = 1.0f / kSpeculative;
     for (int i = 0; i < ns; i++) {
-        const uint32_t* ai = L.scr + (g.scr_aabb + i * kAabbWords) * kLanes;
-        V3 lo_i = ld3(ai, 0), hi_i = ld3(ai, 3);
-        int body_i = ldi(L.w, sw(L, i, S_BODY));
-        int type_bi = ldi(L.w, bw(L, body_i, B_TYPE));
+        const uint32_t* ri = shape_rec(L, i);
+        V3 lo_i = ld3(ri, SS_LO), hi_i = ld3(ri, SS_HI);
+        int body_i = ldi(ri, SS_BODY);
+        int bf_i = ldi(ri, SS_BFLAGS);
         uint64_t cat_i = ldu64(L.w, sw(L, i, S_CATEGORY));
         uint64_t mask_i = ldu64(L.w, sw(L, i, S_MASK));
         for (int j = i + 1; j < ns; j++) {
             /* b3_broadphase_pair (08:45-62): bounds first, then the rest */
-            const uint32_t* aj = L.scr + (g.scr_aabb + j * kAabbWords) * kLanes;
-            V3 lo_j = ld3(aj, 0), hi_j = ld3(aj, 3);
+            const uint32_t* rj = shape_rec(L, j);
+            V3 lo_j = ld3(rj, SS_LO), hi_j = ld3(rj, SS_HI);
             if (!(lo_i.x <= hi_j.x && hi_i.x >= lo_j.x && lo_i.y <= hi_j.y && hi_i.y >= lo_j.y
                     && lo_i.z <= hi_j.z && hi_i.z >= lo_j.z))
                 continue;
-            int body_j = ldi(L.w, sw(L, j, S_BODY));
+            int body_j = ldi(rj, SS_BODY);
+            int bf_j = ldi(rj, SS_BFLAGS);
             if (body_i == body_j) continue;
-            int type_bj = ldi(L.w, bw(L, body_j, B_TYPE));
-            if (type_bi == kStatic && type_bj == kStatic) continue;
+            if (bf_i & bf_j & kBodyStatic) continue;
             if ((cat_i & ldu64(L.w, sw(L, j, S_MASK))) == 0 || (ldu64(L.w, sw(L, j, S_CATEGORY)) & mask_i) == 0)
                 continue;
-            if (joined(L, nj, body_i, body_j)) continue;
+            uint32_t key = pair_key(body_i, body_j);
+            int joined = 0;
+            for (int k = 0; k < nj; k++) joined |= ldu(joint_rec(L, k), JS_KEY) == key;
+            if (joined) continue;
 
-            Posed A = pose_shape(L, i, ld3(L.w, bw(L, body_i, B_POSITION)), ldq(L.w, bw(L, body_i, B_ROTATION)));
-            Posed B = pose_shape(L, j, ld3(L.w, bw(L, body_j, B_POSITION)), ldq(L.w, bw(L, body_j, B_ROTATION)));
             Mani m;
-            collide_pair(&m, A, B);
+            collide_pair(&m, posed_from(ri), posed_from(rj), L.vel);
             if (m.count == 0) continue;
             if (cc >= g.max_c) {
                 overflow = 1;
@@ -482,17 +531,12 @@ B3D_FN void collide_and_prepare(const Lane& L, Soft cs, Soft ss) {
             nc.normal = m.normal;
             nc.t1 = perp(m.normal);
             nc.t2 = cross(nc.t1, m.normal);
-            BodyLite ba = body_lite(L, body_i);
-            BodyLite bb = body_lite(L, body_j);
-            float fa = ldf(L.w, sw(L, i, S_FRICTION)), fb = ldf(L.w, sw(L, j, S_FRICTION));
-            float ea = ldf(L.w, sw(L, i, S_RESTITUTION)), eb = ldf(L.w, sw(L, j, S_RESTITUTION));
-            float rolling = maxf(ldf(L.w, sw(L, i, S_ROLLING)), ldf(L.w, sw(L, j, S_ROLLING)));
-            float friction = sqrtf(fa * fb);
-            float restitution = ea > eb ? ea : eb;
-            int static_contact = ba.type != kDynamic || bb.type != kDynamic;
-            for (int p = 0; p < m.count; p++) {
-                nc.r_a[p] = sub(m.p_a[p], ba.center);
-                nc.r_b[p] = sub(m.p_b[p], bb.center);
+            V3 ca = ld3(ri, SS_CENTER), cb = ld3(rj, SS_CENTER);
+#pragma unroll
+            for (int p = 0; p < kMaxManifold; p++) {
+                if (p >= m.count) continue;
+                nc.r_a[p] = sub(m.p_a[p], ca);
+                nc.r_b[p] = sub(m.p_b[p], cb);
                 nc.base_sep[p] = m.sep[p] - dot(sub(nc.r_b[p], nc.r_a[p]), m.normal);
                 nc.feature[p] = m.feature[p];
                 nc.ni[p] = 0.0f;
@@ -500,108 +544,50 @@ B3D_FN void collide_and_prepare(const Lane& L, Soft cs, Soft ss) {
             nc.fi = V2{0.0f, 0.0f};
             nc.twist = 0.0f;
             nc.roll = zero3();
-            /* warm start from the previous step's cache */
             if (sorted) {
                 while (optr < old_n) {
-                    const uint32_t* o = L.scr + (g.scr_old + optr * kOldWords) * kLanes;
+                    const uint32_t* o = old_rec(L, optr);
                     if (!pair_less(ldi(o, O_SHAPE_A), ldi(o, O_SHAPE_B), i, j)) break;
                     optr++;
                 }
                 if (optr < old_n) {
-                    const uint32_t* o = L.scr + (g.scr_old + optr * kOldWords) * kLanes;
+                    const uint32_t* o = old_rec(L, optr);
                     if (ldi(o, O_SHAPE_A) == i && ldi(o, O_SHAPE_B) == j) warm_from_old(L, optr, &nc);
                 }
             } else {
                 for (int k = 0; k < old_n; k++) {
-                    const uint32_t* o = L.scr + (g.scr_old + k * kOldWords) * kLanes;
+                    const uint32_t* o = old_rec(L, k);
                     if (ldi(o, O_SHAPE_A) == i && ldi(o, O_SHAPE_B) == j) warm_from_old(L, k, &nc);
                 }
             }
-
-            /* b3_prepare_one_contact (08:234-291) */
-            float ma = ba.type == kDynamic ? ba.inv_mass : 0.0f;
-            float mb = bb.type == kDynamic ? bb.inv_mass : 0.0f;
-            M3 ia = ba.type == kDynamic ? ba.inv_i : m3zero();
-            M3 ib = bb.type == kDynamic ? bb.inv_i : m3zero();
-            V3 n = nc.normal;
-            V3 va = vlin(L, body_i), wa = vang(L, body_i);
-            V3 vb = vlin(L, body_j), wb = vang(L, body_j);
-            V3 center_a = zero3(), center_b = zero3();
-            float wsum = 0.0f;
-            float nmass[kMaxManifold], rel_vel[kMaxManifold];
-            for (int p = 0; p < nc.count; p++) {
-                V3 rn_a = cross(nc.r_a[p], n);
-                V3 rn_b = cross(nc.r_b[p], n);
-                float kn = ma + mb + dot(rn_a, mv(ia, rn_a)) + dot(rn_b, mv(ib, rn_b));
-                nmass[p] = kn > 0.0f ? 1.0f / kn : 0.0f;
-                V3 vra = add(va, cross(wa, nc.r_a[p]));
-                V3 vrb = add(vb, cross(wb, nc.r_b[p]));
-                rel_vel[p] = dot(n, sub(vrb, vra));
-                float sep = nc.base_sep[p] + dot(sub(nc.r_b[p], nc.r_a[p]), n);
-                float weight = clampf(2.0f - sep * inv_tau, kMinFrictionW, 1.0f);
-                center_a = madd(center_a, weight, nc.r_a[p]);
-                center_b = madd(center_b, weight, nc.r_b[p]);
-                wsum += weight;
-            }
-            float invw = wsum > 0.0f ? 1.0f / wsum : 0.0f;
-            center_a = scale(center_a, invw);
-            center_b = scale(center_b, invw);
-            V3 rt_a1 = cross(center_a, nc.t1);
-            V3 rt_a2 = cross(center_a, nc.t2);
-            V3 rt_b1 = cross(center_b, nc.t1);
-            V3 rt_b2 = cross(center_b, nc.t2);
-            M2 k2;
-            k2.cx.x = ma + mb + dot(rt_a1, mv(ia, rt_a1)) + dot(rt_b1, mv(ib, rt_b1));
-            k2.cy.y = ma + mb + dot(rt_a2, mv(ia, rt_a2)) + dot(rt_b2, mv(ib, rt_b2));
-            k2.cx.y = dot(rt_a1, mv(ia, rt_a2)) + dot(rt_b1, mv(ib, rt_b2));
-            k2.cy.x = k2.cx.y;
-            M2 tmass = inv2(k2);
-            M3 isum = madd3(ia, ib);
-            float kt = dot(n, mv(isum, n));
-            float twist_mass = kt > 0.0f ? 1.0f / kt : 0.0f;
-
-            /* write the contact row */
+            float fa = ldf(L.w, sw(L, i, S_FRICTION)), fb = ldf(L.w, sw(L, j, S_FRICTION));
+            float ea = ldf(L.w, sw(L, i, S_RESTITUTION)), eb = ldf(L.w, sw(L, j, S_RESTITUTION));
             uint32_t* w = L.w;
             sti(w, cw(L, cc, C_SHAPE_A), i);
             sti(w, cw(L, cc, C_SHAPE_B), j);
             sti(w, cw(L, cc, C_BODY_A), body_i);
             sti(w, cw(L, cc, C_BODY_B), body_j);
             sti(w, cw(L, cc, C_POINT_COUNT), nc.count);
-            sti(w, cw(L, cc, C_STATIC), static_contact);
+            sti(w, cw(L, cc, C_STATIC), !((bf_i & bf_j) & kBodyDynamic));
             st3(w, cw(L, cc, C_NORMAL), nc.normal);
             st3(w, cw(L, cc, C_TANGENT1), nc.t1);
             st3(w, cw(L, cc, C_TANGENT2), nc.t2);
-            for (int p = 0; p < nc.count; p++) {
+#pragma unroll
+            for (int p = 0; p < kMaxManifold; p++) {
+                if (p >= nc.count) continue;
                 st3(w, pw(L, cc, p, P_R_A), nc.r_a[p]);
                 st3(w, pw(L, cc, p, P_R_B), nc.r_b[p]);
                 stf(w, pw(L, cc, p, P_BASE_SEP), nc.base_sep[p]);
-                stf(w, pw(L, cc, p, P_REL_VEL), rel_vel[p]);
                 stf(w, pw(L, cc, p, P_NORMAL_IMPULSE), nc.ni[p]);
-                stf(w, pw(L, cc, p, P_TOTAL_NORMAL), 0.0f);
-                stf(w, pw(L, cc, p, P_NORMAL_MASS), nmass[p]);
-                stf(w, pw(L, cc, p, P_LEVER), len(sub(nc.r_a[p], center_a)));
                 sti(w, pw(L, cc, p, P_FEATURE), (int)nc.feature[p]);
             }
-            st3(w, cw(L, cc, C_CENTER_A), center_a);
-            st3(w, cw(L, cc, C_CENTER_B), center_b);
-            stf(w, cw(L, cc, C_FRICTION), friction);
-            stf(w, cw(L, cc, C_RESTITUTION), restitution);
-            stf(w, cw(L, cc, C_ROLLING), rolling);
-            stf(w, cw(L, cc, C_TWIST_MASS), twist_mass);
+            stf(w, cw(L, cc, C_FRICTION), sqrtf(fa * fb));
+            stf(w, cw(L, cc, C_RESTITUTION), ea > eb ? ea : eb);
+            stf(w, cw(L, cc, C_ROLLING), maxf(ldf(L.w, sw(L, i, S_ROLLING)), ldf(L.w, sw(L, j, S_ROLLING))));
             stf(w, cw(L, cc, C_TWIST_IMPULSE), nc.twist);
             stf(w, cw(L, cc, C_FRICTION_IMPULSE), nc.fi.x);
             stf(w, cw(L, cc, C_FRICTION_IMPULSE + 1), nc.fi.y);
             st3(w, cw(L, cc, C_ROLLING_IMPULSE), nc.roll);
-            stf(w, cw(L, cc, C_TANGENT_MASS), tmass.cx.x);
-            stf(w, cw(L, cc, C_TANGENT_MASS + 1), tmass.cx.y);
-            stf(w, cw(L, cc, C_TANGENT_MASS + 2), tmass.cy.x);
-            stf(w, cw(L, cc, C_TANGENT_MASS + 3), tmass.cy.y);
-            stm3(w, cw(L, cc, C_ROLLING_MASS), inv3(isum));
-            stf(w, cw(L, cc, C_INV_MASS_A), ma);
-            stf(w, cw(L, cc, C_INV_MASS_B), mb);
-            stm3(w, cw(L, cc, C_INV_I_A), ia);
-            stm3(w, cw(L, cc, C_INV_I_B), ib);
-            stsoft(w, cw(L, cc, C_SOFTNESS), static_contact ? ss : cs);
             cc++;
         }
     }
@@ -610,7 +596,81 @@ B3D_FN void collide_and_prepare(const Lane& L, Soft cs, Soft ss) {
     sti(L.w, H_CONTACTS_DROPPED, dropped);
 }
 
-/* b3_prepare_joints (06_joints.inl:161-202). */
+/* b3_prepare_one_contact (08:234-291) for every new contact. */
+B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
+    uint32_t* w = L.w;
+    int cc = ldi(w, H_CONTACT_COUNT);
+    const float inv_tau = 1.0f / kSpeculative;
+    for (int c = 0; c < cc; c++) {
+        int a = ldi(w, cw(L, c, C_BODY_A)), b = ldi(w, cw(L, c, C_BODY_B));
+        int pc = ldi(w, cw(L, c, C_POINT_COUNT));
+        int ta = ldi(w, bw(L, a, B_TYPE)), tb = ldi(w, bw(L, b, B_TYPE));
+        float ma = ta == kDynamic ? ldf(w, bw(L, a, B_INV_MASS)) : 0.0f;
+        float mb = tb == kDynamic ? ldf(w, bw(L, b, B_INV_MASS)) : 0.0f;
+        M3 ia = ta == kDynamic ? ldm3(w, bw(L, a, B_INV_I_WORLD)) : m3zero();
+        M3 ib = tb == kDynamic ? ldm3(w, bw(L, b, B_INV_I_WORLD)) : m3zero();
+        V3 n = ld3(w, cw(L, c, C_NORMAL));
+        V3 t1 = ld3(w, cw(L, c, C_TANGENT1)), t2 = ld3(w, cw(L, c, C_TANGENT2));
+        V3 va = vlin(L, a), wa = vang(L, a);
+        V3 vb = vlin(L, b), wb = vang(L, b);
+        V3 center_a = zero3(), center_b = zero3();
+        float wsum = 0.0f;
+        V3 r_a[kMaxManifold];
+#pragma unroll
+        for (int p = 0; p < kMaxManifold; p++) {
+            if (p >= pc) continue;
+            V3 ra = ld3(w, pw(L, c, p, P_R_A)), rb = ld3(w, pw(L, c, p, P_R_B));
+            r_a[p] = ra;
+            V3 rn_a = cross(ra, n);
+            V3 rn_b = cross(rb, n);
+            float kn = ma + mb + dot(rn_a, mv(ia, rn_a)) + dot(rn_b, mv(ib, rn_b));
+            stf(w, pw(L, c, p, P_NORMAL_MASS), kn > 0.0f ? 1.0f / kn : 0.0f);
+            V3 vra = add(va, cross(wa, ra));
+            V3 vrb = add(vb, cross(wb, rb));
+            stf(w, pw(L, c, p, P_REL_VEL), dot(n, sub(vrb, vra)));
+            stf(w, pw(L, c, p, P_TOTAL_NORMAL), 0.0f);
+            float sep = ldf(w, pw(L, c, p, P_BASE_SEP)) + dot(sub(rb, ra), n);
+            float weight = clampf(2.0f - sep * inv_tau, kMinFrictionW, 1.0f);
+            center_a = madd(center_a, weight, ra);
+            center_b = madd(center_b, weight, rb);
+            wsum += weight;
+        }
+        float invw = wsum > 0.0f ? 1.0f / wsum : 0.0f;
+        center_a = scale(center_a, invw);
+        center_b = scale(center_b, invw);
+#pragma unroll
+        for (int p = 0; p < kMaxManifold; p++)
+            if (p < pc) stf(w, pw(L, c, p, P_LEVER), len(sub(r_a[p], center_a)));
+        V3 rt_a1 = cross(center_a, t1);
+        V3 rt_a2 = cross(center_a, t2);
+        V3 rt_b1 = cross(center_b, t1);
+        V3 rt_b2 = cross(center_b, t2);
+        M2 k2;
+        k2.cx.x = ma + mb + dot(rt_a1, mv(ia, rt_a1)) + dot(rt_b1, mv(ib, rt_b1));
+        k2.cy.y = ma + mb + dot(rt_a2, mv(ia, rt_a2)) + dot(rt_b2, mv(ib, rt_b2));
+        k2.cx.y = dot(rt_a1, mv(ia, rt_a2)) + dot(rt_b1, mv(ib, rt_b2));
+        k2.cy.x = k2.cx.y;
+        M2 tmass = inv2(k2);
+        M3 isum = madd3(ia, ib);
+        float kt = dot(n, mv(isum, n));
+        st3(w, cw(L, c, C_CENTER_A), center_a);
+        st3(w, cw(L, c, C_CENTER_B), center_b);
+        stf(w, cw(L, c, C_TWIST_MASS), kt > 0.0f ? 1.0f / kt : 0.0f);
+        stf(w, cw(L, c, C_TANGENT_MASS), tmass.cx.x);
+        stf(w, cw(L, c, C_TANGENT_MASS + 1), tmass.cx.y);
+        stf(w, cw(L, c, C_TANGENT_MASS + 2), tmass.cy.x);
+        stf(w, cw(L, c, C_TANGENT_MASS + 3), tmass.cy.y);
+        stm3(w, cw(L, c, C_ROLLING_MASS), inv3(isum));
+        stf(w, cw(L, c, C_INV_MASS_A), ma);
+        stf(w, cw(L, c, C_INV_MASS_B), mb);
+        stm3(w, cw(L, c, C_INV_I_A), ia);
+        stm3(w, cw(L, c, C_INV_I_B), ib);
+        stsoft(w, cw(L, c, C_SOFTNESS), ldi(w, cw(L, c, C_STATIC)) ? ss : cs);
+    }
+}
+
+/* b3_prepare_joints (06_joints.inl:161-202), plus the hinge axis through
+ * each inverse inertia, which is fixed for the step. */
 B3D_FN void prepare_joints(const Lane& L, float h) {
     int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
     uint32_t* w = L.w;
@@ -626,7 +686,8 @@ B3D_FN void prepare_joints(const Lane& L, float h) {
         stm3(w, jw(L, i, J_INV_I_A), ia);
         stm3(w, jw(L, i, J_INV_I_B), ib);
         M3 isum = madd3(ia, ib);
-        sti(w, jw(L, i, J_FIXED_ROTATION), dot(isum.cx, cross(isum.cy, isum.cz)) < 1.0e-20f);
+        int fixed = dot(isum.cx, cross(isum.cy, isum.cz)) < 1.0e-20f;
+        sti(w, jw(L, i, J_FIXED_ROTATION), fixed);
         Soft soft = make_soft(ldf(w, jw(L, i, J_CONSTRAINT_HERTZ)), ldf(w, jw(L, i, J_CONSTRAINT_DAMPING)), h);
         stsoft(w, jw(L, i, J_SOFTNESS), soft);
         Q rot_a = ldq(w, bw(L, a, B_ROTATION)), rot_b = ldq(w, bw(L, b, B_ROTATION));
@@ -653,6 +714,9 @@ B3D_FN void prepare_joints(const Lane& L, float h) {
             st3(w, jw(L, i, J_PERP_X), px);
             st3(w, jw(L, i, J_PERP_Y), py);
             stsoft(w, jw(L, i, J_SPRING_SOFTNESS), make_soft(ldf(w, jw(L, i, J_HERTZ)), ldf(w, jw(L, i, J_DAMPING_RATIO)), h));
+            uint32_t* r = joint_rec(L, i);
+            st3(r, JS_IA_AX, fixed ? zero3() : mv(ia, axis));
+            st3(r, JS_IB_AX, fixed ? zero3() : mv(ib, axis));
         }
     }
 }
@@ -717,6 +781,96 @@ B3D_FN void warm_start_joints(const Lane& L) {
     }
 }
 
+/* Point constraint mass (06:241-255). */
+B3D_FN M3 point_k(float ma, float mb, M3 ia, M3 ib, V3 ra, V3 rb) {
+    float msum = ma + mb;
+    M3 k;
+    k.cx = v3(msum, 0.0f, 0.0f);
+    k.cy = v3(0.0f, msum, 0.0f);
+    k.cz = v3(0.0f, 0.0f, msum);
+    k.cx = sub(k.cx, cross(ra, mv(ia, v3(0.0f, ra.z, -ra.y))));
+    k.cy = sub(k.cy, cross(ra, mv(ia, v3(-ra.z, 0.0f, ra.x))));
+    k.cz = sub(k.cz, cross(ra, mv(ia, v3(ra.y, -ra.x, 0.0f))));
+    k.cx = sub(k.cx, cross(rb, mv(ib, v3(0.0f, rb.z, -rb.y))));
+    k.cy = sub(k.cy, cross(rb, mv(ib, v3(-rb.z, 0.0f, rb.x))));
+    k.cz = sub(k.cz, cross(rb, mv(ib, v3(rb.y, -rb.x, 0.0f))));
+    return k;
+}
+
+/* Everything the contact and joint rows need from the bodies' delta poses
+ * (delta_pos, delta_rot), which change only in integrate_positions.  The
+ * reference recomputes these in every row solve (08_contacts.inl:331-333,
+ * 06_joints.inl:257-282, 285-332, 436-642); computing them once per delta
+ * state gives the same bits. */
+B3D_FN void delta_geometry(const Lane& L) {
+    uint32_t* w = L.w;
+    int cc = ldi(w, H_CONTACT_COUNT);
+    for (int c = 0; c < cc; c++) {
+        int a = ldi(w, cw(L, c, C_BODY_A)), b = ldi(w, cw(L, c, C_BODY_B));
+        int pc = ldi(w, cw(L, c, C_POINT_COUNT));
+        V3 n = ld3(w, cw(L, c, C_NORMAL));
+        Q dqa = ldq(w, bw(L, a, B_DELTA_ROT)), dqb = ldq(w, bw(L, b, B_DELTA_ROT));
+        V3 dp = sub(ld3(w, bw(L, b, B_DELTA_POS)), ld3(w, bw(L, a, B_DELTA_POS)));
+        uint32_t* sp = sep_rec(L, c);
+        for (int p = 0; p < pc; p++) {
+            V3 ra = ld3(w, pw(L, c, p, P_R_A)), rb = ld3(w, pw(L, c, p, P_R_B));
+            V3 ds = add(dp, sub(rot(dqb, rb), rot(dqa, ra)));
+            stf(sp, p, dot(ds, n) + ldf(w, pw(L, c, p, P_BASE_SEP)));
+        }
+    }
+    int nj = clampi(ldi(w, H_JOINT_COUNT), 0, L.g.max_j);
+    for (int j = 0; j < nj; j++) {
+        int a = ldi(w, jw(L, j, J_BODY_A)), b = ldi(w, jw(L, j, J_BODY_B));
+        Q dqa = ldq(w, bw(L, a, B_DELTA_ROT)), dqb = ldq(w, bw(L, b, B_DELTA_ROT));
+        V3 dpa = ld3(w, bw(L, a, B_DELTA_POS)), dpb = ld3(w, bw(L, b, B_DELTA_POS));
+        float ma = ldf(w, jw(L, j, J_INV_MASS_A)), mb = ldf(w, jw(L, j, J_INV_MASS_B));
+        M3 ia = ldm3(w, jw(L, j, J_INV_I_A)), ib = ldm3(w, jw(L, j, J_INV_I_B));
+        int fixed = ldi(w, jw(L, j, J_FIXED_ROTATION));
+        uint32_t* r = joint_rec(L, j);
+        Q qa = qmul(dqa, ldq(w, jw(L, j, J_FRAME_Q_A)));
+        Q qb = qmul(dqb, ldq(w, jw(L, j, J_FRAME_Q_B)));
+        if (qdot(qa, qb) < 0.0f) qb = qneg(qb);
+        Q rel = qinv_mul(qa, qb);
+        V3 ra = rot(dqa, ld3(w, jw(L, j, J_FRAME_P_A)));
+        V3 rb = rot(dqb, ld3(w, jw(L, j, J_FRAME_P_B)));
+        st3(r, JS_RA, ra);
+        st3(r, JS_RB, rb);
+        st3(r, JS_PSEP, add(add(sub(dpb, dpa), sub(rb, ra)), ld3(w, jw(L, j, J_DELTA_CENTER))));
+        stm3(r, JS_KINV, inv3(point_k(ma, mb, ia, ib, ra, rb)));
+        if (ldi(w, jw(L, j, J_TYPE)) == kJointWeld) {
+            Q s = rel;
+            if (rel.s < 0.0f) s = qneg(rel);
+            Q diff = q4(-s.v.x, -s.v.y, -s.v.z, 1.0f - s.s);
+            st3(r, JS_CV, neg(rot(qa, scale(qmul(diff, qconj(s)).v, 2.0f))));
+            continue;
+        }
+        int need_twist = (ldi(w, jw(L, j, J_ENABLE_SPRING)) || ldi(w, jw(L, j, J_ENABLE_LIMIT))
+            || ldi(w, jw(L, j, J_ENABLE_MOTOR))) && !fixed;
+        stf(r, JS_TW, need_twist ? twist(rel) : 0.0f);
+        stf(r, JS_RELX, rel.v.x);
+        stf(r, JS_RELY, rel.v.y);
+        if (!fixed) {
+            V3 px, py;
+            hinge_perps(qa, rel, &px, &py);
+            st3(r, JS_PX, px);
+            st3(r, JS_PY, py);
+            /* the solve's latest hinge rows are part of the joint state */
+            st3(w, jw(L, j, J_PERP_X), px);
+            st3(w, jw(L, j, J_PERP_Y), py);
+            M3 isum = madd3(ia, ib);
+            float kxx = dot(px, mv(isum, px));
+            float kyy = dot(py, mv(isum, py));
+            float kxy = dot(px, mv(isum, py));
+            float det = kxx * kyy - kxy * kxy;
+            stf(r, JS_KXX, kxx);
+            stf(r, JS_KYY, kyy);
+            stf(r, JS_KXY, kxy);
+            sti(r, JS_KOK, det > 1.0e-12f);
+            stf(r, JS_KINV2, det > 1.0e-12f ? 1.0f / det : 0.0f);
+        }
+    }
+}
+
 /* Rolling resistance (07_packed.inl:24-45). */
 B3D_FN void solve_rolling(V3 t1, V3 t2, float rolling, float total_n, M3 ia, M3 ib, V3* impulse, V3* wa, V3* wb) {
     if (rolling <= 0.0f) return;
@@ -741,83 +895,121 @@ B3D_FN void solve_rolling(V3 t1, V3 t2, float rolling, float total_n, M3 ia, M3 
     *wb = add(*wb, mv(ib, delta));
 }
 
+/* The contact row as one solve needs it, loaded ahead of use. */
+struct CPoint { V3 ra, rb; float nmass, ni, tn, lever, sep; };
+struct CRow {
+    int a, b, pc;
+    V3 n;
+    float ma, mb;
+    M3 ia, ib;
+    Soft soft;
+    CPoint pt[kMaxManifold];
+    float friction, twist_mass, twist_imp, rolling;
+    V2 fi;
+    V3 t1, t2, ca, cb;
+    M2 tm;
+};
+
+B3D_FN void crow_load(const Lane& L, int c, int relax, CRow* r) {
+    const uint32_t* w = L.w;
+    r->a = ldi(w, cw(L, c, C_BODY_A));
+    r->b = ldi(w, cw(L, c, C_BODY_B));
+    r->pc = ldi(w, cw(L, c, C_POINT_COUNT));
+    r->n = ld3(w, cw(L, c, C_NORMAL));
+    r->ma = ldf(w, cw(L, c, C_INV_MASS_A));
+    r->mb = ldf(w, cw(L, c, C_INV_MASS_B));
+    r->ia = ldm3(w, cw(L, c, C_INV_I_A));
+    r->ib = ldm3(w, cw(L, c, C_INV_I_B));
+    r->soft = ldsoft(w, cw(L, c, C_SOFTNESS));
+    const uint32_t* sp = sep_rec(L, c);
+#pragma unroll
+    for (int p = 0; p < kMaxManifold; p++) {
+        if (p >= r->pc) continue;
+        CPoint& q = r->pt[p];
+        q.ra = ld3(w, pw(L, c, p, P_R_A));
+        q.rb = ld3(w, pw(L, c, p, P_R_B));
+        q.nmass = ldf(w, pw(L, c, p, P_NORMAL_MASS));
+        q.ni = ldf(w, pw(L, c, p, P_NORMAL_IMPULSE));
+        q.tn = ldf(w, pw(L, c, p, P_TOTAL_NORMAL));
+        q.lever = ldf(w, pw(L, c, p, P_LEVER));
+        q.sep = ldf(sp, p);
+    }
+    if (relax) {
+        r->friction = ldf(w, cw(L, c, C_FRICTION));
+        r->twist_mass = ldf(w, cw(L, c, C_TWIST_MASS));
+        r->twist_imp = ldf(w, cw(L, c, C_TWIST_IMPULSE));
+        r->rolling = ldf(w, cw(L, c, C_ROLLING));
+        r->fi.x = ldf(w, cw(L, c, C_FRICTION_IMPULSE));
+        r->fi.y = ldf(w, cw(L, c, C_FRICTION_IMPULSE + 1));
+        r->t1 = ld3(w, cw(L, c, C_TANGENT1));
+        r->t2 = ld3(w, cw(L, c, C_TANGENT2));
+        r->ca = ld3(w, cw(L, c, C_CENTER_A));
+        r->cb = ld3(w, cw(L, c, C_CENTER_B));
+        r->tm.cx.x = ldf(w, cw(L, c, C_TANGENT_MASS));
+        r->tm.cx.y = ldf(w, cw(L, c, C_TANGENT_MASS + 1));
+        r->tm.cy.x = ldf(w, cw(L, c, C_TANGENT_MASS + 2));
+        r->tm.cy.y = ldf(w, cw(L, c, C_TANGENT_MASS + 3));
+    }
+}
+
 /* One contact, b3_solve_one_contact (08:315-413): soft normal rows, then in
  * the relax pass twist friction, 2-D friction at the anchor and rolling. */
-B3D_FN void solve_contact(const Lane& L, int c, float inv_h, float contact_speed, int use_bias) {
+B3D_FN void crow_solve(const Lane& L, int c, CRow& r, float inv_h, float contact_speed, int use_bias) {
     uint32_t* w = L.w;
-    int a = ldi(w, cw(L, c, C_BODY_A)), b = ldi(w, cw(L, c, C_BODY_B));
-    int pc = ldi(w, cw(L, c, C_POINT_COUNT));
-    V3 va = vlin(L, a), wa = vang(L, a), vb = vlin(L, b), wb = vang(L, b);
-    Q dqa = ldq(w, bw(L, a, B_DELTA_ROT)), dqb = ldq(w, bw(L, b, B_DELTA_ROT));
-    V3 dp = sub(ld3(w, bw(L, b, B_DELTA_POS)), ld3(w, bw(L, a, B_DELTA_POS)));
-    V3 n = ld3(w, cw(L, c, C_NORMAL));
-    float ma = ldf(w, cw(L, c, C_INV_MASS_A)), mb = ldf(w, cw(L, c, C_INV_MASS_B));
-    M3 ia = ldm3(w, cw(L, c, C_INV_I_A)), ib = ldm3(w, cw(L, c, C_INV_I_B));
-    Soft soft = ldsoft(w, cw(L, c, C_SOFTNESS));
+    V3 va = vlin(L, r.a), wa = vang(L, r.a), vb = vlin(L, r.b), wb = vang(L, r.b);
+    V3 n = r.n;
     float total_n = 0.0f;
     float twist_lim = 0.0f;
-    for (int p = 0; p < pc; p++) {
-        V3 ra = ld3(w, pw(L, c, p, P_R_A)), rb = ld3(w, pw(L, c, p, P_R_B));
-        V3 ds = add(dp, sub(rot(dqb, rb), rot(dqa, ra)));
-        float sep = dot(ds, n) + ldf(w, pw(L, c, p, P_BASE_SEP));
+#pragma unroll
+    for (int p = 0; p < kMaxManifold; p++) {
+        if (p >= r.pc) continue;
+        CPoint& q = r.pt[p];
+        float sep = q.sep;
         float vbias = 0.0f, mscale = 1.0f, iscale = 0.0f;
         if (sep > 0.0f) {
             vbias = sep * inv_h;
         } else if (use_bias) {
-            vbias = maxf(soft.mass_scale * soft.bias_rate * sep, -contact_speed);
-            mscale = soft.mass_scale;
-            iscale = soft.impulse_scale;
+            vbias = maxf(r.soft.mass_scale * r.soft.bias_rate * sep, -contact_speed);
+            mscale = r.soft.mass_scale;
+            iscale = r.soft.impulse_scale;
         }
-        V3 vra = add(va, cross(wa, ra));
-        V3 vrb = add(vb, cross(wb, rb));
+        V3 vra = add(va, cross(wa, q.ra));
+        V3 vrb = add(vb, cross(wb, q.rb));
         float vn = dot(sub(vrb, vra), n);
-        float old = ldf(w, pw(L, c, p, P_NORMAL_IMPULSE));
-        float dimp = -ldf(w, pw(L, c, p, P_NORMAL_MASS)) * (mscale * vn + vbias) - iscale * old;
-        float nimp = maxf(old + dimp, 0.0f);
-        dimp = nimp - old;
+        float dimp = -q.nmass * (mscale * vn + vbias) - iscale * q.ni;
+        float nimp = maxf(q.ni + dimp, 0.0f);
+        dimp = nimp - q.ni;
         stf(w, pw(L, c, p, P_NORMAL_IMPULSE), nimp);
-        stf(w, pw(L, c, p, P_TOTAL_NORMAL), ldf(w, pw(L, c, p, P_TOTAL_NORMAL)) + nimp);
+        stf(w, pw(L, c, p, P_TOTAL_NORMAL), q.tn + nimp);
         total_n += nimp;
-        twist_lim += ldf(w, pw(L, c, p, P_LEVER)) * nimp;
+        twist_lim += q.lever * nimp;
         V3 P = scale(n, dimp);
-        va = msub(va, ma, P);
-        wa = sub(wa, mv(ia, cross(ra, P)));
-        vb = madd(vb, mb, P);
-        wb = add(wb, mv(ib, cross(rb, P)));
+        va = msub(va, r.ma, P);
+        wa = sub(wa, mv(r.ia, cross(q.ra, P)));
+        vb = madd(vb, r.mb, P);
+        wb = add(wb, mv(r.ib, cross(q.rb, P)));
     }
     if (!use_bias) {
-        float friction = ldf(w, cw(L, c, C_FRICTION));
         float twist_s = dot(n, sub(wb, wa));
-        float max_t = friction * twist_lim;
-        float dtw = -ldf(w, cw(L, c, C_TWIST_MASS)) * twist_s;
-        float old_t = ldf(w, cw(L, c, C_TWIST_IMPULSE));
-        float new_t = clampf(old_t + dtw, -max_t, max_t);
+        float max_t = r.friction * twist_lim;
+        float dtw = -r.twist_mass * twist_s;
+        float new_t = clampf(r.twist_imp + dtw, -max_t, max_t);
         stf(w, cw(L, c, C_TWIST_IMPULSE), new_t);
-        dtw = new_t - old_t;
-        wa = sub(wa, mv(ia, scale(n, dtw)));
-        wb = add(wb, mv(ib, scale(n, dtw)));
+        dtw = new_t - r.twist_imp;
+        wa = sub(wa, mv(r.ia, scale(n, dtw)));
+        wb = add(wb, mv(r.ib, scale(n, dtw)));
 
-        V3 t1 = ld3(w, cw(L, c, C_TANGENT1)), t2 = ld3(w, cw(L, c, C_TANGENT2));
-        V3 ra = ld3(w, cw(L, c, C_CENTER_A)), rb = ld3(w, cw(L, c, C_CENTER_B));
-        V3 vra = add(va, cross(wa, ra));
-        V3 vrb = add(vb, cross(wb, rb));
+        V3 vra = add(va, cross(wa, r.ca));
+        V3 vrb = add(vb, cross(wb, r.cb));
         V3 vr = sub(vrb, vra);
         V2 vt;
-        vt.x = dot(vr, t1);
-        vt.y = dot(vr, t2);
-        M2 tm;
-        tm.cx.x = ldf(w, cw(L, c, C_TANGENT_MASS));
-        tm.cx.y = ldf(w, cw(L, c, C_TANGENT_MASS + 1));
-        tm.cy.x = ldf(w, cw(L, c, C_TANGENT_MASS + 2));
-        tm.cy.y = ldf(w, cw(L, c, C_TANGENT_MASS + 3));
-        V2 tmv = mv2(tm, vt);
-        V2 fi_old;
-        fi_old.x = ldf(w, cw(L, c, C_FRICTION_IMPULSE));
-        fi_old.y = ldf(w, cw(L, c, C_FRICTION_IMPULSE + 1));
+        vt.x = dot(vr, r.t1);
+        vt.y = dot(vr, r.t2);
+        V2 tmv = mv2(r.tm, vt);
         V2 ni;
-        ni.x = fi_old.x - tmv.x;
-        ni.y = fi_old.y - tmv.y;
-        float max_f = friction * total_n;
+        ni.x = r.fi.x - tmv.x;
+        ni.y = r.fi.y - tmv.y;
+        float max_f = r.friction * total_n;
         float fl2 = ni.x * ni.x + ni.y * ni.y;
         if (fl2 > max_f * max_f && fl2 > 0.0f) {
             float sc = rsqrt_scale(max_f, fl2);
@@ -825,29 +1017,42 @@ B3D_FN void solve_contact(const Lane& L, int c, float inv_h, float contact_speed
             ni.y *= sc;
         }
         V2 df;
-        df.x = ni.x - fi_old.x;
-        df.y = ni.y - fi_old.y;
+        df.x = ni.x - r.fi.x;
+        df.y = ni.y - r.fi.y;
         stf(w, cw(L, c, C_FRICTION_IMPULSE), ni.x);
         stf(w, cw(L, c, C_FRICTION_IMPULSE + 1), ni.y);
-        V3 P = add(scale(t1, df.x), scale(t2, df.y));
-        va = msub(va, ma, P);
-        wa = sub(wa, mv(ia, cross(ra, P)));
-        vb = madd(vb, mb, P);
-        wb = add(wb, mv(ib, cross(rb, P)));
-        float rolling = ldf(w, cw(L, c, C_ROLLING));
-        if (rolling > 0.0f) {
+        V3 P = add(scale(r.t1, df.x), scale(r.t2, df.y));
+        va = msub(va, r.ma, P);
+        wa = sub(wa, mv(r.ia, cross(r.ca, P)));
+        vb = madd(vb, r.mb, P);
+        wb = add(wb, mv(r.ib, cross(r.cb, P)));
+        if (r.rolling > 0.0f) {
             V3 ri = ld3(w, cw(L, c, C_ROLLING_IMPULSE));
-            solve_rolling(t1, t2, rolling, total_n, ia, ib, &ri, &wa, &wb);
+            solve_rolling(r.t1, r.t2, r.rolling, total_n, r.ia, r.ib, &ri, &wa, &wb);
             st3(w, cw(L, c, C_ROLLING_IMPULSE), ri);
         }
     }
-    if (is_dyn_flag(L, a)) {
-        set_vlin(L, a, va);
-        set_vang(L, a, wa);
+    if (is_dyn_flag(L, r.a)) {
+        set_vlin(L, r.a, va);
+        set_vang(L, r.a, wa);
     }
-    if (is_dyn_flag(L, b)) {
-        set_vlin(L, b, vb);
-        set_vang(L, b, wb);
+    if (is_dyn_flag(L, r.b)) {
+        set_vlin(L, r.b, vb);
+        set_vang(L, r.b, wb);
+    }
+}
+
+/* b3_solve_contacts (08:415-437): one Gauss-Seidel sweep in contact order,
+ * with the next contact's row loaded while the current one is solved. */
+B3D_FN void solve_contacts(const Lane& L, float inv_h, float contact_speed, int use_bias) {
+    int cc = ldi(L.w, H_CONTACT_COUNT);
+    if (cc <= 0) return;
+    CRow cur, nxt;
+    crow_load(L, 0, !use_bias, &cur);
+    for (int c = 0; c < cc; c++) {
+        if (c + 1 < cc) crow_load(L, c + 1, !use_bias, &nxt);
+        crow_solve(L, c, cur, inv_h, contact_speed, use_bias);
+        cur = nxt;
     }
 }
 
@@ -893,95 +1098,6 @@ B3D_FN void apply_restitution(const Lane& L, float threshold) {
     }
 }
 
-/* Point constraint rows shared by weld and revolute (06:241-282). */
-B3D_FN M3 point_k(float ma, float mb, M3 ia, M3 ib, V3 ra, V3 rb) {
-    float msum = ma + mb;
-    M3 k;
-    k.cx = v3(msum, 0.0f, 0.0f);
-    k.cy = v3(0.0f, msum, 0.0f);
-    k.cz = v3(0.0f, 0.0f, msum);
-    k.cx = sub(k.cx, cross(ra, mv(ia, v3(0.0f, ra.z, -ra.y))));
-    k.cy = sub(k.cy, cross(ra, mv(ia, v3(-ra.z, 0.0f, ra.x))));
-    k.cz = sub(k.cz, cross(ra, mv(ia, v3(ra.y, -ra.x, 0.0f))));
-    k.cx = sub(k.cx, cross(rb, mv(ib, v3(0.0f, rb.z, -rb.y))));
-    k.cy = sub(k.cy, cross(rb, mv(ib, v3(-rb.z, 0.0f, rb.x))));
-    k.cz = sub(k.cz, cross(rb, mv(ib, v3(rb.y, -rb.x, 0.0f))));
-    return k;
-}
-
-struct JointBodies {
-    int a, b;
-    float ma, mb;
-    M3 ia, ib;
-    Q dqa, dqb;   /* delta rotations */
-    V3 dpa, dpb;  /* delta positions */
-};
-
-B3D_FN void solve_point(const Lane& L, int j, const JointBodies& jb, V3* va, V3* wa, V3* vb, V3* wb,
-        Soft soft, int use_bias) {
-    uint32_t* w = L.w;
-    V3 ra = rot(jb.dqa, ld3(w, jw(L, j, J_FRAME_P_A)));
-    V3 rb = rot(jb.dqb, ld3(w, jw(L, j, J_FRAME_P_B)));
-    V3 cdot = sub(add(*vb, cross(*wb, rb)), add(*va, cross(*wa, ra)));
-    V3 bias = zero3();
-    float mscale = 1.0f, iscale = 0.0f;
-    if (use_bias) {
-        V3 sep = add(add(sub(jb.dpb, jb.dpa), sub(rb, ra)), ld3(w, jw(L, j, J_DELTA_CENTER)));
-        bias = scale(sep, soft.bias_rate);
-        mscale = soft.mass_scale;
-        iscale = soft.impulse_scale;
-    }
-    V3 bsol = solve3(point_k(jb.ma, jb.mb, jb.ia, jb.ib, ra, rb), add(cdot, bias));
-    V3 lin_old = ld3(w, jw(L, j, J_LINEAR_IMPULSE));
-    V3 impulse = msub(scale(bsol, -mscale), iscale, lin_old);
-    st3(w, jw(L, j, J_LINEAR_IMPULSE), add(lin_old, impulse));
-    *va = msub(*va, jb.ma, impulse);
-    *wa = sub(*wa, mv(jb.ia, cross(ra, impulse)));
-    *vb = madd(*vb, jb.mb, impulse);
-    *wb = add(*wb, mv(jb.ib, cross(rb, impulse)));
-}
-
-/* b3_solve_weld (06:285-332). */
-B3D_FN void solve_weld(const Lane& L, int j, const JointBodies& jb, int use_bias) {
-    uint32_t* w = L.w;
-    V3 va = vlin(L, jb.a), wa = vang(L, jb.a), vb = vlin(L, jb.b), wb = vang(L, jb.b);
-    Q qa = qmul(jb.dqa, ldq(w, jw(L, j, J_FRAME_Q_A)));
-    Q qb = qmul(jb.dqb, ldq(w, jw(L, j, J_FRAME_Q_B)));
-    if (qdot(qa, qb) < 0.0f) qb = qneg(qb);
-    Q rel = qinv_mul(qa, qb);
-    float ang_hz = ldf(w, jw(L, j, J_ANGULAR_HERTZ));
-    if (!ldi(w, jw(L, j, J_FIXED_ROTATION))) {
-        V3 bias = zero3();
-        float mscale = 1.0f, iscale = 0.0f;
-        if (use_bias || ang_hz > 0.0f) {
-            Q s = rel;
-            if (rel.s < 0.0f) s = qneg(rel);
-            Q diff = q4(-s.v.x, -s.v.y, -s.v.z, 1.0f - s.s);
-            V3 cv = neg(rot(qa, scale(qmul(diff, qconj(s)).v, 2.0f)));
-            Soft as = ldsoft(w, jw(L, j, J_ANGULAR_SPRING));
-            bias = scale(cv, as.bias_rate);
-            mscale = as.mass_scale;
-            iscale = as.impulse_scale;
-        }
-        V3 cdot = sub(wb, wa);
-        V3 ang_old = ld3(w, jw(L, j, J_ANGULAR_IMPULSE));
-        V3 impulse = msub(scale(mv(ldm3(w, jw(L, j, J_ANGULAR_MASS)), add(cdot, bias)), -mscale), iscale, ang_old);
-        st3(w, jw(L, j, J_ANGULAR_IMPULSE), add(ang_old, impulse));
-        wa = sub(wa, mv(jb.ia, impulse));
-        wb = add(wb, mv(jb.ib, impulse));
-    }
-    int lin_bias = use_bias || ldf(w, jw(L, j, J_LINEAR_HERTZ)) > 0.0f;
-    solve_point(L, j, jb, &va, &wa, &vb, &wb, ldsoft(w, jw(L, j, J_LINEAR_SPRING)), lin_bias);
-    if (is_dyn_flag(L, jb.a)) {
-        set_vlin(L, jb.a, va);
-        set_vang(L, jb.a, wa);
-    }
-    if (is_dyn_flag(L, jb.b)) {
-        set_vlin(L, jb.b, vb);
-        set_vang(L, jb.b, wb);
-    }
-}
-
 /* One clamped one-sided limit row (06:419-433). */
 B3D_FN float limit_impulse(float c, float cdot, float inv_h, int use_bias, Soft soft, float axial_mass, float old) {
     float bias = 0.0f, mscale = 1.0f, iscale = 0.0f;
@@ -996,15 +1112,71 @@ B3D_FN float limit_impulse(float c, float cdot, float inv_h, int use_bias, Soft 
     return maxf(old + dimp, 0.0f);
 }
 
+/* Point rows shared by weld and revolute (06:257-282), with the anchors,
+ * separation and inverted mass of the current delta state. */
+B3D_FN void solve_point(const Lane& L, int j, const uint32_t* r, float ma, float mb, M3 ia, M3 ib,
+        V3* va, V3* wa, V3* vb, V3* wb, Soft soft, int use_bias) {
+    uint32_t* w = L.w;
+    V3 ra = ld3(r, JS_RA), rb = ld3(r, JS_RB);
+    V3 cdot = sub(add(*vb, cross(*wb, rb)), add(*va, cross(*wa, ra)));
+    V3 bias = zero3();
+    float mscale = 1.0f, iscale = 0.0f;
+    if (use_bias) {
+        bias = scale(ld3(r, JS_PSEP), soft.bias_rate);
+        mscale = soft.mass_scale;
+        iscale = soft.impulse_scale;
+    }
+    V3 bsol = mv(ldm3(r, JS_KINV), add(cdot, bias));
+    V3 lin_old = ld3(w, jw(L, j, J_LINEAR_IMPULSE));
+    V3 impulse = msub(scale(bsol, -mscale), iscale, lin_old);
+    st3(w, jw(L, j, J_LINEAR_IMPULSE), add(lin_old, impulse));
+    *va = msub(*va, ma, impulse);
+    *wa = sub(*wa, mv(ia, cross(ra, impulse)));
+    *vb = madd(*vb, mb, impulse);
+    *wb = add(*wb, mv(ib, cross(rb, impulse)));
+}
+
+/* b3_solve_weld (06:285-332). */
+B3D_FN void solve_weld(const Lane& L, int j, int a, int b, float ma, float mb, M3 ia, M3 ib, int use_bias) {
+    uint32_t* w = L.w;
+    const uint32_t* r = joint_rec(L, j);
+    V3 va = vlin(L, a), wa = vang(L, a), vb = vlin(L, b), wb = vang(L, b);
+    float ang_hz = ldf(w, jw(L, j, J_ANGULAR_HERTZ));
+    if (!ldi(w, jw(L, j, J_FIXED_ROTATION))) {
+        V3 bias = zero3();
+        float mscale = 1.0f, iscale = 0.0f;
+        if (use_bias || ang_hz > 0.0f) {
+            Soft as = ldsoft(w, jw(L, j, J_ANGULAR_SPRING));
+            bias = scale(ld3(r, JS_CV), as.bias_rate);
+            mscale = as.mass_scale;
+            iscale = as.impulse_scale;
+        }
+        V3 cdot = sub(wb, wa);
+        V3 ang_old = ld3(w, jw(L, j, J_ANGULAR_IMPULSE));
+        V3 impulse = msub(scale(mv(ldm3(w, jw(L, j, J_ANGULAR_MASS)), add(cdot, bias)), -mscale), iscale, ang_old);
+        st3(w, jw(L, j, J_ANGULAR_IMPULSE), add(ang_old, impulse));
+        wa = sub(wa, mv(ia, impulse));
+        wb = add(wb, mv(ib, impulse));
+    }
+    int lin_bias = use_bias || ldf(w, jw(L, j, J_LINEAR_HERTZ)) > 0.0f;
+    solve_point(L, j, r, ma, mb, ia, ib, &va, &wa, &vb, &wb, ldsoft(w, jw(L, j, J_LINEAR_SPRING)), lin_bias);
+    if (is_dyn_flag(L, a)) {
+        set_vlin(L, a, va);
+        set_vang(L, a, wa);
+    }
+    if (is_dyn_flag(L, b)) {
+        set_vlin(L, b, vb);
+        set_vang(L, b, wb);
+    }
+}
+
 /* b3_solve_revolute (06:436-642): spring, motor, lower and upper limit,
  * two perpendicular angular rows, then the point rows. */
-B3D_FN void solve_revolute(const Lane& L, int j, const JointBodies& jb, float h, float inv_h, int use_bias) {
+B3D_FN void solve_revolute(const Lane& L, int j, int a, int b, float ma, float mb, M3 ia, M3 ib, float h,
+        float inv_h, int use_bias) {
     uint32_t* w = L.w;
-    V3 va = vlin(L, jb.a), wa = vang(L, jb.a), vb = vlin(L, jb.b), wb = vang(L, jb.b);
-    Q qa = qmul(jb.dqa, ldq(w, jw(L, j, J_FRAME_Q_A)));
-    Q qb = qmul(jb.dqb, ldq(w, jw(L, j, J_FRAME_Q_B)));
-    if (qdot(qa, qb) < 0.0f) qb = qneg(qb);
-    Q rel = qinv_mul(qa, qb);
+    const uint32_t* r = joint_rec(L, j);
+    V3 va = vlin(L, a), wa = vang(L, a), vb = vlin(L, b), wb = vang(L, b);
     V3 axis = ld3(w, jw(L, j, J_ROTATION_AXIS));
     int fixed = ldi(w, jw(L, j, J_FIXED_ROTATION));
     int en_spring = ldi(w, jw(L, j, J_ENABLE_SPRING));
@@ -1012,13 +1184,9 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JointBodies& jb, float h,
     int en_limit = ldi(w, jw(L, j, J_ENABLE_LIMIT));
     float axial_mass = ldf(w, jw(L, j, J_AXIAL_MASS));
     float max_torque = ldf(w, jw(L, j, J_MAX_MOTOR_TORQUE));
-    V3 ia_ax = zero3(), ib_ax = zero3();
-    float tw = 0.0f;
-    if (!fixed) {
-        ia_ax = mv(jb.ia, axis);
-        ib_ax = mv(jb.ib, axis);
-    }
-    if ((en_spring || en_limit || en_motor) && !fixed) tw = twist(rel);
+    V3 ia_ax = ld3(r, JS_IA_AX), ib_ax = ld3(r, JS_IB_AX);
+    float tw = ldf(r, JS_TW);
+    Soft soft = ldsoft(w, jw(L, j, J_SOFTNESS));
     if (en_spring && !fixed) {
         Soft ss = ldsoft(w, jw(L, j, J_SPRING_SOFTNESS));
         float c = tw - ldf(w, jw(L, j, J_TARGET_ANGLE));
@@ -1059,7 +1227,6 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JointBodies& jb, float h,
         }
     }
     if (en_limit && !fixed) {
-        Soft soft = ldsoft(w, jw(L, j, J_SOFTNESS));
         float old = ldf(w, jw(L, j, J_LOWER_IMPULSE));
         float lo = limit_impulse(tw - ldf(w, jw(L, j, J_LOWER_ANGLE)), dot(sub(wb, wa), axis), inv_h,
             use_bias, soft, axial_mass, old);
@@ -1081,27 +1248,27 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JointBodies& jb, float h,
         bias.y = 0.0f;
         float mscale = 1.0f, iscale = 0.0f;
         if (use_bias) {
-            Soft soft = ldsoft(w, jw(L, j, J_SOFTNESS));
-            bias.x = soft.bias_rate * rel.v.x;
-            bias.y = soft.bias_rate * rel.v.y;
+            bias.x = soft.bias_rate * ldf(r, JS_RELX);
+            bias.y = soft.bias_rate * ldf(r, JS_RELY);
             mscale = soft.mass_scale;
             iscale = soft.impulse_scale;
         }
-        V3 px, py;
-        hinge_perps(qa, rel, &px, &py);
-        st3(w, jw(L, j, J_PERP_X), px);
-        st3(w, jw(L, j, J_PERP_Y), py);
-        M3 isum = madd3(jb.ia, jb.ib);
-        M2 kang;
-        kang.cx.x = dot(px, mv(isum, px));
-        kang.cy.y = dot(py, mv(isum, py));
-        kang.cx.y = dot(px, mv(isum, py));
-        kang.cy.x = kang.cx.y;
+        V3 px = ld3(r, JS_PX), py = ld3(r, JS_PY);
         V3 wrel = sub(wb, wa);
         V2 rhs;
         rhs.x = dot(wrel, px) + bias.x;
         rhs.y = dot(wrel, py) + bias.y;
-        V2 sol = solve2(kang, rhs);
+        /* b3_solve2 (03_math.inl:347-359) with the determinant of this
+         * delta state */
+        V2 sol;
+        sol.x = 0.0f;
+        sol.y = 0.0f;
+        if (ldi(r, JS_KOK)) {
+            float inv = ldf(r, JS_KINV2);
+            float kxx = ldf(r, JS_KXX), kyy = ldf(r, JS_KYY), kxy = ldf(r, JS_KXY);
+            sol.x = inv * (kyy * rhs.x - kxy * rhs.y);
+            sol.y = inv * (-kxy * rhs.x + kxx * rhs.y);
+        }
         V2 old;
         old.x = ldf(w, jw(L, j, J_PERP_IMPULSE));
         old.y = ldf(w, jw(L, j, J_PERP_IMPULSE + 1));
@@ -1111,17 +1278,17 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JointBodies& jb, float h,
         stf(w, jw(L, j, J_PERP_IMPULSE), old.x + dimp.x);
         stf(w, jw(L, j, J_PERP_IMPULSE + 1), old.y + dimp.y);
         V3 ang = add(scale(px, dimp.x), scale(py, dimp.y));
-        wa = sub(wa, mv(jb.ia, ang));
-        wb = add(wb, mv(jb.ib, ang));
+        wa = sub(wa, mv(ia, ang));
+        wb = add(wb, mv(ib, ang));
     }
-    solve_point(L, j, jb, &va, &wa, &vb, &wb, ldsoft(w, jw(L, j, J_SOFTNESS)), use_bias);
-    if (is_dyn_flag(L, jb.a)) {
-        set_vlin(L, jb.a, va);
-        set_vang(L, jb.a, wa);
+    solve_point(L, j, r, ma, mb, ia, ib, &va, &wa, &vb, &wb, soft, use_bias);
+    if (is_dyn_flag(L, a)) {
+        set_vlin(L, a, va);
+        set_vang(L, a, wa);
     }
-    if (is_dyn_flag(L, jb.b)) {
-        set_vlin(L, jb.b, vb);
-        set_vang(L, jb.b, wb);
+    if (is_dyn_flag(L, b)) {
+        set_vlin(L, b, vb);
+        set_vang(L, b, wb);
     }
 }
 
@@ -1132,19 +1299,11 @@ B3D_FN void solve_joints(const Lane& L, float h, float inv_h, int use_bias) {
     int iters = use_bias ? kJointIters : kRelaxIters;
     for (int it = 0; it < iters; it++) {
         for (int j = 0; j < nj; j++) {
-            JointBodies jb;
-            jb.a = ldi(w, jw(L, j, J_BODY_A));
-            jb.b = ldi(w, jw(L, j, J_BODY_B));
-            jb.ma = ldf(w, jw(L, j, J_INV_MASS_A));
-            jb.mb = ldf(w, jw(L, j, J_INV_MASS_B));
-            jb.ia = ldm3(w, jw(L, j, J_INV_I_A));
-            jb.ib = ldm3(w, jw(L, j, J_INV_I_B));
-            jb.dqa = ldq(w, bw(L, jb.a, B_DELTA_ROT));
-            jb.dqb = ldq(w, bw(L, jb.b, B_DELTA_ROT));
-            jb.dpa = ld3(w, bw(L, jb.a, B_DELTA_POS));
-            jb.dpb = ld3(w, bw(L, jb.b, B_DELTA_POS));
-            if (ldi(w, jw(L, j, J_TYPE)) == kJointWeld) solve_weld(L, j, jb, use_bias);
-            else solve_revolute(L, j, jb, h, inv_h, use_bias);
+            int a = ldi(w, jw(L, j, J_BODY_A)), b = ldi(w, jw(L, j, J_BODY_B));
+            float ma = ldf(w, jw(L, j, J_INV_MASS_A)), mb = ldf(w, jw(L, j, J_INV_MASS_B));
+            M3 ia = ldm3(w, jw(L, j, J_INV_I_A)), ib = ldm3(w, jw(L, j, J_INV_I_B));
+            if (ldi(w, jw(L, j, J_TYPE)) == kJointWeld) solve_weld(L, j, a, b, ma, mb, ia, ib, use_bias);
+            else solve_revolute(L, j, a, b, ma, mb, ia, ib, h, inv_h, use_bias);
         }
     }
 }
@@ -1216,8 +1375,9 @@ B3D_FN void finalize(const Lane& L) {
     }
 }
 
-/* One world's b3_step (09_step.inl:148-264, default configuration).  The
- * caller has staged velocities with vel_load and stores them afterwards. */
+/* One world's b3_step (09_step.inl:148-264, default configuration).  Body
+ * velocities are staged in the velocity rows after contact generation (which
+ * uses the same rows for clip polygons) and written back at the end. */
 B3D_FN void step_world(const Lane& L, float dt, int substeps) {
     if (!(dt > 0.0f)) return;
     int subs = substeps < 1 ? 1 : substeps;
@@ -1231,21 +1391,25 @@ B3D_FN void step_world(const Lane& L, float dt, int substeps) {
     float contact_speed = ldf(L.w, H_CONTACT_SPEED);
     float rest_threshold = ldf(L.w, H_RESTITUTION_THRESHOLD);
 
-    collide_and_prepare(L, cs, ss);
+    find_contacts(L);
+    vel_load(L);
+    prepare_contacts(L, cs, ss);
     prepare_joints(L, h);
     warm_start_contacts(L);
     warm_start_joints(L);
-    int cc = ldi(L.w, H_CONTACT_COUNT);
+    delta_geometry(L);
     for (int s = 0; s < subs; s++) {
         integrate_velocities(L, h);
-        for (int c = 0; c < cc; c++) solve_contact(L, c, inv_h, contact_speed, 1);
+        solve_contacts(L, inv_h, contact_speed, 1);
         solve_joints(L, h, inv_h, 1);
         integrate_positions(L, h, inv_dt);
-        for (int c = 0; c < cc; c++) solve_contact(L, c, inv_h, contact_speed, 0);
+        delta_geometry(L);
+        solve_contacts(L, inv_h, contact_speed, 0);
         solve_joints(L, h, inv_h, 0);
         apply_restitution(L, rest_threshold);
     }
     finalize(L);
+    vel_store(L);
 }
 
 }  // namespace b3d

@@ -84,13 +84,11 @@ void emu_step(uint32_t* tiles, int count, unsigned long long sig, float dt, int 
     if (!geometry_of(sig, &g, &wb)) return;
     int ntiles = (count + kLanes - 1) / kLanes;
     std::vector<uint32_t> scratch((size_t)ntiles * g.scr_words * kLanes);
-    std::vector<float> vel((size_t)g.max_b * kVelWords * kLanes);
+    std::vector<float> vel((size_t)lds_rows(g) * kLanes);
     for (int w = 0; w < count; w++) {
         if (step_mask && !step_mask[w]) continue;
         Lane L = lane_of(tiles, scratch.data(), vel.data(), g, w);
-        vel_load(L);
         step_world(L, dt, substeps);
-        vel_store(L);
     }
 }
 
