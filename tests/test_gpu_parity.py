@@ -208,3 +208,26 @@ def test_invalid_arguments_do_not_launch():
     assert b3_batch_step_gpu(eng.handle, 0.0, 4) == 0
     torch.cuda.synchronize()
     assert (eng.download().view(np.uint8) == before.view(np.uint8)).all()
+
+
+@pytest.mark.parametrize("scene", [1, 2, 3, 4, 5])
+def test_against_reference_fixtures(scene):
+    """The device against the reference's own outputs (tests/golden):
+    bit-exact where the step path has no atan2f (scenes without hinges);
+    for hinge scenes contact indices exact and the first step's body state
+    within 1e-4 relative / 1e-5 absolute."""
+    from test_oracle_golden import golden
+    states, checkpoints = golden(scene)
+    init = states["initial"]
+    eng = _engine(init, scene)
+    t = 0
+    for cp in checkpoints:
+        gpu_run(eng, scene, t, cp - t)
+        t = cp
+        got, ref = eng.download(), states["step%d" % cp]
+        if scene in (1, 2, 4):
+            bad = diff_words(got, ref, scenes.SCENES[scene].sig)
+            assert len(bad) == 0, describe(bad, got, ref, init)
+        elif cp == checkpoints[0]:
+            assert contact_keys(got) == contact_keys(ref)
+            assert_close_state(got, ref)
