@@ -134,7 +134,20 @@ def main():
     ap.add_argument("--worlds", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only copy MIB MiB device-to-device 10 times with a plain copy kernel (for scaling "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_per_launch": n * 4}))
+        return
     if args.gpus != 1:
         print("bench.py: the engine runs on one GPU; worlds are independent and would shard by world index "
               "with no exchange, but only --gpus 1 is measured here", file=sys.stderr)

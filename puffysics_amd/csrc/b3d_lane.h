@@ -194,14 +194,24 @@ constexpr int J_SPRING_SOFTNESS = B3D_W(B3Joint, spring_softness);
 
 /* old warm-cache record in scratch (the reference's B3Warm, 02_types.inl:133-142) */
 constexpr int O_SHAPE_A = 0, O_SHAPE_B = 1, O_POINT_COUNT = 2, O_FEATURE = 3, O_NORMAL_IMPULSE = 7,
-              O_FRICTION_IMPULSE = 11, O_TWIST_IMPULSE = 13, O_ROLLING_IMPULSE = 14, kOldWords = 17;
+              O_FRICTION_IMPULSE = 11, O_TWIST_IMPULSE = 13, O_ROLLING_IMPULSE = 14, O_KEY = 17, kOldWords = 18;
 
-/* Per-step shape record in scratch: world pose, size, owning body and
- * padded bounds, written once per step by the shape pass so that the pair
- * loop never follows a body index. */
+/* Per-step shape record in scratch: world pose, size and owning body,
+ * written once per step by the shape pass so that the pair loop never
+ * follows a body index.  The padded bounds go to LDS when they fit (or to
+ * the scratch bounds area). */
 constexpr int SS_P = 0, SS_Q = 3, SS_RADIUS = 7, SS_HALF = 8, SS_TYPE = 11, SS_BODY = 12, SS_BFLAGS = 13,
-              SS_LO = 14, SS_HI = 17, SS_CENTER = 20, kShapeScr = 23;
+              SS_CENTER = 14, kShapeScr = 17;
 constexpr int kBodyStatic = 1, kBodyDynamic = 2;   /* SS_BFLAGS bits */
+/* Loops over bodies, shapes and contacts run in chunks, every load of a
+ * chunk issued before any of its results is used. */
+constexpr int kChunk = 4;
+constexpr int kShapeChunk = 4;
+/* Per-step body record: the velocity increments of 09_step.inl:5-18 (all
+ * their inputs are fixed for the step), the damping factors, and the body
+ * kind (type and axis-lock flags). */
+constexpr int BS_DV = 0, BS_DW = 3, BS_LD = 6, BS_AD = 7, BS_KIND = 8, kBodyScr = 9;
+constexpr int kKindDynamic = 1 << 8, kKindStatic = 1 << 9;  /* BS_KIND bits; low byte = lock flags */
 /* Contact point separations for the current delta poses. */
 constexpr int kSepScr = 4;
 /* Joint record in scratch: the joint-connection key and the hinge axis
@@ -226,7 +236,7 @@ struct Geometry {
     int max_b, max_s, max_c, max_j;
     int bo, so, co, jo;   /* word offsets of bodies, shapes, contacts, joints */
     int world_words;      /* words per world (sizeof(B3World) / 4) */
-    int scr_shape, scr_old, scr_sep, scr_joint, scr_words;
+    int scr_shape, scr_old, scr_sep, scr_joint, scr_body, scr_bounds, scr_words;
 };
 
 /* Geometry of a capacity signature; false when it is invalid. */
@@ -247,7 +257,9 @@ B3D_FN bool geometry_of(unsigned long long sig, Geometry* g, size_t* world_bytes
     g->scr_old = g->scr_shape + g->max_s * kShapeScr;
     g->scr_sep = g->scr_old + g->max_c * kOldWords;
     g->scr_joint = g->scr_sep + g->max_c * kSepScr;
-    g->scr_words = g->scr_joint + g->max_j * kJointScr;
+    g->scr_body = g->scr_joint + g->max_j * kJointScr;
+    g->scr_bounds = g->scr_body + g->max_b * kBodyScr;
+    g->scr_words = g->scr_bounds + g->max_s * 6;
     *world_bytes = L.world_size;
     return true;
 }
@@ -261,10 +273,16 @@ struct Lane {
     Geometry g;
 };
 
+/* Shape bounds stay in the LDS rows during contact generation when the
+ * rows of kClipWords + 6 max_s words fit in this many words per lane;
+ * otherwise they go to scratch. */
+constexpr int kMaxLdsRows = 160;
+B3D_FN bool bounds_in_lds(const Geometry& g) { return kClipWords + 6 * g.max_s <= kMaxLdsRows; }
 /* Words of LDS rows per lane that one step needs. */
 B3D_FN int lds_rows(const Geometry& g) {
     int v = g.max_b * kVelWords;
-    return v > kClipWords ? v : kClipWords;
+    int f = bounds_in_lds(g) ? kClipWords + 6 * g.max_s : kClipWords;
+    return v > f ? v : f;
 }
 
 /* Word ranges [lo[i], hi[i]) that a snapshot restore copies: header,
@@ -318,10 +336,22 @@ B3D_FN int body_count(const Lane& L) { return clampi(ldi(L.w, H_BODY_COUNT), 0, 
 /* Stage velocities and flags of every body into the velocity rows. */
 B3D_FN void vel_load(const Lane& L) {
     int nb = body_count(L);
-    for (int b = 0; b < nb; b++) {
-        float* v = L.vel + b * kVelWords * kLanes;
-        for (int c = 0; c < 6; c++) v[c * kLanes] = ldf(L.w, bw(L, b, B_LIN_VEL + c));
-        v[6 * kLanes] = ldf(L.w, bw(L, b, B_FLAGS));
+    for (int b0 = 0; b0 < nb; b0 += 4) {
+        float v[4][kVelWords];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if (b0 + k >= nb) continue;
+#pragma unroll
+            for (int c = 0; c < 6; c++) v[k][c] = ldf(L.w, bw(L, b0 + k, B_LIN_VEL + c));
+            v[k][6] = ldf(L.w, bw(L, b0 + k, B_FLAGS));
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            if (b0 + k >= nb) continue;
+            float* row = L.vel + (b0 + k) * kVelWords * kLanes;
+#pragma unroll
+            for (int c = 0; c < kVelWords; c++) row[c * kLanes] = v[k][c];
+        }
     }
 }
 B3D_FN void vel_store(const Lane& L) {
@@ -373,32 +403,66 @@ B3D_FN uint32_t* shape_rec(const Lane& L, int s) { return L.scr + (L.g.scr_shape
 B3D_FN uint32_t* old_rec(const Lane& L, int k) { return L.scr + (L.g.scr_old + k * kOldWords) * kLanes; }
 B3D_FN uint32_t* sep_rec(const Lane& L, int c) { return L.scr + (L.g.scr_sep + c * kSepScr) * kLanes; }
 B3D_FN uint32_t* joint_rec(const Lane& L, int j) { return L.scr + (L.g.scr_joint + j * kJointScr) * kLanes; }
+B3D_FN uint32_t* body_rec(const Lane& L, int b) { return L.scr + (L.g.scr_body + b * kBodyScr) * kLanes; }
 B3D_FN uint32_t pair_key(int a, int b) { return a < b ? ((uint32_t)a << 16) | (uint32_t)b : ((uint32_t)b << 16) | (uint32_t)a; }
 
 /* Shape pass: world pose, padded bounds and owning-body facts of every
- * shape (b3_shape_aabb plus the 0.02 pad, 08_contacts.inl:109-114). */
-B3D_FN void shape_pass(const Lane& L, int ns) {
+ * shape (b3_shape_aabb plus the 0.02 pad, 08_contacts.inl:109-114).  The
+ * bounds go to `bounds` (lane-strided lo.xyz, hi.xyz per shape), the rest to
+ * the shape records.  Shapes are done in chunks, body poses requested for a
+ * whole chunk at once. */
+B3D_FN void shape_pass(const Lane& L, int ns, float* bounds) {
     V3 pad = v3(kSpeculative, kSpeculative, kSpeculative);
-    for (int s = 0; s < ns; s++) {
-        int b = ldi(L.w, sw(L, s, S_BODY));
-        V3 bpos = ld3(L.w, bw(L, b, B_POSITION));
-        Q brot = ldq(L.w, bw(L, b, B_ROTATION));
-        V3 center = ld3(L.w, bw(L, b, B_CENTER));
-        int btype = ldi(L.w, bw(L, b, B_TYPE));
-        Posed P = pose_shape(L, s, bpos, brot);
-        V3 lo, hi;
-        shape_aabb(P, &lo, &hi);
-        uint32_t* r = shape_rec(L, s);
-        st3(r, SS_P, P.p);
-        stq(r, SS_Q, P.q);
-        stf(r, SS_RADIUS, P.radius);
-        st3(r, SS_HALF, P.half);
-        sti(r, SS_TYPE, P.type);
-        sti(r, SS_BODY, b);
-        sti(r, SS_BFLAGS, (btype == kStatic ? kBodyStatic : 0) | (btype == kDynamic ? kBodyDynamic : 0));
-        st3(r, SS_LO, sub(lo, pad));
-        st3(r, SS_HI, add(hi, pad));
-        st3(r, SS_CENTER, center);
+    for (int s0 = 0; s0 < ns; s0 += kShapeChunk) {
+        int b[kShapeChunk];
+#pragma unroll
+        for (int k = 0; k < kShapeChunk; k++)
+            if (s0 + k < ns) b[k] = ldi(L.w, sw(L, s0 + k, S_BODY));
+        V3 bpos[kShapeChunk], center[kShapeChunk];
+        Q brot[kShapeChunk];
+        int btype[kShapeChunk];
+        Posed P[kShapeChunk];
+#pragma unroll
+        for (int k = 0; k < kShapeChunk; k++) {
+            int s = s0 + k;
+            if (s >= ns) continue;
+            bpos[k] = ld3(L.w, bw(L, b[k], B_POSITION));
+            brot[k] = ldq(L.w, bw(L, b[k], B_ROTATION));
+            center[k] = ld3(L.w, bw(L, b[k], B_CENTER));
+            btype[k] = ldi(L.w, bw(L, b[k], B_TYPE));
+            P[k].type = ldi(L.w, sw(L, s, S_TYPE));
+            P[k].p = ld3(L.w, sw(L, s, S_LOCAL_POS));
+            P[k].q = ldq(L.w, sw(L, s, S_LOCAL_ROT));
+            P[k].radius = ldf(L.w, sw(L, s, S_RADIUS));
+            P[k].half = ld3(L.w, sw(L, s, S_HALF));
+        }
+#pragma unroll
+        for (int k = 0; k < kShapeChunk; k++) {
+            int s = s0 + k;
+            if (s >= ns) continue;
+            /* b3_shape_pos / b3_shape_rot (04_world.inl:293-299) */
+            P[k].p = xf(bpos[k], brot[k], P[k].p);
+            P[k].q = qmul(brot[k], P[k].q);
+            V3 lo, hi;
+            shape_aabb(P[k], &lo, &hi);
+            uint32_t* r = shape_rec(L, s);
+            st3(r, SS_P, P[k].p);
+            stq(r, SS_Q, P[k].q);
+            stf(r, SS_RADIUS, P[k].radius);
+            st3(r, SS_HALF, P[k].half);
+            sti(r, SS_TYPE, P[k].type);
+            sti(r, SS_BODY, b[k]);
+            sti(r, SS_BFLAGS, (btype[k] == kStatic ? kBodyStatic : 0) | (btype[k] == kDynamic ? kBodyDynamic : 0));
+            st3(r, SS_CENTER, center[k]);
+            float* bd = bounds + s * 6 * kLanes;
+            V3 l = sub(lo, pad), h = add(hi, pad);
+            bd[0] = l.x;
+            bd[kLanes] = l.y;
+            bd[2 * kLanes] = l.z;
+            bd[3 * kLanes] = h.x;
+            bd[4 * kLanes] = h.y;
+            bd[5 * kLanes] = h.z;
+        }
     }
 }
 
@@ -412,22 +476,62 @@ B3D_FN Posed posed_from(const uint32_t* r) {
     return P;
 }
 
-/* Copy one contact's warm-start data into the old-cache scratch
- * (08_contacts.inl:65-91). */
-B3D_FN void save_old(const Lane& L, int k) {
-    uint32_t* o = old_rec(L, k);
-    int pc = clampi(ldi(L.w, cw(L, k, C_POINT_COUNT)), 0, kMaxManifold);
-    sti(o, O_SHAPE_A, ldi(L.w, cw(L, k, C_SHAPE_A)));
-    sti(o, O_SHAPE_B, ldi(L.w, cw(L, k, C_SHAPE_B)));
-    sti(o, O_POINT_COUNT, pc);
-    for (int p = 0; p < pc; p++) {
-        sti(o, O_FEATURE + p, ldi(L.w, pw(L, k, p, P_FEATURE)));
-        stf(o, O_NORMAL_IMPULSE + p, ldf(L.w, pw(L, k, p, P_NORMAL_IMPULSE)));
+/* Shape pair (i, j) as one ordered 32-bit key (shape ids are below 2^16). */
+B3D_FN uint32_t shape_key(int i, int j) { return ((uint32_t)i << 16) | (uint32_t)j; }
+
+/* Copy the contacts' warm-start data into the old-cache scratch
+ * (08_contacts.inl:65-91); returns whether their shape pairs are strictly
+ * increasing, as every list the step itself writes is. */
+B3D_FN int save_old(const Lane& L, int old_n) {
+    int sorted = 1;
+    uint32_t prev = 0;
+    for (int k0 = 0; k0 < old_n; k0 += kChunk) {
+        int sa[kChunk], sb[kChunk], pc[kChunk];
+        uint32_t feat[kChunk][kMaxManifold];
+        float ni[kChunk][kMaxManifold], fx[kChunk], fy[kChunk], tw[kChunk];
+        V3 roll[kChunk];
+#pragma unroll
+        for (int q = 0; q < kChunk; q++) {
+            int k = k0 + q;
+            if (k >= old_n) continue;
+            sa[q] = ldi(L.w, cw(L, k, C_SHAPE_A));
+            sb[q] = ldi(L.w, cw(L, k, C_SHAPE_B));
+            pc[q] = clampi(ldi(L.w, cw(L, k, C_POINT_COUNT)), 0, kMaxManifold);
+#pragma unroll
+            for (int p = 0; p < kMaxManifold; p++) {
+                feat[q][p] = ldu(L.w, pw(L, k, p, P_FEATURE));
+                ni[q][p] = ldf(L.w, pw(L, k, p, P_NORMAL_IMPULSE));
+            }
+            fx[q] = ldf(L.w, cw(L, k, C_FRICTION_IMPULSE));
+            fy[q] = ldf(L.w, cw(L, k, C_FRICTION_IMPULSE + 1));
+            tw[q] = ldf(L.w, cw(L, k, C_TWIST_IMPULSE));
+            roll[q] = ld3(L.w, cw(L, k, C_ROLLING_IMPULSE));
+        }
+#pragma unroll
+        for (int q = 0; q < kChunk; q++) {
+            int k = k0 + q;
+            if (k >= old_n) continue;
+            uint32_t* o = old_rec(L, k);
+            uint32_t key = shape_key(sa[q], sb[q]);
+            if (k > 0 && !(prev < key && (uint32_t)sa[q] < 65536u && (uint32_t)sb[q] < 65536u)) sorted = 0;
+            prev = key;
+            sti(o, O_SHAPE_A, sa[q]);
+            sti(o, O_SHAPE_B, sb[q]);
+            sti(o, O_POINT_COUNT, pc[q]);
+            sti(o, O_KEY, (int)key);
+#pragma unroll
+            for (int p = 0; p < kMaxManifold; p++) {
+                if (p >= pc[q]) continue;
+                sti(o, O_FEATURE + p, (int)feat[q][p]);
+                stf(o, O_NORMAL_IMPULSE + p, ni[q][p]);
+            }
+            stf(o, O_FRICTION_IMPULSE, fx[q]);
+            stf(o, O_FRICTION_IMPULSE + 1, fy[q]);
+            stf(o, O_TWIST_IMPULSE, tw[q]);
+            st3(o, O_ROLLING_IMPULSE, roll[q]);
+        }
     }
-    stf(o, O_FRICTION_IMPULSE, ldf(L.w, cw(L, k, C_FRICTION_IMPULSE)));
-    stf(o, O_FRICTION_IMPULSE + 1, ldf(L.w, cw(L, k, C_FRICTION_IMPULSE + 1)));
-    stf(o, O_TWIST_IMPULSE, ldf(L.w, cw(L, k, C_TWIST_IMPULSE)));
-    st3(o, O_ROLLING_IMPULSE, ld3(L.w, cw(L, k, C_ROLLING_IMPULSE)));
+    return sorted;
 }
 
 /* A new contact assembled in registers before it is written out. */
@@ -448,12 +552,19 @@ struct NewContact {
 B3D_FN void warm_from_old(const Lane& L, int k, NewContact* nc) {
     const uint32_t* o = old_rec(L, k);
     int opc = ldi(o, O_POINT_COUNT);
+    uint32_t of[kMaxManifold];
+    float oi[kMaxManifold];
+#pragma unroll
+    for (int q = 0; q < kMaxManifold; q++) {
+        of[q] = ldu(o, O_FEATURE + q);
+        oi[q] = ldf(o, O_NORMAL_IMPULSE + q);
+    }
 #pragma unroll
     for (int p = 0; p < kMaxManifold; p++) {
         if (p >= nc->count) continue;
 #pragma unroll
         for (int q = 0; q < kMaxManifold; q++)
-            if (q < opc && nc->feature[p] == ldu(o, O_FEATURE + q)) nc->ni[p] = ldf(o, O_NORMAL_IMPULSE + q);
+            if (q < opc && nc->feature[p] == of[q]) nc->ni[p] = oi[q];
     }
     nc->fi.x = ldf(o, O_FRICTION_IMPULSE);
     nc->fi.y = ldf(o, O_FRICTION_IMPULSE + 1);
@@ -463,75 +574,67 @@ B3D_FN void warm_from_old(const Lane& L, int k, NewContact* nc) {
 
 B3D_FN int pair_less(int a0, int b0, int a1, int b1) { return a0 < a1 || (a0 == a1 && b0 < b1); }
 
-/* Contact generation and warm start: b3_find_contacts (08_contacts.inl:
- * 64-173) with b3_contact_from_mani (08:5-39).  The prepared fields are
- * filled in by prepare_contacts. */
-B3D_FN void find_contacts(const Lane& L) {
+B3D_FN bool overlaps(const float* bi, const float* bj) {
+    return bi[0] <= bj[3 * kLanes] && bi[3 * kLanes] >= bj[0] && bi[kLanes] <= bj[4 * kLanes]
+        && bi[4 * kLanes] >= bj[kLanes] && bi[2 * kLanes] <= bj[5 * kLanes] && bi[5 * kLanes] >= bj[2 * kLanes];
+}
+
+/* The ordered pair loop of b3_find_contacts (08_contacts.inl:115-172):
+ * broadphase filter (08:45-62), narrowphase, overflow accounting, warm
+ * start and b3_contact_from_mani (08:5-39).  `bounds` holds the padded
+ * shape bounds (LDS or scratch). */
+B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int old_n, int sorted) {
     const Geometry& g = L.g;
-    int old_n = clampi(ldi(L.w, H_CONTACT_COUNT), 0, g.max_c);
-    int sorted = 1;
-    int pa_prev = 0, pb_prev = 0;
-    for (int k = 0; k < old_n; k++) {
-        save_old(L, k);
-        int a = ldi(L.w, cw(L, k, C_SHAPE_A)), b = ldi(L.w, cw(L, k, C_SHAPE_B));
-        if (k > 0 && !pair_less(pa_prev, pb_prev, a, b)) sorted = 0;
-        pa_prev = a;
-        pb_prev = b;
-    }
-    int ns = clampi(ldi(L.w, H_SHAPE_COUNT), 0, g.max_s);
-    int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, g.max_j);
-    shape_pass(L, ns);
-    /* joint-connected body pairs (08:95-108) as sorted-pair keys */
-    for (int j = 0; j < nj; j++) {
-        uint32_t key = 0xffffffffu;
-        if (!ldi(L.w, jw(L, j, J_COLLIDE_CONNECTED)))
-            key = pair_key(ldi(L.w, jw(L, j, J_BODY_A)), ldi(L.w, jw(L, j, J_BODY_B)));
-        sti(joint_rec(L, j), JS_KEY, (int)key);
-    }
     int cc = 0;
     int overflow = ldi(L.w, H_CONTACT_OVERFLOW);
     int dropped = ldi(L.w, H_CONTACTS_DROPPED);
     int optr = 0;
     for (int i = 0; i < ns; i++) {
+        const float* bi = bounds + i * 6 * kLanes;
         const uint32_t* ri = shape_rec(L, i);
-        V3 lo_i = ld3(ri, SS_LO), hi_i = ld3(ri, SS_HI);
         int body_i = ldi(ri, SS_BODY);
         int bf_i = ldi(ri, SS_BFLAGS);
         uint64_t cat_i = ldu64(L.w, sw(L, i, S_CATEGORY));
         uint64_t mask_i = ldu64(L.w, sw(L, i, S_MASK));
+        Posed A = posed_from(ri);
+        V3 ca = ld3(ri, SS_CENTER);
+        float fa = ldf(L.w, sw(L, i, S_FRICTION));
+        float ea = ldf(L.w, sw(L, i, S_RESTITUTION));
+        float rla = ldf(L.w, sw(L, i, S_ROLLING));
         for (int j = i + 1; j < ns; j++) {
-            /* b3_broadphase_pair (08:45-62): bounds first, then the rest */
+            if (!overlaps(bi, bounds + j * 6 * kLanes)) continue;
+            /* everything the pair needs, requested at once */
             const uint32_t* rj = shape_rec(L, j);
-            V3 lo_j = ld3(rj, SS_LO), hi_j = ld3(rj, SS_HI);
-            if (!(lo_i.x <= hi_j.x && hi_i.x >= lo_j.x && lo_i.y <= hi_j.y && hi_i.y >= lo_j.y
-                    && lo_i.z <= hi_j.z && hi_i.z >= lo_j.z))
-                continue;
             int body_j = ldi(rj, SS_BODY);
             int bf_j = ldi(rj, SS_BFLAGS);
+            uint64_t cat_j = ldu64(L.w, sw(L, j, S_CATEGORY));
+            uint64_t mask_j = ldu64(L.w, sw(L, j, S_MASK));
+            Posed B = posed_from(rj);
+            V3 cb = ld3(rj, SS_CENTER);
+            float fb = ldf(L.w, sw(L, j, S_FRICTION));
+            float eb = ldf(L.w, sw(L, j, S_RESTITUTION));
+            float rlb = ldf(L.w, sw(L, j, S_ROLLING));
             if (body_i == body_j) continue;
             if (bf_i & bf_j & kBodyStatic) continue;
-            if ((cat_i & ldu64(L.w, sw(L, j, S_MASK))) == 0 || (ldu64(L.w, sw(L, j, S_CATEGORY)) & mask_i) == 0)
-                continue;
+            if ((cat_i & mask_j) == 0 || (cat_j & mask_i) == 0) continue;
             uint32_t key = pair_key(body_i, body_j);
             int joined = 0;
             for (int k = 0; k < nj; k++) joined |= ldu(joint_rec(L, k), JS_KEY) == key;
             if (joined) continue;
 
             Mani m;
-            collide_pair(&m, posed_from(ri), posed_from(rj), L.vel);
+            collide_pair(&m, A, B, L.vel);
             if (m.count == 0) continue;
             if (cc >= g.max_c) {
                 overflow = 1;
                 dropped++;
                 continue;
             }
-            /* b3_contact_from_mani (08:5-39) */
             NewContact nc;
             nc.count = m.count;
             nc.normal = m.normal;
             nc.t1 = perp(m.normal);
             nc.t2 = cross(nc.t1, m.normal);
-            V3 ca = ld3(ri, SS_CENTER), cb = ld3(rj, SS_CENTER);
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
                 if (p >= m.count) continue;
@@ -544,24 +647,22 @@ B3D_FN void find_contacts(const Lane& L) {
             nc.fi = V2{0.0f, 0.0f};
             nc.twist = 0.0f;
             nc.roll = zero3();
+            /* warm start from the previous step's cache: every matching old
+             * pair, the last one winning (08:154-170) */
             if (sorted) {
-                while (optr < old_n) {
-                    const uint32_t* o = old_rec(L, optr);
-                    if (!pair_less(ldi(o, O_SHAPE_A), ldi(o, O_SHAPE_B), i, j)) break;
+                uint32_t want = shape_key(i, j);
+                uint32_t have = optr < old_n ? ldu(old_rec(L, optr), O_KEY) : 0xffffffffu;
+                while (optr < old_n && have < want) {
                     optr++;
+                    have = optr < old_n ? ldu(old_rec(L, optr), O_KEY) : 0xffffffffu;
                 }
-                if (optr < old_n) {
-                    const uint32_t* o = old_rec(L, optr);
-                    if (ldi(o, O_SHAPE_A) == i && ldi(o, O_SHAPE_B) == j) warm_from_old(L, optr, &nc);
-                }
+                if (optr < old_n && have == want) warm_from_old(L, optr, &nc);
             } else {
                 for (int k = 0; k < old_n; k++) {
                     const uint32_t* o = old_rec(L, k);
                     if (ldi(o, O_SHAPE_A) == i && ldi(o, O_SHAPE_B) == j) warm_from_old(L, k, &nc);
                 }
             }
-            float fa = ldf(L.w, sw(L, i, S_FRICTION)), fb = ldf(L.w, sw(L, j, S_FRICTION));
-            float ea = ldf(L.w, sw(L, i, S_RESTITUTION)), eb = ldf(L.w, sw(L, j, S_RESTITUTION));
             uint32_t* w = L.w;
             sti(w, cw(L, cc, C_SHAPE_A), i);
             sti(w, cw(L, cc, C_SHAPE_B), j);
@@ -583,7 +684,7 @@ B3D_FN void find_contacts(const Lane& L) {
             }
             stf(w, cw(L, cc, C_FRICTION), sqrtf(fa * fb));
             stf(w, cw(L, cc, C_RESTITUTION), ea > eb ? ea : eb);
-            stf(w, cw(L, cc, C_ROLLING), maxf(ldf(L.w, sw(L, i, S_ROLLING)), ldf(L.w, sw(L, j, S_ROLLING))));
+            stf(w, cw(L, cc, C_ROLLING), maxf(rla, rlb));
             stf(w, cw(L, cc, C_TWIST_IMPULSE), nc.twist);
             stf(w, cw(L, cc, C_FRICTION_IMPULSE), nc.fi.x);
             stf(w, cw(L, cc, C_FRICTION_IMPULSE + 1), nc.fi.y);
@@ -596,76 +697,138 @@ B3D_FN void find_contacts(const Lane& L) {
     sti(L.w, H_CONTACTS_DROPPED, dropped);
 }
 
-/* b3_prepare_one_contact (08:234-291) for every new contact. */
+/* Contact generation and warm start: b3_find_contacts (08_contacts.inl:
+ * 64-173).  The prepared fields are filled in by prepare_contacts. */
+B3D_FN void find_contacts(const Lane& L) {
+    const Geometry& g = L.g;
+    int old_n = clampi(ldi(L.w, H_CONTACT_COUNT), 0, g.max_c);
+    int sorted = save_old(L, old_n);
+    int ns = clampi(ldi(L.w, H_SHAPE_COUNT), 0, g.max_s);
+    int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, g.max_j);
+    /* joint-connected body pairs (08:95-108) as sorted-pair keys */
+    for (int j = 0; j < nj; j++) {
+        uint32_t key = 0xffffffffu;
+        if (!ldi(L.w, jw(L, j, J_COLLIDE_CONNECTED)))
+            key = pair_key(ldi(L.w, jw(L, j, J_BODY_A)), ldi(L.w, jw(L, j, J_BODY_B)));
+        sti(joint_rec(L, j), JS_KEY, (int)key);
+    }
+    if (bounds_in_lds(g)) {
+        float* bounds = L.vel + kClipWords * kLanes;
+        shape_pass(L, ns, bounds);
+        find_pairs(L, bounds, ns, nj, old_n, sorted);
+    } else {
+        float* bounds = (float*)(L.scr + g.scr_bounds * kLanes);
+        shape_pass(L, ns, bounds);
+        find_pairs(L, bounds, ns, nj, old_n, sorted);
+    }
+}
+
+/* b3_prepare_one_contact (08:234-291) for every new contact, two contacts
+ * at a time: their heads, then their bodies and points, then the math. */
+constexpr int kPrepChunk = 2;
 B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
     uint32_t* w = L.w;
     int cc = ldi(w, H_CONTACT_COUNT);
     const float inv_tau = 1.0f / kSpeculative;
-    for (int c = 0; c < cc; c++) {
-        int a = ldi(w, cw(L, c, C_BODY_A)), b = ldi(w, cw(L, c, C_BODY_B));
-        int pc = ldi(w, cw(L, c, C_POINT_COUNT));
-        int ta = ldi(w, bw(L, a, B_TYPE)), tb = ldi(w, bw(L, b, B_TYPE));
-        float ma = ta == kDynamic ? ldf(w, bw(L, a, B_INV_MASS)) : 0.0f;
-        float mb = tb == kDynamic ? ldf(w, bw(L, b, B_INV_MASS)) : 0.0f;
-        M3 ia = ta == kDynamic ? ldm3(w, bw(L, a, B_INV_I_WORLD)) : m3zero();
-        M3 ib = tb == kDynamic ? ldm3(w, bw(L, b, B_INV_I_WORLD)) : m3zero();
-        V3 n = ld3(w, cw(L, c, C_NORMAL));
-        V3 t1 = ld3(w, cw(L, c, C_TANGENT1)), t2 = ld3(w, cw(L, c, C_TANGENT2));
-        V3 va = vlin(L, a), wa = vang(L, a);
-        V3 vb = vlin(L, b), wb = vang(L, b);
-        V3 center_a = zero3(), center_b = zero3();
-        float wsum = 0.0f;
-        V3 r_a[kMaxManifold];
+    for (int c0 = 0; c0 < cc; c0 += kPrepChunk) {
+        int a[kPrepChunk], b[kPrepChunk], pc[kPrepChunk], st[kPrepChunk];
 #pragma unroll
-        for (int p = 0; p < kMaxManifold; p++) {
-            if (p >= pc) continue;
-            V3 ra = ld3(w, pw(L, c, p, P_R_A)), rb = ld3(w, pw(L, c, p, P_R_B));
-            r_a[p] = ra;
-            V3 rn_a = cross(ra, n);
-            V3 rn_b = cross(rb, n);
-            float kn = ma + mb + dot(rn_a, mv(ia, rn_a)) + dot(rn_b, mv(ib, rn_b));
-            stf(w, pw(L, c, p, P_NORMAL_MASS), kn > 0.0f ? 1.0f / kn : 0.0f);
-            V3 vra = add(va, cross(wa, ra));
-            V3 vrb = add(vb, cross(wb, rb));
-            stf(w, pw(L, c, p, P_REL_VEL), dot(n, sub(vrb, vra)));
-            stf(w, pw(L, c, p, P_TOTAL_NORMAL), 0.0f);
-            float sep = ldf(w, pw(L, c, p, P_BASE_SEP)) + dot(sub(rb, ra), n);
-            float weight = clampf(2.0f - sep * inv_tau, kMinFrictionW, 1.0f);
-            center_a = madd(center_a, weight, ra);
-            center_b = madd(center_b, weight, rb);
-            wsum += weight;
+        for (int k = 0; k < kPrepChunk; k++) {
+            int c = c0 + k;
+            if (c >= cc) continue;
+            a[k] = ldi(w, cw(L, c, C_BODY_A));
+            b[k] = ldi(w, cw(L, c, C_BODY_B));
+            pc[k] = ldi(w, cw(L, c, C_POINT_COUNT));
+            st[k] = ldi(w, cw(L, c, C_STATIC));
         }
-        float invw = wsum > 0.0f ? 1.0f / wsum : 0.0f;
-        center_a = scale(center_a, invw);
-        center_b = scale(center_b, invw);
+        int ta[kPrepChunk], tb[kPrepChunk];
+        float ima[kPrepChunk], imb[kPrepChunk];
+        M3 iwa[kPrepChunk], iwb[kPrepChunk];
+        V3 n[kPrepChunk], t1[kPrepChunk], t2[kPrepChunk], ra[kPrepChunk][kMaxManifold], rb[kPrepChunk][kMaxManifold];
+        float bs[kPrepChunk][kMaxManifold];
 #pragma unroll
-        for (int p = 0; p < kMaxManifold; p++)
-            if (p < pc) stf(w, pw(L, c, p, P_LEVER), len(sub(r_a[p], center_a)));
-        V3 rt_a1 = cross(center_a, t1);
-        V3 rt_a2 = cross(center_a, t2);
-        V3 rt_b1 = cross(center_b, t1);
-        V3 rt_b2 = cross(center_b, t2);
-        M2 k2;
-        k2.cx.x = ma + mb + dot(rt_a1, mv(ia, rt_a1)) + dot(rt_b1, mv(ib, rt_b1));
-        k2.cy.y = ma + mb + dot(rt_a2, mv(ia, rt_a2)) + dot(rt_b2, mv(ib, rt_b2));
-        k2.cx.y = dot(rt_a1, mv(ia, rt_a2)) + dot(rt_b1, mv(ib, rt_b2));
-        k2.cy.x = k2.cx.y;
-        M2 tmass = inv2(k2);
-        M3 isum = madd3(ia, ib);
-        float kt = dot(n, mv(isum, n));
-        st3(w, cw(L, c, C_CENTER_A), center_a);
-        st3(w, cw(L, c, C_CENTER_B), center_b);
-        stf(w, cw(L, c, C_TWIST_MASS), kt > 0.0f ? 1.0f / kt : 0.0f);
-        stf(w, cw(L, c, C_TANGENT_MASS), tmass.cx.x);
-        stf(w, cw(L, c, C_TANGENT_MASS + 1), tmass.cx.y);
-        stf(w, cw(L, c, C_TANGENT_MASS + 2), tmass.cy.x);
-        stf(w, cw(L, c, C_TANGENT_MASS + 3), tmass.cy.y);
-        stm3(w, cw(L, c, C_ROLLING_MASS), inv3(isum));
-        stf(w, cw(L, c, C_INV_MASS_A), ma);
-        stf(w, cw(L, c, C_INV_MASS_B), mb);
-        stm3(w, cw(L, c, C_INV_I_A), ia);
-        stm3(w, cw(L, c, C_INV_I_B), ib);
-        stsoft(w, cw(L, c, C_SOFTNESS), ldi(w, cw(L, c, C_STATIC)) ? ss : cs);
+        for (int k = 0; k < kPrepChunk; k++) {
+            int c = c0 + k;
+            if (c >= cc) continue;
+            ta[k] = ldi(w, bw(L, a[k], B_TYPE));
+            tb[k] = ldi(w, bw(L, b[k], B_TYPE));
+            ima[k] = ldf(w, bw(L, a[k], B_INV_MASS));
+            imb[k] = ldf(w, bw(L, b[k], B_INV_MASS));
+            iwa[k] = ldm3(w, bw(L, a[k], B_INV_I_WORLD));
+            iwb[k] = ldm3(w, bw(L, b[k], B_INV_I_WORLD));
+            n[k] = ld3(w, cw(L, c, C_NORMAL));
+            t1[k] = ld3(w, cw(L, c, C_TANGENT1));
+            t2[k] = ld3(w, cw(L, c, C_TANGENT2));
+#pragma unroll
+            for (int p = 0; p < kMaxManifold; p++) {
+                if (p >= pc[k]) continue;
+                ra[k][p] = ld3(w, pw(L, c, p, P_R_A));
+                rb[k][p] = ld3(w, pw(L, c, p, P_R_B));
+                bs[k][p] = ldf(w, pw(L, c, p, P_BASE_SEP));
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kPrepChunk; k++) {
+            int c = c0 + k;
+            if (c >= cc) continue;
+            float ma = ta[k] == kDynamic ? ima[k] : 0.0f;
+            float mb = tb[k] == kDynamic ? imb[k] : 0.0f;
+            M3 ia = ta[k] == kDynamic ? iwa[k] : m3zero();
+            M3 ib = tb[k] == kDynamic ? iwb[k] : m3zero();
+            V3 va = vlin(L, a[k]), wa = vang(L, a[k]);
+            V3 vb = vlin(L, b[k]), wb = vang(L, b[k]);
+            V3 center_a = zero3(), center_b = zero3();
+            float wsum = 0.0f;
+#pragma unroll
+            for (int p = 0; p < kMaxManifold; p++) {
+                if (p >= pc[k]) continue;
+                V3 rap = ra[k][p], rbp = rb[k][p];
+                V3 rn_a = cross(rap, n[k]);
+                V3 rn_b = cross(rbp, n[k]);
+                float kn = ma + mb + dot(rn_a, mv(ia, rn_a)) + dot(rn_b, mv(ib, rn_b));
+                stf(w, pw(L, c, p, P_NORMAL_MASS), kn > 0.0f ? 1.0f / kn : 0.0f);
+                V3 vra = add(va, cross(wa, rap));
+                V3 vrb = add(vb, cross(wb, rbp));
+                stf(w, pw(L, c, p, P_REL_VEL), dot(n[k], sub(vrb, vra)));
+                stf(w, pw(L, c, p, P_TOTAL_NORMAL), 0.0f);
+                float sep = bs[k][p] + dot(sub(rbp, rap), n[k]);
+                float weight = clampf(2.0f - sep * inv_tau, kMinFrictionW, 1.0f);
+                center_a = madd(center_a, weight, rap);
+                center_b = madd(center_b, weight, rbp);
+                wsum += weight;
+            }
+            float invw = wsum > 0.0f ? 1.0f / wsum : 0.0f;
+            center_a = scale(center_a, invw);
+            center_b = scale(center_b, invw);
+#pragma unroll
+            for (int p = 0; p < kMaxManifold; p++)
+                if (p < pc[k]) stf(w, pw(L, c, p, P_LEVER), len(sub(ra[k][p], center_a)));
+            V3 rt_a1 = cross(center_a, t1[k]);
+            V3 rt_a2 = cross(center_a, t2[k]);
+            V3 rt_b1 = cross(center_b, t1[k]);
+            V3 rt_b2 = cross(center_b, t2[k]);
+            M2 k2;
+            k2.cx.x = ma + mb + dot(rt_a1, mv(ia, rt_a1)) + dot(rt_b1, mv(ib, rt_b1));
+            k2.cy.y = ma + mb + dot(rt_a2, mv(ia, rt_a2)) + dot(rt_b2, mv(ib, rt_b2));
+            k2.cx.y = dot(rt_a1, mv(ia, rt_a2)) + dot(rt_b1, mv(ib, rt_b2));
+            k2.cy.x = k2.cx.y;
+            M2 tmass = inv2(k2);
+            M3 isum = madd3(ia, ib);
+            float kt = dot(n[k], mv(isum, n[k]));
+            st3(w, cw(L, c, C_CENTER_A), center_a);
+            st3(w, cw(L, c, C_CENTER_B), center_b);
+            stf(w, cw(L, c, C_TWIST_MASS), kt > 0.0f ? 1.0f / kt : 0.0f);
+            stf(w, cw(L, c, C_TANGENT_MASS), tmass.cx.x);
+            stf(w, cw(L, c, C_TANGENT_MASS + 1), tmass.cx.y);
+            stf(w, cw(L, c, C_TANGENT_MASS + 2), tmass.cy.x);
+            stf(w, cw(L, c, C_TANGENT_MASS + 3), tmass.cy.y);
+            stm3(w, cw(L, c, C_ROLLING_MASS), inv3(isum));
+            stf(w, cw(L, c, C_INV_MASS_A), ma);
+            stf(w, cw(L, c, C_INV_MASS_B), mb);
+            stm3(w, cw(L, c, C_INV_I_A), ia);
+            stm3(w, cw(L, c, C_INV_I_B), ib);
+            stsoft(w, cw(L, c, C_SOFTNESS), st[k] ? ss : cs);
+        }
     }
 }
 
@@ -728,28 +891,69 @@ B3D_FN void apply_impulse(const Lane& L, int b, float m, M3 i, V3 r, V3 p, float
     set_vang(L, b, add(vang(L, b), mv(i, scale(cross(r, p), s))));
 }
 
-/* b3_warm_start over contacts (08:194-232, 293-313). */
+/* b3_warm_start over contacts (08:194-232, 293-313), two contacts at a
+ * time: heads, then rows, then the impulses in contact order. */
 B3D_FN void warm_start_contacts(const Lane& L) {
     int cc = ldi(L.w, H_CONTACT_COUNT);
     const uint32_t* w = L.w;
-    for (int c = 0; c < cc; c++) {
-        int a = ldi(w, cw(L, c, C_BODY_A)), b = ldi(w, cw(L, c, C_BODY_B));
-        int pc = ldi(w, cw(L, c, C_POINT_COUNT));
-        float ma = ldf(w, cw(L, c, C_INV_MASS_A)), mb = ldf(w, cw(L, c, C_INV_MASS_B));
-        M3 ia = ldm3(w, cw(L, c, C_INV_I_A)), ib = ldm3(w, cw(L, c, C_INV_I_B));
-        V3 n = ld3(w, cw(L, c, C_NORMAL));
-        for (int p = 0; p < pc; p++) {
-            V3 P = scale(n, ldf(w, pw(L, c, p, P_NORMAL_IMPULSE)));
-            apply_impulse(L, a, ma, ia, ld3(w, pw(L, c, p, P_R_A)), P, -1.0f);
-            apply_impulse(L, b, mb, ib, ld3(w, pw(L, c, p, P_R_B)), P, 1.0f);
+    for (int c0 = 0; c0 < cc; c0 += kPrepChunk) {
+        int a[kPrepChunk], b[kPrepChunk], pc[kPrepChunk];
+#pragma unroll
+        for (int k = 0; k < kPrepChunk; k++) {
+            int c = c0 + k;
+            if (c >= cc) continue;
+            a[k] = ldi(w, cw(L, c, C_BODY_A));
+            b[k] = ldi(w, cw(L, c, C_BODY_B));
+            pc[k] = ldi(w, cw(L, c, C_POINT_COUNT));
         }
-        V3 f = add(scale(ld3(w, cw(L, c, C_TANGENT1)), ldf(w, cw(L, c, C_FRICTION_IMPULSE))),
-            scale(ld3(w, cw(L, c, C_TANGENT2)), ldf(w, cw(L, c, C_FRICTION_IMPULSE + 1))));
-        apply_impulse(L, a, ma, ia, ld3(w, cw(L, c, C_CENTER_A)), f, -1.0f);
-        apply_impulse(L, b, mb, ib, ld3(w, cw(L, c, C_CENTER_B)), f, 1.0f);
-        V3 tr = add(scale(n, ldf(w, cw(L, c, C_TWIST_IMPULSE))), ld3(w, cw(L, c, C_ROLLING_IMPULSE)));
-        if (is_dyn_flag(L, a)) set_vang(L, a, sub(vang(L, a), mv(ia, tr)));
-        if (is_dyn_flag(L, b)) set_vang(L, b, add(vang(L, b), mv(ib, tr)));
+        float ma[kPrepChunk], mb[kPrepChunk], ni[kPrepChunk][kMaxManifold], tw[kPrepChunk];
+        M3 ia[kPrepChunk], ib[kPrepChunk];
+        V3 n[kPrepChunk], ra[kPrepChunk][kMaxManifold], rb[kPrepChunk][kMaxManifold], t1[kPrepChunk], t2[kPrepChunk];
+        V3 ca[kPrepChunk], cb[kPrepChunk], roll[kPrepChunk];
+        V2 fi[kPrepChunk];
+#pragma unroll
+        for (int k = 0; k < kPrepChunk; k++) {
+            int c = c0 + k;
+            if (c >= cc) continue;
+            ma[k] = ldf(w, cw(L, c, C_INV_MASS_A));
+            mb[k] = ldf(w, cw(L, c, C_INV_MASS_B));
+            ia[k] = ldm3(w, cw(L, c, C_INV_I_A));
+            ib[k] = ldm3(w, cw(L, c, C_INV_I_B));
+            n[k] = ld3(w, cw(L, c, C_NORMAL));
+#pragma unroll
+            for (int p = 0; p < kMaxManifold; p++) {
+                if (p >= pc[k]) continue;
+                ni[k][p] = ldf(w, pw(L, c, p, P_NORMAL_IMPULSE));
+                ra[k][p] = ld3(w, pw(L, c, p, P_R_A));
+                rb[k][p] = ld3(w, pw(L, c, p, P_R_B));
+            }
+            t1[k] = ld3(w, cw(L, c, C_TANGENT1));
+            t2[k] = ld3(w, cw(L, c, C_TANGENT2));
+            fi[k].x = ldf(w, cw(L, c, C_FRICTION_IMPULSE));
+            fi[k].y = ldf(w, cw(L, c, C_FRICTION_IMPULSE + 1));
+            ca[k] = ld3(w, cw(L, c, C_CENTER_A));
+            cb[k] = ld3(w, cw(L, c, C_CENTER_B));
+            tw[k] = ldf(w, cw(L, c, C_TWIST_IMPULSE));
+            roll[k] = ld3(w, cw(L, c, C_ROLLING_IMPULSE));
+        }
+#pragma unroll
+        for (int k = 0; k < kPrepChunk; k++) {
+            int c = c0 + k;
+            if (c >= cc) continue;
+#pragma unroll
+            for (int p = 0; p < kMaxManifold; p++) {
+                if (p >= pc[k]) continue;
+                V3 P = scale(n[k], ni[k][p]);
+                apply_impulse(L, a[k], ma[k], ia[k], ra[k][p], P, -1.0f);
+                apply_impulse(L, b[k], mb[k], ib[k], rb[k][p], P, 1.0f);
+            }
+            V3 f = add(scale(t1[k], fi[k].x), scale(t2[k], fi[k].y));
+            apply_impulse(L, a[k], ma[k], ia[k], ca[k], f, -1.0f);
+            apply_impulse(L, b[k], mb[k], ib[k], cb[k], f, 1.0f);
+            V3 tr = add(scale(n[k], tw[k]), roll[k]);
+            if (is_dyn_flag(L, a[k])) set_vang(L, a[k], sub(vang(L, a[k]), mv(ia[k], tr)));
+            if (is_dyn_flag(L, b[k])) set_vang(L, b[k], add(vang(L, b[k]), mv(ib[k], tr)));
+        }
     }
 }
 
@@ -805,68 +1009,129 @@ B3D_FN M3 point_k(float ma, float mb, M3 ia, M3 ib, V3 ra, V3 rb) {
 B3D_FN void delta_geometry(const Lane& L) {
     uint32_t* w = L.w;
     int cc = ldi(w, H_CONTACT_COUNT);
-    for (int c = 0; c < cc; c++) {
-        int a = ldi(w, cw(L, c, C_BODY_A)), b = ldi(w, cw(L, c, C_BODY_B));
-        int pc = ldi(w, cw(L, c, C_POINT_COUNT));
-        V3 n = ld3(w, cw(L, c, C_NORMAL));
-        Q dqa = ldq(w, bw(L, a, B_DELTA_ROT)), dqb = ldq(w, bw(L, b, B_DELTA_ROT));
-        V3 dp = sub(ld3(w, bw(L, b, B_DELTA_POS)), ld3(w, bw(L, a, B_DELTA_POS)));
-        uint32_t* sp = sep_rec(L, c);
-        for (int p = 0; p < pc; p++) {
-            V3 ra = ld3(w, pw(L, c, p, P_R_A)), rb = ld3(w, pw(L, c, p, P_R_B));
-            V3 ds = add(dp, sub(rot(dqb, rb), rot(dqa, ra)));
-            stf(sp, p, dot(ds, n) + ldf(w, pw(L, c, p, P_BASE_SEP)));
+    for (int c0 = 0; c0 < cc; c0 += kChunk) {
+        int a[kChunk], b[kChunk], pc[kChunk];
+#pragma unroll
+        for (int k = 0; k < kChunk; k++) {
+            int c = c0 + k;
+            if (c >= cc) continue;
+            a[k] = ldi(w, cw(L, c, C_BODY_A));
+            b[k] = ldi(w, cw(L, c, C_BODY_B));
+            pc[k] = ldi(w, cw(L, c, C_POINT_COUNT));
+        }
+        V3 n[kChunk], dp[kChunk], ra[kChunk][kMaxManifold], rb[kChunk][kMaxManifold];
+        Q dqa[kChunk], dqb[kChunk];
+        float bs[kChunk][kMaxManifold];
+#pragma unroll
+        for (int k = 0; k < kChunk; k++) {
+            int c = c0 + k;
+            if (c >= cc) continue;
+            n[k] = ld3(w, cw(L, c, C_NORMAL));
+            dqa[k] = ldq(w, bw(L, a[k], B_DELTA_ROT));
+            dqb[k] = ldq(w, bw(L, b[k], B_DELTA_ROT));
+            dp[k] = sub(ld3(w, bw(L, b[k], B_DELTA_POS)), ld3(w, bw(L, a[k], B_DELTA_POS)));
+#pragma unroll
+            for (int p = 0; p < kMaxManifold; p++) {
+                if (p >= pc[k]) continue;
+                ra[k][p] = ld3(w, pw(L, c, p, P_R_A));
+                rb[k][p] = ld3(w, pw(L, c, p, P_R_B));
+                bs[k][p] = ldf(w, pw(L, c, p, P_BASE_SEP));
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kChunk; k++) {
+            int c = c0 + k;
+            if (c >= cc) continue;
+            uint32_t* sp = sep_rec(L, c);
+#pragma unroll
+            for (int p = 0; p < kMaxManifold; p++) {
+                if (p >= pc[k]) continue;
+                V3 ds = add(dp[k], sub(rot(dqb[k], rb[k][p]), rot(dqa[k], ra[k][p])));
+                stf(sp, p, dot(ds, n[k]) + bs[k][p]);
+            }
         }
     }
     int nj = clampi(ldi(w, H_JOINT_COUNT), 0, L.g.max_j);
-    for (int j = 0; j < nj; j++) {
-        int a = ldi(w, jw(L, j, J_BODY_A)), b = ldi(w, jw(L, j, J_BODY_B));
-        Q dqa = ldq(w, bw(L, a, B_DELTA_ROT)), dqb = ldq(w, bw(L, b, B_DELTA_ROT));
-        V3 dpa = ld3(w, bw(L, a, B_DELTA_POS)), dpb = ld3(w, bw(L, b, B_DELTA_POS));
-        float ma = ldf(w, jw(L, j, J_INV_MASS_A)), mb = ldf(w, jw(L, j, J_INV_MASS_B));
-        M3 ia = ldm3(w, jw(L, j, J_INV_I_A)), ib = ldm3(w, jw(L, j, J_INV_I_B));
-        int fixed = ldi(w, jw(L, j, J_FIXED_ROTATION));
-        uint32_t* r = joint_rec(L, j);
-        Q qa = qmul(dqa, ldq(w, jw(L, j, J_FRAME_Q_A)));
-        Q qb = qmul(dqb, ldq(w, jw(L, j, J_FRAME_Q_B)));
-        if (qdot(qa, qb) < 0.0f) qb = qneg(qb);
-        Q rel = qinv_mul(qa, qb);
-        V3 ra = rot(dqa, ld3(w, jw(L, j, J_FRAME_P_A)));
-        V3 rb = rot(dqb, ld3(w, jw(L, j, J_FRAME_P_B)));
-        st3(r, JS_RA, ra);
-        st3(r, JS_RB, rb);
-        st3(r, JS_PSEP, add(add(sub(dpb, dpa), sub(rb, ra)), ld3(w, jw(L, j, J_DELTA_CENTER))));
-        stm3(r, JS_KINV, inv3(point_k(ma, mb, ia, ib, ra, rb)));
-        if (ldi(w, jw(L, j, J_TYPE)) == kJointWeld) {
-            Q s = rel;
-            if (rel.s < 0.0f) s = qneg(rel);
-            Q diff = q4(-s.v.x, -s.v.y, -s.v.z, 1.0f - s.s);
-            st3(r, JS_CV, neg(rot(qa, scale(qmul(diff, qconj(s)).v, 2.0f))));
-            continue;
+    for (int j0 = 0; j0 < nj; j0 += kPrepChunk) {
+        int a[kPrepChunk], b[kPrepChunk];
+#pragma unroll
+        for (int k = 0; k < kPrepChunk; k++) {
+            int j = j0 + k;
+            if (j >= nj) continue;
+            a[k] = ldi(w, jw(L, j, J_BODY_A));
+            b[k] = ldi(w, jw(L, j, J_BODY_B));
         }
-        int need_twist = (ldi(w, jw(L, j, J_ENABLE_SPRING)) || ldi(w, jw(L, j, J_ENABLE_LIMIT))
-            || ldi(w, jw(L, j, J_ENABLE_MOTOR))) && !fixed;
-        stf(r, JS_TW, need_twist ? twist(rel) : 0.0f);
-        stf(r, JS_RELX, rel.v.x);
-        stf(r, JS_RELY, rel.v.y);
-        if (!fixed) {
-            V3 px, py;
-            hinge_perps(qa, rel, &px, &py);
-            st3(r, JS_PX, px);
-            st3(r, JS_PY, py);
-            /* the solve's latest hinge rows are part of the joint state */
-            st3(w, jw(L, j, J_PERP_X), px);
-            st3(w, jw(L, j, J_PERP_Y), py);
-            M3 isum = madd3(ia, ib);
-            float kxx = dot(px, mv(isum, px));
-            float kyy = dot(py, mv(isum, py));
-            float kxy = dot(px, mv(isum, py));
-            float det = kxx * kyy - kxy * kxy;
-            stf(r, JS_KXX, kxx);
-            stf(r, JS_KYY, kyy);
-            stf(r, JS_KXY, kxy);
-            sti(r, JS_KOK, det > 1.0e-12f);
-            stf(r, JS_KINV2, det > 1.0e-12f ? 1.0f / det : 0.0f);
+        Q dqa[kPrepChunk], dqb[kPrepChunk], fqa[kPrepChunk], fqb[kPrepChunk];
+        V3 dpa[kPrepChunk], dpb[kPrepChunk], fpa[kPrepChunk], fpb[kPrepChunk], dcen[kPrepChunk];
+        float ma[kPrepChunk], mb[kPrepChunk];
+        M3 ia[kPrepChunk], ib[kPrepChunk];
+        int fixed[kPrepChunk], type[kPrepChunk], en[kPrepChunk];
+#pragma unroll
+        for (int k = 0; k < kPrepChunk; k++) {
+            int j = j0 + k;
+            if (j >= nj) continue;
+            dqa[k] = ldq(w, bw(L, a[k], B_DELTA_ROT));
+            dqb[k] = ldq(w, bw(L, b[k], B_DELTA_ROT));
+            dpa[k] = ld3(w, bw(L, a[k], B_DELTA_POS));
+            dpb[k] = ld3(w, bw(L, b[k], B_DELTA_POS));
+            ma[k] = ldf(w, jw(L, j, J_INV_MASS_A));
+            mb[k] = ldf(w, jw(L, j, J_INV_MASS_B));
+            ia[k] = ldm3(w, jw(L, j, J_INV_I_A));
+            ib[k] = ldm3(w, jw(L, j, J_INV_I_B));
+            fixed[k] = ldi(w, jw(L, j, J_FIXED_ROTATION));
+            type[k] = ldi(w, jw(L, j, J_TYPE));
+            en[k] = ldi(w, jw(L, j, J_ENABLE_SPRING)) | ldi(w, jw(L, j, J_ENABLE_LIMIT)) | ldi(w, jw(L, j, J_ENABLE_MOTOR));
+            fqa[k] = ldq(w, jw(L, j, J_FRAME_Q_A));
+            fqb[k] = ldq(w, jw(L, j, J_FRAME_Q_B));
+            fpa[k] = ld3(w, jw(L, j, J_FRAME_P_A));
+            fpb[k] = ld3(w, jw(L, j, J_FRAME_P_B));
+            dcen[k] = ld3(w, jw(L, j, J_DELTA_CENTER));
+        }
+#pragma unroll
+        for (int k = 0; k < kPrepChunk; k++) {
+            int j = j0 + k;
+            if (j >= nj) continue;
+            uint32_t* r = joint_rec(L, j);
+            Q qa = qmul(dqa[k], fqa[k]);
+            Q qb = qmul(dqb[k], fqb[k]);
+            if (qdot(qa, qb) < 0.0f) qb = qneg(qb);
+            Q rel = qinv_mul(qa, qb);
+            V3 ra = rot(dqa[k], fpa[k]);
+            V3 rb = rot(dqb[k], fpb[k]);
+            st3(r, JS_RA, ra);
+            st3(r, JS_RB, rb);
+            st3(r, JS_PSEP, add(add(sub(dpb[k], dpa[k]), sub(rb, ra)), dcen[k]));
+            stm3(r, JS_KINV, inv3(point_k(ma[k], mb[k], ia[k], ib[k], ra, rb)));
+            if (type[k] == kJointWeld) {
+                Q sq = rel;
+                if (rel.s < 0.0f) sq = qneg(rel);
+                Q diff = q4(-sq.v.x, -sq.v.y, -sq.v.z, 1.0f - sq.s);
+                st3(r, JS_CV, neg(rot(qa, scale(qmul(diff, qconj(sq)).v, 2.0f))));
+                continue;
+            }
+            int need_twist = en[k] && !fixed[k];
+            stf(r, JS_TW, need_twist ? twist(rel) : 0.0f);
+            stf(r, JS_RELX, rel.v.x);
+            stf(r, JS_RELY, rel.v.y);
+            if (!fixed[k]) {
+                V3 px, py;
+                hinge_perps(qa, rel, &px, &py);
+                st3(r, JS_PX, px);
+                st3(r, JS_PY, py);
+                /* the solve's latest hinge rows are part of the joint state */
+                st3(w, jw(L, j, J_PERP_X), px);
+                st3(w, jw(L, j, J_PERP_Y), py);
+                M3 isum = madd3(ia[k], ib[k]);
+                float kxx = dot(px, mv(isum, px));
+                float kyy = dot(py, mv(isum, py));
+                float kxy = dot(px, mv(isum, py));
+                float det = kxx * kyy - kxy * kxy;
+                stf(r, JS_KXX, kxx);
+                stf(r, JS_KYY, kyy);
+                stf(r, JS_KXY, kxy);
+                sti(r, JS_KOK, det > 1.0e-12f);
+                stf(r, JS_KINV2, det > 1.0e-12f ? 1.0f / det : 0.0f);
+            }
         }
     }
 }
@@ -910,28 +1175,46 @@ struct CRow {
     M2 tm;
 };
 
-B3D_FN void crow_load(const Lane& L, int c, int relax, CRow* r) {
+/* The first words of a contact row, loaded two contacts ahead so that the
+ * rest of the row can be loaded one contact ahead without waiting. */
+struct CHead { int a, b, pc; };
+
+B3D_FN CHead chead_load(const Lane& L, int c) {
+    CHead h;
+    h.a = ldi(L.w, cw(L, c, C_BODY_A));
+    h.b = ldi(L.w, cw(L, c, C_BODY_B));
+    h.pc = ldi(L.w, cw(L, c, C_POINT_COUNT));
+    return h;
+}
+
+/* Masses and softness of a row: loaded when its solve starts. */
+B3D_FN void crow_masses(const Lane& L, int c, CRow* r) {
     const uint32_t* w = L.w;
-    r->a = ldi(w, cw(L, c, C_BODY_A));
-    r->b = ldi(w, cw(L, c, C_BODY_B));
-    r->pc = ldi(w, cw(L, c, C_POINT_COUNT));
-    r->n = ld3(w, cw(L, c, C_NORMAL));
     r->ma = ldf(w, cw(L, c, C_INV_MASS_A));
     r->mb = ldf(w, cw(L, c, C_INV_MASS_B));
     r->ia = ldm3(w, cw(L, c, C_INV_I_A));
     r->ib = ldm3(w, cw(L, c, C_INV_I_B));
     r->soft = ldsoft(w, cw(L, c, C_SOFTNESS));
+}
+
+/* Normal, points and friction data of a row: loaded one contact ahead. */
+B3D_FN void crow_load(const Lane& L, int c, CHead h, int relax, CRow* r) {
+    const uint32_t* w = L.w;
+    r->a = h.a;
+    r->b = h.b;
+    r->pc = h.pc;
+    r->n = ld3(w, cw(L, c, C_NORMAL));
     const uint32_t* sp = sep_rec(L, c);
 #pragma unroll
     for (int p = 0; p < kMaxManifold; p++) {
-        if (p >= r->pc) continue;
+        if (p >= h.pc) continue;
         CPoint& q = r->pt[p];
         q.ra = ld3(w, pw(L, c, p, P_R_A));
         q.rb = ld3(w, pw(L, c, p, P_R_B));
         q.nmass = ldf(w, pw(L, c, p, P_NORMAL_MASS));
         q.ni = ldf(w, pw(L, c, p, P_NORMAL_IMPULSE));
         q.tn = ldf(w, pw(L, c, p, P_TOTAL_NORMAL));
-        q.lever = ldf(w, pw(L, c, p, P_LEVER));
+        q.lever = relax ? ldf(w, pw(L, c, p, P_LEVER)) : 0.0f;
         q.sep = ldf(sp, p);
     }
     if (relax) {
@@ -1042,17 +1325,25 @@ B3D_FN void crow_solve(const Lane& L, int c, CRow& r, float inv_h, float contact
     }
 }
 
-/* b3_solve_contacts (08:415-437): one Gauss-Seidel sweep in contact order,
- * with the next contact's row loaded while the current one is solved. */
+/* b3_solve_contacts (08:415-437): one Gauss-Seidel sweep in contact order.
+ * Row c+1 is in flight while row c is solved, and the head of row c+2 while
+ * row c+1 loads. */
 B3D_FN void solve_contacts(const Lane& L, float inv_h, float contact_speed, int use_bias) {
     int cc = ldi(L.w, H_CONTACT_COUNT);
     if (cc <= 0) return;
+    int relax = !use_bias;
+    CHead h1 = chead_load(L, 0);
     CRow cur, nxt;
-    crow_load(L, 0, !use_bias, &cur);
+    crow_load(L, 0, h1, relax, &cur);
+    if (cc > 1) h1 = chead_load(L, 1);
     for (int c = 0; c < cc; c++) {
-        if (c + 1 < cc) crow_load(L, c + 1, !use_bias, &nxt);
+        CHead h2 = h1;
+        if (c + 2 < cc) h2 = chead_load(L, c + 2);
+        crow_masses(L, c, &cur);
+        if (c + 1 < cc) crow_load(L, c + 1, h1, relax, &nxt);
         crow_solve(L, c, cur, inv_h, contact_speed, use_bias);
         cur = nxt;
+        h1 = h2;
     }
 }
 
@@ -1098,6 +1389,147 @@ B3D_FN void apply_restitution(const Lane& L, float threshold) {
     }
 }
 
+/* A joint row as one solve needs it: the prepared constants, the delta
+ * state geometry and the accumulated impulses. */
+struct JHead { int a, b, type; };
+struct JRow {
+    int a, b, type, fixed, en_spring, en_motor, en_limit;
+    float ma, mb;
+    M3 ia, ib;
+    Soft soft;
+    V3 ra, rb, psep, lin_imp;
+    M3 kinv;
+    /* revolute */
+    V3 axis, ia_ax, ib_ax, px, py;
+    float axial_mass, max_torque, speed, target, lower, upper;
+    Soft spring_soft;
+    float tw, relx, rely, kxx, kyy, kxy, kinv2;
+    int kok;
+    float spring_imp, motor_imp, lower_imp, upper_imp;
+    V2 perp_imp;
+    /* weld */
+    float ang_hz, lin_hz;
+    Soft ang_spring, lin_spring;
+    V3 cv, ang_imp;
+    M3 ang_mass;
+};
+
+B3D_FN JHead jhead_load(const Lane& L, int j) {
+    JHead h;
+    h.a = ldi(L.w, jw(L, j, J_BODY_A));
+    h.b = ldi(L.w, jw(L, j, J_BODY_B));
+    h.type = ldi(L.w, jw(L, j, J_TYPE));
+    return h;
+}
+
+B3D_FN void jrow_load(const Lane& L, int j, JHead h, JRow* r) {
+    const uint32_t* w = L.w;
+    const uint32_t* g = joint_rec(L, j);
+    r->a = h.a;
+    r->b = h.b;
+    r->type = h.type;
+    r->fixed = ldi(w, jw(L, j, J_FIXED_ROTATION));
+    r->ma = ldf(w, jw(L, j, J_INV_MASS_A));
+    r->mb = ldf(w, jw(L, j, J_INV_MASS_B));
+    r->ia = ldm3(w, jw(L, j, J_INV_I_A));
+    r->ib = ldm3(w, jw(L, j, J_INV_I_B));
+    r->soft = ldsoft(w, jw(L, j, J_SOFTNESS));
+    r->ra = ld3(g, JS_RA);
+    r->rb = ld3(g, JS_RB);
+    r->psep = ld3(g, JS_PSEP);
+    r->kinv = ldm3(g, JS_KINV);
+    r->lin_imp = ld3(w, jw(L, j, J_LINEAR_IMPULSE));
+    if (h.type == kJointWeld) {
+        r->ang_hz = ldf(w, jw(L, j, J_ANGULAR_HERTZ));
+        r->lin_hz = ldf(w, jw(L, j, J_LINEAR_HERTZ));
+        r->ang_spring = ldsoft(w, jw(L, j, J_ANGULAR_SPRING));
+        r->lin_spring = ldsoft(w, jw(L, j, J_LINEAR_SPRING));
+        r->cv = ld3(g, JS_CV);
+        r->ang_imp = ld3(w, jw(L, j, J_ANGULAR_IMPULSE));
+        r->ang_mass = ldm3(w, jw(L, j, J_ANGULAR_MASS));
+        return;
+    }
+    r->en_spring = ldi(w, jw(L, j, J_ENABLE_SPRING));
+    r->en_motor = ldi(w, jw(L, j, J_ENABLE_MOTOR));
+    r->en_limit = ldi(w, jw(L, j, J_ENABLE_LIMIT));
+    r->axis = ld3(w, jw(L, j, J_ROTATION_AXIS));
+    r->ia_ax = ld3(g, JS_IA_AX);
+    r->ib_ax = ld3(g, JS_IB_AX);
+    r->px = ld3(g, JS_PX);
+    r->py = ld3(g, JS_PY);
+    r->axial_mass = ldf(w, jw(L, j, J_AXIAL_MASS));
+    r->max_torque = ldf(w, jw(L, j, J_MAX_MOTOR_TORQUE));
+    r->speed = ldf(w, jw(L, j, J_MOTOR_SPEED));
+    r->target = ldf(w, jw(L, j, J_TARGET_ANGLE));
+    r->lower = ldf(w, jw(L, j, J_LOWER_ANGLE));
+    r->upper = ldf(w, jw(L, j, J_UPPER_ANGLE));
+    r->spring_soft = ldsoft(w, jw(L, j, J_SPRING_SOFTNESS));
+    r->tw = ldf(g, JS_TW);
+    r->relx = ldf(g, JS_RELX);
+    r->rely = ldf(g, JS_RELY);
+    r->kxx = ldf(g, JS_KXX);
+    r->kyy = ldf(g, JS_KYY);
+    r->kxy = ldf(g, JS_KXY);
+    r->kinv2 = ldf(g, JS_KINV2);
+    r->kok = ldi(g, JS_KOK);
+    r->spring_imp = ldf(w, jw(L, j, J_SPRING_IMPULSE));
+    r->motor_imp = ldf(w, jw(L, j, J_MOTOR_IMPULSE));
+    r->lower_imp = ldf(w, jw(L, j, J_LOWER_IMPULSE));
+    r->upper_imp = ldf(w, jw(L, j, J_UPPER_IMPULSE));
+    r->perp_imp.x = ldf(w, jw(L, j, J_PERP_IMPULSE));
+    r->perp_imp.y = ldf(w, jw(L, j, J_PERP_IMPULSE + 1));
+}
+
+/* Point rows shared by weld and revolute (06:257-282), with the anchors,
+ * separation and inverted mass of the current delta state. */
+B3D_FN void solve_point(const Lane& L, int j, const JRow& r, V3* va, V3* wa, V3* vb, V3* wb, Soft soft,
+        int use_bias) {
+    V3 cdot = sub(add(*vb, cross(*wb, r.rb)), add(*va, cross(*wa, r.ra)));
+    V3 bias = zero3();
+    float mscale = 1.0f, iscale = 0.0f;
+    if (use_bias) {
+        bias = scale(r.psep, soft.bias_rate);
+        mscale = soft.mass_scale;
+        iscale = soft.impulse_scale;
+    }
+    V3 bsol = mv(r.kinv, add(cdot, bias));
+    V3 impulse = msub(scale(bsol, -mscale), iscale, r.lin_imp);
+    st3(L.w, jw(L, j, J_LINEAR_IMPULSE), add(r.lin_imp, impulse));
+    *va = msub(*va, r.ma, impulse);
+    *wa = sub(*wa, mv(r.ia, cross(r.ra, impulse)));
+    *vb = madd(*vb, r.mb, impulse);
+    *wb = add(*wb, mv(r.ib, cross(r.rb, impulse)));
+}
+
+/* b3_solve_weld (06:285-332). */
+B3D_FN void solve_weld(const Lane& L, int j, const JRow& r, int use_bias) {
+    V3 va = vlin(L, r.a), wa = vang(L, r.a), vb = vlin(L, r.b), wb = vang(L, r.b);
+    if (!r.fixed) {
+        V3 bias = zero3();
+        float mscale = 1.0f, iscale = 0.0f;
+        if (use_bias || r.ang_hz > 0.0f) {
+            bias = scale(r.cv, r.ang_spring.bias_rate);
+            mscale = r.ang_spring.mass_scale;
+            iscale = r.ang_spring.impulse_scale;
+        }
+        V3 cdot = sub(wb, wa);
+        V3 impulse = msub(scale(mv(r.ang_mass, add(cdot, bias)), -mscale), iscale, r.ang_imp);
+        st3(L.w, jw(L, j, J_ANGULAR_IMPULSE), add(r.ang_imp, impulse));
+        wa = sub(wa, mv(r.ia, impulse));
+        wb = add(wb, mv(r.ib, impulse));
+    }
+    int lin_bias = use_bias || r.lin_hz > 0.0f;
+    solve_point(L, j, r, &va, &wa, &vb, &wb, r.lin_spring, lin_bias);
+    if (is_dyn_flag(L, r.a)) {
+        set_vlin(L, r.a, va);
+        set_vang(L, r.a, wa);
+    }
+    if (is_dyn_flag(L, r.b)) {
+        set_vlin(L, r.b, vb);
+        set_vang(L, r.b, wb);
+    }
+}
+
 /* One clamped one-sided limit row (06:419-433). */
 B3D_FN float limit_impulse(float c, float cdot, float inv_h, int use_bias, Soft soft, float axial_mass, float old) {
     float bias = 0.0f, mscale = 1.0f, iscale = 0.0f;
@@ -1112,135 +1544,66 @@ B3D_FN float limit_impulse(float c, float cdot, float inv_h, int use_bias, Soft 
     return maxf(old + dimp, 0.0f);
 }
 
-/* Point rows shared by weld and revolute (06:257-282), with the anchors,
- * separation and inverted mass of the current delta state. */
-B3D_FN void solve_point(const Lane& L, int j, const uint32_t* r, float ma, float mb, M3 ia, M3 ib,
-        V3* va, V3* wa, V3* vb, V3* wb, Soft soft, int use_bias) {
-    uint32_t* w = L.w;
-    V3 ra = ld3(r, JS_RA), rb = ld3(r, JS_RB);
-    V3 cdot = sub(add(*vb, cross(*wb, rb)), add(*va, cross(*wa, ra)));
-    V3 bias = zero3();
-    float mscale = 1.0f, iscale = 0.0f;
-    if (use_bias) {
-        bias = scale(ld3(r, JS_PSEP), soft.bias_rate);
-        mscale = soft.mass_scale;
-        iscale = soft.impulse_scale;
-    }
-    V3 bsol = mv(ldm3(r, JS_KINV), add(cdot, bias));
-    V3 lin_old = ld3(w, jw(L, j, J_LINEAR_IMPULSE));
-    V3 impulse = msub(scale(bsol, -mscale), iscale, lin_old);
-    st3(w, jw(L, j, J_LINEAR_IMPULSE), add(lin_old, impulse));
-    *va = msub(*va, ma, impulse);
-    *wa = sub(*wa, mv(ia, cross(ra, impulse)));
-    *vb = madd(*vb, mb, impulse);
-    *wb = add(*wb, mv(ib, cross(rb, impulse)));
-}
-
-/* b3_solve_weld (06:285-332). */
-B3D_FN void solve_weld(const Lane& L, int j, int a, int b, float ma, float mb, M3 ia, M3 ib, int use_bias) {
-    uint32_t* w = L.w;
-    const uint32_t* r = joint_rec(L, j);
-    V3 va = vlin(L, a), wa = vang(L, a), vb = vlin(L, b), wb = vang(L, b);
-    float ang_hz = ldf(w, jw(L, j, J_ANGULAR_HERTZ));
-    if (!ldi(w, jw(L, j, J_FIXED_ROTATION))) {
-        V3 bias = zero3();
-        float mscale = 1.0f, iscale = 0.0f;
-        if (use_bias || ang_hz > 0.0f) {
-            Soft as = ldsoft(w, jw(L, j, J_ANGULAR_SPRING));
-            bias = scale(ld3(r, JS_CV), as.bias_rate);
-            mscale = as.mass_scale;
-            iscale = as.impulse_scale;
-        }
-        V3 cdot = sub(wb, wa);
-        V3 ang_old = ld3(w, jw(L, j, J_ANGULAR_IMPULSE));
-        V3 impulse = msub(scale(mv(ldm3(w, jw(L, j, J_ANGULAR_MASS)), add(cdot, bias)), -mscale), iscale, ang_old);
-        st3(w, jw(L, j, J_ANGULAR_IMPULSE), add(ang_old, impulse));
-        wa = sub(wa, mv(ia, impulse));
-        wb = add(wb, mv(ib, impulse));
-    }
-    int lin_bias = use_bias || ldf(w, jw(L, j, J_LINEAR_HERTZ)) > 0.0f;
-    solve_point(L, j, r, ma, mb, ia, ib, &va, &wa, &vb, &wb, ldsoft(w, jw(L, j, J_LINEAR_SPRING)), lin_bias);
-    if (is_dyn_flag(L, a)) {
-        set_vlin(L, a, va);
-        set_vang(L, a, wa);
-    }
-    if (is_dyn_flag(L, b)) {
-        set_vlin(L, b, vb);
-        set_vang(L, b, wb);
-    }
-}
-
 /* b3_solve_revolute (06:436-642): spring, motor, lower and upper limit,
  * two perpendicular angular rows, then the point rows. */
-B3D_FN void solve_revolute(const Lane& L, int j, int a, int b, float ma, float mb, M3 ia, M3 ib, float h,
-        float inv_h, int use_bias) {
+B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float inv_h, int use_bias) {
     uint32_t* w = L.w;
-    const uint32_t* r = joint_rec(L, j);
-    V3 va = vlin(L, a), wa = vang(L, a), vb = vlin(L, b), wb = vang(L, b);
-    V3 axis = ld3(w, jw(L, j, J_ROTATION_AXIS));
-    int fixed = ldi(w, jw(L, j, J_FIXED_ROTATION));
-    int en_spring = ldi(w, jw(L, j, J_ENABLE_SPRING));
-    int en_motor = ldi(w, jw(L, j, J_ENABLE_MOTOR));
-    int en_limit = ldi(w, jw(L, j, J_ENABLE_LIMIT));
-    float axial_mass = ldf(w, jw(L, j, J_AXIAL_MASS));
-    float max_torque = ldf(w, jw(L, j, J_MAX_MOTOR_TORQUE));
-    V3 ia_ax = ld3(r, JS_IA_AX), ib_ax = ld3(r, JS_IB_AX);
-    float tw = ldf(r, JS_TW);
-    Soft soft = ldsoft(w, jw(L, j, J_SOFTNESS));
-    if (en_spring && !fixed) {
-        Soft ss = ldsoft(w, jw(L, j, J_SPRING_SOFTNESS));
-        float c = tw - ldf(w, jw(L, j, J_TARGET_ANGLE));
+    V3 va = vlin(L, r.a), wa = vang(L, r.a), vb = vlin(L, r.b), wb = vang(L, r.b);
+    V3 axis = r.axis;
+    int fixed = r.fixed;
+    float axial_mass = r.axial_mass;
+    float tw = r.tw;
+    if (r.en_spring && !fixed) {
+        Soft ss = r.spring_soft;
+        float c = tw - r.target;
         float bias = ss.bias_rate * c;
         float cdot = dot(sub(wb, wa), axis);
-        float old = ldf(w, jw(L, j, J_SPRING_IMPULSE));
+        float old = r.spring_imp;
         float dimp = -ss.mass_scale * axial_mass * (cdot + bias) - ss.impulse_scale * old;
         float nimp = old + dimp;
-        if (max_torque > 0.0f) {
-            float maxp = max_torque * h;
+        if (r.max_torque > 0.0f) {
+            float maxp = r.max_torque * h;
             nimp = clampf(nimp, -maxp, maxp);
         }
         dimp = nimp - old;
         stf(w, jw(L, j, J_SPRING_IMPULSE), nimp);
-        wa = msub(wa, dimp, ia_ax);
-        wb = madd(wb, dimp, ib_ax);
+        wa = msub(wa, dimp, r.ia_ax);
+        wb = madd(wb, dimp, r.ib_ax);
     }
-    if (en_motor && !fixed) {
-        float speed = ldf(w, jw(L, j, J_MOTOR_SPEED));
+    if (r.en_motor && !fixed) {
         int blocked = 0;
-        if (en_limit) {
-            if (tw >= ldf(w, jw(L, j, J_UPPER_ANGLE)) - 0.01f && speed > 0.0f) blocked = 1;
-            if (tw <= ldf(w, jw(L, j, J_LOWER_ANGLE)) + 0.01f && speed < 0.0f) blocked = 1;
+        if (r.en_limit) {
+            if (tw >= r.upper - 0.01f && r.speed > 0.0f) blocked = 1;
+            if (tw <= r.lower + 0.01f && r.speed < 0.0f) blocked = 1;
         }
         if (blocked) {
             stf(w, jw(L, j, J_MOTOR_IMPULSE), 0.0f);
         } else {
-            float old = ldf(w, jw(L, j, J_MOTOR_IMPULSE));
-            float cdot = dot(sub(wb, wa), axis) - speed;
+            float old = r.motor_imp;
+            float cdot = dot(sub(wb, wa), axis) - r.speed;
             float dimp = -axial_mass * cdot;
             float nimp = old + dimp;
-            float maxp = max_torque * h;
+            float maxp = r.max_torque * h;
             nimp = clampf(nimp, -maxp, maxp);
             dimp = nimp - old;
             stf(w, jw(L, j, J_MOTOR_IMPULSE), nimp);
-            wa = msub(wa, dimp, ia_ax);
-            wb = madd(wb, dimp, ib_ax);
+            wa = msub(wa, dimp, r.ia_ax);
+            wb = madd(wb, dimp, r.ib_ax);
         }
     }
-    if (en_limit && !fixed) {
-        float old = ldf(w, jw(L, j, J_LOWER_IMPULSE));
-        float lo = limit_impulse(tw - ldf(w, jw(L, j, J_LOWER_ANGLE)), dot(sub(wb, wa), axis), inv_h,
-            use_bias, soft, axial_mass, old);
+    if (r.en_limit && !fixed) {
+        float old = r.lower_imp;
+        float lo = limit_impulse(tw - r.lower, dot(sub(wb, wa), axis), inv_h, use_bias, r.soft, axial_mass, old);
         stf(w, jw(L, j, J_LOWER_IMPULSE), lo);
         float dimp = lo - old;
-        wa = msub(wa, dimp, ia_ax);
-        wb = madd(wb, dimp, ib_ax);
-        old = ldf(w, jw(L, j, J_UPPER_IMPULSE));
-        float up = limit_impulse(ldf(w, jw(L, j, J_UPPER_ANGLE)) - tw, dot(sub(wa, wb), axis), inv_h,
-            use_bias, soft, axial_mass, old);
+        wa = msub(wa, dimp, r.ia_ax);
+        wb = madd(wb, dimp, r.ib_ax);
+        old = r.upper_imp;
+        float up = limit_impulse(r.upper - tw, dot(sub(wa, wb), axis), inv_h, use_bias, r.soft, axial_mass, old);
         stf(w, jw(L, j, J_UPPER_IMPULSE), up);
         dimp = up - old;
-        wa = madd(wa, dimp, ia_ax);
-        wb = msub(wb, dimp, ib_ax);
+        wa = madd(wa, dimp, r.ia_ax);
+        wb = msub(wb, dimp, r.ib_ax);
     }
     if (!fixed) {
         V2 bias;
@@ -1248,81 +1611,130 @@ B3D_FN void solve_revolute(const Lane& L, int j, int a, int b, float ma, float m
         bias.y = 0.0f;
         float mscale = 1.0f, iscale = 0.0f;
         if (use_bias) {
-            bias.x = soft.bias_rate * ldf(r, JS_RELX);
-            bias.y = soft.bias_rate * ldf(r, JS_RELY);
-            mscale = soft.mass_scale;
-            iscale = soft.impulse_scale;
+            bias.x = r.soft.bias_rate * r.relx;
+            bias.y = r.soft.bias_rate * r.rely;
+            mscale = r.soft.mass_scale;
+            iscale = r.soft.impulse_scale;
         }
-        V3 px = ld3(r, JS_PX), py = ld3(r, JS_PY);
         V3 wrel = sub(wb, wa);
         V2 rhs;
-        rhs.x = dot(wrel, px) + bias.x;
-        rhs.y = dot(wrel, py) + bias.y;
+        rhs.x = dot(wrel, r.px) + bias.x;
+        rhs.y = dot(wrel, r.py) + bias.y;
         /* b3_solve2 (03_math.inl:347-359) with the determinant of this
          * delta state */
         V2 sol;
         sol.x = 0.0f;
         sol.y = 0.0f;
-        if (ldi(r, JS_KOK)) {
-            float inv = ldf(r, JS_KINV2);
-            float kxx = ldf(r, JS_KXX), kyy = ldf(r, JS_KYY), kxy = ldf(r, JS_KXY);
-            sol.x = inv * (kyy * rhs.x - kxy * rhs.y);
-            sol.y = inv * (-kxy * rhs.x + kxx * rhs.y);
+        if (r.kok) {
+            sol.x = r.kinv2 * (r.kyy * rhs.x - r.kxy * rhs.y);
+            sol.y = r.kinv2 * (-r.kxy * rhs.x + r.kxx * rhs.y);
         }
-        V2 old;
-        old.x = ldf(w, jw(L, j, J_PERP_IMPULSE));
-        old.y = ldf(w, jw(L, j, J_PERP_IMPULSE + 1));
         V2 dimp;
-        dimp.x = -mscale * sol.x - iscale * old.x;
-        dimp.y = -mscale * sol.y - iscale * old.y;
-        stf(w, jw(L, j, J_PERP_IMPULSE), old.x + dimp.x);
-        stf(w, jw(L, j, J_PERP_IMPULSE + 1), old.y + dimp.y);
-        V3 ang = add(scale(px, dimp.x), scale(py, dimp.y));
-        wa = sub(wa, mv(ia, ang));
-        wb = add(wb, mv(ib, ang));
+        dimp.x = -mscale * sol.x - iscale * r.perp_imp.x;
+        dimp.y = -mscale * sol.y - iscale * r.perp_imp.y;
+        stf(w, jw(L, j, J_PERP_IMPULSE), r.perp_imp.x + dimp.x);
+        stf(w, jw(L, j, J_PERP_IMPULSE + 1), r.perp_imp.y + dimp.y);
+        V3 ang = add(scale(r.px, dimp.x), scale(r.py, dimp.y));
+        wa = sub(wa, mv(r.ia, ang));
+        wb = add(wb, mv(r.ib, ang));
     }
-    solve_point(L, j, r, ma, mb, ia, ib, &va, &wa, &vb, &wb, soft, use_bias);
-    if (is_dyn_flag(L, a)) {
-        set_vlin(L, a, va);
-        set_vang(L, a, wa);
+    solve_point(L, j, r, &va, &wa, &vb, &wb, r.soft, use_bias);
+    if (is_dyn_flag(L, r.a)) {
+        set_vlin(L, r.a, va);
+        set_vang(L, r.a, wa);
     }
-    if (is_dyn_flag(L, b)) {
-        set_vlin(L, b, vb);
-        set_vang(L, b, wb);
+    if (is_dyn_flag(L, r.b)) {
+        set_vlin(L, r.b, vb);
+        set_vang(L, r.b, wb);
     }
 }
 
-/* b3_solve_joints_global (07_packed.inl:48-81): sweeps in joint order. */
+/* b3_solve_joints_global (07_packed.inl:48-81): sweeps in joint order; all
+ * of a joint's row is requested before its rows are solved. */
 B3D_FN void solve_joints(const Lane& L, float h, float inv_h, int use_bias) {
-    uint32_t* w = L.w;
-    int nj = clampi(ldi(w, H_JOINT_COUNT), 0, L.g.max_j);
+    int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
+    if (nj <= 0) return;
     int iters = use_bias ? kJointIters : kRelaxIters;
     for (int it = 0; it < iters; it++) {
         for (int j = 0; j < nj; j++) {
-            int a = ldi(w, jw(L, j, J_BODY_A)), b = ldi(w, jw(L, j, J_BODY_B));
-            float ma = ldf(w, jw(L, j, J_INV_MASS_A)), mb = ldf(w, jw(L, j, J_INV_MASS_B));
-            M3 ia = ldm3(w, jw(L, j, J_INV_I_A)), ib = ldm3(w, jw(L, j, J_INV_I_B));
-            if (ldi(w, jw(L, j, J_TYPE)) == kJointWeld) solve_weld(L, j, a, b, ma, mb, ia, ib, use_bias);
-            else solve_revolute(L, j, a, b, ma, mb, ia, ib, h, inv_h, use_bias);
+            JRow r;
+            jrow_load(L, j, jhead_load(L, j), &r);
+            if (r.type == kJointWeld) solve_weld(L, j, r, use_bias);
+            else solve_revolute(L, j, r, h, inv_h, use_bias);
+        }
+    }
+}
+
+/* Per-step body record (see BS_*): the velocity increments of gravity and
+ * the applied force / torque and the damping factors of 09_step.inl:5-18,
+ * whose inputs do not change during a step. */
+B3D_FN void body_prepass(const Lane& L, float h) {
+    uint32_t* w = L.w;
+    V3 g = ld3(w, H_GRAVITY);
+    int nb = body_count(L);
+    for (int b0 = 0; b0 < nb; b0 += kChunk) {
+        int type[kChunk];
+        uint32_t flags[kChunk];
+        float inv_mass[kChunk], lin_d[kChunk], ang_d[kChunk], gscale[kChunk];
+        V3 force[kChunk], torque[kChunk];
+        M3 iw[kChunk];
+#pragma unroll
+        for (int k = 0; k < kChunk; k++) {
+            int b = b0 + k;
+            if (b >= nb) continue;
+            type[k] = ldi(w, bw(L, b, B_TYPE));
+            flags[k] = ldu(w, bw(L, b, B_FLAGS));
+            inv_mass[k] = ldf(w, bw(L, b, B_INV_MASS));
+            lin_d[k] = ldf(w, bw(L, b, B_LINEAR_DAMPING));
+            ang_d[k] = ldf(w, bw(L, b, B_ANGULAR_DAMPING));
+            gscale[k] = ldf(w, bw(L, b, B_GRAVITY_SCALE));
+            force[k] = ld3(w, bw(L, b, B_FORCE));
+            torque[k] = ld3(w, bw(L, b, B_TORQUE));
+            iw[k] = ldm3(w, bw(L, b, B_INV_I_WORLD));
+        }
+#pragma unroll
+        for (int k = 0; k < kChunk; k++) {
+            int b = b0 + k;
+            if (b >= nb) continue;
+            uint32_t* r = body_rec(L, b);
+            int kind = (int)(flags[k] & 0xffu) | (type[k] == kDynamic ? kKindDynamic : 0)
+                | (type[k] == kStatic ? kKindStatic : 0);
+            sti(r, BS_KIND, kind);
+            if (type[k] != kDynamic) continue;
+            float gs = inv_mass[k] > 0.0f ? gscale[k] : 0.0f;
+            st3(r, BS_DV, add(scale(force[k], h * inv_mass[k]), scale(g, h * gs)));
+            st3(r, BS_DW, scale(mv(iw[k], torque[k]), h));
+            stf(r, BS_LD, 1.0f / (1.0f + h * lin_d[k]));
+            stf(r, BS_AD, 1.0f / (1.0f + h * ang_d[k]));
         }
     }
 }
 
 /* Gravity, applied force and damping for dynamic bodies (09_step.inl:5-18, 41-53). */
-B3D_FN void integrate_velocities(const Lane& L, float h) {
-    uint32_t* w = L.w;
-    V3 g = ld3(w, H_GRAVITY);
+B3D_FN void integrate_velocities(const Lane& L) {
     int nb = body_count(L);
-    for (int b = 0; b < nb; b++) {
-        if (ldi(w, bw(L, b, B_TYPE)) != kDynamic) continue;
-        float inv_mass = ldf(w, bw(L, b, B_INV_MASS));
-        float ld = 1.0f / (1.0f + h * ldf(w, bw(L, b, B_LINEAR_DAMPING)));
-        float ad = 1.0f / (1.0f + h * ldf(w, bw(L, b, B_ANGULAR_DAMPING)));
-        float gs = inv_mass > 0.0f ? ldf(w, bw(L, b, B_GRAVITY_SCALE)) : 0.0f;
-        V3 dv = add(scale(ld3(w, bw(L, b, B_FORCE)), h * inv_mass), scale(g, h * gs));
-        set_vlin(L, b, madd(dv, ld, vlin(L, b)));
-        V3 dw = scale(mv(ldm3(w, bw(L, b, B_INV_I_WORLD)), ld3(w, bw(L, b, B_TORQUE))), h);
-        set_vang(L, b, madd(dw, ad, vang(L, b)));
+    for (int b0 = 0; b0 < nb; b0 += kChunk) {
+        int kind[kChunk];
+        V3 dv[kChunk], dw[kChunk];
+        float ld[kChunk], ad[kChunk];
+#pragma unroll
+        for (int k = 0; k < kChunk; k++) {
+            int b = b0 + k;
+            if (b >= nb) continue;
+            const uint32_t* r = body_rec(L, b);
+            kind[k] = ldi(r, BS_KIND);
+            dv[k] = ld3(r, BS_DV);
+            dw[k] = ld3(r, BS_DW);
+            ld[k] = ldf(r, BS_LD);
+            ad[k] = ldf(r, BS_AD);
+        }
+#pragma unroll
+        for (int k = 0; k < kChunk; k++) {
+            int b = b0 + k;
+            if (b >= nb || !(kind[k] & kKindDynamic)) continue;
+            set_vlin(L, b, madd(dv[k], ld[k], vlin(L, b)));
+            set_vang(L, b, madd(dw[k], ad[k], vang(L, b)));
+        }
     }
 }
 
@@ -1334,24 +1746,39 @@ B3D_FN void integrate_positions(const Lane& L, float h, float inv_dt) {
     float max_lin2 = max_lin * max_lin;
     float max_ang2 = max_ang * max_ang;
     int nb = body_count(L);
-    for (int b = 0; b < nb; b++) {
-        if (ldi(w, bw(L, b, B_TYPE)) == kStatic) continue;
-        uint32_t flags = ldu(w, bw(L, b, B_FLAGS));
-        V3 v = vlin(L, b), av = vang(L, b);
-        if (flags & 0x01u) v.x = 0.0f;
-        if (flags & 0x02u) v.y = 0.0f;
-        if (flags & 0x04u) v.z = 0.0f;
-        if (flags & 0x08u) av.x = 0.0f;
-        if (flags & 0x10u) av.y = 0.0f;
-        if (flags & 0x20u) av.z = 0.0f;
-        float v2 = len2(v);
-        if (v2 > max_lin2 && v2 > 0.0f) v = scale(v, rsqrt_scale(max_lin, v2));
-        float w2 = len2(av);
-        if (w2 > max_ang2 && w2 > 0.0f) av = scale(av, rsqrt_scale(max_ang, w2));
-        set_vlin(L, b, v);
-        set_vang(L, b, av);
-        st3(w, bw(L, b, B_DELTA_POS), madd(ld3(w, bw(L, b, B_DELTA_POS)), h, v));
-        stq(w, bw(L, b, B_DELTA_ROT), qintegrate(ldq(w, bw(L, b, B_DELTA_ROT)), scale(av, h)));
+    for (int b0 = 0; b0 < nb; b0 += kChunk) {
+        int kind[kChunk];
+        V3 dp[kChunk];
+        Q dq[kChunk];
+#pragma unroll
+        for (int k = 0; k < kChunk; k++) {
+            int b = b0 + k;
+            if (b >= nb) continue;
+            kind[k] = ldi(body_rec(L, b), BS_KIND);
+            dp[k] = ld3(w, bw(L, b, B_DELTA_POS));
+            dq[k] = ldq(w, bw(L, b, B_DELTA_ROT));
+        }
+#pragma unroll
+        for (int k = 0; k < kChunk; k++) {
+            int b = b0 + k;
+            if (b >= nb || (kind[k] & kKindStatic)) continue;
+            uint32_t flags = (uint32_t)kind[k];
+            V3 v = vlin(L, b), av = vang(L, b);
+            if (flags & 0x01u) v.x = 0.0f;
+            if (flags & 0x02u) v.y = 0.0f;
+            if (flags & 0x04u) v.z = 0.0f;
+            if (flags & 0x08u) av.x = 0.0f;
+            if (flags & 0x10u) av.y = 0.0f;
+            if (flags & 0x20u) av.z = 0.0f;
+            float v2 = len2(v);
+            if (v2 > max_lin2 && v2 > 0.0f) v = scale(v, rsqrt_scale(max_lin, v2));
+            float w2 = len2(av);
+            if (w2 > max_ang2 && w2 > 0.0f) av = scale(av, rsqrt_scale(max_ang, w2));
+            set_vlin(L, b, v);
+            set_vang(L, b, av);
+            st3(w, bw(L, b, B_DELTA_POS), madd(dp[k], h, v));
+            stq(w, bw(L, b, B_DELTA_ROT), qintegrate(dq[k], scale(av, h)));
+        }
     }
 }
 
@@ -1359,19 +1786,37 @@ B3D_FN void integrate_positions(const Lane& L, float h, float inv_dt) {
 B3D_FN void finalize(const Lane& L) {
     uint32_t* w = L.w;
     int nb = body_count(L);
-    for (int b = 0; b < nb; b++) {
-        int type = ldi(w, bw(L, b, B_TYPE));
-        if (type == kStatic) continue;
-        V3 center = add(ld3(w, bw(L, b, B_CENTER)), ld3(w, bw(L, b, B_DELTA_POS)));
-        Q r = qnorm(qmul(ldq(w, bw(L, b, B_DELTA_ROT)), ldq(w, bw(L, b, B_ROTATION))));
-        st3(w, bw(L, b, B_CENTER), center);
-        stq(w, bw(L, b, B_ROTATION), r);
-        st3(w, bw(L, b, B_POSITION), sub(center, rot(r, ld3(w, bw(L, b, B_LOCAL_CENTER)))));
-        st3(w, bw(L, b, B_DELTA_POS), zero3());
-        stq(w, bw(L, b, B_DELTA_ROT), qid());
-        st3(w, bw(L, b, B_FORCE), zero3());
-        st3(w, bw(L, b, B_TORQUE), zero3());
-        if (type == kDynamic) stm3(w, bw(L, b, B_INV_I_WORLD), world_inv_i(r, ld3(w, bw(L, b, B_INV_INERTIA))));
+    for (int b0 = 0; b0 < nb; b0 += kChunk) {
+        int type[kChunk];
+        V3 center[kChunk], dp[kChunk], lc[kChunk], inv_i[kChunk];
+        Q dq[kChunk], rq[kChunk];
+#pragma unroll
+        for (int k = 0; k < kChunk; k++) {
+            int b = b0 + k;
+            if (b >= nb) continue;
+            type[k] = ldi(w, bw(L, b, B_TYPE));
+            center[k] = ld3(w, bw(L, b, B_CENTER));
+            dp[k] = ld3(w, bw(L, b, B_DELTA_POS));
+            dq[k] = ldq(w, bw(L, b, B_DELTA_ROT));
+            rq[k] = ldq(w, bw(L, b, B_ROTATION));
+            lc[k] = ld3(w, bw(L, b, B_LOCAL_CENTER));
+            inv_i[k] = ld3(w, bw(L, b, B_INV_INERTIA));
+        }
+#pragma unroll
+        for (int k = 0; k < kChunk; k++) {
+            int b = b0 + k;
+            if (b >= nb || type[k] == kStatic) continue;
+            V3 c = add(center[k], dp[k]);
+            Q r = qnorm(qmul(dq[k], rq[k]));
+            st3(w, bw(L, b, B_CENTER), c);
+            stq(w, bw(L, b, B_ROTATION), r);
+            st3(w, bw(L, b, B_POSITION), sub(c, rot(r, lc[k])));
+            st3(w, bw(L, b, B_DELTA_POS), zero3());
+            stq(w, bw(L, b, B_DELTA_ROT), qid());
+            st3(w, bw(L, b, B_FORCE), zero3());
+            st3(w, bw(L, b, B_TORQUE), zero3());
+            if (type[k] == kDynamic) stm3(w, bw(L, b, B_INV_I_WORLD), world_inv_i(r, inv_i[k]));
+        }
     }
 }
 
@@ -1395,11 +1840,12 @@ B3D_FN void step_world(const Lane& L, float dt, int substeps) {
     vel_load(L);
     prepare_contacts(L, cs, ss);
     prepare_joints(L, h);
+    body_prepass(L, h);
     warm_start_contacts(L);
     warm_start_joints(L);
     delta_geometry(L);
     for (int s = 0; s < subs; s++) {
-        integrate_velocities(L, h);
+        integrate_velocities(L);
         solve_contacts(L, inv_h, contact_speed, 1);
         solve_joints(L, h, inv_h, 1);
         integrate_positions(L, h, inv_dt);
