@@ -212,17 +212,20 @@ constexpr int kShapeChunk = 4;
  * kind (type and axis-lock flags). */
 constexpr int BS_DV = 0, BS_DW = 3, BS_LD = 6, BS_AD = 7, BS_KIND = 8, kBodyScr = 9;
 constexpr int kKindDynamic = 1 << 8, kKindStatic = 1 << 9;  /* BS_KIND bits; low byte = lock flags */
-/* Contact point separations for the current delta poses. */
-constexpr int kSepScr = 4;
-/* Joint record in scratch: the joint-connection key and the hinge axis
- * through each inverse inertia (per step), then everything that depends
- * only on the bodies' delta poses (recomputed after every position
- * update): twist angle, hinge perpendicular rows and their 2x2 mass, point
- * anchors, point separation and the inverted 3x3 point mass, and the weld's
- * angular error. */
-constexpr int JS_KEY = 0, JS_IA_AX = 1, JS_IB_AX = 4, JS_TW = 7, JS_RELX = 8, JS_RELY = 9, JS_PX = 10,
-              JS_PY = 13, JS_KXX = 16, JS_KYY = 17, JS_KXY = 18, JS_KINV2 = 19, JS_KOK = 20, JS_RA = 21,
-              JS_RB = 24, JS_PSEP = 27, JS_KINV = 30, JS_CV = 39, kJointScr = 42;
+/* Per-contact scratch head, written by the pair loop: bodies (a | b << 16),
+ * point count and facts about the pair (pc | flags << 8), then the point
+ * separations of the current delta poses. */
+constexpr int CH_AB = 0, CH_INFO = 1, CH_SEP = 2, kContactScr = 6;
+constexpr int CF_DYN_A = 1, CF_DYN_B = 2, CF_STATIC = 4, CF_RESTITUTION = 8, CF_ROLLING = 16;
+/* Joint record in scratch: the joint-connection key, the head written by
+ * prepare_joints (bodies a | b << 16 and JF_* flags), then everything that
+ * depends only on the bodies' delta poses (recomputed after every position
+ * update): twist angle, the hinge perpendicular rows and the relative
+ * rotation's x, y, the point anchors and separation, and the weld's angular
+ * error. */
+constexpr int JS_KEY = 0, JS_AB = 1, JS_INFO = 2, JS_TW = 3, JS_RELX = 4, JS_RELY = 5, JS_PX = 6, JS_PY = 9,
+              JS_RA = 12, JS_RB = 15, JS_PSEP = 18, JS_CV = 21, kJointScr = 24;
+constexpr int JF_WELD = 1, JF_FIXED = 2, JF_SPRING = 4, JF_MOTOR = 8, JF_LIMIT = 16, JF_DYN_A = 32, JF_DYN_B = 64;
 
 constexpr int kStatic = 0, kKinematic = 1, kDynamic = 2;
 constexpr uint32_t kFlagDynamic = 0x00001000u;
@@ -256,7 +259,7 @@ B3D_FN bool geometry_of(unsigned long long sig, Geometry* g, size_t* world_bytes
     g->scr_shape = 0;
     g->scr_old = g->scr_shape + g->max_s * kShapeScr;
     g->scr_sep = g->scr_old + g->max_c * kOldWords;
-    g->scr_joint = g->scr_sep + g->max_c * kSepScr;
+    g->scr_joint = g->scr_sep + g->max_c * kContactScr;
     g->scr_body = g->scr_joint + g->max_j * kJointScr;
     g->scr_bounds = g->scr_body + g->max_b * kBodyScr;
     g->scr_words = g->scr_bounds + g->max_s * 6;
@@ -401,7 +404,19 @@ B3D_FN void shape_aabb(const Posed& P, V3* lo, V3* hi) {
 
 B3D_FN uint32_t* shape_rec(const Lane& L, int s) { return L.scr + (L.g.scr_shape + s * kShapeScr) * kLanes; }
 B3D_FN uint32_t* old_rec(const Lane& L, int k) { return L.scr + (L.g.scr_old + k * kOldWords) * kLanes; }
-B3D_FN uint32_t* sep_rec(const Lane& L, int c) { return L.scr + (L.g.scr_sep + c * kSepScr) * kLanes; }
+B3D_FN uint32_t* chead_rec(const Lane& L, int c) { return L.scr + (L.g.scr_sep + c * kContactScr) * kLanes; }
+/* A contact's head: bodies, point count and CF_* flags. */
+struct CHead { int a, b, pc, flags; };
+B3D_FN CHead chead_load(const Lane& L, int c) {
+    const uint32_t* hd = chead_rec(L, c);
+    uint32_t ab = ldu(hd, CH_AB), info = ldu(hd, CH_INFO);
+    CHead h;
+    h.a = (int)(ab & 0xffffu);
+    h.b = (int)(ab >> 16);
+    h.pc = (int)(info & 0xffu);
+    h.flags = (int)(info >> 8);
+    return h;
+}
 B3D_FN uint32_t* joint_rec(const Lane& L, int j) { return L.scr + (L.g.scr_joint + j * kJointScr) * kLanes; }
 B3D_FN uint32_t* body_rec(const Lane& L, int b) { return L.scr + (L.g.scr_body + b * kBodyScr) * kLanes; }
 B3D_FN uint32_t pair_key(int a, int b) { return a < b ? ((uint32_t)a << 16) | (uint32_t)b : ((uint32_t)b << 16) | (uint32_t)a; }
@@ -682,9 +697,17 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
                 stf(w, pw(L, cc, p, P_NORMAL_IMPULSE), nc.ni[p]);
                 sti(w, pw(L, cc, p, P_FEATURE), (int)nc.feature[p]);
             }
+            float restitution = ea > eb ? ea : eb;
+            float rolling = maxf(rla, rlb);
             stf(w, cw(L, cc, C_FRICTION), sqrtf(fa * fb));
-            stf(w, cw(L, cc, C_RESTITUTION), ea > eb ? ea : eb);
-            stf(w, cw(L, cc, C_ROLLING), maxf(rla, rlb));
+            stf(w, cw(L, cc, C_RESTITUTION), restitution);
+            stf(w, cw(L, cc, C_ROLLING), rolling);
+            int info = (bf_i & kBodyDynamic ? CF_DYN_A : 0) | (bf_j & kBodyDynamic ? CF_DYN_B : 0)
+                | (!((bf_i & bf_j) & kBodyDynamic) ? CF_STATIC : 0) | (restitution != 0.0f ? CF_RESTITUTION : 0)
+                | (!(rolling <= 0.0f) ? CF_ROLLING : 0);
+            uint32_t* hd = chead_rec(L, cc);
+            sti(hd, CH_AB, body_i | (body_j << 16));
+            sti(hd, CH_INFO, nc.count | (info << 8));
             stf(w, cw(L, cc, C_TWIST_IMPULSE), nc.twist);
             stf(w, cw(L, cc, C_FRICTION_IMPULSE), nc.fi.x);
             stf(w, cw(L, cc, C_FRICTION_IMPULSE + 1), nc.fi.y);
@@ -731,17 +754,17 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
     int cc = ldi(w, H_CONTACT_COUNT);
     const float inv_tau = 1.0f / kSpeculative;
     for (int c0 = 0; c0 < cc; c0 += kPrepChunk) {
-        int a[kPrepChunk], b[kPrepChunk], pc[kPrepChunk], st[kPrepChunk];
+        int a[kPrepChunk], b[kPrepChunk], pc[kPrepChunk], fl[kPrepChunk];
 #pragma unroll
         for (int k = 0; k < kPrepChunk; k++) {
             int c = c0 + k;
             if (c >= cc) continue;
-            a[k] = ldi(w, cw(L, c, C_BODY_A));
-            b[k] = ldi(w, cw(L, c, C_BODY_B));
-            pc[k] = ldi(w, cw(L, c, C_POINT_COUNT));
-            st[k] = ldi(w, cw(L, c, C_STATIC));
+            CHead hd = chead_load(L, c);
+            a[k] = hd.a;
+            b[k] = hd.b;
+            pc[k] = hd.pc;
+            fl[k] = hd.flags;
         }
-        int ta[kPrepChunk], tb[kPrepChunk];
         float ima[kPrepChunk], imb[kPrepChunk];
         M3 iwa[kPrepChunk], iwb[kPrepChunk];
         V3 n[kPrepChunk], t1[kPrepChunk], t2[kPrepChunk], ra[kPrepChunk][kMaxManifold], rb[kPrepChunk][kMaxManifold];
@@ -750,12 +773,18 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
         for (int k = 0; k < kPrepChunk; k++) {
             int c = c0 + k;
             if (c >= cc) continue;
-            ta[k] = ldi(w, bw(L, a[k], B_TYPE));
-            tb[k] = ldi(w, bw(L, b[k], B_TYPE));
-            ima[k] = ldf(w, bw(L, a[k], B_INV_MASS));
-            imb[k] = ldf(w, bw(L, b[k], B_INV_MASS));
-            iwa[k] = ldm3(w, bw(L, a[k], B_INV_I_WORLD));
-            iwb[k] = ldm3(w, bw(L, b[k], B_INV_I_WORLD));
+            ima[k] = 0.0f;
+            imb[k] = 0.0f;
+            iwa[k] = m3zero();
+            iwb[k] = m3zero();
+            if (fl[k] & CF_DYN_A) {
+                ima[k] = ldf(w, bw(L, a[k], B_INV_MASS));
+                iwa[k] = ldm3(w, bw(L, a[k], B_INV_I_WORLD));
+            }
+            if (fl[k] & CF_DYN_B) {
+                imb[k] = ldf(w, bw(L, b[k], B_INV_MASS));
+                iwb[k] = ldm3(w, bw(L, b[k], B_INV_I_WORLD));
+            }
             n[k] = ld3(w, cw(L, c, C_NORMAL));
             t1[k] = ld3(w, cw(L, c, C_TANGENT1));
             t2[k] = ld3(w, cw(L, c, C_TANGENT2));
@@ -771,10 +800,9 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
         for (int k = 0; k < kPrepChunk; k++) {
             int c = c0 + k;
             if (c >= cc) continue;
-            float ma = ta[k] == kDynamic ? ima[k] : 0.0f;
-            float mb = tb[k] == kDynamic ? imb[k] : 0.0f;
-            M3 ia = ta[k] == kDynamic ? iwa[k] : m3zero();
-            M3 ib = tb[k] == kDynamic ? iwb[k] : m3zero();
+            /* zero unless the body is dynamic (08:236-241) */
+            float ma = ima[k], mb = imb[k];
+            M3 ia = iwa[k], ib = iwb[k];
             V3 va = vlin(L, a[k]), wa = vang(L, a[k]);
             V3 vb = vlin(L, b[k]), wb = vang(L, b[k]);
             V3 center_a = zero3(), center_b = zero3();
@@ -827,7 +855,7 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
             stf(w, cw(L, c, C_INV_MASS_B), mb);
             stm3(w, cw(L, c, C_INV_I_A), ia);
             stm3(w, cw(L, c, C_INV_I_B), ib);
-            stsoft(w, cw(L, c, C_SOFTNESS), st[k] ? ss : cs);
+            stsoft(w, cw(L, c, C_SOFTNESS), (fl[k] & CF_STATIC) ? ss : cs);
         }
     }
 }
@@ -851,6 +879,13 @@ B3D_FN void prepare_joints(const Lane& L, float h) {
         M3 isum = madd3(ia, ib);
         int fixed = dot(isum.cx, cross(isum.cy, isum.cz)) < 1.0e-20f;
         sti(w, jw(L, i, J_FIXED_ROTATION), fixed);
+        int jtype = ldi(w, jw(L, i, J_TYPE));
+        int info = (jtype == kJointWeld ? JF_WELD : 0) | (fixed ? JF_FIXED : 0)
+            | (ldi(w, jw(L, i, J_ENABLE_SPRING)) ? JF_SPRING : 0) | (ldi(w, jw(L, i, J_ENABLE_MOTOR)) ? JF_MOTOR : 0)
+            | (ldi(w, jw(L, i, J_ENABLE_LIMIT)) ? JF_LIMIT : 0) | (ta == kDynamic ? JF_DYN_A : 0)
+            | (tb == kDynamic ? JF_DYN_B : 0);
+        sti(joint_rec(L, i), JS_AB, a | (b << 16));
+        sti(joint_rec(L, i), JS_INFO, info);
         Soft soft = make_soft(ldf(w, jw(L, i, J_CONSTRAINT_HERTZ)), ldf(w, jw(L, i, J_CONSTRAINT_DAMPING)), h);
         stsoft(w, jw(L, i, J_SOFTNESS), soft);
         Q rot_a = ldq(w, bw(L, a, B_ROTATION)), rot_b = ldq(w, bw(L, b, B_ROTATION));
@@ -861,7 +896,7 @@ B3D_FN void prepare_joints(const Lane& L, float h) {
         st3(w, jw(L, i, J_FRAME_P_A), rot(rot_a, sub(ld3(w, jw(L, i, J_LOCAL_ANCHOR_A)), ld3(w, bw(L, a, B_LOCAL_CENTER)))));
         st3(w, jw(L, i, J_FRAME_P_B), rot(rot_b, sub(ld3(w, jw(L, i, J_LOCAL_ANCHOR_B)), ld3(w, bw(L, b, B_LOCAL_CENTER)))));
         st3(w, jw(L, i, J_DELTA_CENTER), sub(ld3(w, bw(L, b, B_CENTER)), ld3(w, bw(L, a, B_CENTER))));
-        if (ldi(w, jw(L, i, J_TYPE)) == kJointWeld) {
+        if (jtype == kJointWeld) {
             stm3(w, jw(L, i, J_ANGULAR_MASS), inv3(isum));
             float lh = ldf(w, jw(L, i, J_LINEAR_HERTZ)), ah = ldf(w, jw(L, i, J_ANGULAR_HERTZ));
             stsoft(w, jw(L, i, J_LINEAR_SPRING), lh == 0.0f ? soft : make_soft(lh, ldf(w, jw(L, i, J_LINEAR_DAMPING)), h));
@@ -877,9 +912,6 @@ B3D_FN void prepare_joints(const Lane& L, float h) {
             st3(w, jw(L, i, J_PERP_X), px);
             st3(w, jw(L, i, J_PERP_Y), py);
             stsoft(w, jw(L, i, J_SPRING_SOFTNESS), make_soft(ldf(w, jw(L, i, J_HERTZ)), ldf(w, jw(L, i, J_DAMPING_RATIO)), h));
-            uint32_t* r = joint_rec(L, i);
-            st3(r, JS_IA_AX, fixed ? zero3() : mv(ia, axis));
-            st3(r, JS_IB_AX, fixed ? zero3() : mv(ib, axis));
         }
     }
 }
@@ -897,14 +929,16 @@ B3D_FN void warm_start_contacts(const Lane& L) {
     int cc = ldi(L.w, H_CONTACT_COUNT);
     const uint32_t* w = L.w;
     for (int c0 = 0; c0 < cc; c0 += kPrepChunk) {
-        int a[kPrepChunk], b[kPrepChunk], pc[kPrepChunk];
+        int a[kPrepChunk], b[kPrepChunk], pc[kPrepChunk], fl[kPrepChunk];
 #pragma unroll
         for (int k = 0; k < kPrepChunk; k++) {
             int c = c0 + k;
             if (c >= cc) continue;
-            a[k] = ldi(w, cw(L, c, C_BODY_A));
-            b[k] = ldi(w, cw(L, c, C_BODY_B));
-            pc[k] = ldi(w, cw(L, c, C_POINT_COUNT));
+            CHead hd = chead_load(L, c);
+            a[k] = hd.a;
+            b[k] = hd.b;
+            pc[k] = hd.pc;
+            fl[k] = hd.flags;
         }
         float ma[kPrepChunk], mb[kPrepChunk], ni[kPrepChunk][kMaxManifold], tw[kPrepChunk];
         M3 ia[kPrepChunk], ib[kPrepChunk];
@@ -915,10 +949,18 @@ B3D_FN void warm_start_contacts(const Lane& L) {
         for (int k = 0; k < kPrepChunk; k++) {
             int c = c0 + k;
             if (c >= cc) continue;
-            ma[k] = ldf(w, cw(L, c, C_INV_MASS_A));
-            mb[k] = ldf(w, cw(L, c, C_INV_MASS_B));
-            ia[k] = ldm3(w, cw(L, c, C_INV_I_A));
-            ib[k] = ldm3(w, cw(L, c, C_INV_I_B));
+            ma[k] = 0.0f;
+            mb[k] = 0.0f;
+            ia[k] = m3zero();
+            ib[k] = m3zero();
+            if (fl[k] & CF_DYN_A) {
+                ma[k] = ldf(w, cw(L, c, C_INV_MASS_A));
+                ia[k] = ldm3(w, cw(L, c, C_INV_I_A));
+            }
+            if (fl[k] & CF_DYN_B) {
+                mb[k] = ldf(w, cw(L, c, C_INV_MASS_B));
+                ib[k] = ldm3(w, cw(L, c, C_INV_I_B));
+            }
             n[k] = ld3(w, cw(L, c, C_NORMAL));
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
@@ -928,7 +970,7 @@ B3D_FN void warm_start_contacts(const Lane& L) {
                 rb[k][p] = ld3(w, pw(L, c, p, P_R_B));
             }
             t1[k] = ld3(w, cw(L, c, C_TANGENT1));
-            t2[k] = ld3(w, cw(L, c, C_TANGENT2));
+            t2[k] = cross(t1[k], n[k]);
             fi[k].x = ldf(w, cw(L, c, C_FRICTION_IMPULSE));
             fi[k].y = ldf(w, cw(L, c, C_FRICTION_IMPULSE + 1));
             ca[k] = ld3(w, cw(L, c, C_CENTER_A));
@@ -1015,9 +1057,10 @@ B3D_FN void delta_geometry(const Lane& L) {
         for (int k = 0; k < kChunk; k++) {
             int c = c0 + k;
             if (c >= cc) continue;
-            a[k] = ldi(w, cw(L, c, C_BODY_A));
-            b[k] = ldi(w, cw(L, c, C_BODY_B));
-            pc[k] = ldi(w, cw(L, c, C_POINT_COUNT));
+            CHead hd = chead_load(L, c);
+            a[k] = hd.a;
+            b[k] = hd.b;
+            pc[k] = hd.pc;
         }
         V3 n[kChunk], dp[kChunk], ra[kChunk][kMaxManifold], rb[kChunk][kMaxManifold];
         Q dqa[kChunk], dqb[kChunk];
@@ -1042,30 +1085,29 @@ B3D_FN void delta_geometry(const Lane& L) {
         for (int k = 0; k < kChunk; k++) {
             int c = c0 + k;
             if (c >= cc) continue;
-            uint32_t* sp = sep_rec(L, c);
+            uint32_t* sp = chead_rec(L, c);
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
                 if (p >= pc[k]) continue;
                 V3 ds = add(dp[k], sub(rot(dqb[k], rb[k][p]), rot(dqa[k], ra[k][p])));
-                stf(sp, p, dot(ds, n[k]) + bs[k][p]);
+                stf(sp, CH_SEP + p, dot(ds, n[k]) + bs[k][p]);
             }
         }
     }
     int nj = clampi(ldi(w, H_JOINT_COUNT), 0, L.g.max_j);
     for (int j0 = 0; j0 < nj; j0 += kPrepChunk) {
-        int a[kPrepChunk], b[kPrepChunk];
+        int a[kPrepChunk], b[kPrepChunk], info[kPrepChunk];
 #pragma unroll
         for (int k = 0; k < kPrepChunk; k++) {
             int j = j0 + k;
             if (j >= nj) continue;
-            a[k] = ldi(w, jw(L, j, J_BODY_A));
-            b[k] = ldi(w, jw(L, j, J_BODY_B));
+            uint32_t ab = ldu(joint_rec(L, j), JS_AB);
+            a[k] = (int)(ab & 0xffffu);
+            b[k] = (int)(ab >> 16);
+            info[k] = ldi(joint_rec(L, j), JS_INFO);
         }
         Q dqa[kPrepChunk], dqb[kPrepChunk], fqa[kPrepChunk], fqb[kPrepChunk];
         V3 dpa[kPrepChunk], dpb[kPrepChunk], fpa[kPrepChunk], fpb[kPrepChunk], dcen[kPrepChunk];
-        float ma[kPrepChunk], mb[kPrepChunk];
-        M3 ia[kPrepChunk], ib[kPrepChunk];
-        int fixed[kPrepChunk], type[kPrepChunk], en[kPrepChunk];
 #pragma unroll
         for (int k = 0; k < kPrepChunk; k++) {
             int j = j0 + k;
@@ -1074,13 +1116,6 @@ B3D_FN void delta_geometry(const Lane& L) {
             dqb[k] = ldq(w, bw(L, b[k], B_DELTA_ROT));
             dpa[k] = ld3(w, bw(L, a[k], B_DELTA_POS));
             dpb[k] = ld3(w, bw(L, b[k], B_DELTA_POS));
-            ma[k] = ldf(w, jw(L, j, J_INV_MASS_A));
-            mb[k] = ldf(w, jw(L, j, J_INV_MASS_B));
-            ia[k] = ldm3(w, jw(L, j, J_INV_I_A));
-            ib[k] = ldm3(w, jw(L, j, J_INV_I_B));
-            fixed[k] = ldi(w, jw(L, j, J_FIXED_ROTATION));
-            type[k] = ldi(w, jw(L, j, J_TYPE));
-            en[k] = ldi(w, jw(L, j, J_ENABLE_SPRING)) | ldi(w, jw(L, j, J_ENABLE_LIMIT)) | ldi(w, jw(L, j, J_ENABLE_MOTOR));
             fqa[k] = ldq(w, jw(L, j, J_FRAME_Q_A));
             fqb[k] = ldq(w, jw(L, j, J_FRAME_Q_B));
             fpa[k] = ld3(w, jw(L, j, J_FRAME_P_A));
@@ -1101,19 +1136,20 @@ B3D_FN void delta_geometry(const Lane& L) {
             st3(r, JS_RA, ra);
             st3(r, JS_RB, rb);
             st3(r, JS_PSEP, add(add(sub(dpb[k], dpa[k]), sub(rb, ra)), dcen[k]));
-            stm3(r, JS_KINV, inv3(point_k(ma[k], mb[k], ia[k], ib[k], ra, rb)));
-            if (type[k] == kJointWeld) {
+            int fixed = info[k] & JF_FIXED;
+            if (info[k] & JF_WELD) {
+                if (fixed) continue;
                 Q sq = rel;
                 if (rel.s < 0.0f) sq = qneg(rel);
                 Q diff = q4(-sq.v.x, -sq.v.y, -sq.v.z, 1.0f - sq.s);
                 st3(r, JS_CV, neg(rot(qa, scale(qmul(diff, qconj(sq)).v, 2.0f))));
                 continue;
             }
-            int need_twist = en[k] && !fixed[k];
+            int need_twist = (info[k] & (JF_SPRING | JF_MOTOR | JF_LIMIT)) && !fixed;
             stf(r, JS_TW, need_twist ? twist(rel) : 0.0f);
             stf(r, JS_RELX, rel.v.x);
             stf(r, JS_RELY, rel.v.y);
-            if (!fixed[k]) {
+            if (!fixed) {
                 V3 px, py;
                 hinge_perps(qa, rel, &px, &py);
                 st3(r, JS_PX, px);
@@ -1121,16 +1157,6 @@ B3D_FN void delta_geometry(const Lane& L) {
                 /* the solve's latest hinge rows are part of the joint state */
                 st3(w, jw(L, j, J_PERP_X), px);
                 st3(w, jw(L, j, J_PERP_Y), py);
-                M3 isum = madd3(ia[k], ib[k]);
-                float kxx = dot(px, mv(isum, px));
-                float kyy = dot(py, mv(isum, py));
-                float kxy = dot(px, mv(isum, py));
-                float det = kxx * kyy - kxy * kxy;
-                stf(r, JS_KXX, kxx);
-                stf(r, JS_KYY, kyy);
-                stf(r, JS_KXY, kxy);
-                sti(r, JS_KOK, det > 1.0e-12f);
-                stf(r, JS_KINV2, det > 1.0e-12f ? 1.0f / det : 0.0f);
             }
         }
     }
@@ -1163,7 +1189,7 @@ B3D_FN void solve_rolling(V3 t1, V3 t2, float rolling, float total_n, M3 ia, M3 
 /* The contact row as one solve needs it, loaded ahead of use. */
 struct CPoint { V3 ra, rb; float nmass, ni, tn, lever, sep; };
 struct CRow {
-    int a, b, pc;
+    int a, b, pc, flags;
     V3 n;
     float ma, mb;
     M3 ia, ib;
@@ -1175,26 +1201,25 @@ struct CRow {
     M2 tm;
 };
 
-/* The first words of a contact row, loaded two contacts ahead so that the
- * rest of the row can be loaded one contact ahead without waiting. */
-struct CHead { int a, b, pc; };
-
-B3D_FN CHead chead_load(const Lane& L, int c) {
-    CHead h;
-    h.a = ldi(L.w, cw(L, c, C_BODY_A));
-    h.b = ldi(L.w, cw(L, c, C_BODY_B));
-    h.pc = ldi(L.w, cw(L, c, C_POINT_COUNT));
-    return h;
-}
-
-/* Masses and softness of a row: loaded when its solve starts. */
-B3D_FN void crow_masses(const Lane& L, int c, CRow* r) {
+/* Masses of a row, loaded when its solve starts.  A body that is not
+ * dynamic has exactly zero mass and inertia in the row (prepare_contacts
+ * writes m3zero()), so those are not loaded.  The softness is the world's
+ * static or dynamic contact softness. */
+B3D_FN void crow_masses(const Lane& L, int c, CRow* r, Soft cs, Soft ss) {
     const uint32_t* w = L.w;
-    r->ma = ldf(w, cw(L, c, C_INV_MASS_A));
-    r->mb = ldf(w, cw(L, c, C_INV_MASS_B));
-    r->ia = ldm3(w, cw(L, c, C_INV_I_A));
-    r->ib = ldm3(w, cw(L, c, C_INV_I_B));
-    r->soft = ldsoft(w, cw(L, c, C_SOFTNESS));
+    r->ma = 0.0f;
+    r->mb = 0.0f;
+    r->ia = m3zero();
+    r->ib = m3zero();
+    if (r->flags & CF_DYN_A) {
+        r->ma = ldf(w, cw(L, c, C_INV_MASS_A));
+        r->ia = ldm3(w, cw(L, c, C_INV_I_A));
+    }
+    if (r->flags & CF_DYN_B) {
+        r->mb = ldf(w, cw(L, c, C_INV_MASS_B));
+        r->ib = ldm3(w, cw(L, c, C_INV_I_B));
+    }
+    r->soft = (r->flags & CF_STATIC) ? ss : cs;
 }
 
 /* Normal, points and friction data of a row: loaded one contact ahead. */
@@ -1203,8 +1228,9 @@ B3D_FN void crow_load(const Lane& L, int c, CHead h, int relax, CRow* r) {
     r->a = h.a;
     r->b = h.b;
     r->pc = h.pc;
+    r->flags = h.flags;
     r->n = ld3(w, cw(L, c, C_NORMAL));
-    const uint32_t* sp = sep_rec(L, c);
+    const uint32_t* sp = chead_rec(L, c);
 #pragma unroll
     for (int p = 0; p < kMaxManifold; p++) {
         if (p >= h.pc) continue;
@@ -1215,22 +1241,24 @@ B3D_FN void crow_load(const Lane& L, int c, CHead h, int relax, CRow* r) {
         q.ni = ldf(w, pw(L, c, p, P_NORMAL_IMPULSE));
         q.tn = ldf(w, pw(L, c, p, P_TOTAL_NORMAL));
         q.lever = relax ? ldf(w, pw(L, c, p, P_LEVER)) : 0.0f;
-        q.sep = ldf(sp, p);
+        q.sep = ldf(sp, CH_SEP + p);
     }
     if (relax) {
         r->friction = ldf(w, cw(L, c, C_FRICTION));
         r->twist_mass = ldf(w, cw(L, c, C_TWIST_MASS));
         r->twist_imp = ldf(w, cw(L, c, C_TWIST_IMPULSE));
-        r->rolling = ldf(w, cw(L, c, C_ROLLING));
+        r->rolling = (r->flags & CF_ROLLING) ? ldf(w, cw(L, c, C_ROLLING)) : 0.0f;
         r->fi.x = ldf(w, cw(L, c, C_FRICTION_IMPULSE));
         r->fi.y = ldf(w, cw(L, c, C_FRICTION_IMPULSE + 1));
         r->t1 = ld3(w, cw(L, c, C_TANGENT1));
-        r->t2 = ld3(w, cw(L, c, C_TANGENT2));
+        /* tangent2 = tangent1 x normal as written by b3_contact_from_mani */
+        r->t2 = cross(r->t1, r->n);
         r->ca = ld3(w, cw(L, c, C_CENTER_A));
         r->cb = ld3(w, cw(L, c, C_CENTER_B));
+        /* the inverse of a symmetric 2x2 is stored symmetric bit for bit */
         r->tm.cx.x = ldf(w, cw(L, c, C_TANGENT_MASS));
         r->tm.cx.y = ldf(w, cw(L, c, C_TANGENT_MASS + 1));
-        r->tm.cy.x = ldf(w, cw(L, c, C_TANGENT_MASS + 2));
+        r->tm.cy.x = r->tm.cx.y;
         r->tm.cy.y = ldf(w, cw(L, c, C_TANGENT_MASS + 3));
     }
 }
@@ -1309,7 +1337,7 @@ B3D_FN void crow_solve(const Lane& L, int c, CRow& r, float inv_h, float contact
         wa = sub(wa, mv(r.ia, cross(r.ca, P)));
         vb = madd(vb, r.mb, P);
         wb = add(wb, mv(r.ib, cross(r.cb, P)));
-        if (r.rolling > 0.0f) {
+        if (r.flags & CF_ROLLING) {
             V3 ri = ld3(w, cw(L, c, C_ROLLING_IMPULSE));
             solve_rolling(r.t1, r.t2, r.rolling, total_n, r.ia, r.ib, &ri, &wa, &wb);
             st3(w, cw(L, c, C_ROLLING_IMPULSE), ri);
@@ -1328,7 +1356,7 @@ B3D_FN void crow_solve(const Lane& L, int c, CRow& r, float inv_h, float contact
 /* b3_solve_contacts (08:415-437): one Gauss-Seidel sweep in contact order.
  * Row c+1 is in flight while row c is solved, and the head of row c+2 while
  * row c+1 loads. */
-B3D_FN void solve_contacts(const Lane& L, float inv_h, float contact_speed, int use_bias) {
+B3D_FN void solve_contacts(const Lane& L, float inv_h, float contact_speed, int use_bias, Soft cs, Soft ss) {
     int cc = ldi(L.w, H_CONTACT_COUNT);
     if (cc <= 0) return;
     int relax = !use_bias;
@@ -1339,7 +1367,7 @@ B3D_FN void solve_contacts(const Lane& L, float inv_h, float contact_speed, int 
     for (int c = 0; c < cc; c++) {
         CHead h2 = h1;
         if (c + 2 < cc) h2 = chead_load(L, c + 2);
-        crow_masses(L, c, &cur);
+        crow_masses(L, c, &cur, cs, ss);
         if (c + 1 < cc) crow_load(L, c + 1, h1, relax, &nxt);
         crow_solve(L, c, cur, inv_h, contact_speed, use_bias);
         cur = nxt;
@@ -1352,10 +1380,10 @@ B3D_FN void apply_restitution(const Lane& L, float threshold) {
     uint32_t* w = L.w;
     int cc = ldi(w, H_CONTACT_COUNT);
     for (int c = 0; c < cc; c++) {
+        CHead hd = chead_load(L, c);
+        if (!(hd.flags & CF_RESTITUTION)) continue;
         float e = ldf(w, cw(L, c, C_RESTITUTION));
-        if (e == 0.0f) continue;
-        int a = ldi(w, cw(L, c, C_BODY_A)), b = ldi(w, cw(L, c, C_BODY_B));
-        int pc = ldi(w, cw(L, c, C_POINT_COUNT));
+        int a = hd.a, b = hd.b, pc = hd.pc;
         V3 va = vlin(L, a), wa = vang(L, a), vb = vlin(L, b), wb = vang(L, b);
         V3 n = ld3(w, cw(L, c, C_NORMAL));
         float ma = ldf(w, cw(L, c, C_INV_MASS_A)), mb = ldf(w, cw(L, c, C_INV_MASS_B));
@@ -1391,20 +1419,18 @@ B3D_FN void apply_restitution(const Lane& L, float threshold) {
 
 /* A joint row as one solve needs it: the prepared constants, the delta
  * state geometry and the accumulated impulses. */
-struct JHead { int a, b, type; };
+struct JHead { int a, b, info; };
 struct JRow {
-    int a, b, type, fixed, en_spring, en_motor, en_limit;
+    int a, b, info;
     float ma, mb;
     M3 ia, ib;
     Soft soft;
     V3 ra, rb, psep, lin_imp;
-    M3 kinv;
     /* revolute */
-    V3 axis, ia_ax, ib_ax, px, py;
+    V3 axis, px, py;
     float axial_mass, max_torque, speed, target, lower, upper;
     Soft spring_soft;
-    float tw, relx, rely, kxx, kyy, kxy, kinv2;
-    int kok;
+    float tw, relx, rely;
     float spring_imp, motor_imp, lower_imp, upper_imp;
     V2 perp_imp;
     /* weld */
@@ -1415,69 +1441,85 @@ struct JRow {
 };
 
 B3D_FN JHead jhead_load(const Lane& L, int j) {
+    const uint32_t* r = joint_rec(L, j);
+    uint32_t ab = ldu(r, JS_AB);
     JHead h;
-    h.a = ldi(L.w, jw(L, j, J_BODY_A));
-    h.b = ldi(L.w, jw(L, j, J_BODY_B));
-    h.type = ldi(L.w, jw(L, j, J_TYPE));
+    h.a = (int)(ab & 0xffffu);
+    h.b = (int)(ab >> 16);
+    h.info = ldi(r, JS_INFO);
     return h;
 }
 
+/* Everything one solve of joint j reads.  Fields of disabled rows and the
+ * masses of bodies that are not dynamic (exact zeros in the row) are not
+ * loaded. */
 B3D_FN void jrow_load(const Lane& L, int j, JHead h, JRow* r) {
     const uint32_t* w = L.w;
     const uint32_t* g = joint_rec(L, j);
+    int f = h.info;
     r->a = h.a;
     r->b = h.b;
-    r->type = h.type;
-    r->fixed = ldi(w, jw(L, j, J_FIXED_ROTATION));
-    r->ma = ldf(w, jw(L, j, J_INV_MASS_A));
-    r->mb = ldf(w, jw(L, j, J_INV_MASS_B));
-    r->ia = ldm3(w, jw(L, j, J_INV_I_A));
-    r->ib = ldm3(w, jw(L, j, J_INV_I_B));
+    r->info = f;
+    r->ma = 0.0f;
+    r->mb = 0.0f;
+    r->ia = m3zero();
+    r->ib = m3zero();
+    if (f & JF_DYN_A) {
+        r->ma = ldf(w, jw(L, j, J_INV_MASS_A));
+        r->ia = ldm3(w, jw(L, j, J_INV_I_A));
+    }
+    if (f & JF_DYN_B) {
+        r->mb = ldf(w, jw(L, j, J_INV_MASS_B));
+        r->ib = ldm3(w, jw(L, j, J_INV_I_B));
+    }
     r->soft = ldsoft(w, jw(L, j, J_SOFTNESS));
     r->ra = ld3(g, JS_RA);
     r->rb = ld3(g, JS_RB);
     r->psep = ld3(g, JS_PSEP);
-    r->kinv = ldm3(g, JS_KINV);
     r->lin_imp = ld3(w, jw(L, j, J_LINEAR_IMPULSE));
-    if (h.type == kJointWeld) {
-        r->ang_hz = ldf(w, jw(L, j, J_ANGULAR_HERTZ));
+    int fixed = f & JF_FIXED;
+    if (f & JF_WELD) {
         r->lin_hz = ldf(w, jw(L, j, J_LINEAR_HERTZ));
-        r->ang_spring = ldsoft(w, jw(L, j, J_ANGULAR_SPRING));
         r->lin_spring = ldsoft(w, jw(L, j, J_LINEAR_SPRING));
-        r->cv = ld3(g, JS_CV);
-        r->ang_imp = ld3(w, jw(L, j, J_ANGULAR_IMPULSE));
-        r->ang_mass = ldm3(w, jw(L, j, J_ANGULAR_MASS));
+        if (!fixed) {
+            r->ang_hz = ldf(w, jw(L, j, J_ANGULAR_HERTZ));
+            r->ang_spring = ldsoft(w, jw(L, j, J_ANGULAR_SPRING));
+            r->cv = ld3(g, JS_CV);
+            r->ang_imp = ld3(w, jw(L, j, J_ANGULAR_IMPULSE));
+            r->ang_mass = ldm3(w, jw(L, j, J_ANGULAR_MASS));
+        }
         return;
     }
-    r->en_spring = ldi(w, jw(L, j, J_ENABLE_SPRING));
-    r->en_motor = ldi(w, jw(L, j, J_ENABLE_MOTOR));
-    r->en_limit = ldi(w, jw(L, j, J_ENABLE_LIMIT));
+    if (fixed) return;
     r->axis = ld3(w, jw(L, j, J_ROTATION_AXIS));
-    r->ia_ax = ld3(g, JS_IA_AX);
-    r->ib_ax = ld3(g, JS_IB_AX);
     r->px = ld3(g, JS_PX);
     r->py = ld3(g, JS_PY);
-    r->axial_mass = ldf(w, jw(L, j, J_AXIAL_MASS));
-    r->max_torque = ldf(w, jw(L, j, J_MAX_MOTOR_TORQUE));
-    r->speed = ldf(w, jw(L, j, J_MOTOR_SPEED));
-    r->target = ldf(w, jw(L, j, J_TARGET_ANGLE));
-    r->lower = ldf(w, jw(L, j, J_LOWER_ANGLE));
-    r->upper = ldf(w, jw(L, j, J_UPPER_ANGLE));
-    r->spring_soft = ldsoft(w, jw(L, j, J_SPRING_SOFTNESS));
-    r->tw = ldf(g, JS_TW);
     r->relx = ldf(g, JS_RELX);
     r->rely = ldf(g, JS_RELY);
-    r->kxx = ldf(g, JS_KXX);
-    r->kyy = ldf(g, JS_KYY);
-    r->kxy = ldf(g, JS_KXY);
-    r->kinv2 = ldf(g, JS_KINV2);
-    r->kok = ldi(g, JS_KOK);
-    r->spring_imp = ldf(w, jw(L, j, J_SPRING_IMPULSE));
-    r->motor_imp = ldf(w, jw(L, j, J_MOTOR_IMPULSE));
-    r->lower_imp = ldf(w, jw(L, j, J_LOWER_IMPULSE));
-    r->upper_imp = ldf(w, jw(L, j, J_UPPER_IMPULSE));
     r->perp_imp.x = ldf(w, jw(L, j, J_PERP_IMPULSE));
     r->perp_imp.y = ldf(w, jw(L, j, J_PERP_IMPULSE + 1));
+    if (f & (JF_SPRING | JF_MOTOR | JF_LIMIT)) {
+        r->tw = ldf(g, JS_TW);
+        r->axial_mass = ldf(w, jw(L, j, J_AXIAL_MASS));
+    }
+    if (f & (JF_SPRING | JF_MOTOR)) r->max_torque = ldf(w, jw(L, j, J_MAX_MOTOR_TORQUE));
+    if (f & JF_SPRING) {
+        r->target = ldf(w, jw(L, j, J_TARGET_ANGLE));
+        r->spring_soft = ldsoft(w, jw(L, j, J_SPRING_SOFTNESS));
+        r->spring_imp = ldf(w, jw(L, j, J_SPRING_IMPULSE));
+    }
+    if (f & JF_MOTOR) {
+        r->speed = ldf(w, jw(L, j, J_MOTOR_SPEED));
+        r->motor_imp = ldf(w, jw(L, j, J_MOTOR_IMPULSE));
+    }
+    if (f & (JF_MOTOR | JF_LIMIT)) {
+        r->lower = ldf(w, jw(L, j, J_LOWER_ANGLE));
+        r->upper = ldf(w, jw(L, j, J_UPPER_ANGLE));
+    }
+    if (f & JF_LIMIT) {
+        r->lower_imp = ldf(w, jw(L, j, J_LOWER_IMPULSE));
+        r->upper_imp = ldf(w, jw(L, j, J_UPPER_IMPULSE));
+    }
 }
 
 /* Point rows shared by weld and revolute (06:257-282), with the anchors,
@@ -1492,7 +1534,8 @@ B3D_FN void solve_point(const Lane& L, int j, const JRow& r, V3* va, V3* wa, V3*
         mscale = soft.mass_scale;
         iscale = soft.impulse_scale;
     }
-    V3 bsol = mv(r.kinv, add(cdot, bias));
+    /* b3_solve3 of the point mass (06:241-255, 03_math.inl:343-345) */
+    V3 bsol = solve3(point_k(r.ma, r.mb, r.ia, r.ib, r.ra, r.rb), add(cdot, bias));
     V3 impulse = msub(scale(bsol, -mscale), iscale, r.lin_imp);
     st3(L.w, jw(L, j, J_LINEAR_IMPULSE), add(r.lin_imp, impulse));
     *va = msub(*va, r.ma, impulse);
@@ -1504,7 +1547,7 @@ B3D_FN void solve_point(const Lane& L, int j, const JRow& r, V3* va, V3* wa, V3*
 /* b3_solve_weld (06:285-332). */
 B3D_FN void solve_weld(const Lane& L, int j, const JRow& r, int use_bias) {
     V3 va = vlin(L, r.a), wa = vang(L, r.a), vb = vlin(L, r.b), wb = vang(L, r.b);
-    if (!r.fixed) {
+    if (!(r.info & JF_FIXED)) {
         V3 bias = zero3();
         float mscale = 1.0f, iscale = 0.0f;
         if (use_bias || r.ang_hz > 0.0f) {
@@ -1550,10 +1593,16 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
     uint32_t* w = L.w;
     V3 va = vlin(L, r.a), wa = vang(L, r.a), vb = vlin(L, r.b), wb = vang(L, r.b);
     V3 axis = r.axis;
-    int fixed = r.fixed;
+    int fixed = r.info & JF_FIXED;
+    int en_spring = r.info & JF_SPRING, en_motor = r.info & JF_MOTOR, en_limit = r.info & JF_LIMIT;
     float axial_mass = r.axial_mass;
     float tw = r.tw;
-    if (r.en_spring && !fixed) {
+    V3 ia_ax = zero3(), ib_ax = zero3();
+    if (!fixed) {
+        ia_ax = mv(r.ia, axis);
+        ib_ax = mv(r.ib, axis);
+    }
+    if (en_spring && !fixed) {
         Soft ss = r.spring_soft;
         float c = tw - r.target;
         float bias = ss.bias_rate * c;
@@ -1567,12 +1616,12 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
         }
         dimp = nimp - old;
         stf(w, jw(L, j, J_SPRING_IMPULSE), nimp);
-        wa = msub(wa, dimp, r.ia_ax);
-        wb = madd(wb, dimp, r.ib_ax);
+        wa = msub(wa, dimp, ia_ax);
+        wb = madd(wb, dimp, ib_ax);
     }
-    if (r.en_motor && !fixed) {
+    if (en_motor && !fixed) {
         int blocked = 0;
-        if (r.en_limit) {
+        if (en_limit) {
             if (tw >= r.upper - 0.01f && r.speed > 0.0f) blocked = 1;
             if (tw <= r.lower + 0.01f && r.speed < 0.0f) blocked = 1;
         }
@@ -1587,23 +1636,23 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
             nimp = clampf(nimp, -maxp, maxp);
             dimp = nimp - old;
             stf(w, jw(L, j, J_MOTOR_IMPULSE), nimp);
-            wa = msub(wa, dimp, r.ia_ax);
-            wb = madd(wb, dimp, r.ib_ax);
+            wa = msub(wa, dimp, ia_ax);
+            wb = madd(wb, dimp, ib_ax);
         }
     }
-    if (r.en_limit && !fixed) {
+    if (en_limit && !fixed) {
         float old = r.lower_imp;
         float lo = limit_impulse(tw - r.lower, dot(sub(wb, wa), axis), inv_h, use_bias, r.soft, axial_mass, old);
         stf(w, jw(L, j, J_LOWER_IMPULSE), lo);
         float dimp = lo - old;
-        wa = msub(wa, dimp, r.ia_ax);
-        wb = madd(wb, dimp, r.ib_ax);
+        wa = msub(wa, dimp, ia_ax);
+        wb = madd(wb, dimp, ib_ax);
         old = r.upper_imp;
         float up = limit_impulse(r.upper - tw, dot(sub(wa, wb), axis), inv_h, use_bias, r.soft, axial_mass, old);
         stf(w, jw(L, j, J_UPPER_IMPULSE), up);
         dimp = up - old;
-        wa = madd(wa, dimp, r.ia_ax);
-        wb = msub(wb, dimp, r.ib_ax);
+        wa = madd(wa, dimp, ia_ax);
+        wb = msub(wb, dimp, ib_ax);
     }
     if (!fixed) {
         V2 bias;
@@ -1620,15 +1669,13 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
         V2 rhs;
         rhs.x = dot(wrel, r.px) + bias.x;
         rhs.y = dot(wrel, r.py) + bias.y;
-        /* b3_solve2 (03_math.inl:347-359) with the determinant of this
-         * delta state */
-        V2 sol;
-        sol.x = 0.0f;
-        sol.y = 0.0f;
-        if (r.kok) {
-            sol.x = r.kinv2 * (r.kyy * rhs.x - r.kxy * rhs.y);
-            sol.y = r.kinv2 * (-r.kxy * rhs.x + r.kxx * rhs.y);
-        }
+        M3 isum = madd3(r.ia, r.ib);
+        M2 kang;
+        kang.cx.x = dot(r.px, mv(isum, r.px));
+        kang.cy.y = dot(r.py, mv(isum, r.py));
+        kang.cx.y = dot(r.px, mv(isum, r.py));
+        kang.cy.x = kang.cx.y;
+        V2 sol = solve2(kang, rhs);
         V2 dimp;
         dimp.x = -mscale * sol.x - iscale * r.perp_imp.x;
         dimp.y = -mscale * sol.y - iscale * r.perp_imp.y;
@@ -1659,7 +1706,7 @@ B3D_FN void solve_joints(const Lane& L, float h, float inv_h, int use_bias) {
         for (int j = 0; j < nj; j++) {
             JRow r;
             jrow_load(L, j, jhead_load(L, j), &r);
-            if (r.type == kJointWeld) solve_weld(L, j, r, use_bias);
+            if (r.info & JF_WELD) solve_weld(L, j, r, use_bias);
             else solve_revolute(L, j, r, h, inv_h, use_bias);
         }
     }
@@ -1846,11 +1893,11 @@ B3D_FN void step_world(const Lane& L, float dt, int substeps) {
     delta_geometry(L);
     for (int s = 0; s < subs; s++) {
         integrate_velocities(L);
-        solve_contacts(L, inv_h, contact_speed, 1);
+        solve_contacts(L, inv_h, contact_speed, 1, cs, ss);
         solve_joints(L, h, inv_h, 1);
         integrate_positions(L, h, inv_dt);
         delta_geometry(L);
-        solve_contacts(L, inv_h, contact_speed, 0);
+        solve_contacts(L, inv_h, contact_speed, 0, cs, ss);
         solve_joints(L, h, inv_h, 0);
         apply_restitution(L, rest_threshold);
     }

@@ -158,3 +158,106 @@ def diff_words(a, b, sig):
     m = live_word_mask(a, sig) & live_word_mask(b, sig)
     d = (words(a) != words(b)) & m
     return np.argwhere(d)
+
+
+# ---- coverage worlds: features the five benchmark scenes do not reach ----
+
+def feature_worlds(count, seed=7, hinges=True):
+    """Worlds of capacity set 16/16/32/8 (puffysics_amd.creation) mixing
+    weld joints (rigid and soft), spring-only and fixed-rotation hinges,
+    kinematic movers, restitution, rolling resistance, axis locks, damping,
+    gravity scale, collide_connected, category/mask filtering, and (every
+    fourth world) a pile dense enough to overflow the contact capacity.
+    `hinges=False` leaves out revolute joints (no atan2f on the path)."""
+    from puffysics_amd import creation as cr
+    from puffysics_amd.b3types import B3_DYNAMIC, B3_KINEMATIC, B3_STATIC
+    rng = np.random.default_rng(seed)
+    w = cr.new_worlds(count, gravity=(0.0, -9.81, 0.0))
+    for k in range(count):
+        g = cr.body(w, k, B3_STATIC, (0.0, -0.5, 0.0))
+        cr.box(w, k, g, (5.0, 0.5, 5.0), restitution=float(rng.choice([0.0, 0.3])))
+        if k % 4 == 3:
+            # overflow pile: 14 small spheres packed in a 3 x 3 x 2 block
+            for i in range(14):
+                p = (0.1 * (i % 3), 0.12 + 0.1 * (i // 9), 0.1 * ((i // 3) % 3))
+                b = cr.body(w, k, B3_DYNAMIC, p)
+                cr.sphere(w, k, b, 0.1)
+                cr.finalize_mass(w, k, b)
+            continue
+        kin = cr.body(w, k, B3_KINEMATIC, (-1.0, 0.35, 0.0), lin_vel=(0.4, 0.0, 0.0), ang_vel=(0.0, 0.5, 0.0))
+        cr.box(w, k, kin, (0.3, 0.3, 0.3))
+        bodies = []
+        for i in range(7):
+            p = (rng.uniform(-0.8, 0.8), rng.uniform(0.15, 1.5), rng.uniform(-0.8, 0.8))
+            ang = rng.uniform(-1, 1, 3)
+            q = np.concatenate([np.sin(0.5) * ang / np.linalg.norm(ang), [np.cos(0.5)]])
+            b = cr.body(w, k, B3_DYNAMIC, p, rot=tuple(q), lin_vel=tuple(rng.uniform(-1, 1, 3)))
+            kind = i % 3
+            if kind == 0:
+                cr.sphere(w, k, b, rng.uniform(0.1, 0.25), restitution=float(rng.choice([0.0, 0.5])))
+            elif kind == 1:
+                cr.box(w, k, b, tuple(rng.uniform(0.1, 0.25, 3)))
+            else:
+                cr.capsule(w, k, b, rng.uniform(0.1, 0.2), rng.uniform(0.05, 0.12))
+            cr.finalize_mass(w, k, b)
+            bodies.append(b)
+        bd = w["bodies"]
+        sh = w["shapes"]
+        bd["linear_damping"][k, bodies[0]] = 0.3
+        bd["angular_damping"][k, bodies[1]] = 0.5
+        bd["gravity_scale"][k, bodies[2]] = 0.5
+        bd["flags"][k, bodies[3]] |= 0x08 | 0x10 | 0x20          # angular locks
+        bd["flags"][k, bodies[4]] |= 0x04                        # linear z lock
+        sh["rolling"][k, 3] = 0.05                               # rolling resistance on one shape
+        sh["mask"][k, 4] = 0xfffffffffffffffe                    # ignores category bit 0 ...
+        sh["category"][k, 0] = 1                                 # ... which the ground box holds
+        j = cr.weld(w, k, bodies[5], bodies[6], (0.2, 0.0, 0.0), (-0.2, 0.0, 0.0))
+        if k % 2:
+            w["joints"]["linear_hertz"][k, j] = 5.0
+            w["joints"]["linear_damping"][k, j] = 0.7
+            w["joints"]["angular_hertz"][k, j] = 3.0
+            w["joints"]["angular_damping"][k, j] = 0.5
+        if hinges:
+            j = cr.revolute(w, k, bodies[1], bodies[2], (0.0, 0.2, 0.0), (0.0, -0.2, 0.0), (1.0, 0.0, 0.0))
+            cr.joint_spring(w, k, j, 0.4, 4.0, 0.7)
+            w["joints"]["collide_connected"][k, j] = 1
+            j = cr.revolute(w, k, g, kin, (1.0, 0.5, 0.0), (0.0, 0.0, 0.0), (0.0, 1.0, 0.0))  # fixed rotation
+            cr.joint_limits(w, k, j, -0.3, 0.3)
+            j = cr.revolute(w, k, g, bodies[0], (0.5, 1.0, 0.5), (0.0, 0.1, 0.0), (0.0, 0.0, 1.0))
+            cr.joint_limits(w, k, j, -0.4, 0.6)
+            cr.joint_motor(w, k, j, 0.5, 2.0)
+            cr.joint_spring(w, k, j, -0.2, 2.0, 1.0)
+    return w
+
+
+def oracle_step_batch(worlds, sig, dt, substeps, active=None):
+    """b3_batch_step over a contiguous batch on the oracle."""
+    lib = oracle()
+    lib.ocpu_batch_step.argtypes = [_vp, C.c_size_t, C.c_size_t, _i, _ull, _f, _i, _vp]
+    act = None if active is None else np.ascontiguousarray(active, np.uint8)
+    return lib.ocpu_batch_step(worlds.ctypes.data, worlds.dtype.itemsize, 0, len(worlds), sig, dt, substeps,
+                               None if act is None else act.ctypes.data)
+
+
+class EmuSig:
+    """Word-transposed tiles of any signature stepped by the host build of
+    the lane code, without scene inputs."""
+
+    def __init__(self, sig, worlds):
+        self.sig = sig
+        self.count = len(worlds)
+        self.dtype = worlds.dtype
+        words_ = emu().emu_world_words(sig)
+        self.tiles = np.zeros(((self.count + 63) // 64) * words_ * 64, np.uint32)
+        w = np.ascontiguousarray(worlds)
+        emu().emu_upload(w.ctypes.data, self.count, sig, self.tiles.ctypes.data)
+
+    def step(self, dt, substeps, active=None):
+        act = None if active is None else np.ascontiguousarray(active, np.uint8)
+        emu().emu_step(self.tiles.ctypes.data, self.count, self.sig, dt, substeps,
+                       None if act is None else act.ctypes.data)
+
+    def worlds(self):
+        out = np.zeros(self.count, dtype=self.dtype)
+        emu().emu_download(self.tiles.ctypes.data, self.count, self.sig, out.ctypes.data)
+        return out

@@ -29,3 +29,28 @@ def test_lane_code_matches_oracle(scene, count, steps):
     # the run did something: contacts exist where the scene has any
     if scene != 3:
         assert ref["contact_count"].sum() > 0
+
+
+def test_lane_code_covers_every_feature():
+    """Welds (rigid and soft), spring-only and fixed hinges, kinematic
+    bodies, restitution, rolling, locks, damping, filters and contact
+    overflow: bit-exact against the oracle over 80 steps."""
+    from b3test import EmuSig, feature_worlds, oracle_step_batch
+    from puffysics_amd.creation import CUSTOM_SIG
+    worlds = feature_worlds(40)
+    ref = clone(worlds)
+    emu = EmuSig(CUSTOM_SIG, worlds)
+    active = (np.arange(40) % 5 != 2).astype(np.uint8)
+    for t in range(80):
+        act = active if t % 3 == 0 else None
+        oracle_step_batch(ref, CUSTOM_SIG, 1.0 / 60.0, 4, act)
+        emu.step(1.0 / 60.0, 4, act)
+    got = emu.worlds()
+    bad = diff_words(got, ref, CUSTOM_SIG)
+    assert len(bad) == 0, bad[:10].tolist()
+    # the features are really exercised
+    assert ref["contact_overflow"][3::4].all() and ref["contacts_dropped"].max() > 0
+    assert (ref["contact_count"] > 0).all()
+    j = ref["joints"]
+    assert (j["fixed_rotation"][:, 2][np.arange(40) % 4 != 3] == 1).all()
+    assert np.abs(j["angular_impulse"]["x"][:, 0]).max() > 0           # welds carry load

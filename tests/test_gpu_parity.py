@@ -231,3 +231,42 @@ def test_against_reference_fixtures(scene):
         elif cp == checkpoints[0]:
             assert contact_keys(got) == contact_keys(ref)
             assert_close_state(got, ref)
+
+
+def test_feature_worlds_without_hinges_bit_exact():
+    """Welds, kinematic bodies, restitution, rolling, locks, damping,
+    filters and contact overflow on the device: bit-identical to the oracle
+    over 80 steps with a step mask on every third step."""
+    from b3test import feature_worlds, oracle_step_batch
+    from puffysics_amd.creation import CUSTOM_SIG
+    from puffysics_amd.engine import B3Engine
+    worlds = feature_worlds(100, hinges=False)
+    ref = clone(worlds)
+    eng = B3Engine(worlds, CUSTOM_SIG)
+    active = (np.arange(100) % 5 != 2).astype(np.uint8)
+    d_active = torch.from_numpy(active).cuda()
+    for t in range(80):
+        act = t % 3 == 0
+        oracle_step_batch(ref, CUSTOM_SIG, 1.0 / 60.0, 4, active if act else None)
+        eng.step(1.0 / 60.0, 4, d_active if act else None)
+    torch.cuda.synchronize()
+    got = eng.download()
+    bad = diff_words(got, ref, CUSTOM_SIG)
+    assert len(bad) == 0, describe(bad, got, ref, worlds)
+    assert ref["contacts_dropped"].max() > 0
+
+
+def test_feature_worlds_with_hinges_one_step():
+    from b3test import feature_worlds, oracle_step_batch
+    from puffysics_amd.creation import CUSTOM_SIG
+    from puffysics_amd.engine import B3Engine
+    worlds = feature_worlds(100)
+    oracle_step_batch(worlds, CUSTOM_SIG, 1.0 / 60.0, 4)   # warm caches and impulses
+    ref = clone(worlds)
+    eng = B3Engine(worlds, CUSTOM_SIG)
+    oracle_step_batch(ref, CUSTOM_SIG, 1.0 / 60.0, 4)
+    eng.step(1.0 / 60.0, 4)
+    torch.cuda.synchronize()
+    got = eng.download()
+    assert contact_keys(got) == contact_keys(ref)
+    assert_close_state(got, ref)
