@@ -10,7 +10,8 @@
  * Kernels:
  *   b3k_upload / b3k_download  AoS <-> tiles, transposed through LDS in
  *                              64 x 64 word blocks (both sides coalesced)
- *   b3k_restore                masked snapshot restore; the wave copies one
+ *   b3k_restore                masked restore from the snapshots (plain
+ *                              B3World structs); the wave copies one
  *                              resetting world at a time with all 64 lanes
  *   b3k_step                   optional fused restore, then one b3_step per
  *                              selected lane; LDS holds the lane's clip
@@ -77,30 +78,25 @@ __global__ __launch_bounds__(kXposeThreads) void b3k_download(const uint32_t* __
 
 /* ---- masked restore ---- */
 
-/* Copy words [k0, k1) of the world in lane `l` from snapshot to live, one
- * word per lane of the wave. */
-__device__ __forceinline__ void copy_words(uint32_t* __restrict__ live, const uint32_t* __restrict__ snap,
-        int l, int k0, int k1) {
-    for (int k = k0 + (int)threadIdx.x; k < k1; k += 64) live[(size_t)k * 64 + l] = snap[(size_t)k * 64 + l];
-}
-
-/* Restore the resetting worlds of this workgroup's tile, one world at a
- * time with all 64 lanes. */
+/* Restore the resetting worlds of this workgroup's tile from the snapshots,
+ * which are kept as plain B3World structs (AoS): one world at a time, the 64
+ * lanes read 64 consecutive snapshot words and write them to their rows of
+ * the tile. */
 __device__ void restore_tile(uint32_t* live, const uint32_t* snap, const Geometry& g, int count,
         const unsigned char* reset) {
     int tile = blockIdx.x;
     int w = tile * 64 + (int)threadIdx.x;
     int want = w < count && reset[w] != 0;
     uint64_t bits = __ballot(want);
-    size_t base = (size_t)tile * g.world_words * 64;
-    uint32_t* lt = live + base;
-    const uint32_t* st = snap + base;
+    uint32_t* lt = live + (size_t)tile * g.world_words * 64;
     while (bits) {
         int l = __builtin_ctzll(bits);
         bits &= bits - 1;
+        const uint32_t* src = snap + (size_t)(tile * 64 + l) * g.world_words;
         int lo[3], hi[3];
-        restore_ranges(g, (int)st[(size_t)H_CONTACT_COUNT * 64 + l], lo, hi);
-        for (int r = 0; r < 3; r++) copy_words(lt, st, l, lo[r], hi[r]);
+        restore_ranges(g, (int)src[H_CONTACT_COUNT], lo, hi);
+        for (int r = 0; r < 3; r++)
+            for (int k = lo[r] + (int)threadIdx.x; k < hi[r]; k += 64) lt[(size_t)k * 64 + l] = src[k];
     }
 }
 
@@ -123,12 +119,7 @@ __global__ __launch_bounds__(64) void b3k_step(uint32_t* live, const uint32_t* s
     int lane = threadIdx.x;
     int w = tile * 64 + lane;
     if (w >= count || (step_mask && !step_mask[w])) return;
-    Lane L;
-    L.w = live + (size_t)tile * g.world_words * 64 + lane;
-    L.scr = scratch + (size_t)tile * g.scr_words * 64 + lane;
-    L.vel = vel_rows + lane;
-    L.g = g;
-    step_world(L, dt, substeps);
+    step_world(lane_view(live, scratch, vel_rows, g, tile, lane), dt, substeps);
 }
 
 /* ---- inputs and stats ---- */
@@ -292,8 +283,8 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
     if (e->tiles > 0) {
         size_t tiles_bytes = (size_t)e->tiles * e->tile_words * 4;
         if ((err = hipMalloc((void**)&e->live, tiles_bytes)) != hipSuccess
-                || (err = hipMalloc((void**)&e->snap, tiles_bytes)) != hipSuccess
-                || (err = hipMalloc((void**)&e->scratch, (size_t)e->tiles * g.scr_words * 64 * 4)) != hipSuccess
+                || (err = hipMalloc((void**)&e->snap, (size_t)e->count * world_bytes)) != hipSuccess
+                || (err = hipMalloc((void**)&e->scratch, (size_t)e->tiles * g.tile_scr_words * 4)) != hipSuccess
                 || (err = hipMalloc((void**)&e->staging, (size_t)e->count * world_bytes)) != hipSuccess) {
             (void)b3_engine_destroy(e);
             return err;
@@ -305,7 +296,7 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
         }
         /* Snapshots default to the initial worlds. */
         err = put_worlds(e, host, e->live);
-        if (err == hipSuccess) err = put_worlds(e, host, e->snap);
+        if (err == hipSuccess) err = hipMemcpy(e->snap, host, (size_t)e->count * world_bytes, hipMemcpyHostToDevice);
         free(host);
         if (err != hipSuccess) {
             (void)b3_engine_destroy(e);
@@ -337,7 +328,8 @@ hipError_t b3_engine_set_snapshots(B3Engine* e, const void* initial) {
     if (err != hipSuccess) return err;
     for (int i = 0; i < e->count; i++)
         if (!world_valid((const unsigned char*)initial + (size_t)i * e->world_bytes, e->g)) return hipErrorInvalidValue;
-    return put_worlds(e, (const unsigned char*)initial, e->snap);
+    if (e->count == 0) return hipSuccess;
+    return hipMemcpy(e->snap, initial, (size_t)e->count * e->world_bytes, hipMemcpyHostToDevice);
 }
 
 hipError_t b3_engine_upload(B3Engine* e, B3Batch worlds) {
@@ -382,9 +374,10 @@ hipError_t b3_batch_restore_gpu(B3Engine* e, const unsigned char* reset, hipStre
     hipError_t err = on_device(e);
     if (err != hipSuccess) return err;
     if (!reset) {
-        /* NULL restores every world: one device-to-device copy. */
-        err = hipMemcpyAsync(e->live, e->snap, (size_t)e->tiles * e->tile_words * 4, hipMemcpyDeviceToDevice, stream);
-        return err;
+        /* NULL restores every world: the whole structs, transposed into the tiles. */
+        dim3 grid((unsigned)((e->g.world_words + 63) / 64), (unsigned)e->tiles);
+        b3k_upload<<<grid, kXposeThreads, 0, stream>>>(e->snap, e->live, e->count, e->g.world_words);
+        return hipGetLastError();
     }
     b3k_restore<<<e->tiles, 64, 0, stream>>>(e->live, e->snap, e->g, e->count, reset);
     return hipGetLastError();

@@ -17,7 +17,7 @@ struct B3Engine {
     size_t world_bytes;
     size_t tile_words;
     uint32_t* live;
-    uint32_t* snap;
+    uint32_t* snap;          /* count * world_bytes, AoS reset snapshots */
     uint32_t* scratch;
     unsigned char* staging;  /* count * world_bytes, AoS, for up/download */
     size_t lds_bytes;

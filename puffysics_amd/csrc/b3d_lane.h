@@ -196,12 +196,14 @@ constexpr int J_SPRING_SOFTNESS = B3D_W(B3Joint, spring_softness);
 constexpr int O_SHAPE_A = 0, O_SHAPE_B = 1, O_POINT_COUNT = 2, O_FEATURE = 3, O_NORMAL_IMPULSE = 7,
               O_FRICTION_IMPULSE = 11, O_TWIST_IMPULSE = 13, O_ROLLING_IMPULSE = 14, O_KEY = 17, kOldWords = 18;
 
-/* Per-step shape record in scratch: world pose, size and owning body,
- * written once per step by the shape pass so that the pair loop never
- * follows a body index.  The padded bounds go to LDS when they fit (or to
- * the scratch bounds area). */
+/* Per-step shape record in scratch: world pose, size and owning body, the
+ * collision filter and the material, written once per step by the shape
+ * pass so that the pair loop reads one record per shape and never follows
+ * a body index.  The padded bounds go to LDS when they fit (or to the
+ * scratch bounds area). */
 constexpr int SS_P = 0, SS_Q = 3, SS_RADIUS = 7, SS_HALF = 8, SS_TYPE = 11, SS_BODY = 12, SS_BFLAGS = 13,
-              SS_CENTER = 14, kShapeScr = 17;
+              SS_CENTER = 14, SS_CATEGORY = 17, SS_MASK = 19, SS_FRICTION = 21, SS_RESTITUTION = 22,
+              SS_ROLLING = 23, kShapeScr = 24;
 constexpr int kBodyStatic = 1, kBodyDynamic = 2;   /* SS_BFLAGS bits */
 /* Loops over bodies, shapes and contacts run in chunks, every load of a
  * chunk issued before any of its results is used. */
@@ -212,11 +214,35 @@ constexpr int kShapeChunk = 4;
  * kind (type and axis-lock flags). */
 constexpr int BS_DV = 0, BS_DW = 3, BS_LD = 6, BS_AD = 7, BS_KIND = 8, kBodyScr = 9;
 constexpr int kKindDynamic = 1 << 8, kKindStatic = 1 << 9;  /* BS_KIND bits; low byte = lock flags */
-/* Per-contact scratch head, written by the pair loop: bodies (a | b << 16),
- * point count and facts about the pair (pc | flags << 8), then the point
- * separations of the current delta poses. */
-constexpr int CH_AB = 0, CH_INFO = 1, CH_SEP = 2, kContactScr = 6;
+/* Per-contact scratch head, written by the pair loop for prepare_contacts:
+ * bodies (a | b << 16), point count and facts about the pair
+ * (pc | flags << 8). */
+constexpr int CH_AB = 0, CH_INFO = 1, kContactScr = 2;
 constexpr int CF_DYN_A = 1, CF_DYN_B = 2, CF_STATIC = 4, CF_RESTITUTION = 8, CF_ROLLING = 16;
+
+/* Packed contact records.  Past the per-lane words, a tile's scratch is
+ * quad rows: 64 slots of 4 words (1 KB).  Contact c of a lane owns kCRows
+ * rows in slot `rank`, the number of the tile's stepping lanes below it that
+ * also have a contact c; the kPRows rows of its point p use the rank among
+ * the lanes whose contact c has a point p.  Every loop over contacts visits
+ * c in the same order in all lanes, so the lanes that touch a row in one
+ * access touch one contiguous span of it, and a quad is one 16-byte access.
+ * The record holds everything the solver sweeps, warm start and restitution
+ * read (prepare_contacts writes it once per step), and the impulses they
+ * update, which go back to the world's contact rows at the end of the step.
+ * Word k of a record is component k % 4 of quad row k / 4. */
+constexpr int kRowWords = kLanes * 4;
+constexpr int R_AB = 0, R_INFO = 1, R_FRICTION = 2, R_TWIST_MASS = 3,   /* row 0: head */
+              R_N = 4, R_ROLLING = 7,                                   /* row 1 */
+              R_MA = 8, R_IA = 9,                                       /* rows 2-4: body a (10 words) */
+              R_IB_ZYZ = 18, R_MB = 20, R_IB = 21,                      /* rows 4-6: body b (10 words) */
+              R_T1 = 28, R_TM_XX = 31, R_CA = 32, R_TM_XY = 35, R_CB = 36, R_TM_YY = 39,
+              R_FI = 40, R_TWIST = 42, R_RESTITUTION = 43,              /* row 10 */
+              R_ROLL = 44,                                              /* row 11 */
+              R_REL_VEL = 48,                                           /* row 12: restitution only */
+              kCRows = 13;
+constexpr int PR_RA = 0, PR_NMASS = 3, PR_RB = 4, PR_BASE_SEP = 7, PR_NI = 8, PR_TN = 9, PR_SEP = 10,
+              PR_LEVER = 11, kPRows = 3;
 /* Joint record in scratch: the joint-connection key, the head written by
  * prepare_joints (bodies a | b << 16 and JF_* flags), then everything that
  * depends only on the bodies' delta poses (recomputed after every position
@@ -239,7 +265,10 @@ struct Geometry {
     int max_b, max_s, max_c, max_j;
     int bo, so, co, jo;   /* word offsets of bodies, shapes, contacts, joints */
     int world_words;      /* words per world (sizeof(B3World) / 4) */
-    int scr_shape, scr_old, scr_sep, scr_joint, scr_body, scr_bounds, scr_words;
+    int scr_shape, scr_old, scr_sep, scr_joint, scr_body, scr_bounds, scr_cand;
+    int scr_words;        /* per-lane scratch words (a multiple of 4) */
+    int q_ct, q_pt;       /* first quad row of the contact and point records */
+    int tile_scr_words;   /* scratch words per tile: 64 lanes' words, then the quad rows */
 };
 
 /* Geometry of a capacity signature; false when it is invalid. */
@@ -262,7 +291,12 @@ B3D_FN bool geometry_of(unsigned long long sig, Geometry* g, size_t* world_bytes
     g->scr_joint = g->scr_sep + g->max_c * kContactScr;
     g->scr_body = g->scr_joint + g->max_j * kJointScr;
     g->scr_bounds = g->scr_body + g->max_b * kBodyScr;
-    g->scr_words = g->scr_bounds + g->max_s * 6;
+    g->scr_cand = g->scr_bounds + g->max_s * 6;
+    g->scr_words = (g->scr_cand + g->max_s * (g->max_s - 1) / 2 + 3) & ~3;
+    g->q_ct = 0;
+    g->q_pt = g->q_ct + g->max_c * kCRows;
+    int qrows = g->q_pt + g->max_c * kMaxManifold * kPRows;
+    g->tile_scr_words = g->scr_words * kLanes + qrows * kRowWords;
     *world_bytes = L.world_size;
     return true;
 }
@@ -271,10 +305,37 @@ B3D_FN bool geometry_of(unsigned long long sig, Geometry* g, size_t* world_bytes
 struct Lane {
     uint32_t* w;    /* live tile + lane */
     uint32_t* scr;  /* scratch tile + lane */
+    uint32_t* sq;   /* the tile's scratch quad rows */
     float* vel;     /* velocity rows + lane; before the velocities are
                        staged the same rows hold the clip polygons */
+    int lane;
     Geometry g;
 };
+
+/* The lane view of world `lane` of tile `tile`. */
+B3D_FN Lane lane_view(uint32_t* live, uint32_t* scratch, float* vel_rows, const Geometry& g, int tile, int lane) {
+    Lane L;
+    L.w = live + (size_t)tile * g.world_words * kLanes + lane;
+    L.scr = scratch ? scratch + (size_t)tile * g.tile_scr_words + lane : nullptr;
+    L.sq = scratch ? scratch + (size_t)tile * g.tile_scr_words + (size_t)g.scr_words * kLanes : nullptr;
+    L.vel = vel_rows ? vel_rows + lane : nullptr;
+    L.lane = lane;
+    L.g = g;
+    return L;
+}
+
+/* Rank of this lane among the lanes executing this point together: the slot
+ * of its packed record.  Lanes run one at a time in a host build, where the
+ * lane index serves. */
+B3D_FN int wave_slot(const Lane& L) {
+#ifdef __HIP_DEVICE_COMPILE__
+    (void)L;
+    uint64_t m = __ballot(1);
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+#else
+    return L.lane;
+#endif
+}
 
 /* Shape bounds stay in the LDS rows during contact generation when the
  * rows of kClipWords + 6 max_s words fit in this many words per lane;
@@ -317,6 +378,15 @@ B3D_FN void stm3(uint32_t* p, int k, M3 m) { st3(p, k, m.cx); st3(p, k + 3, m.cy
 B3D_FN Soft ldsoft(const uint32_t* p, int k) { Soft s; s.bias_rate = ldf(p, k); s.mass_scale = ldf(p, k + 1); s.impulse_scale = ldf(p, k + 2); return s; }
 B3D_FN void stsoft(uint32_t* p, int k, Soft s) { stf(p, k, s.bias_rate); stf(p, k + 1, s.mass_scale); stf(p, k + 2, s.impulse_scale); }
 B3D_FN uint64_t ldu64(const uint32_t* p, int k) { return (uint64_t)ldu(p, k) | ((uint64_t)ldu(p, k + 1) << 32); }
+
+/* ---- packed record access (word k at quad row k / 4, component k % 4) ---- */
+B3D_FN float qf(const uint32_t* r, int k) { return __builtin_bit_cast(float, r[(k >> 2) * kRowWords + (k & 3)]); }
+B3D_FN uint32_t qu(const uint32_t* r, int k) { return r[(k >> 2) * kRowWords + (k & 3)]; }
+B3D_FN void qsf(uint32_t* r, int k, float v) { r[(k >> 2) * kRowWords + (k & 3)] = __builtin_bit_cast(uint32_t, v); }
+B3D_FN void qsu(uint32_t* r, int k, uint32_t v) { r[(k >> 2) * kRowWords + (k & 3)] = v; }
+B3D_FN V3 q3(const uint32_t* r, int k) { return v3(qf(r, k), qf(r, k + 1), qf(r, k + 2)); }
+B3D_FN void qs3(uint32_t* r, int k, V3 v) { qsf(r, k, v.x); qsf(r, k + 1, v.y); qsf(r, k + 2, v.z); }
+
 
 B3D_FN int bw(const Lane& L, int b, int f) { return L.g.bo + b * kBodyWords + f; }
 B3D_FN int sw(const Lane& L, int s, int f) { return L.g.so + s * kShapeWords + f; }
@@ -405,17 +475,78 @@ B3D_FN void shape_aabb(const Posed& P, V3* lo, V3* hi) {
 B3D_FN uint32_t* shape_rec(const Lane& L, int s) { return L.scr + (L.g.scr_shape + s * kShapeScr) * kLanes; }
 B3D_FN uint32_t* old_rec(const Lane& L, int k) { return L.scr + (L.g.scr_old + k * kOldWords) * kLanes; }
 B3D_FN uint32_t* chead_rec(const Lane& L, int c) { return L.scr + (L.g.scr_sep + c * kContactScr) * kLanes; }
-/* A contact's head: bodies, point count and CF_* flags. */
-struct CHead { int a, b, pc, flags; };
-B3D_FN CHead chead_load(const Lane& L, int c) {
-    const uint32_t* hd = chead_rec(L, c);
-    uint32_t ab = ldu(hd, CH_AB), info = ldu(hd, CH_INFO);
+/* Packed record of contact c and of its point p (see kCRows). */
+B3D_FN uint32_t* crec(const Lane& L, int c, int slot) {
+    return L.sq + (size_t)(L.g.q_ct + c * kCRows) * kRowWords + slot * 4;
+}
+B3D_FN uint32_t* prec(const Lane& L, int c, int p, int slot) {
+    return L.sq + (size_t)(L.g.q_pt + (c * kMaxManifold + p) * kPRows) * kRowWords + slot * 4;
+}
+/* A contact's head: bodies, point count and CF_* flags, with its record
+ * slot and, from a packed record, friction and twist mass. */
+struct CHead { int a, b, pc, flags, slot; float friction, twist_mass; };
+B3D_FN CHead head_of(uint32_t ab, uint32_t info) {
     CHead h;
     h.a = (int)(ab & 0xffffu);
     h.b = (int)(ab >> 16);
     h.pc = (int)(info & 0xffu);
     h.flags = (int)(info >> 8);
+    h.slot = 0;
+    h.friction = 0.0f;
+    h.twist_mass = 0.0f;
     return h;
+}
+/* The head the pair loop left for prepare_contacts. */
+B3D_FN CHead chead_load(const Lane& L, int c) {
+    const uint32_t* hd = chead_rec(L, c);
+    return head_of(ldu(hd, CH_AB), ldu(hd, CH_INFO));
+}
+/* The head of a packed record; call where exactly the lanes with a contact
+ * c run. */
+B3D_FN CHead rhead_load(const Lane& L, int c) {
+    int slot = wave_slot(L);
+    const uint32_t* r = crec(L, c, slot);
+    CHead h = head_of(qu(r, R_AB), qu(r, R_INFO));
+    h.slot = slot;
+    h.friction = qf(r, R_FRICTION);
+    h.twist_mass = qf(r, R_TWIST_MASS);
+    return h;
+}
+/* Inverse masses and world inertias of a record's bodies: exact zeros for a
+ * body that is not dynamic (08:236-241), which are therefore not stored. */
+B3D_FN void rec_masses(const uint32_t* r, int flags, float* ma, M3* ia, float* mb, M3* ib) {
+    *ma = 0.0f;
+    *mb = 0.0f;
+    *ia = m3zero();
+    *ib = m3zero();
+    if (flags & CF_DYN_A) {
+        *ma = qf(r, R_MA);
+        ia->cx = q3(r, R_IA);
+        ia->cy = q3(r, R_IA + 3);
+        ia->cz = q3(r, R_IA + 6);
+    }
+    if (flags & CF_DYN_B) {
+        *mb = qf(r, R_MB);
+        ib->cx = q3(r, R_IB);
+        ib->cy = q3(r, R_IB + 3);
+        ib->cz = v3(qf(r, R_IB + 6), qf(r, R_IB_ZYZ), qf(r, R_IB_ZYZ + 1));
+    }
+}
+B3D_FN void rec_store_masses(uint32_t* r, int flags, float ma, M3 ia, float mb, M3 ib) {
+    if (flags & CF_DYN_A) {
+        qsf(r, R_MA, ma);
+        qs3(r, R_IA, ia.cx);
+        qs3(r, R_IA + 3, ia.cy);
+        qs3(r, R_IA + 6, ia.cz);
+    }
+    if (flags & CF_DYN_B) {
+        qsf(r, R_MB, mb);
+        qs3(r, R_IB, ib.cx);
+        qs3(r, R_IB + 3, ib.cy);
+        qsf(r, R_IB + 6, ib.cz.x);
+        qsf(r, R_IB_ZYZ, ib.cz.y);
+        qsf(r, R_IB_ZYZ + 1, ib.cz.z);
+    }
 }
 B3D_FN uint32_t* joint_rec(const Lane& L, int j) { return L.scr + (L.g.scr_joint + j * kJointScr) * kLanes; }
 B3D_FN uint32_t* body_rec(const Lane& L, int b) { return L.scr + (L.g.scr_body + b * kBodyScr) * kLanes; }
@@ -437,10 +568,17 @@ B3D_FN void shape_pass(const Lane& L, int ns, float* bounds) {
         Q brot[kShapeChunk];
         int btype[kShapeChunk];
         Posed P[kShapeChunk];
+        uint32_t filt[kShapeChunk][4];
+        float mat[kShapeChunk][3];
 #pragma unroll
         for (int k = 0; k < kShapeChunk; k++) {
             int s = s0 + k;
             if (s >= ns) continue;
+#pragma unroll
+            for (int f = 0; f < 4; f++) filt[k][f] = ldu(L.w, sw(L, s, S_CATEGORY + f));
+            mat[k][0] = ldf(L.w, sw(L, s, S_FRICTION));
+            mat[k][1] = ldf(L.w, sw(L, s, S_RESTITUTION));
+            mat[k][2] = ldf(L.w, sw(L, s, S_ROLLING));
             bpos[k] = ld3(L.w, bw(L, b[k], B_POSITION));
             brot[k] = ldq(L.w, bw(L, b[k], B_ROTATION));
             center[k] = ld3(L.w, bw(L, b[k], B_CENTER));
@@ -469,6 +607,11 @@ B3D_FN void shape_pass(const Lane& L, int ns, float* bounds) {
             sti(r, SS_BODY, b[k]);
             sti(r, SS_BFLAGS, (btype[k] == kStatic ? kBodyStatic : 0) | (btype[k] == kDynamic ? kBodyDynamic : 0));
             st3(r, SS_CENTER, center[k]);
+#pragma unroll
+            for (int f = 0; f < 4; f++) sti(r, SS_CATEGORY + f, (int)filt[k][f]);
+            stf(r, SS_FRICTION, mat[k][0]);
+            stf(r, SS_RESTITUTION, mat[k][1]);
+            stf(r, SS_ROLLING, mat[k][2]);
             float* bd = bounds + s * 6 * kLanes;
             V3 l = sub(lo, pad), h = add(hi, pad);
             bd[0] = l.x;
@@ -562,89 +705,127 @@ struct NewContact {
     V3 roll;
 };
 
-/* Take the impulses of old record k for the points whose feature matches
- * (08_contacts.inl:154-170; the last matching old point wins). */
-B3D_FN void warm_from_old(const Lane& L, int k, NewContact* nc) {
-    const uint32_t* o = old_rec(L, k);
-    int opc = ldi(o, O_POINT_COUNT);
-    uint32_t of[kMaxManifold];
-    float oi[kMaxManifold];
-#pragma unroll
-    for (int q = 0; q < kMaxManifold; q++) {
-        of[q] = ldu(o, O_FEATURE + q);
-        oi[q] = ldf(o, O_NORMAL_IMPULSE + q);
-    }
-#pragma unroll
-    for (int p = 0; p < kMaxManifold; p++) {
-        if (p >= nc->count) continue;
-#pragma unroll
-        for (int q = 0; q < kMaxManifold; q++)
-            if (q < opc && nc->feature[p] == of[q]) nc->ni[p] = oi[q];
-    }
-    nc->fi.x = ldf(o, O_FRICTION_IMPULSE);
-    nc->fi.y = ldf(o, O_FRICTION_IMPULSE + 1);
-    nc->twist = ldf(o, O_TWIST_IMPULSE);
-    nc->roll = ld3(o, O_ROLLING_IMPULSE);
-}
-
-B3D_FN int pair_less(int a0, int b0, int a1, int b1) { return a0 < a1 || (a0 == a1 && b0 < b1); }
-
 B3D_FN bool overlaps(const float* bi, const float* bj) {
     return bi[0] <= bj[3 * kLanes] && bi[3 * kLanes] >= bj[0] && bi[kLanes] <= bj[4 * kLanes]
         && bi[4 * kLanes] >= bj[kLanes] && bi[2 * kLanes] <= bj[5 * kLanes] && bi[5 * kLanes] >= bj[2 * kLanes];
 }
 
+/* The pair loop's view of one shape (its per-step shape record). */
+struct PairShape {
+    Posed P;
+    V3 center;
+    int body, bflags;
+    uint64_t cat, mask;
+    float friction, restitution, rolling;
+};
+B3D_FN void pshape_load(const Lane& L, int s, PairShape* d) {
+    const uint32_t* r = shape_rec(L, s);
+    d->P = posed_from(r);
+    d->center = ld3(r, SS_CENTER);
+    d->body = ldi(r, SS_BODY);
+    d->bflags = ldi(r, SS_BFLAGS);
+    d->cat = ldu64(r, SS_CATEGORY);
+    d->mask = ldu64(r, SS_MASK);
+    d->friction = ldf(r, SS_FRICTION);
+    d->restitution = ldf(r, SS_RESTITUTION);
+    d->rolling = ldf(r, SS_ROLLING);
+}
+
+/* One old contact's warm-start data (the reference's B3Warm). */
+struct OldWarm {
+    uint32_t key;
+    int pc;
+    uint32_t feat[kMaxManifold];
+    float ni[kMaxManifold];
+    V2 fi;
+    float twist;
+    V3 roll;
+};
+B3D_FN void old_load(const Lane& L, int k, OldWarm* o) {
+    const uint32_t* r = old_rec(L, k);
+    o->key = ldu(r, O_KEY);
+    o->pc = ldi(r, O_POINT_COUNT);
+#pragma unroll
+    for (int q = 0; q < kMaxManifold; q++) {
+        o->feat[q] = ldu(r, O_FEATURE + q);
+        o->ni[q] = ldf(r, O_NORMAL_IMPULSE + q);
+    }
+    o->fi.x = ldf(r, O_FRICTION_IMPULSE);
+    o->fi.y = ldf(r, O_FRICTION_IMPULSE + 1);
+    o->twist = ldf(r, O_TWIST_IMPULSE);
+    o->roll = ld3(r, O_ROLLING_IMPULSE);
+}
+/* The impulses of an old contact for the points whose feature matches
+ * (08_contacts.inl:154-170; the last matching old point wins). */
+B3D_FN void warm_apply(const OldWarm& o, NewContact* nc) {
+#pragma unroll
+    for (int p = 0; p < kMaxManifold; p++) {
+        if (p >= nc->count) continue;
+#pragma unroll
+        for (int q = 0; q < kMaxManifold; q++)
+            if (q < o.pc && nc->feature[p] == o.feat[q]) nc->ni[p] = o.ni[q];
+    }
+    nc->fi = o.fi;
+    nc->twist = o.twist;
+    nc->roll = o.roll;
+}
+
 /* The ordered pair loop of b3_find_contacts (08_contacts.inl:115-172):
  * broadphase filter (08:45-62), narrowphase, overflow accounting, warm
  * start and b3_contact_from_mani (08:5-39).  `bounds` holds the padded
- * shape bounds (LDS or scratch). */
+ * shape bounds (LDS or scratch).
+ *
+ * First the bounds test of every pair i < j lists the overlapping pairs in
+ * (i, j) order in scratch; then the list is walked with the next pair's
+ * shape records in flight while the current pair is tested and collided.
+ * When the old contact list is strictly sorted (every list the step writes
+ * is), the warm-start lookup is a merge whose next old record is loaded as
+ * soon as the previous one is consumed. */
 B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int old_n, int sorted) {
     const Geometry& g = L.g;
+    uint32_t* cand = L.scr + g.scr_cand * kLanes;
+    int ncand = 0;
+    for (int i = 0; i < ns; i++) {
+        const float* bi = bounds + i * 6 * kLanes;
+        for (int j = i + 1; j < ns; j++) {
+            if (!overlaps(bi, bounds + j * 6 * kLanes)) continue;
+            sti(cand, ncand, (int)shape_key(i, j));
+            ncand++;
+        }
+    }
     int cc = 0;
     int overflow = ldi(L.w, H_CONTACT_OVERFLOW);
     int dropped = ldi(L.w, H_CONTACTS_DROPPED);
     int optr = 0;
-    for (int i = 0; i < ns; i++) {
-        const float* bi = bounds + i * 6 * kLanes;
-        const uint32_t* ri = shape_rec(L, i);
-        int body_i = ldi(ri, SS_BODY);
-        int bf_i = ldi(ri, SS_BFLAGS);
-        uint64_t cat_i = ldu64(L.w, sw(L, i, S_CATEGORY));
-        uint64_t mask_i = ldu64(L.w, sw(L, i, S_MASK));
-        Posed A = posed_from(ri);
-        V3 ca = ld3(ri, SS_CENTER);
-        float fa = ldf(L.w, sw(L, i, S_FRICTION));
-        float ea = ldf(L.w, sw(L, i, S_RESTITUTION));
-        float rla = ldf(L.w, sw(L, i, S_ROLLING));
-        for (int j = i + 1; j < ns; j++) {
-            if (!overlaps(bi, bounds + j * 6 * kLanes)) continue;
-            /* everything the pair needs, requested at once */
-            const uint32_t* rj = shape_rec(L, j);
-            int body_j = ldi(rj, SS_BODY);
-            int bf_j = ldi(rj, SS_BFLAGS);
-            uint64_t cat_j = ldu64(L.w, sw(L, j, S_CATEGORY));
-            uint64_t mask_j = ldu64(L.w, sw(L, j, S_MASK));
-            Posed B = posed_from(rj);
-            V3 cb = ld3(rj, SS_CENTER);
-            float fb = ldf(L.w, sw(L, j, S_FRICTION));
-            float eb = ldf(L.w, sw(L, j, S_RESTITUTION));
-            float rlb = ldf(L.w, sw(L, j, S_ROLLING));
-            if (body_i == body_j) continue;
-            if (bf_i & bf_j & kBodyStatic) continue;
-            if ((cat_i & mask_j) == 0 || (cat_j & mask_i) == 0) continue;
-            uint32_t key = pair_key(body_i, body_j);
-            int joined = 0;
-            for (int k = 0; k < nj; k++) joined |= ldu(joint_rec(L, k), JS_KEY) == key;
-            if (joined) continue;
-
-            Mani m;
-            collide_pair(&m, A, B, L.vel);
-            if (m.count == 0) continue;
-            if (cc >= g.max_c) {
-                overflow = 1;
-                dropped++;
-                continue;
-            }
+    OldWarm orec;
+    if (sorted && old_n > 0) old_load(L, 0, &orec);
+    PairShape A, B, An, Bn;
+    uint32_t key = 0, key1 = 0;
+    if (ncand > 0) {
+        key = ldu(cand, 0);
+        pshape_load(L, (int)(key >> 16), &A);
+        pshape_load(L, (int)(key & 0xffffu), &B);
+    }
+    if (ncand > 1) key1 = ldu(cand, 1);
+    for (int t = 0; t < ncand; t++) {
+        uint32_t key2 = t + 2 < ncand ? ldu(cand, t + 2) : 0u;
+        if (t + 1 < ncand) {
+            if ((key1 >> 16) != (key >> 16)) pshape_load(L, (int)(key1 >> 16), &An);
+            else An = A;
+            pshape_load(L, (int)(key1 & 0xffffu), &Bn);
+        }
+        int i = (int)(key >> 16), j = (int)(key & 0xffffu);
+        int joined = 0;
+        for (int k = 0; k < nj; k++) joined |= ldu(joint_rec(L, k), JS_KEY) == pair_key(A.body, B.body);
+        bool skip = A.body == B.body || (A.bflags & B.bflags & kBodyStatic) || (A.cat & B.mask) == 0
+            || (B.cat & A.mask) == 0 || joined;
+        Mani m;
+        m.count = 0;
+        if (!skip) collide_pair(&m, A.P, B.P, L.vel);
+        if (m.count > 0 && cc >= g.max_c) {
+            overflow = 1;
+            dropped++;
+        } else if (m.count > 0) {
             NewContact nc;
             nc.count = m.count;
             nc.normal = m.normal;
@@ -653,8 +834,8 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
                 if (p >= m.count) continue;
-                nc.r_a[p] = sub(m.p_a[p], ca);
-                nc.r_b[p] = sub(m.p_b[p], cb);
+                nc.r_a[p] = sub(m.p_a[p], A.center);
+                nc.r_b[p] = sub(m.p_b[p], B.center);
                 nc.base_sep[p] = m.sep[p] - dot(sub(nc.r_b[p], nc.r_a[p]), m.normal);
                 nc.feature[p] = m.feature[p];
                 nc.ni[p] = 0.0f;
@@ -664,27 +845,34 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
             nc.roll = zero3();
             /* warm start from the previous step's cache: every matching old
              * pair, the last one winning (08:154-170) */
+            uint32_t want = shape_key(i, j);
             if (sorted) {
-                uint32_t want = shape_key(i, j);
-                uint32_t have = optr < old_n ? ldu(old_rec(L, optr), O_KEY) : 0xffffffffu;
-                while (optr < old_n && have < want) {
+                while (optr < old_n && orec.key < want) {
                     optr++;
-                    have = optr < old_n ? ldu(old_rec(L, optr), O_KEY) : 0xffffffffu;
+                    if (optr < old_n) old_load(L, optr, &orec);
                 }
-                if (optr < old_n && have == want) warm_from_old(L, optr, &nc);
+                if (optr < old_n && orec.key == want) {
+                    warm_apply(orec, &nc);
+                    optr++;
+                    if (optr < old_n) old_load(L, optr, &orec);
+                }
             } else {
                 for (int k = 0; k < old_n; k++) {
                     const uint32_t* o = old_rec(L, k);
-                    if (ldi(o, O_SHAPE_A) == i && ldi(o, O_SHAPE_B) == j) warm_from_old(L, k, &nc);
+                    if (ldi(o, O_SHAPE_A) == i && ldi(o, O_SHAPE_B) == j) {
+                        OldWarm ow;
+                        old_load(L, k, &ow);
+                        warm_apply(ow, &nc);
+                    }
                 }
             }
             uint32_t* w = L.w;
             sti(w, cw(L, cc, C_SHAPE_A), i);
             sti(w, cw(L, cc, C_SHAPE_B), j);
-            sti(w, cw(L, cc, C_BODY_A), body_i);
-            sti(w, cw(L, cc, C_BODY_B), body_j);
+            sti(w, cw(L, cc, C_BODY_A), A.body);
+            sti(w, cw(L, cc, C_BODY_B), B.body);
             sti(w, cw(L, cc, C_POINT_COUNT), nc.count);
-            sti(w, cw(L, cc, C_STATIC), !((bf_i & bf_j) & kBodyDynamic));
+            sti(w, cw(L, cc, C_STATIC), !((A.bflags & B.bflags) & kBodyDynamic));
             st3(w, cw(L, cc, C_NORMAL), nc.normal);
             st3(w, cw(L, cc, C_TANGENT1), nc.t1);
             st3(w, cw(L, cc, C_TANGENT2), nc.t2);
@@ -697,16 +885,16 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
                 stf(w, pw(L, cc, p, P_NORMAL_IMPULSE), nc.ni[p]);
                 sti(w, pw(L, cc, p, P_FEATURE), (int)nc.feature[p]);
             }
-            float restitution = ea > eb ? ea : eb;
-            float rolling = maxf(rla, rlb);
-            stf(w, cw(L, cc, C_FRICTION), sqrtf(fa * fb));
+            float restitution = A.restitution > B.restitution ? A.restitution : B.restitution;
+            float rolling = maxf(A.rolling, B.rolling);
+            stf(w, cw(L, cc, C_FRICTION), sqrtf(A.friction * B.friction));
             stf(w, cw(L, cc, C_RESTITUTION), restitution);
             stf(w, cw(L, cc, C_ROLLING), rolling);
-            int info = (bf_i & kBodyDynamic ? CF_DYN_A : 0) | (bf_j & kBodyDynamic ? CF_DYN_B : 0)
-                | (!((bf_i & bf_j) & kBodyDynamic) ? CF_STATIC : 0) | (restitution != 0.0f ? CF_RESTITUTION : 0)
+            int info = (A.bflags & kBodyDynamic ? CF_DYN_A : 0) | (B.bflags & kBodyDynamic ? CF_DYN_B : 0)
+                | (!((A.bflags & B.bflags) & kBodyDynamic) ? CF_STATIC : 0) | (restitution != 0.0f ? CF_RESTITUTION : 0)
                 | (!(rolling <= 0.0f) ? CF_ROLLING : 0);
             uint32_t* hd = chead_rec(L, cc);
-            sti(hd, CH_AB, body_i | (body_j << 16));
+            sti(hd, CH_AB, A.body | (B.body << 16));
             sti(hd, CH_INFO, nc.count | (info << 8));
             stf(w, cw(L, cc, C_TWIST_IMPULSE), nc.twist);
             stf(w, cw(L, cc, C_FRICTION_IMPULSE), nc.fi.x);
@@ -714,6 +902,10 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
             st3(w, cw(L, cc, C_ROLLING_IMPULSE), nc.roll);
             cc++;
         }
+        A = An;
+        B = Bn;
+        key = key1;
+        key1 = key2;
     }
     sti(L.w, H_CONTACT_COUNT, cc);
     sti(L.w, H_CONTACT_OVERFLOW, overflow);
@@ -747,18 +939,23 @@ B3D_FN void find_contacts(const Lane& L) {
 }
 
 /* b3_prepare_one_contact (08:234-291) for every new contact, two contacts
- * at a time: their heads, then their bodies and points, then the math. */
+ * at a time: their heads, then their bodies and points, then the math.  The
+ * prepared fields go to the world's contact rows and, with everything else
+ * the solver reads, to the contact's packed record, whose point separations
+ * start at the step's initial delta poses. */
 constexpr int kPrepChunk = 2;
 B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
     uint32_t* w = L.w;
     int cc = ldi(w, H_CONTACT_COUNT);
     const float inv_tau = 1.0f / kSpeculative;
     for (int c0 = 0; c0 < cc; c0 += kPrepChunk) {
-        int a[kPrepChunk], b[kPrepChunk], pc[kPrepChunk], fl[kPrepChunk];
+        int a[kPrepChunk], b[kPrepChunk], pc[kPrepChunk], fl[kPrepChunk], slot[kPrepChunk];
+        int pslot[kPrepChunk][kMaxManifold];
 #pragma unroll
         for (int k = 0; k < kPrepChunk; k++) {
             int c = c0 + k;
             if (c >= cc) continue;
+            slot[k] = wave_slot(L);
             CHead hd = chead_load(L, c);
             a[k] = hd.a;
             b[k] = hd.b;
@@ -767,7 +964,8 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
         }
         float ima[kPrepChunk], imb[kPrepChunk];
         M3 iwa[kPrepChunk], iwb[kPrepChunk];
-        V3 n[kPrepChunk], t1[kPrepChunk], t2[kPrepChunk], ra[kPrepChunk][kMaxManifold], rb[kPrepChunk][kMaxManifold];
+        V3 n[kPrepChunk], t1[kPrepChunk], ra[kPrepChunk][kMaxManifold], rb[kPrepChunk][kMaxManifold], dp[kPrepChunk];
+        Q dqa[kPrepChunk], dqb[kPrepChunk];
         float bs[kPrepChunk][kMaxManifold];
 #pragma unroll
         for (int k = 0; k < kPrepChunk; k++) {
@@ -785,12 +983,15 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
                 imb[k] = ldf(w, bw(L, b[k], B_INV_MASS));
                 iwb[k] = ldm3(w, bw(L, b[k], B_INV_I_WORLD));
             }
+            dqa[k] = ldq(w, bw(L, a[k], B_DELTA_ROT));
+            dqb[k] = ldq(w, bw(L, b[k], B_DELTA_ROT));
+            dp[k] = sub(ld3(w, bw(L, b[k], B_DELTA_POS)), ld3(w, bw(L, a[k], B_DELTA_POS)));
             n[k] = ld3(w, cw(L, c, C_NORMAL));
             t1[k] = ld3(w, cw(L, c, C_TANGENT1));
-            t2[k] = ld3(w, cw(L, c, C_TANGENT2));
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
                 if (p >= pc[k]) continue;
+                pslot[k][p] = wave_slot(L);
                 ra[k][p] = ld3(w, pw(L, c, p, P_R_A));
                 rb[k][p] = ld3(w, pw(L, c, p, P_R_B));
                 bs[k][p] = ldf(w, pw(L, c, p, P_BASE_SEP));
@@ -800,41 +1001,61 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
         for (int k = 0; k < kPrepChunk; k++) {
             int c = c0 + k;
             if (c >= cc) continue;
+            uint32_t* r = crec(L, c, slot[k]);
             /* zero unless the body is dynamic (08:236-241) */
             float ma = ima[k], mb = imb[k];
             M3 ia = iwa[k], ib = iwb[k];
             V3 va = vlin(L, a[k]), wa = vang(L, a[k]);
             V3 vb = vlin(L, b[k]), wb = vang(L, b[k]);
+            /* tangent2 = tangent1 x normal as written by b3_contact_from_mani */
+            V3 t2 = cross(t1[k], n[k]);
             V3 center_a = zero3(), center_b = zero3();
             float wsum = 0.0f;
+            float rel_vel[kMaxManifold];
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
                 if (p >= pc[k]) continue;
+                uint32_t* pr = prec(L, c, p, pslot[k][p]);
                 V3 rap = ra[k][p], rbp = rb[k][p];
                 V3 rn_a = cross(rap, n[k]);
                 V3 rn_b = cross(rbp, n[k]);
                 float kn = ma + mb + dot(rn_a, mv(ia, rn_a)) + dot(rn_b, mv(ib, rn_b));
-                stf(w, pw(L, c, p, P_NORMAL_MASS), kn > 0.0f ? 1.0f / kn : 0.0f);
+                float nmass = kn > 0.0f ? 1.0f / kn : 0.0f;
+                stf(w, pw(L, c, p, P_NORMAL_MASS), nmass);
                 V3 vra = add(va, cross(wa, rap));
                 V3 vrb = add(vb, cross(wb, rbp));
-                stf(w, pw(L, c, p, P_REL_VEL), dot(n[k], sub(vrb, vra)));
-                stf(w, pw(L, c, p, P_TOTAL_NORMAL), 0.0f);
+                rel_vel[p] = dot(n[k], sub(vrb, vra));
+                stf(w, pw(L, c, p, P_REL_VEL), rel_vel[p]);
                 float sep = bs[k][p] + dot(sub(rbp, rap), n[k]);
                 float weight = clampf(2.0f - sep * inv_tau, kMinFrictionW, 1.0f);
                 center_a = madd(center_a, weight, rap);
                 center_b = madd(center_b, weight, rbp);
                 wsum += weight;
+                /* the solver's separation at the initial delta poses (the
+                 * reference's per-row form, 08_contacts.inl:331-333) */
+                V3 ds = add(dp[k], sub(rot(dqb[k], rbp), rot(dqa[k], rap)));
+                qs3(pr, PR_RA, rap);
+                qsf(pr, PR_NMASS, nmass);
+                qs3(pr, PR_RB, rbp);
+                qsf(pr, PR_BASE_SEP, bs[k][p]);
+                qsf(pr, PR_NI, ldf(w, pw(L, c, p, P_NORMAL_IMPULSE)));
+                qsf(pr, PR_TN, 0.0f);
+                qsf(pr, PR_SEP, dot(ds, n[k]) + bs[k][p]);
             }
             float invw = wsum > 0.0f ? 1.0f / wsum : 0.0f;
             center_a = scale(center_a, invw);
             center_b = scale(center_b, invw);
 #pragma unroll
-            for (int p = 0; p < kMaxManifold; p++)
-                if (p < pc[k]) stf(w, pw(L, c, p, P_LEVER), len(sub(ra[k][p], center_a)));
+            for (int p = 0; p < kMaxManifold; p++) {
+                if (p >= pc[k]) continue;
+                float lever = len(sub(ra[k][p], center_a));
+                stf(w, pw(L, c, p, P_LEVER), lever);
+                qsf(prec(L, c, p, pslot[k][p]), PR_LEVER, lever);
+            }
             V3 rt_a1 = cross(center_a, t1[k]);
-            V3 rt_a2 = cross(center_a, t2[k]);
+            V3 rt_a2 = cross(center_a, t2);
             V3 rt_b1 = cross(center_b, t1[k]);
-            V3 rt_b2 = cross(center_b, t2[k]);
+            V3 rt_b2 = cross(center_b, t2);
             M2 k2;
             k2.cx.x = ma + mb + dot(rt_a1, mv(ia, rt_a1)) + dot(rt_b1, mv(ib, rt_b1));
             k2.cy.y = ma + mb + dot(rt_a2, mv(ia, rt_a2)) + dot(rt_b2, mv(ib, rt_b2));
@@ -843,9 +1064,10 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
             M2 tmass = inv2(k2);
             M3 isum = madd3(ia, ib);
             float kt = dot(n[k], mv(isum, n[k]));
+            float twist_mass = kt > 0.0f ? 1.0f / kt : 0.0f;
             st3(w, cw(L, c, C_CENTER_A), center_a);
             st3(w, cw(L, c, C_CENTER_B), center_b);
-            stf(w, cw(L, c, C_TWIST_MASS), kt > 0.0f ? 1.0f / kt : 0.0f);
+            stf(w, cw(L, c, C_TWIST_MASS), twist_mass);
             stf(w, cw(L, c, C_TANGENT_MASS), tmass.cx.x);
             stf(w, cw(L, c, C_TANGENT_MASS + 1), tmass.cx.y);
             stf(w, cw(L, c, C_TANGENT_MASS + 2), tmass.cy.x);
@@ -856,6 +1078,30 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
             stm3(w, cw(L, c, C_INV_I_A), ia);
             stm3(w, cw(L, c, C_INV_I_B), ib);
             stsoft(w, cw(L, c, C_SOFTNESS), (fl[k] & CF_STATIC) ? ss : cs);
+            /* the packed record */
+            qsu(r, R_AB, (uint32_t)(a[k] | (b[k] << 16)));
+            qsu(r, R_INFO, (uint32_t)(pc[k] | (fl[k] << 8)));
+            qsf(r, R_FRICTION, ldf(w, cw(L, c, C_FRICTION)));
+            qsf(r, R_TWIST_MASS, twist_mass);
+            qs3(r, R_N, n[k]);
+            qsf(r, R_ROLLING, ldf(w, cw(L, c, C_ROLLING)));
+            rec_store_masses(r, fl[k], ma, ia, mb, ib);
+            qs3(r, R_T1, t1[k]);
+            qsf(r, R_TM_XX, tmass.cx.x);
+            qs3(r, R_CA, center_a);
+            qsf(r, R_TM_XY, tmass.cx.y);
+            qs3(r, R_CB, center_b);
+            qsf(r, R_TM_YY, tmass.cy.y);
+            qsf(r, R_FI, ldf(w, cw(L, c, C_FRICTION_IMPULSE)));
+            qsf(r, R_FI + 1, ldf(w, cw(L, c, C_FRICTION_IMPULSE + 1)));
+            qsf(r, R_TWIST, ldf(w, cw(L, c, C_TWIST_IMPULSE)));
+            qsf(r, R_RESTITUTION, ldf(w, cw(L, c, C_RESTITUTION)));
+            qs3(r, R_ROLL, ld3(w, cw(L, c, C_ROLLING_IMPULSE)));
+            if (fl[k] & CF_RESTITUTION) {
+#pragma unroll
+                for (int p = 0; p < kMaxManifold; p++)
+                    if (p < pc[k]) qsf(r, R_REL_VEL + p, rel_vel[p]);
+            }
         }
     }
 }
@@ -865,53 +1111,102 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
 B3D_FN void prepare_joints(const Lane& L, float h) {
     int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
     uint32_t* w = L.w;
-    for (int i = 0; i < nj; i++) {
-        int a = ldi(w, jw(L, i, J_BODY_A)), b = ldi(w, jw(L, i, J_BODY_B));
-        int ta = ldi(w, bw(L, a, B_TYPE)), tb = ldi(w, bw(L, b, B_TYPE));
-        float ma = ta == kDynamic ? ldf(w, bw(L, a, B_INV_MASS)) : 0.0f;
-        float mb = tb == kDynamic ? ldf(w, bw(L, b, B_INV_MASS)) : 0.0f;
-        M3 ia = ta == kDynamic ? ldm3(w, bw(L, a, B_INV_I_WORLD)) : m3zero();
-        M3 ib = tb == kDynamic ? ldm3(w, bw(L, b, B_INV_I_WORLD)) : m3zero();
-        stf(w, jw(L, i, J_INV_MASS_A), ma);
-        stf(w, jw(L, i, J_INV_MASS_B), mb);
-        stm3(w, jw(L, i, J_INV_I_A), ia);
-        stm3(w, jw(L, i, J_INV_I_B), ib);
-        M3 isum = madd3(ia, ib);
-        int fixed = dot(isum.cx, cross(isum.cy, isum.cz)) < 1.0e-20f;
-        sti(w, jw(L, i, J_FIXED_ROTATION), fixed);
-        int jtype = ldi(w, jw(L, i, J_TYPE));
-        int info = (jtype == kJointWeld ? JF_WELD : 0) | (fixed ? JF_FIXED : 0)
-            | (ldi(w, jw(L, i, J_ENABLE_SPRING)) ? JF_SPRING : 0) | (ldi(w, jw(L, i, J_ENABLE_MOTOR)) ? JF_MOTOR : 0)
-            | (ldi(w, jw(L, i, J_ENABLE_LIMIT)) ? JF_LIMIT : 0) | (ta == kDynamic ? JF_DYN_A : 0)
-            | (tb == kDynamic ? JF_DYN_B : 0);
-        sti(joint_rec(L, i), JS_AB, a | (b << 16));
-        sti(joint_rec(L, i), JS_INFO, info);
-        Soft soft = make_soft(ldf(w, jw(L, i, J_CONSTRAINT_HERTZ)), ldf(w, jw(L, i, J_CONSTRAINT_DAMPING)), h);
-        stsoft(w, jw(L, i, J_SOFTNESS), soft);
-        Q rot_a = ldq(w, bw(L, a, B_ROTATION)), rot_b = ldq(w, bw(L, b, B_ROTATION));
-        Q fqa = qmul(rot_a, ldq(w, jw(L, i, J_LOCAL_ROT_A)));
-        Q fqb = qmul(rot_b, ldq(w, jw(L, i, J_LOCAL_ROT_B)));
-        stq(w, jw(L, i, J_FRAME_Q_A), fqa);
-        stq(w, jw(L, i, J_FRAME_Q_B), fqb);
-        st3(w, jw(L, i, J_FRAME_P_A), rot(rot_a, sub(ld3(w, jw(L, i, J_LOCAL_ANCHOR_A)), ld3(w, bw(L, a, B_LOCAL_CENTER)))));
-        st3(w, jw(L, i, J_FRAME_P_B), rot(rot_b, sub(ld3(w, jw(L, i, J_LOCAL_ANCHOR_B)), ld3(w, bw(L, b, B_LOCAL_CENTER)))));
-        st3(w, jw(L, i, J_DELTA_CENTER), sub(ld3(w, bw(L, b, B_CENTER)), ld3(w, bw(L, a, B_CENTER))));
-        if (jtype == kJointWeld) {
-            stm3(w, jw(L, i, J_ANGULAR_MASS), inv3(isum));
-            float lh = ldf(w, jw(L, i, J_LINEAR_HERTZ)), ah = ldf(w, jw(L, i, J_ANGULAR_HERTZ));
-            stsoft(w, jw(L, i, J_LINEAR_SPRING), lh == 0.0f ? soft : make_soft(lh, ldf(w, jw(L, i, J_LINEAR_DAMPING)), h));
-            stsoft(w, jw(L, i, J_ANGULAR_SPRING), ah == 0.0f ? soft : make_soft(ah, ldf(w, jw(L, i, J_ANGULAR_DAMPING)), h));
-        } else {
-            V3 axis = rot(fqa, v3(0.0f, 0.0f, 1.0f));
-            float k = dot(axis, mv(isum, axis));
-            stf(w, jw(L, i, J_AXIAL_MASS), k > 0.0f ? 1.0f / k : 0.0f);
-            st3(w, jw(L, i, J_ROTATION_AXIS), axis);
-            Q rel = qinv_mul(fqa, fqb);
-            V3 px, py;
-            hinge_perps(fqa, rel, &px, &py);
-            st3(w, jw(L, i, J_PERP_X), px);
-            st3(w, jw(L, i, J_PERP_Y), py);
-            stsoft(w, jw(L, i, J_SPRING_SOFTNESS), make_soft(ldf(w, jw(L, i, J_HERTZ)), ldf(w, jw(L, i, J_DAMPING_RATIO)), h));
+    for (int j0 = 0; j0 < nj; j0 += kPrepChunk) {
+        /* the joints' own fields, then (through their body indices) the bodies' */
+        int a[kPrepChunk], b[kPrepChunk], jtype[kPrepChunk], en[kPrepChunk];
+        float chz[kPrepChunk], cdr[kPrepChunk], lh[kPrepChunk], ld[kPrepChunk], ah[kPrepChunk], ad[kPrepChunk];
+        float hz[kPrepChunk], dr[kPrepChunk];
+        Q lra[kPrepChunk], lrb[kPrepChunk];
+        V3 laa[kPrepChunk], lab[kPrepChunk];
+#pragma unroll
+        for (int k = 0; k < kPrepChunk; k++) {
+            int i = j0 + k;
+            if (i >= nj) continue;
+            a[k] = ldi(w, jw(L, i, J_BODY_A));
+            b[k] = ldi(w, jw(L, i, J_BODY_B));
+            jtype[k] = ldi(w, jw(L, i, J_TYPE));
+            en[k] = (ldi(w, jw(L, i, J_ENABLE_SPRING)) ? JF_SPRING : 0) | (ldi(w, jw(L, i, J_ENABLE_MOTOR)) ? JF_MOTOR : 0)
+                | (ldi(w, jw(L, i, J_ENABLE_LIMIT)) ? JF_LIMIT : 0);
+            chz[k] = ldf(w, jw(L, i, J_CONSTRAINT_HERTZ));
+            cdr[k] = ldf(w, jw(L, i, J_CONSTRAINT_DAMPING));
+            lra[k] = ldq(w, jw(L, i, J_LOCAL_ROT_A));
+            lrb[k] = ldq(w, jw(L, i, J_LOCAL_ROT_B));
+            laa[k] = ld3(w, jw(L, i, J_LOCAL_ANCHOR_A));
+            lab[k] = ld3(w, jw(L, i, J_LOCAL_ANCHOR_B));
+            lh[k] = ldf(w, jw(L, i, J_LINEAR_HERTZ));
+            ld[k] = ldf(w, jw(L, i, J_LINEAR_DAMPING));
+            ah[k] = ldf(w, jw(L, i, J_ANGULAR_HERTZ));
+            ad[k] = ldf(w, jw(L, i, J_ANGULAR_DAMPING));
+            hz[k] = ldf(w, jw(L, i, J_HERTZ));
+            dr[k] = ldf(w, jw(L, i, J_DAMPING_RATIO));
+        }
+        int ta[kPrepChunk], tb[kPrepChunk];
+        float ima[kPrepChunk], imb[kPrepChunk];
+        M3 iwa[kPrepChunk], iwb[kPrepChunk];
+        Q rot_a[kPrepChunk], rot_b[kPrepChunk];
+        V3 lca[kPrepChunk], lcb[kPrepChunk], cen_a[kPrepChunk], cen_b[kPrepChunk];
+#pragma unroll
+        for (int k = 0; k < kPrepChunk; k++) {
+            int i = j0 + k;
+            if (i >= nj) continue;
+            ta[k] = ldi(w, bw(L, a[k], B_TYPE));
+            tb[k] = ldi(w, bw(L, b[k], B_TYPE));
+            ima[k] = ldf(w, bw(L, a[k], B_INV_MASS));
+            imb[k] = ldf(w, bw(L, b[k], B_INV_MASS));
+            iwa[k] = ldm3(w, bw(L, a[k], B_INV_I_WORLD));
+            iwb[k] = ldm3(w, bw(L, b[k], B_INV_I_WORLD));
+            rot_a[k] = ldq(w, bw(L, a[k], B_ROTATION));
+            rot_b[k] = ldq(w, bw(L, b[k], B_ROTATION));
+            lca[k] = ld3(w, bw(L, a[k], B_LOCAL_CENTER));
+            lcb[k] = ld3(w, bw(L, b[k], B_LOCAL_CENTER));
+            cen_a[k] = ld3(w, bw(L, a[k], B_CENTER));
+            cen_b[k] = ld3(w, bw(L, b[k], B_CENTER));
+        }
+#pragma unroll
+        for (int k = 0; k < kPrepChunk; k++) {
+            int i = j0 + k;
+            if (i >= nj) continue;
+            /* zero unless the body is dynamic */
+            float ma = ta[k] == kDynamic ? ima[k] : 0.0f;
+            float mb = tb[k] == kDynamic ? imb[k] : 0.0f;
+            M3 ia = ta[k] == kDynamic ? iwa[k] : m3zero();
+            M3 ib = tb[k] == kDynamic ? iwb[k] : m3zero();
+            stf(w, jw(L, i, J_INV_MASS_A), ma);
+            stf(w, jw(L, i, J_INV_MASS_B), mb);
+            stm3(w, jw(L, i, J_INV_I_A), ia);
+            stm3(w, jw(L, i, J_INV_I_B), ib);
+            M3 isum = madd3(ia, ib);
+            int fixed = dot(isum.cx, cross(isum.cy, isum.cz)) < 1.0e-20f;
+            sti(w, jw(L, i, J_FIXED_ROTATION), fixed);
+            int info = (jtype[k] == kJointWeld ? JF_WELD : 0) | (fixed ? JF_FIXED : 0) | en[k]
+                | (ta[k] == kDynamic ? JF_DYN_A : 0) | (tb[k] == kDynamic ? JF_DYN_B : 0);
+            sti(joint_rec(L, i), JS_AB, a[k] | (b[k] << 16));
+            sti(joint_rec(L, i), JS_INFO, info);
+            Soft soft = make_soft(chz[k], cdr[k], h);
+            stsoft(w, jw(L, i, J_SOFTNESS), soft);
+            Q fqa = qmul(rot_a[k], lra[k]);
+            Q fqb = qmul(rot_b[k], lrb[k]);
+            stq(w, jw(L, i, J_FRAME_Q_A), fqa);
+            stq(w, jw(L, i, J_FRAME_Q_B), fqb);
+            st3(w, jw(L, i, J_FRAME_P_A), rot(rot_a[k], sub(laa[k], lca[k])));
+            st3(w, jw(L, i, J_FRAME_P_B), rot(rot_b[k], sub(lab[k], lcb[k])));
+            st3(w, jw(L, i, J_DELTA_CENTER), sub(cen_b[k], cen_a[k]));
+            if (jtype[k] == kJointWeld) {
+                stm3(w, jw(L, i, J_ANGULAR_MASS), inv3(isum));
+                stsoft(w, jw(L, i, J_LINEAR_SPRING), lh[k] == 0.0f ? soft : make_soft(lh[k], ld[k], h));
+                stsoft(w, jw(L, i, J_ANGULAR_SPRING), ah[k] == 0.0f ? soft : make_soft(ah[k], ad[k], h));
+            } else {
+                V3 axis = rot(fqa, v3(0.0f, 0.0f, 1.0f));
+                float kk = dot(axis, mv(isum, axis));
+                stf(w, jw(L, i, J_AXIAL_MASS), kk > 0.0f ? 1.0f / kk : 0.0f);
+                st3(w, jw(L, i, J_ROTATION_AXIS), axis);
+                Q rel = qinv_mul(fqa, fqb);
+                V3 px, py;
+                hinge_perps(fqa, rel, &px, &py);
+                st3(w, jw(L, i, J_PERP_X), px);
+                st3(w, jw(L, i, J_PERP_Y), py);
+                stsoft(w, jw(L, i, J_SPRING_SOFTNESS), make_soft(hz[k], dr[k], h));
+            }
         }
     }
 }
@@ -924,77 +1219,64 @@ B3D_FN void apply_impulse(const Lane& L, int b, float m, M3 i, V3 r, V3 p, float
 }
 
 /* b3_warm_start over contacts (08:194-232, 293-313), two contacts at a
- * time: heads, then rows, then the impulses in contact order. */
+ * time: heads, then records, then the impulses in contact order. */
 B3D_FN void warm_start_contacts(const Lane& L) {
     int cc = ldi(L.w, H_CONTACT_COUNT);
-    const uint32_t* w = L.w;
     for (int c0 = 0; c0 < cc; c0 += kPrepChunk) {
-        int a[kPrepChunk], b[kPrepChunk], pc[kPrepChunk], fl[kPrepChunk];
+        CHead hd[kPrepChunk];
 #pragma unroll
         for (int k = 0; k < kPrepChunk; k++) {
             int c = c0 + k;
             if (c >= cc) continue;
-            CHead hd = chead_load(L, c);
-            a[k] = hd.a;
-            b[k] = hd.b;
-            pc[k] = hd.pc;
-            fl[k] = hd.flags;
+            hd[k] = rhead_load(L, c);
         }
         float ma[kPrepChunk], mb[kPrepChunk], ni[kPrepChunk][kMaxManifold], tw[kPrepChunk];
         M3 ia[kPrepChunk], ib[kPrepChunk];
-        V3 n[kPrepChunk], ra[kPrepChunk][kMaxManifold], rb[kPrepChunk][kMaxManifold], t1[kPrepChunk], t2[kPrepChunk];
+        V3 n[kPrepChunk], ra[kPrepChunk][kMaxManifold], rb[kPrepChunk][kMaxManifold], t1[kPrepChunk];
         V3 ca[kPrepChunk], cb[kPrepChunk], roll[kPrepChunk];
         V2 fi[kPrepChunk];
 #pragma unroll
         for (int k = 0; k < kPrepChunk; k++) {
             int c = c0 + k;
             if (c >= cc) continue;
-            ma[k] = 0.0f;
-            mb[k] = 0.0f;
-            ia[k] = m3zero();
-            ib[k] = m3zero();
-            if (fl[k] & CF_DYN_A) {
-                ma[k] = ldf(w, cw(L, c, C_INV_MASS_A));
-                ia[k] = ldm3(w, cw(L, c, C_INV_I_A));
-            }
-            if (fl[k] & CF_DYN_B) {
-                mb[k] = ldf(w, cw(L, c, C_INV_MASS_B));
-                ib[k] = ldm3(w, cw(L, c, C_INV_I_B));
-            }
-            n[k] = ld3(w, cw(L, c, C_NORMAL));
+            const uint32_t* r = crec(L, c, hd[k].slot);
+            rec_masses(r, hd[k].flags, &ma[k], &ia[k], &mb[k], &ib[k]);
+            n[k] = q3(r, R_N);
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
-                if (p >= pc[k]) continue;
-                ni[k][p] = ldf(w, pw(L, c, p, P_NORMAL_IMPULSE));
-                ra[k][p] = ld3(w, pw(L, c, p, P_R_A));
-                rb[k][p] = ld3(w, pw(L, c, p, P_R_B));
+                if (p >= hd[k].pc) continue;
+                const uint32_t* pr = prec(L, c, p, wave_slot(L));
+                ni[k][p] = qf(pr, PR_NI);
+                ra[k][p] = q3(pr, PR_RA);
+                rb[k][p] = q3(pr, PR_RB);
             }
-            t1[k] = ld3(w, cw(L, c, C_TANGENT1));
-            t2[k] = cross(t1[k], n[k]);
-            fi[k].x = ldf(w, cw(L, c, C_FRICTION_IMPULSE));
-            fi[k].y = ldf(w, cw(L, c, C_FRICTION_IMPULSE + 1));
-            ca[k] = ld3(w, cw(L, c, C_CENTER_A));
-            cb[k] = ld3(w, cw(L, c, C_CENTER_B));
-            tw[k] = ldf(w, cw(L, c, C_TWIST_IMPULSE));
-            roll[k] = ld3(w, cw(L, c, C_ROLLING_IMPULSE));
+            t1[k] = q3(r, R_T1);
+            fi[k].x = qf(r, R_FI);
+            fi[k].y = qf(r, R_FI + 1);
+            ca[k] = q3(r, R_CA);
+            cb[k] = q3(r, R_CB);
+            tw[k] = qf(r, R_TWIST);
+            roll[k] = q3(r, R_ROLL);
         }
 #pragma unroll
         for (int k = 0; k < kPrepChunk; k++) {
             int c = c0 + k;
             if (c >= cc) continue;
+            int a = hd[k].a, b = hd[k].b;
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
-                if (p >= pc[k]) continue;
+                if (p >= hd[k].pc) continue;
                 V3 P = scale(n[k], ni[k][p]);
-                apply_impulse(L, a[k], ma[k], ia[k], ra[k][p], P, -1.0f);
-                apply_impulse(L, b[k], mb[k], ib[k], rb[k][p], P, 1.0f);
+                apply_impulse(L, a, ma[k], ia[k], ra[k][p], P, -1.0f);
+                apply_impulse(L, b, mb[k], ib[k], rb[k][p], P, 1.0f);
             }
-            V3 f = add(scale(t1[k], fi[k].x), scale(t2[k], fi[k].y));
-            apply_impulse(L, a[k], ma[k], ia[k], ca[k], f, -1.0f);
-            apply_impulse(L, b[k], mb[k], ib[k], cb[k], f, 1.0f);
+            V3 t2 = cross(t1[k], n[k]);
+            V3 f = add(scale(t1[k], fi[k].x), scale(t2, fi[k].y));
+            apply_impulse(L, a, ma[k], ia[k], ca[k], f, -1.0f);
+            apply_impulse(L, b, mb[k], ib[k], cb[k], f, 1.0f);
             V3 tr = add(scale(n[k], tw[k]), roll[k]);
-            if (is_dyn_flag(L, a[k])) set_vang(L, a[k], sub(vang(L, a[k]), mv(ia[k], tr)));
-            if (is_dyn_flag(L, b[k])) set_vang(L, b[k], add(vang(L, b[k]), mv(ib[k], tr)));
+            if (is_dyn_flag(L, a)) set_vang(L, a, sub(vang(L, a), mv(ia[k], tr)));
+            if (is_dyn_flag(L, b)) set_vang(L, b, add(vang(L, b), mv(ib[k], tr)));
         }
     }
 }
@@ -1048,52 +1330,64 @@ B3D_FN M3 point_k(float ma, float mb, M3 ia, M3 ib, V3 ra, V3 rb) {
  * reference recomputes these in every row solve (08_contacts.inl:331-333,
  * 06_joints.inl:257-282, 285-332, 436-642); computing them once per delta
  * state gives the same bits. */
-B3D_FN void delta_geometry(const Lane& L) {
-    uint32_t* w = L.w;
+B3D_FN void joint_geometry(const Lane& L);
+
+/* Point separations of the current delta poses into the packed records. */
+B3D_FN void contact_geometry(const Lane& L) {
+    const uint32_t* w = L.w;
     int cc = ldi(w, H_CONTACT_COUNT);
     for (int c0 = 0; c0 < cc; c0 += kChunk) {
-        int a[kChunk], b[kChunk], pc[kChunk];
+        CHead hd[kChunk];
 #pragma unroll
         for (int k = 0; k < kChunk; k++) {
             int c = c0 + k;
             if (c >= cc) continue;
-            CHead hd = chead_load(L, c);
-            a[k] = hd.a;
-            b[k] = hd.b;
-            pc[k] = hd.pc;
+            hd[k] = rhead_load(L, c);
         }
         V3 n[kChunk], dp[kChunk], ra[kChunk][kMaxManifold], rb[kChunk][kMaxManifold];
         Q dqa[kChunk], dqb[kChunk];
         float bs[kChunk][kMaxManifold];
+        int ps[kChunk][kMaxManifold];
 #pragma unroll
         for (int k = 0; k < kChunk; k++) {
             int c = c0 + k;
             if (c >= cc) continue;
-            n[k] = ld3(w, cw(L, c, C_NORMAL));
-            dqa[k] = ldq(w, bw(L, a[k], B_DELTA_ROT));
-            dqb[k] = ldq(w, bw(L, b[k], B_DELTA_ROT));
-            dp[k] = sub(ld3(w, bw(L, b[k], B_DELTA_POS)), ld3(w, bw(L, a[k], B_DELTA_POS)));
+            n[k] = q3(crec(L, c, hd[k].slot), R_N);
+            dqa[k] = ldq(w, bw(L, hd[k].a, B_DELTA_ROT));
+            dqb[k] = ldq(w, bw(L, hd[k].b, B_DELTA_ROT));
+            dp[k] = sub(ld3(w, bw(L, hd[k].b, B_DELTA_POS)), ld3(w, bw(L, hd[k].a, B_DELTA_POS)));
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
-                if (p >= pc[k]) continue;
-                ra[k][p] = ld3(w, pw(L, c, p, P_R_A));
-                rb[k][p] = ld3(w, pw(L, c, p, P_R_B));
-                bs[k][p] = ldf(w, pw(L, c, p, P_BASE_SEP));
+                if (p >= hd[k].pc) continue;
+                ps[k][p] = wave_slot(L);
+                const uint32_t* pr = prec(L, c, p, ps[k][p]);
+                ra[k][p] = q3(pr, PR_RA);
+                rb[k][p] = q3(pr, PR_RB);
+                bs[k][p] = qf(pr, PR_BASE_SEP);
             }
         }
 #pragma unroll
         for (int k = 0; k < kChunk; k++) {
             int c = c0 + k;
             if (c >= cc) continue;
-            uint32_t* sp = chead_rec(L, c);
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
-                if (p >= pc[k]) continue;
+                if (p >= hd[k].pc) continue;
                 V3 ds = add(dp[k], sub(rot(dqb[k], rb[k][p]), rot(dqa[k], ra[k][p])));
-                stf(sp, CH_SEP + p, dot(ds, n[k]) + bs[k][p]);
+                qsf(prec(L, c, p, ps[k][p]), PR_SEP, dot(ds, n[k]) + bs[k][p]);
             }
         }
     }
+}
+
+B3D_FN void delta_geometry(const Lane& L) {
+    contact_geometry(L);
+    joint_geometry(L);
+}
+
+/* The joint rows' delta-pose geometry. */
+B3D_FN void joint_geometry(const Lane& L) {
+    uint32_t* w = L.w;
     int nj = clampi(ldi(w, H_JOINT_COUNT), 0, L.g.max_j);
     for (int j0 = 0; j0 < nj; j0 += kPrepChunk) {
         int a[kPrepChunk], b[kPrepChunk], info[kPrepChunk];
@@ -1187,9 +1481,9 @@ B3D_FN void solve_rolling(V3 t1, V3 t2, float rolling, float total_n, M3 ia, M3 
 }
 
 /* The contact row as one solve needs it, loaded ahead of use. */
-struct CPoint { V3 ra, rb; float nmass, ni, tn, lever, sep; };
+struct CPoint { V3 ra, rb; float nmass, ni, tn, lever, sep; int slot; };
 struct CRow {
-    int a, b, pc, flags;
+    int a, b, pc, flags, slot;
     V3 n;
     float ma, mb;
     M3 ia, ib;
@@ -1201,72 +1495,61 @@ struct CRow {
     M2 tm;
 };
 
-/* Masses of a row, loaded when its solve starts.  A body that is not
- * dynamic has exactly zero mass and inertia in the row (prepare_contacts
- * writes m3zero()), so those are not loaded.  The softness is the world's
- * static or dynamic contact softness. */
+/* Masses of a row, loaded when its solve starts; the softness is the
+ * world's static or dynamic contact softness. */
 B3D_FN void crow_masses(const Lane& L, int c, CRow* r, Soft cs, Soft ss) {
-    const uint32_t* w = L.w;
-    r->ma = 0.0f;
-    r->mb = 0.0f;
-    r->ia = m3zero();
-    r->ib = m3zero();
-    if (r->flags & CF_DYN_A) {
-        r->ma = ldf(w, cw(L, c, C_INV_MASS_A));
-        r->ia = ldm3(w, cw(L, c, C_INV_I_A));
-    }
-    if (r->flags & CF_DYN_B) {
-        r->mb = ldf(w, cw(L, c, C_INV_MASS_B));
-        r->ib = ldm3(w, cw(L, c, C_INV_I_B));
-    }
+    rec_masses(crec(L, c, r->slot), r->flags, &r->ma, &r->ia, &r->mb, &r->ib);
     r->soft = (r->flags & CF_STATIC) ? ss : cs;
 }
 
-/* Normal, points and friction data of a row: loaded one contact ahead. */
+/* Normal, points and friction data of a row: loaded one contact ahead.
+ * Call where exactly the lanes with a contact c run. */
 B3D_FN void crow_load(const Lane& L, int c, CHead h, int relax, CRow* r) {
-    const uint32_t* w = L.w;
+    const uint32_t* rc = crec(L, c, h.slot);
     r->a = h.a;
     r->b = h.b;
     r->pc = h.pc;
     r->flags = h.flags;
-    r->n = ld3(w, cw(L, c, C_NORMAL));
-    const uint32_t* sp = chead_rec(L, c);
+    r->slot = h.slot;
+    r->friction = h.friction;
+    r->twist_mass = h.twist_mass;
+    r->n = q3(rc, R_N);
+    r->rolling = qf(rc, R_ROLLING);
 #pragma unroll
     for (int p = 0; p < kMaxManifold; p++) {
         if (p >= h.pc) continue;
         CPoint& q = r->pt[p];
-        q.ra = ld3(w, pw(L, c, p, P_R_A));
-        q.rb = ld3(w, pw(L, c, p, P_R_B));
-        q.nmass = ldf(w, pw(L, c, p, P_NORMAL_MASS));
-        q.ni = ldf(w, pw(L, c, p, P_NORMAL_IMPULSE));
-        q.tn = ldf(w, pw(L, c, p, P_TOTAL_NORMAL));
-        q.lever = relax ? ldf(w, pw(L, c, p, P_LEVER)) : 0.0f;
-        q.sep = ldf(sp, CH_SEP + p);
+        q.slot = wave_slot(L);
+        const uint32_t* pr = prec(L, c, p, q.slot);
+        q.ra = q3(pr, PR_RA);
+        q.nmass = qf(pr, PR_NMASS);
+        q.rb = q3(pr, PR_RB);
+        q.ni = qf(pr, PR_NI);
+        q.tn = qf(pr, PR_TN);
+        q.sep = qf(pr, PR_SEP);
+        q.lever = relax ? qf(pr, PR_LEVER) : 0.0f;
     }
     if (relax) {
-        r->friction = ldf(w, cw(L, c, C_FRICTION));
-        r->twist_mass = ldf(w, cw(L, c, C_TWIST_MASS));
-        r->twist_imp = ldf(w, cw(L, c, C_TWIST_IMPULSE));
-        r->rolling = (r->flags & CF_ROLLING) ? ldf(w, cw(L, c, C_ROLLING)) : 0.0f;
-        r->fi.x = ldf(w, cw(L, c, C_FRICTION_IMPULSE));
-        r->fi.y = ldf(w, cw(L, c, C_FRICTION_IMPULSE + 1));
-        r->t1 = ld3(w, cw(L, c, C_TANGENT1));
+        r->fi.x = qf(rc, R_FI);
+        r->fi.y = qf(rc, R_FI + 1);
+        r->twist_imp = qf(rc, R_TWIST);
+        r->t1 = q3(rc, R_T1);
         /* tangent2 = tangent1 x normal as written by b3_contact_from_mani */
         r->t2 = cross(r->t1, r->n);
-        r->ca = ld3(w, cw(L, c, C_CENTER_A));
-        r->cb = ld3(w, cw(L, c, C_CENTER_B));
+        r->ca = q3(rc, R_CA);
+        r->cb = q3(rc, R_CB);
         /* the inverse of a symmetric 2x2 is stored symmetric bit for bit */
-        r->tm.cx.x = ldf(w, cw(L, c, C_TANGENT_MASS));
-        r->tm.cx.y = ldf(w, cw(L, c, C_TANGENT_MASS + 1));
+        r->tm.cx.x = qf(rc, R_TM_XX);
+        r->tm.cx.y = qf(rc, R_TM_XY);
         r->tm.cy.x = r->tm.cx.y;
-        r->tm.cy.y = ldf(w, cw(L, c, C_TANGENT_MASS + 3));
+        r->tm.cy.y = qf(rc, R_TM_YY);
     }
 }
 
 /* One contact, b3_solve_one_contact (08:315-413): soft normal rows, then in
  * the relax pass twist friction, 2-D friction at the anchor and rolling. */
 B3D_FN void crow_solve(const Lane& L, int c, CRow& r, float inv_h, float contact_speed, int use_bias) {
-    uint32_t* w = L.w;
+    uint32_t* rc = crec(L, c, r.slot);
     V3 va = vlin(L, r.a), wa = vang(L, r.a), vb = vlin(L, r.b), wb = vang(L, r.b);
     V3 n = r.n;
     float total_n = 0.0f;
@@ -1290,8 +1573,9 @@ B3D_FN void crow_solve(const Lane& L, int c, CRow& r, float inv_h, float contact
         float dimp = -q.nmass * (mscale * vn + vbias) - iscale * q.ni;
         float nimp = maxf(q.ni + dimp, 0.0f);
         dimp = nimp - q.ni;
-        stf(w, pw(L, c, p, P_NORMAL_IMPULSE), nimp);
-        stf(w, pw(L, c, p, P_TOTAL_NORMAL), q.tn + nimp);
+        uint32_t* pr = prec(L, c, p, q.slot);
+        qsf(pr, PR_NI, nimp);
+        qsf(pr, PR_TN, q.tn + nimp);
         total_n += nimp;
         twist_lim += q.lever * nimp;
         V3 P = scale(n, dimp);
@@ -1305,7 +1589,7 @@ B3D_FN void crow_solve(const Lane& L, int c, CRow& r, float inv_h, float contact
         float max_t = r.friction * twist_lim;
         float dtw = -r.twist_mass * twist_s;
         float new_t = clampf(r.twist_imp + dtw, -max_t, max_t);
-        stf(w, cw(L, c, C_TWIST_IMPULSE), new_t);
+        qsf(rc, R_TWIST, new_t);
         dtw = new_t - r.twist_imp;
         wa = sub(wa, mv(r.ia, scale(n, dtw)));
         wb = add(wb, mv(r.ib, scale(n, dtw)));
@@ -1330,17 +1614,17 @@ B3D_FN void crow_solve(const Lane& L, int c, CRow& r, float inv_h, float contact
         V2 df;
         df.x = ni.x - r.fi.x;
         df.y = ni.y - r.fi.y;
-        stf(w, cw(L, c, C_FRICTION_IMPULSE), ni.x);
-        stf(w, cw(L, c, C_FRICTION_IMPULSE + 1), ni.y);
+        qsf(rc, R_FI, ni.x);
+        qsf(rc, R_FI + 1, ni.y);
         V3 P = add(scale(r.t1, df.x), scale(r.t2, df.y));
         va = msub(va, r.ma, P);
         wa = sub(wa, mv(r.ia, cross(r.ca, P)));
         vb = madd(vb, r.mb, P);
         wb = add(wb, mv(r.ib, cross(r.cb, P)));
         if (r.flags & CF_ROLLING) {
-            V3 ri = ld3(w, cw(L, c, C_ROLLING_IMPULSE));
+            V3 ri = q3(rc, R_ROLL);
             solve_rolling(r.t1, r.t2, r.rolling, total_n, r.ia, r.ib, &ri, &wa, &wb);
-            st3(w, cw(L, c, C_ROLLING_IMPULSE), ri);
+            qs3(rc, R_ROLL, ri);
         }
     }
     if (is_dyn_flag(L, r.a)) {
@@ -1354,21 +1638,24 @@ B3D_FN void crow_solve(const Lane& L, int c, CRow& r, float inv_h, float contact
 }
 
 /* b3_solve_contacts (08:415-437): one Gauss-Seidel sweep in contact order.
- * Row c+1 is in flight while row c is solved, and the head of row c+2 while
- * row c+1 loads. */
+ * Row c+1 (masses included) is in flight while row c is solved, and the
+ * head of row c+2 while row c+1 loads. */
 B3D_FN void solve_contacts(const Lane& L, float inv_h, float contact_speed, int use_bias, Soft cs, Soft ss) {
     int cc = ldi(L.w, H_CONTACT_COUNT);
     if (cc <= 0) return;
     int relax = !use_bias;
-    CHead h1 = chead_load(L, 0);
+    CHead h1 = rhead_load(L, 0);
     CRow cur, nxt;
     crow_load(L, 0, h1, relax, &cur);
-    if (cc > 1) h1 = chead_load(L, 1);
+    crow_masses(L, 0, &cur, cs, ss);
+    if (cc > 1) h1 = rhead_load(L, 1);
     for (int c = 0; c < cc; c++) {
         CHead h2 = h1;
-        if (c + 2 < cc) h2 = chead_load(L, c + 2);
-        crow_masses(L, c, &cur, cs, ss);
-        if (c + 1 < cc) crow_load(L, c + 1, h1, relax, &nxt);
+        if (c + 2 < cc) h2 = rhead_load(L, c + 2);
+        if (c + 1 < cc) {
+            crow_load(L, c + 1, h1, relax, &nxt);
+            crow_masses(L, c + 1, &nxt, cs, ss);
+        }
         crow_solve(L, c, cur, inv_h, contact_speed, use_bias);
         cur = nxt;
         h1 = h2;
@@ -1377,29 +1664,37 @@ B3D_FN void solve_contacts(const Lane& L, float inv_h, float contact_speed, int 
 
 /* b3_apply_restitution (08:439-480). */
 B3D_FN void apply_restitution(const Lane& L, float threshold) {
-    uint32_t* w = L.w;
-    int cc = ldi(w, H_CONTACT_COUNT);
+    int cc = ldi(L.w, H_CONTACT_COUNT);
     for (int c = 0; c < cc; c++) {
-        CHead hd = chead_load(L, c);
+        CHead hd = rhead_load(L, c);
+        int ps[kMaxManifold];
+#pragma unroll
+        for (int p = 0; p < kMaxManifold; p++)
+            if (p < hd.pc) ps[p] = wave_slot(L);
         if (!(hd.flags & CF_RESTITUTION)) continue;
-        float e = ldf(w, cw(L, c, C_RESTITUTION));
-        int a = hd.a, b = hd.b, pc = hd.pc;
+        const uint32_t* r = crec(L, c, hd.slot);
+        float e = qf(r, R_RESTITUTION);
+        int a = hd.a, b = hd.b;
         V3 va = vlin(L, a), wa = vang(L, a), vb = vlin(L, b), wb = vang(L, b);
-        V3 n = ld3(w, cw(L, c, C_NORMAL));
-        float ma = ldf(w, cw(L, c, C_INV_MASS_A)), mb = ldf(w, cw(L, c, C_INV_MASS_B));
-        M3 ia = ldm3(w, cw(L, c, C_INV_I_A)), ib = ldm3(w, cw(L, c, C_INV_I_B));
-        for (int p = 0; p < pc; p++) {
-            float rv = ldf(w, pw(L, c, p, P_REL_VEL));
-            if (rv > -threshold || ldf(w, pw(L, c, p, P_TOTAL_NORMAL)) == 0.0f) continue;
-            V3 ra = ld3(w, pw(L, c, p, P_R_A)), rb = ld3(w, pw(L, c, p, P_R_B));
+        V3 n = q3(r, R_N);
+        float ma, mb;
+        M3 ia, ib;
+        rec_masses(r, hd.flags, &ma, &ia, &mb, &ib);
+#pragma unroll
+        for (int p = 0; p < kMaxManifold; p++) {
+            if (p >= hd.pc) continue;
+            uint32_t* pr = prec(L, c, p, ps[p]);
+            float rv = qf(r, R_REL_VEL + p);
+            if (rv > -threshold || qf(pr, PR_TN) == 0.0f) continue;
+            V3 ra = q3(pr, PR_RA), rb = q3(pr, PR_RB);
             V3 vra = add(va, cross(wa, ra));
             V3 vrb = add(vb, cross(wb, rb));
             float vn = dot(sub(vrb, vra), n);
-            float old = ldf(w, pw(L, c, p, P_NORMAL_IMPULSE));
-            float imp = -ldf(w, pw(L, c, p, P_NORMAL_MASS)) * (vn + e * rv);
+            float old = qf(pr, PR_NI);
+            float imp = -qf(pr, PR_NMASS) * (vn + e * rv);
             float nimp = maxf(old + imp, 0.0f);
             imp = nimp - old;
-            stf(w, pw(L, c, p, P_NORMAL_IMPULSE), nimp);
+            qsf(pr, PR_NI, nimp);
             V3 P = scale(n, imp);
             va = msub(va, ma, P);
             wa = sub(wa, mv(ia, cross(ra, P)));
@@ -1413,6 +1708,57 @@ B3D_FN void apply_restitution(const Lane& L, float threshold) {
         if (is_dyn_flag(L, b)) {
             set_vlin(L, b, vb);
             set_vang(L, b, wb);
+        }
+    }
+}
+
+/* The impulses the sweeps and restitution accumulated, back into the
+ * world's contact rows (the warm-start cache of the next step). */
+B3D_FN void contact_writeback(const Lane& L) {
+    uint32_t* w = L.w;
+    int cc = ldi(w, H_CONTACT_COUNT);
+    for (int c0 = 0; c0 < cc; c0 += kChunk) {
+        CHead hd[kChunk];
+#pragma unroll
+        for (int k = 0; k < kChunk; k++) {
+            int c = c0 + k;
+            if (c >= cc) continue;
+            hd[k] = rhead_load(L, c);
+        }
+        float ni[kChunk][kMaxManifold], tn[kChunk][kMaxManifold], tw[kChunk];
+        V2 fi[kChunk];
+        V3 roll[kChunk];
+#pragma unroll
+        for (int k = 0; k < kChunk; k++) {
+            int c = c0 + k;
+            if (c >= cc) continue;
+            const uint32_t* r = crec(L, c, hd[k].slot);
+#pragma unroll
+            for (int p = 0; p < kMaxManifold; p++) {
+                if (p >= hd[k].pc) continue;
+                const uint32_t* pr = prec(L, c, p, wave_slot(L));
+                ni[k][p] = qf(pr, PR_NI);
+                tn[k][p] = qf(pr, PR_TN);
+            }
+            fi[k].x = qf(r, R_FI);
+            fi[k].y = qf(r, R_FI + 1);
+            tw[k] = qf(r, R_TWIST);
+            if (hd[k].flags & CF_ROLLING) roll[k] = q3(r, R_ROLL);
+        }
+#pragma unroll
+        for (int k = 0; k < kChunk; k++) {
+            int c = c0 + k;
+            if (c >= cc) continue;
+#pragma unroll
+            for (int p = 0; p < kMaxManifold; p++) {
+                if (p >= hd[k].pc) continue;
+                stf(w, pw(L, c, p, P_NORMAL_IMPULSE), ni[k][p]);
+                stf(w, pw(L, c, p, P_TOTAL_NORMAL), tn[k][p]);
+            }
+            stf(w, cw(L, c, C_FRICTION_IMPULSE), fi[k].x);
+            stf(w, cw(L, c, C_FRICTION_IMPULSE + 1), fi[k].y);
+            stf(w, cw(L, c, C_TWIST_IMPULSE), tw[k]);
+            if (hd[k].flags & CF_ROLLING) st3(w, cw(L, c, C_ROLLING_IMPULSE), roll[k]);
         }
     }
 }
@@ -1701,14 +2047,26 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
 B3D_FN void solve_joints(const Lane& L, float h, float inv_h, int use_bias) {
     int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
     if (nj <= 0) return;
-    int iters = use_bias ? kJointIters : kRelaxIters;
-    for (int it = 0; it < iters; it++) {
-        for (int j = 0; j < nj; j++) {
-            JRow r;
-            jrow_load(L, j, jhead_load(L, j), &r);
-            if (r.info & JF_WELD) solve_weld(L, j, r, use_bias);
-            else solve_revolute(L, j, r, h, inv_h, use_bias);
-        }
+    /* solve t of the sweeps is joint t % nj; the row of solve t+1 is in
+     * flight during solve t (a different joint's row unless nj == 1, when it
+     * is loaded after the solve that writes it), the head of t+2 before */
+    int total = (use_bias ? kJointIters : kRelaxIters) * nj;
+    JHead h1 = jhead_load(L, nj > 1 ? 1 : 0);
+    JRow cur, nxt;
+    jrow_load(L, 0, jhead_load(L, 0), &cur);
+    int j = 0;
+    for (int t = 0; t < total; t++) {
+        int jn = j + 1 == nj ? 0 : j + 1;
+        int jnn = jn + 1 == nj ? 0 : jn + 1;
+        JHead h2 = h1;
+        if (t + 2 < total) h2 = jhead_load(L, jnn);
+        if (t + 1 < total && nj > 1) jrow_load(L, jn, h1, &nxt);
+        if (cur.info & JF_WELD) solve_weld(L, j, cur, use_bias);
+        else solve_revolute(L, j, cur, h, inv_h, use_bias);
+        if (t + 1 < total && nj == 1) jrow_load(L, jn, h1, &nxt);
+        cur = nxt;
+        h1 = h2;
+        j = jn;
     }
 }
 
@@ -1885,12 +2243,12 @@ B3D_FN void step_world(const Lane& L, float dt, int substeps) {
 
     find_contacts(L);
     vel_load(L);
+    body_prepass(L, h);
     prepare_contacts(L, cs, ss);
     prepare_joints(L, h);
-    body_prepass(L, h);
     warm_start_contacts(L);
     warm_start_joints(L);
-    delta_geometry(L);
+    joint_geometry(L);   /* the contacts' initial separations come from prepare_contacts */
     for (int s = 0; s < subs; s++) {
         integrate_velocities(L);
         solve_contacts(L, inv_h, contact_speed, 1, cs, ss);
@@ -1901,6 +2259,7 @@ B3D_FN void step_world(const Lane& L, float dt, int substeps) {
         solve_joints(L, h, inv_h, 0);
         apply_restitution(L, rest_threshold);
     }
+    contact_writeback(L);
     finalize(L);
     vel_store(L);
 }

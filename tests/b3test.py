@@ -90,10 +90,9 @@ class EmuBatch:
         words = emu().emu_world_words(self.sc.sig)
         ntiles = (self.count + 63) // 64
         self.tiles = np.zeros(ntiles * words * 64, np.uint32)
-        self.snap = np.zeros_like(self.tiles)
         w = np.ascontiguousarray(worlds)
+        self.snap = w.view(np.uint32).copy()   # snapshots stay plain B3World structs
         emu().emu_upload(w.ctypes.data, self.count, self.sc.sig, self.tiles.ctypes.data)
-        emu().emu_upload(w.ctypes.data, self.count, self.sc.sig, self.snap.ctypes.data)
 
     def run(self, t0, nsteps, seed=scenes.SEED):
         e = emu()

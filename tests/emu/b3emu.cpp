@@ -30,7 +30,7 @@ int emu_world_words(unsigned long long sig) {
 int emu_scratch_words(unsigned long long sig) {
     Geometry g;
     size_t wb;
-    return geometry_of(sig, &g, &wb) ? g.scr_words : 0;
+    return geometry_of(sig, &g, &wb) ? g.tile_scr_words : 0;
 }
 
 void emu_upload(const uint32_t* aos, int count, unsigned long long sig, uint32_t* tiles) {
@@ -53,6 +53,8 @@ void emu_download(const uint32_t* tiles, int count, unsigned long long sig, uint
             aos[(size_t)w * g.world_words + k] = tiles[((size_t)(w / kLanes) * g.world_words + k) * kLanes + w % kLanes];
 }
 
+/* Masked restore from AoS snapshots (plain B3World structs), as the engine
+ * keeps them. */
 void emu_restore(uint32_t* tiles, const uint32_t* snap, int count, unsigned long long sig, const unsigned char* reset) {
     Geometry g;
     size_t wb;
@@ -60,21 +62,16 @@ void emu_restore(uint32_t* tiles, const uint32_t* snap, int count, unsigned long
     for (int w = 0; w < count; w++) {
         if (reset && !reset[w]) continue;
         size_t base = (size_t)(w / kLanes) * g.world_words * kLanes + w % kLanes;
+        const uint32_t* src = snap + (size_t)w * g.world_words;
         int lo[3], hi[3];
-        restore_ranges(g, (int)snap[base + (size_t)H_CONTACT_COUNT * kLanes], lo, hi);
+        restore_ranges(g, (int)src[H_CONTACT_COUNT], lo, hi);
         for (int r = 0; r < 3; r++)
-            for (int k = lo[r]; k < hi[r]; k++) tiles[base + (size_t)k * kLanes] = snap[base + (size_t)k * kLanes];
+            for (int k = lo[r]; k < hi[r]; k++) tiles[base + (size_t)k * kLanes] = src[k];
     }
 }
 
 static Lane lane_of(uint32_t* tiles, uint32_t* scratch, float* vel, const Geometry& g, int w) {
-    Lane L;
-    int t = w / kLanes, l = w % kLanes;
-    L.w = tiles + (size_t)t * g.world_words * kLanes + l;
-    L.scr = scratch ? scratch + (size_t)t * g.scr_words * kLanes + l : nullptr;
-    L.vel = vel ? vel + l : nullptr;
-    L.g = g;
-    return L;
+    return lane_view(tiles, scratch, vel, g, w / kLanes, w % kLanes);
 }
 
 void emu_step(uint32_t* tiles, int count, unsigned long long sig, float dt, int substeps,
@@ -83,7 +80,7 @@ void emu_step(uint32_t* tiles, int count, unsigned long long sig, float dt, int 
     size_t wb;
     if (!geometry_of(sig, &g, &wb)) return;
     int ntiles = (count + kLanes - 1) / kLanes;
-    std::vector<uint32_t> scratch((size_t)ntiles * g.scr_words * kLanes);
+    std::vector<uint32_t> scratch((size_t)ntiles * g.tile_scr_words);
     std::vector<float> vel((size_t)lds_rows(g) * kLanes);
     for (int w = 0; w < count; w++) {
         if (step_mask && !step_mask[w]) continue;

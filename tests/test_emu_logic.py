@@ -54,3 +54,19 @@ def test_lane_code_covers_every_feature():
     j = ref["joints"]
     assert (j["fixed_rotation"][:, 2][np.arange(40) % 4 != 3] == 1).all()
     assert np.abs(j["angular_impulse"]["x"][:, 0]).max() > 0           # welds carry load
+
+
+def test_lane_code_single_joint_worlds():
+    """Coverage worlds without hinges hold one weld joint each, so every
+    joint sweep solves the same joint twice in a row."""
+    from b3test import EmuSig, feature_worlds, oracle_step_batch
+    from puffysics_amd.creation import CUSTOM_SIG
+    worlds = feature_worlds(24, seed=11, hinges=False)
+    assert set(worlds["joint_count"].tolist()) <= {0, 1}
+    ref = clone(worlds)
+    emu = EmuSig(CUSTOM_SIG, worlds)
+    for t in range(40):
+        oracle_step_batch(ref, CUSTOM_SIG, 1.0 / 60.0, 4)
+        emu.step(1.0 / 60.0, 4)
+    bad = diff_words(emu.worlds(), ref, CUSTOM_SIG)
+    assert len(bad) == 0, bad[:10].tolist()
