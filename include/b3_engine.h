@@ -101,6 +101,20 @@ hipError_t b3_batch_stats_gpu(B3Engine* engine, B3StepStats* out, hipStream_t st
  * where world_words = sizeof(B3World) / 4 of the engine's signature. */
 hipError_t b3_engine_device_view(const B3Engine* engine, void** tiles, size_t* world_words);
 
+/* Step options, a bit set (0 after b3_engine_create).  No counterpart in
+ * the reference, whose contact structs double as solver scratch.
+ *
+ * B3_ENGINE_KEEP_SOLVER_FIELDS: also write the fields b3_prepare_one_contact
+ * derives for every new contact (08_contacts.inl:234-291: inv_mass_a/b,
+ * inv_i_a/b, softness, normal_mass, rel_vel, lever, center_a/b,
+ * tangent_mass, twist_mass, rolling_mass) to the world's contact rows.  The
+ * engine's solver keeps them in its own scratch and every step rewrites them
+ * before use, so without the option they hold stale values in downloaded
+ * worlds; every other field, and every body and joint, is the same either
+ * way.  Set it to compare whole B3World structs with the reference. */
+#define B3_ENGINE_KEEP_SOLVER_FIELDS 1u
+hipError_t b3_engine_set_options(B3Engine* engine, unsigned int options);
+
 #ifdef __cplusplus
 }
 #endif

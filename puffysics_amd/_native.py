@@ -28,6 +28,7 @@ ENGINE_SYMBOLS = [
     ("b3_batch_apply_gpu", _i, [_vp, _vp, _vp, _vp, _vp, _vp]),
     ("b3_batch_stats_gpu", _i, [_vp, _vp, _vp]),
     ("b3_engine_device_view", _i, [_vp, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]),
+    ("b3_engine_set_options", _i, [_vp, C.c_uint]),
     ("b3w_masks_gpu", _i, [_i, _ull, _i, _i, _vp, _vp, _vp]),
     ("b3w_inputs_gpu", _i, [_vp, _i, _ull, _i, _vp, _vp]),
 ]

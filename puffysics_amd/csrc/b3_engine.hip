@@ -109,7 +109,7 @@ __global__ __launch_bounds__(64) void b3k_restore(uint32_t* live, const uint32_t
 
 __global__ __launch_bounds__(64) void b3k_step(uint32_t* live, const uint32_t* snap, uint32_t* scratch,
         Geometry g, int count, float dt, int substeps, const unsigned char* step_mask,
-        const unsigned char* reset_mask) {
+        const unsigned char* reset_mask, unsigned int opts) {
     extern __shared__ float vel_rows[];
     if (reset_mask) {
         restore_tile(live, snap, g, count, reset_mask);
@@ -119,7 +119,7 @@ __global__ __launch_bounds__(64) void b3k_step(uint32_t* live, const uint32_t* s
     int lane = threadIdx.x;
     int w = tile * 64 + lane;
     if (w >= count || (step_mask && !step_mask[w])) return;
-    step_world(lane_view(live, scratch, vel_rows, g, tile, lane), dt, substeps);
+    step_world(lane_view(live, scratch, vel_rows, g, tile, lane, opts), dt, substeps);
 }
 
 /* ---- inputs and stats ---- */
@@ -391,7 +391,7 @@ hipError_t b3_batch_step_gpu(B3Engine* e, float dt, int substeps, const unsigned
     if (err != hipSuccess) return err;
     if (dt == 0.0f) return reset_mask ? b3_batch_restore_gpu(e, reset_mask, stream) : hipSuccess;
     b3k_step<<<e->tiles, 64, e->lds_bytes, stream>>>(e->live, e->snap, e->scratch, e->g, e->count, dt, substeps,
-        step_mask, reset_mask);
+        step_mask, reset_mask, e->options);
     return hipGetLastError();
 }
 
@@ -418,6 +418,12 @@ hipError_t b3_engine_device_view(const B3Engine* e, void** tiles, size_t* world_
     if (!e || !tiles || !world_words) return hipErrorInvalidValue;
     *tiles = e->live;
     *world_words = (size_t)e->g.world_words;
+    return hipSuccess;
+}
+
+hipError_t b3_engine_set_options(B3Engine* e, unsigned int options) {
+    if (!e || (options & ~B3_ENGINE_KEEP_SOLVER_FIELDS)) return hipErrorInvalidValue;
+    e->options = options;
     return hipSuccess;
 }
 

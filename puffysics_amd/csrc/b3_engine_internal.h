@@ -21,6 +21,7 @@ struct B3Engine {
     uint32_t* scratch;
     unsigned char* staging;  /* count * world_bytes, AoS, for up/download */
     size_t lds_bytes;
+    unsigned int options;    /* B3_ENGINE_* step options */
 };
 
 #endif

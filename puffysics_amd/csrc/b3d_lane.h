@@ -240,9 +240,15 @@ constexpr int R_AB = 0, R_INFO = 1, R_FRICTION = 2, R_TWIST_MASS = 3,   /* row 0
               R_FI = 40, R_TWIST = 42, R_RESTITUTION = 43,              /* row 10 */
               R_ROLL = 44,                                              /* row 11 */
               R_REL_VEL = 48,                                           /* row 12: restitution only */
-              kCRows = 13;
-constexpr int PR_RA = 0, PR_NMASS = 3, PR_RB = 4, PR_BASE_SEP = 7, PR_NI = 8, PR_TN = 9, PR_SEP = 10,
-              PR_LEVER = 11, kPRows = 3;
+              R_SEP = 52,                                               /* row 13: point separations */
+              R_BASE_SEP = 56,                                          /* row 14 */
+              R_NI = 60, R_TN = 61,                                     /* rows 15-16: point p at +2p */
+              kCRows = 17;
+/* Point records: anchors, normal mass and twist lever.  A contact's
+ * per-point values that change during the step (separation, accumulated
+ * impulses) sit in whole rows of the contact record, so that each update
+ * writes full quads. */
+constexpr int PR_RA = 0, PR_NMASS = 3, PR_RB = 4, PR_LEVER = 7, kPRows = 2;
 /* Joint record in scratch: the joint-connection key, the head written by
  * prepare_joints (bodies a | b << 16 and JF_* flags), then everything that
  * depends only on the bodies' delta poses (recomputed after every position
@@ -309,12 +315,25 @@ struct Lane {
     float* vel;     /* velocity rows + lane; before the velocities are
                        staged the same rows hold the clip polygons */
     int lane;
+    unsigned int opts;  /* kKeepSolverFields */
     Geometry g;
 };
 
+/* Option: also write the prepared solver fields of every new contact
+ * (b3_prepare_one_contact's inverse masses and inertias, softness, normal
+ * and tangent masses, relative velocities, twist levers and mass, friction
+ * anchors and rolling mass) to the world's contact rows.  The step itself
+ * reads them from the packed records, and every step recomputes them before
+ * use, so without the option those fields of a downloaded contact are
+ * stale; everything else is identical.  Same value as
+ * B3_ENGINE_KEEP_SOLVER_FIELDS. */
+constexpr unsigned int kKeepSolverFields = 1u;
+
 /* The lane view of world `lane` of tile `tile`. */
-B3D_FN Lane lane_view(uint32_t* live, uint32_t* scratch, float* vel_rows, const Geometry& g, int tile, int lane) {
+B3D_FN Lane lane_view(uint32_t* live, uint32_t* scratch, float* vel_rows, const Geometry& g, int tile, int lane,
+        unsigned int opts = 0) {
     Lane L;
+    L.opts = opts;
     L.w = live + (size_t)tile * g.world_words * kLanes + lane;
     L.scr = scratch ? scratch + (size_t)tile * g.tile_scr_words + lane : nullptr;
     L.sq = scratch ? scratch + (size_t)tile * g.tile_scr_words + (size_t)g.scr_words * kLanes : nullptr;
@@ -966,11 +985,21 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
         M3 iwa[kPrepChunk], iwb[kPrepChunk];
         V3 n[kPrepChunk], t1[kPrepChunk], ra[kPrepChunk][kMaxManifold], rb[kPrepChunk][kMaxManifold], dp[kPrepChunk];
         Q dqa[kPrepChunk], dqb[kPrepChunk];
-        float bs[kPrepChunk][kMaxManifold];
+        float bs[kPrepChunk][kMaxManifold], ni[kPrepChunk][kMaxManifold];
+        float fric[kPrepChunk], rest[kPrepChunk], roll_c[kPrepChunk], tw[kPrepChunk];
+        V2 fi[kPrepChunk];
+        V3 roll[kPrepChunk];
 #pragma unroll
         for (int k = 0; k < kPrepChunk; k++) {
             int c = c0 + k;
             if (c >= cc) continue;
+            fric[k] = ldf(w, cw(L, c, C_FRICTION));
+            rest[k] = ldf(w, cw(L, c, C_RESTITUTION));
+            roll_c[k] = ldf(w, cw(L, c, C_ROLLING));
+            fi[k].x = ldf(w, cw(L, c, C_FRICTION_IMPULSE));
+            fi[k].y = ldf(w, cw(L, c, C_FRICTION_IMPULSE + 1));
+            tw[k] = ldf(w, cw(L, c, C_TWIST_IMPULSE));
+            roll[k] = ld3(w, cw(L, c, C_ROLLING_IMPULSE));
             ima[k] = 0.0f;
             imb[k] = 0.0f;
             iwa[k] = m3zero();
@@ -995,6 +1024,7 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
                 ra[k][p] = ld3(w, pw(L, c, p, P_R_A));
                 rb[k][p] = ld3(w, pw(L, c, p, P_R_B));
                 bs[k][p] = ldf(w, pw(L, c, p, P_BASE_SEP));
+                ni[k][p] = ldf(w, pw(L, c, p, P_NORMAL_IMPULSE));
             }
         }
 #pragma unroll
@@ -1011,21 +1041,24 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
             V3 t2 = cross(t1[k], n[k]);
             V3 center_a = zero3(), center_b = zero3();
             float wsum = 0.0f;
-            float rel_vel[kMaxManifold];
+            float rel_vel[kMaxManifold], nmass[kMaxManifold], sep0[kMaxManifold], bsp[kMaxManifold],
+                nip[kMaxManifold];
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
+                rel_vel[p] = 0.0f;
+                nmass[p] = 0.0f;
+                sep0[p] = 0.0f;
+                bsp[p] = 0.0f;
+                nip[p] = 0.0f;
                 if (p >= pc[k]) continue;
-                uint32_t* pr = prec(L, c, p, pslot[k][p]);
                 V3 rap = ra[k][p], rbp = rb[k][p];
                 V3 rn_a = cross(rap, n[k]);
                 V3 rn_b = cross(rbp, n[k]);
                 float kn = ma + mb + dot(rn_a, mv(ia, rn_a)) + dot(rn_b, mv(ib, rn_b));
-                float nmass = kn > 0.0f ? 1.0f / kn : 0.0f;
-                stf(w, pw(L, c, p, P_NORMAL_MASS), nmass);
+                nmass[p] = kn > 0.0f ? 1.0f / kn : 0.0f;
                 V3 vra = add(va, cross(wa, rap));
                 V3 vrb = add(vb, cross(wb, rbp));
                 rel_vel[p] = dot(n[k], sub(vrb, vra));
-                stf(w, pw(L, c, p, P_REL_VEL), rel_vel[p]);
                 float sep = bs[k][p] + dot(sub(rbp, rap), n[k]);
                 float weight = clampf(2.0f - sep * inv_tau, kMinFrictionW, 1.0f);
                 center_a = madd(center_a, weight, rap);
@@ -1034,13 +1067,9 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
                 /* the solver's separation at the initial delta poses (the
                  * reference's per-row form, 08_contacts.inl:331-333) */
                 V3 ds = add(dp[k], sub(rot(dqb[k], rbp), rot(dqa[k], rap)));
-                qs3(pr, PR_RA, rap);
-                qsf(pr, PR_NMASS, nmass);
-                qs3(pr, PR_RB, rbp);
-                qsf(pr, PR_BASE_SEP, bs[k][p]);
-                qsf(pr, PR_NI, ldf(w, pw(L, c, p, P_NORMAL_IMPULSE)));
-                qsf(pr, PR_TN, 0.0f);
-                qsf(pr, PR_SEP, dot(ds, n[k]) + bs[k][p]);
+                sep0[p] = dot(ds, n[k]) + bs[k][p];
+                bsp[p] = bs[k][p];
+                nip[p] = ni[k][p];
             }
             float invw = wsum > 0.0f ? 1.0f / wsum : 0.0f;
             center_a = scale(center_a, invw);
@@ -1049,8 +1078,16 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
             for (int p = 0; p < kMaxManifold; p++) {
                 if (p >= pc[k]) continue;
                 float lever = len(sub(ra[k][p], center_a));
-                stf(w, pw(L, c, p, P_LEVER), lever);
-                qsf(prec(L, c, p, pslot[k][p]), PR_LEVER, lever);
+                uint32_t* pr = prec(L, c, p, pslot[k][p]);
+                qs3(pr, PR_RA, ra[k][p]);
+                qsf(pr, PR_NMASS, nmass[p]);
+                qs3(pr, PR_RB, rb[k][p]);
+                qsf(pr, PR_LEVER, lever);
+                if (L.opts & kKeepSolverFields) {
+                    stf(w, pw(L, c, p, P_NORMAL_MASS), nmass[p]);
+                    stf(w, pw(L, c, p, P_REL_VEL), rel_vel[p]);
+                    stf(w, pw(L, c, p, P_LEVER), lever);
+                }
             }
             V3 rt_a1 = cross(center_a, t1[k]);
             V3 rt_a2 = cross(center_a, t2);
@@ -1065,26 +1102,28 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
             M3 isum = madd3(ia, ib);
             float kt = dot(n[k], mv(isum, n[k]));
             float twist_mass = kt > 0.0f ? 1.0f / kt : 0.0f;
-            st3(w, cw(L, c, C_CENTER_A), center_a);
-            st3(w, cw(L, c, C_CENTER_B), center_b);
-            stf(w, cw(L, c, C_TWIST_MASS), twist_mass);
-            stf(w, cw(L, c, C_TANGENT_MASS), tmass.cx.x);
-            stf(w, cw(L, c, C_TANGENT_MASS + 1), tmass.cx.y);
-            stf(w, cw(L, c, C_TANGENT_MASS + 2), tmass.cy.x);
-            stf(w, cw(L, c, C_TANGENT_MASS + 3), tmass.cy.y);
-            stm3(w, cw(L, c, C_ROLLING_MASS), inv3(isum));
-            stf(w, cw(L, c, C_INV_MASS_A), ma);
-            stf(w, cw(L, c, C_INV_MASS_B), mb);
-            stm3(w, cw(L, c, C_INV_I_A), ia);
-            stm3(w, cw(L, c, C_INV_I_B), ib);
-            stsoft(w, cw(L, c, C_SOFTNESS), (fl[k] & CF_STATIC) ? ss : cs);
+            if (L.opts & kKeepSolverFields) {
+                st3(w, cw(L, c, C_CENTER_A), center_a);
+                st3(w, cw(L, c, C_CENTER_B), center_b);
+                stf(w, cw(L, c, C_TWIST_MASS), twist_mass);
+                stf(w, cw(L, c, C_TANGENT_MASS), tmass.cx.x);
+                stf(w, cw(L, c, C_TANGENT_MASS + 1), tmass.cx.y);
+                stf(w, cw(L, c, C_TANGENT_MASS + 2), tmass.cy.x);
+                stf(w, cw(L, c, C_TANGENT_MASS + 3), tmass.cy.y);
+                stm3(w, cw(L, c, C_ROLLING_MASS), inv3(isum));
+                stf(w, cw(L, c, C_INV_MASS_A), ma);
+                stf(w, cw(L, c, C_INV_MASS_B), mb);
+                stm3(w, cw(L, c, C_INV_I_A), ia);
+                stm3(w, cw(L, c, C_INV_I_B), ib);
+                stsoft(w, cw(L, c, C_SOFTNESS), (fl[k] & CF_STATIC) ? ss : cs);
+            }
             /* the packed record */
             qsu(r, R_AB, (uint32_t)(a[k] | (b[k] << 16)));
             qsu(r, R_INFO, (uint32_t)(pc[k] | (fl[k] << 8)));
-            qsf(r, R_FRICTION, ldf(w, cw(L, c, C_FRICTION)));
+            qsf(r, R_FRICTION, fric[k]);
             qsf(r, R_TWIST_MASS, twist_mass);
             qs3(r, R_N, n[k]);
-            qsf(r, R_ROLLING, ldf(w, cw(L, c, C_ROLLING)));
+            qsf(r, R_ROLLING, roll_c[k]);
             rec_store_masses(r, fl[k], ma, ia, mb, ib);
             qs3(r, R_T1, t1[k]);
             qsf(r, R_TM_XX, tmass.cx.x);
@@ -1092,15 +1131,31 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
             qsf(r, R_TM_XY, tmass.cx.y);
             qs3(r, R_CB, center_b);
             qsf(r, R_TM_YY, tmass.cy.y);
-            qsf(r, R_FI, ldf(w, cw(L, c, C_FRICTION_IMPULSE)));
-            qsf(r, R_FI + 1, ldf(w, cw(L, c, C_FRICTION_IMPULSE + 1)));
-            qsf(r, R_TWIST, ldf(w, cw(L, c, C_TWIST_IMPULSE)));
-            qsf(r, R_RESTITUTION, ldf(w, cw(L, c, C_RESTITUTION)));
-            qs3(r, R_ROLL, ld3(w, cw(L, c, C_ROLLING_IMPULSE)));
+            qsf(r, R_FI, fi[k].x);
+            qsf(r, R_FI + 1, fi[k].y);
+            qsf(r, R_TWIST, tw[k]);
+            qsf(r, R_RESTITUTION, rest[k]);
+            qs3(r, R_ROLL, roll[k]);
             if (fl[k] & CF_RESTITUTION) {
 #pragma unroll
-                for (int p = 0; p < kMaxManifold; p++)
-                    if (p < pc[k]) qsf(r, R_REL_VEL + p, rel_vel[p]);
+                for (int p = 0; p < kMaxManifold; p++) qsf(r, R_REL_VEL + p, rel_vel[p]);
+            }
+#pragma unroll
+            for (int p = 0; p < kMaxManifold; p++) {
+                qsf(r, R_SEP + p, sep0[p]);
+                qsf(r, R_BASE_SEP + p, bsp[p]);
+            }
+#pragma unroll
+            for (int p = 0; p < 2; p++) {
+                qsf(r, R_NI + 2 * p, nip[p]);
+                qsf(r, R_TN + 2 * p, 0.0f);
+            }
+            if (pc[k] > 2) {
+#pragma unroll
+                for (int p = 2; p < kMaxManifold; p++) {
+                    qsf(r, R_NI + 2 * p, nip[p]);
+                    qsf(r, R_TN + 2 * p, 0.0f);
+                }
             }
         }
     }
@@ -1246,7 +1301,7 @@ B3D_FN void warm_start_contacts(const Lane& L) {
             for (int p = 0; p < kMaxManifold; p++) {
                 if (p >= hd[k].pc) continue;
                 const uint32_t* pr = prec(L, c, p, wave_slot(L));
-                ni[k][p] = qf(pr, PR_NI);
+                ni[k][p] = qf(r, R_NI + 2 * p);
                 ra[k][p] = q3(pr, PR_RA);
                 rb[k][p] = q3(pr, PR_RB);
             }
@@ -1347,35 +1402,40 @@ B3D_FN void contact_geometry(const Lane& L) {
         V3 n[kChunk], dp[kChunk], ra[kChunk][kMaxManifold], rb[kChunk][kMaxManifold];
         Q dqa[kChunk], dqb[kChunk];
         float bs[kChunk][kMaxManifold];
-        int ps[kChunk][kMaxManifold];
 #pragma unroll
         for (int k = 0; k < kChunk; k++) {
             int c = c0 + k;
             if (c >= cc) continue;
-            n[k] = q3(crec(L, c, hd[k].slot), R_N);
+            const uint32_t* r = crec(L, c, hd[k].slot);
+            n[k] = q3(r, R_N);
             dqa[k] = ldq(w, bw(L, hd[k].a, B_DELTA_ROT));
             dqb[k] = ldq(w, bw(L, hd[k].b, B_DELTA_ROT));
             dp[k] = sub(ld3(w, bw(L, hd[k].b, B_DELTA_POS)), ld3(w, bw(L, hd[k].a, B_DELTA_POS)));
 #pragma unroll
+            for (int p = 0; p < kMaxManifold; p++) bs[k][p] = qf(r, R_BASE_SEP + p);
+#pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
                 if (p >= hd[k].pc) continue;
-                ps[k][p] = wave_slot(L);
-                const uint32_t* pr = prec(L, c, p, ps[k][p]);
+                const uint32_t* pr = prec(L, c, p, wave_slot(L));
                 ra[k][p] = q3(pr, PR_RA);
                 rb[k][p] = q3(pr, PR_RB);
-                bs[k][p] = qf(pr, PR_BASE_SEP);
             }
         }
 #pragma unroll
         for (int k = 0; k < kChunk; k++) {
             int c = c0 + k;
             if (c >= cc) continue;
+            float sep[kMaxManifold];
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
+                sep[p] = 0.0f;
                 if (p >= hd[k].pc) continue;
                 V3 ds = add(dp[k], sub(rot(dqb[k], rb[k][p]), rot(dqa[k], ra[k][p])));
-                qsf(prec(L, c, p, ps[k][p]), PR_SEP, dot(ds, n[k]) + bs[k][p]);
+                sep[p] = dot(ds, n[k]) + bs[k][p];
             }
+            uint32_t* r = crec(L, c, hd[k].slot);
+#pragma unroll
+            for (int p = 0; p < kMaxManifold; p++) qsf(r, R_SEP + p, sep[p]);
         }
     }
 }
@@ -1481,7 +1541,7 @@ B3D_FN void solve_rolling(V3 t1, V3 t2, float rolling, float total_n, M3 ia, M3 
 }
 
 /* The contact row as one solve needs it, loaded ahead of use. */
-struct CPoint { V3 ra, rb; float nmass, ni, tn, lever, sep; int slot; };
+struct CPoint { V3 ra, rb; float nmass, ni, tn, lever, sep; };
 struct CRow {
     int a, b, pc, flags, slot;
     V3 n;
@@ -1517,17 +1577,18 @@ B3D_FN void crow_load(const Lane& L, int c, CHead h, int relax, CRow* r) {
     r->rolling = qf(rc, R_ROLLING);
 #pragma unroll
     for (int p = 0; p < kMaxManifold; p++) {
-        if (p >= h.pc) continue;
         CPoint& q = r->pt[p];
-        q.slot = wave_slot(L);
-        const uint32_t* pr = prec(L, c, p, q.slot);
+        q.ni = 0.0f;
+        q.tn = 0.0f;
+        if (p >= h.pc) continue;
+        const uint32_t* pr = prec(L, c, p, wave_slot(L));
         q.ra = q3(pr, PR_RA);
         q.nmass = qf(pr, PR_NMASS);
         q.rb = q3(pr, PR_RB);
-        q.ni = qf(pr, PR_NI);
-        q.tn = qf(pr, PR_TN);
-        q.sep = qf(pr, PR_SEP);
         q.lever = relax ? qf(pr, PR_LEVER) : 0.0f;
+        q.sep = qf(rc, R_SEP + p);
+        q.ni = qf(rc, R_NI + 2 * p);
+        q.tn = qf(rc, R_TN + 2 * p);
     }
     if (relax) {
         r->fi.x = qf(rc, R_FI);
@@ -1573,9 +1634,8 @@ B3D_FN void crow_solve(const Lane& L, int c, CRow& r, float inv_h, float contact
         float dimp = -q.nmass * (mscale * vn + vbias) - iscale * q.ni;
         float nimp = maxf(q.ni + dimp, 0.0f);
         dimp = nimp - q.ni;
-        uint32_t* pr = prec(L, c, p, q.slot);
-        qsf(pr, PR_NI, nimp);
-        qsf(pr, PR_TN, q.tn + nimp);
+        q.ni = nimp;
+        q.tn = q.tn + nimp;
         total_n += nimp;
         twist_lim += q.lever * nimp;
         V3 P = scale(n, dimp);
@@ -1583,6 +1643,19 @@ B3D_FN void crow_solve(const Lane& L, int c, CRow& r, float inv_h, float contact
         wa = sub(wa, mv(r.ia, cross(q.ra, P)));
         vb = madd(vb, r.mb, P);
         wb = add(wb, mv(r.ib, cross(q.rb, P)));
+    }
+    /* the accumulated impulses go back as whole quads */
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        qsf(rc, R_NI + 2 * p, r.pt[p].ni);
+        qsf(rc, R_TN + 2 * p, r.pt[p].tn);
+    }
+    if (r.pc > 2) {
+#pragma unroll
+        for (int p = 2; p < kMaxManifold; p++) {
+            qsf(rc, R_NI + 2 * p, r.pt[p].ni);
+            qsf(rc, R_TN + 2 * p, r.pt[p].tn);
+        }
     }
     if (!use_bias) {
         float twist_s = dot(n, sub(wb, wa));
@@ -1672,6 +1745,7 @@ B3D_FN void apply_restitution(const Lane& L, float threshold) {
         for (int p = 0; p < kMaxManifold; p++)
             if (p < hd.pc) ps[p] = wave_slot(L);
         if (!(hd.flags & CF_RESTITUTION)) continue;
+        uint32_t* rw = crec(L, c, hd.slot);
         const uint32_t* r = crec(L, c, hd.slot);
         float e = qf(r, R_RESTITUTION);
         int a = hd.a, b = hd.b;
@@ -1683,18 +1757,18 @@ B3D_FN void apply_restitution(const Lane& L, float threshold) {
 #pragma unroll
         for (int p = 0; p < kMaxManifold; p++) {
             if (p >= hd.pc) continue;
-            uint32_t* pr = prec(L, c, p, ps[p]);
+            const uint32_t* pr = prec(L, c, p, ps[p]);
             float rv = qf(r, R_REL_VEL + p);
-            if (rv > -threshold || qf(pr, PR_TN) == 0.0f) continue;
+            if (rv > -threshold || qf(r, R_TN + 2 * p) == 0.0f) continue;
             V3 ra = q3(pr, PR_RA), rb = q3(pr, PR_RB);
             V3 vra = add(va, cross(wa, ra));
             V3 vrb = add(vb, cross(wb, rb));
             float vn = dot(sub(vrb, vra), n);
-            float old = qf(pr, PR_NI);
+            float old = qf(r, R_NI + 2 * p);
             float imp = -qf(pr, PR_NMASS) * (vn + e * rv);
             float nimp = maxf(old + imp, 0.0f);
             imp = nimp - old;
-            qsf(pr, PR_NI, nimp);
+            qsf(rw, R_NI + 2 * p, nimp);
             V3 P = scale(n, imp);
             va = msub(va, ma, P);
             wa = sub(wa, mv(ia, cross(ra, P)));
@@ -1736,9 +1810,8 @@ B3D_FN void contact_writeback(const Lane& L) {
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
                 if (p >= hd[k].pc) continue;
-                const uint32_t* pr = prec(L, c, p, wave_slot(L));
-                ni[k][p] = qf(pr, PR_NI);
-                tn[k][p] = qf(pr, PR_TN);
+                ni[k][p] = qf(r, R_NI + 2 * p);
+                tn[k][p] = qf(r, R_TN + 2 * p);
             }
             fi[k].x = qf(r, R_FI);
             fi[k].y = qf(r, R_FI + 1);

@@ -68,6 +68,9 @@ def b3_batch_apply_gpu(engine, force=None, torque=None, linear_impulse=None, mas
                                                    _ptr(mask), _stream(stream))
 
 
+B3_ENGINE_KEEP_SOLVER_FIELDS = 1
+
+
 class B3Engine:
     """A batch of worlds resident on the current HIP device."""
 
@@ -104,6 +107,10 @@ class B3Engine:
                 self._h = C.c_void_p()
         except Exception:
             pass
+
+    def set_options(self, options):
+        """B3_ENGINE_* option bits (KEEP_SOLVER_FIELDS)."""
+        self._check("b3_engine_set_options", self._lib.b3_engine_set_options(self._h, options))
 
     def set_snapshots(self, worlds):
         worlds = np.ascontiguousarray(worlds, dtype=self.dtype)

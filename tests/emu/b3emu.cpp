@@ -70,8 +70,13 @@ void emu_restore(uint32_t* tiles, const uint32_t* snap, int count, unsigned long
     }
 }
 
+/* Step options (kKeepSolverFields by default, so that whole worlds compare
+ * word for word with the oracle). */
+static unsigned int g_opts = kKeepSolverFields;
+void emu_set_options(unsigned int opts) { g_opts = opts; }
+
 static Lane lane_of(uint32_t* tiles, uint32_t* scratch, float* vel, const Geometry& g, int w) {
-    return lane_view(tiles, scratch, vel, g, w / kLanes, w % kLanes);
+    return lane_view(tiles, scratch, vel, g, w / kLanes, w % kLanes, g_opts);
 }
 
 void emu_step(uint32_t* tiles, int count, unsigned long long sig, float dt, int substeps,
