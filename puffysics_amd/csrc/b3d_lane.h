@@ -201,19 +201,26 @@ constexpr int O_SHAPE_A = 0, O_SHAPE_B = 1, O_POINT_COUNT = 2, O_FEATURE = 3, O_
  * pass so that the pair loop reads one record per shape and never follows
  * a body index.  The padded bounds go to LDS when they fit (or to the
  * scratch bounds area). */
-constexpr int SS_P = 0, SS_Q = 3, SS_RADIUS = 7, SS_HALF = 8, SS_TYPE = 11, SS_BODY = 12, SS_BFLAGS = 13,
-              SS_CENTER = 14, SS_CATEGORY = 17, SS_MASK = 19, SS_FRICTION = 21, SS_RESTITUTION = 22,
-              SS_ROLLING = 23, kShapeScr = 24;
+constexpr int SS_P = 0, SS_RADIUS = 3, SS_Q = 4, SS_HALF = 8, SS_TYPE = 11, SS_CENTER = 12, SS_BODY = 15,
+              SS_CATEGORY = 16, SS_MASK = 18, SS_BFLAGS = 20, SS_FRICTION = 21, SS_RESTITUTION = 22,
+              SS_ROLLING = 23, kShapeRows = 6;
 constexpr int kBodyStatic = 1, kBodyDynamic = 2;   /* SS_BFLAGS bits */
 /* Loops over bodies, shapes and contacts run in chunks, every load of a
  * chunk issued before any of its results is used. */
 constexpr int kChunk = 4;
 constexpr int kShapeChunk = 4;
-/* Per-step body record: the velocity increments of 09_step.inl:5-18 (all
- * their inputs are fixed for the step), the damping factors, and the body
- * kind (type and axis-lock flags). */
-constexpr int BS_DV = 0, BS_DW = 3, BS_LD = 6, BS_AD = 7, BS_KIND = 8, kBodyScr = 9;
-constexpr int kKindDynamic = 1 << 8, kKindStatic = 1 << 9;  /* BS_KIND bits; low byte = lock flags */
+/* Per-step body records: the velocity increments of 09_step.inl:5-18 (all
+ * their inputs are fixed for the step) and the damping factors (BS_*); the
+ * delta pose, which the step keeps here and commits in finalize, and the
+ * body kind (type and axis-lock flags) (BD_*). */
+constexpr int BS_DV = 0, BS_LD = 3, BS_DW = 4, BS_AD = 7, kBodyRows = 2;
+constexpr int BD_DP = 0, BD_KIND = 3, BD_DQ = 4, kDeltaRows = 2;
+constexpr int kKindDynamic = 1 << 8, kKindStatic = 1 << 9;  /* BD_KIND bits; low byte = lock flags */
+/* BD_KIND bits: the world's delta pose, force or torque words at the start
+ * of the step are not already the bits finalize writes (zero, identity), so
+ * finalize must write them (the writes are skipped when they would not
+ * change a bit). */
+constexpr int kKindClearDelta = 1 << 10, kKindClearForce = 1 << 11;
 /* Per-contact scratch head, written by the pair loop for prepare_contacts:
  * bodies (a | b << 16), point count and facts about the pair
  * (pc | flags << 8). */
@@ -271,9 +278,10 @@ struct Geometry {
     int max_b, max_s, max_c, max_j;
     int bo, so, co, jo;   /* word offsets of bodies, shapes, contacts, joints */
     int world_words;      /* words per world (sizeof(B3World) / 4) */
-    int scr_shape, scr_old, scr_sep, scr_joint, scr_body, scr_bounds, scr_cand;
+    int scr_old, scr_sep, scr_joint, scr_bounds, scr_cand;
     int scr_words;        /* per-lane scratch words (a multiple of 4) */
     int q_ct, q_pt;       /* first quad row of the contact and point records */
+    int q_body, q_delta, q_shape;  /* first quad row of the body, delta-pose and shape records */
     int tile_scr_words;   /* scratch words per tile: 64 lanes' words, then the quad rows */
 };
 
@@ -291,17 +299,18 @@ B3D_FN bool geometry_of(unsigned long long sig, Geometry* g, size_t* world_bytes
     g->co = (int)(L.contacts_off / 4);
     g->jo = (int)(L.joints_off / 4);
     g->world_words = (int)(L.world_size / 4);
-    g->scr_shape = 0;
-    g->scr_old = g->scr_shape + g->max_s * kShapeScr;
+    g->scr_old = 0;
     g->scr_sep = g->scr_old + g->max_c * kOldWords;
     g->scr_joint = g->scr_sep + g->max_c * kContactScr;
-    g->scr_body = g->scr_joint + g->max_j * kJointScr;
-    g->scr_bounds = g->scr_body + g->max_b * kBodyScr;
+    g->scr_bounds = g->scr_joint + g->max_j * kJointScr;
     g->scr_cand = g->scr_bounds + g->max_s * 6;
-    g->scr_words = (g->scr_cand + g->max_s * (g->max_s - 1) / 2 + 3) & ~3;
+    g->scr_words = (g->scr_cand + g->max_s * (g->max_s - 1) + 3) & ~3;
     g->q_ct = 0;
     g->q_pt = g->q_ct + g->max_c * kCRows;
-    int qrows = g->q_pt + g->max_c * kMaxManifold * kPRows;
+    g->q_body = g->q_pt + g->max_c * kMaxManifold * kPRows;
+    g->q_delta = g->q_body + g->max_b * kBodyRows;
+    g->q_shape = g->q_delta + g->max_b * kDeltaRows;
+    int qrows = g->q_shape + g->max_s * kShapeRows;
     g->tile_scr_words = g->scr_words * kLanes + qrows * kRowWords;
     *world_bytes = L.world_size;
     return true;
@@ -315,6 +324,8 @@ struct Lane {
     float* vel;     /* velocity rows + lane; before the velocities are
                        staged the same rows hold the clip polygons */
     int lane;
+    int sslot;          /* rank among the tile's stepping lanes: the slot of
+                           the body, delta-pose and shape records */
     unsigned int opts;  /* kKeepSolverFields */
     Geometry g;
 };
@@ -334,6 +345,7 @@ B3D_FN Lane lane_view(uint32_t* live, uint32_t* scratch, float* vel_rows, const 
         unsigned int opts = 0) {
     Lane L;
     L.opts = opts;
+    L.sslot = lane;
     L.w = live + (size_t)tile * g.world_words * kLanes + lane;
     L.scr = scratch ? scratch + (size_t)tile * g.tile_scr_words + lane : nullptr;
     L.sq = scratch ? scratch + (size_t)tile * g.tile_scr_words + (size_t)g.scr_words * kLanes : nullptr;
@@ -405,6 +417,21 @@ B3D_FN void qsf(uint32_t* r, int k, float v) { r[(k >> 2) * kRowWords + (k & 3)]
 B3D_FN void qsu(uint32_t* r, int k, uint32_t v) { r[(k >> 2) * kRowWords + (k & 3)] = v; }
 B3D_FN V3 q3(const uint32_t* r, int k) { return v3(qf(r, k), qf(r, k + 1), qf(r, k + 2)); }
 B3D_FN void qs3(uint32_t* r, int k, V3 v) { qsf(r, k, v.x); qsf(r, k + 1, v.y); qsf(r, k + 2, v.z); }
+B3D_FN Q qq(const uint32_t* r, int k) { return q4(qf(r, k), qf(r, k + 1), qf(r, k + 2), qf(r, k + 3)); }
+B3D_FN void qsq(uint32_t* r, int k, Q q) { qs3(r, k, q.v); qsf(r, k + 3, q.s); }
+B3D_FN uint64_t qu64(const uint32_t* r, int k) { return (uint64_t)qu(r, k) | ((uint64_t)qu(r, k + 1) << 32); }
+
+/* ---- packed word rows (word k of a record at quad row k / 4, word row
+ * k % 4 of it; slot s at column s) ---- */
+B3D_FN float rf(const uint32_t* r, int k) { return __builtin_bit_cast(float, r[(k >> 2) * kRowWords + (k & 3) * kLanes]); }
+B3D_FN uint32_t ru(const uint32_t* r, int k) { return r[(k >> 2) * kRowWords + (k & 3) * kLanes]; }
+B3D_FN void rsf(uint32_t* r, int k, float v) { r[(k >> 2) * kRowWords + (k & 3) * kLanes] = __builtin_bit_cast(uint32_t, v); }
+B3D_FN void rsu(uint32_t* r, int k, uint32_t v) { r[(k >> 2) * kRowWords + (k & 3) * kLanes] = v; }
+B3D_FN V3 r3(const uint32_t* r, int k) { return v3(rf(r, k), rf(r, k + 1), rf(r, k + 2)); }
+B3D_FN void rs3(uint32_t* r, int k, V3 v) { rsf(r, k, v.x); rsf(r, k + 1, v.y); rsf(r, k + 2, v.z); }
+B3D_FN Q rq4(const uint32_t* r, int k) { return q4(rf(r, k), rf(r, k + 1), rf(r, k + 2), rf(r, k + 3)); }
+B3D_FN void rsq(uint32_t* r, int k, Q q) { rs3(r, k, q.v); rsf(r, k + 3, q.s); }
+B3D_FN uint64_t ru64(const uint32_t* r, int k) { return (uint64_t)ru(r, k) | ((uint64_t)ru(r, k + 1) << 32); }
 
 
 B3D_FN int bw(const Lane& L, int b, int f) { return L.g.bo + b * kBodyWords + f; }
@@ -491,7 +518,9 @@ B3D_FN void shape_aabb(const Posed& P, V3* lo, V3* hi) {
     *hi = add(P.p, e);
 }
 
-B3D_FN uint32_t* shape_rec(const Lane& L, int s) { return L.scr + (L.g.scr_shape + s * kShapeScr) * kLanes; }
+B3D_FN uint32_t* shape_rec(const Lane& L, int s) {
+    return L.sq + (size_t)(L.g.q_shape + s * kShapeRows) * kRowWords + L.sslot;
+}
 B3D_FN uint32_t* old_rec(const Lane& L, int k) { return L.scr + (L.g.scr_old + k * kOldWords) * kLanes; }
 B3D_FN uint32_t* chead_rec(const Lane& L, int c) { return L.scr + (L.g.scr_sep + c * kContactScr) * kLanes; }
 /* Packed record of contact c and of its point p (see kCRows). */
@@ -568,8 +597,15 @@ B3D_FN void rec_store_masses(uint32_t* r, int flags, float ma, M3 ia, float mb, 
     }
 }
 B3D_FN uint32_t* joint_rec(const Lane& L, int j) { return L.scr + (L.g.scr_joint + j * kJointScr) * kLanes; }
-B3D_FN uint32_t* body_rec(const Lane& L, int b) { return L.scr + (L.g.scr_body + b * kBodyScr) * kLanes; }
+B3D_FN uint32_t* body_rec(const Lane& L, int b) {
+    return L.sq + (size_t)(L.g.q_body + b * kBodyRows) * kRowWords + L.sslot;
+}
+B3D_FN uint32_t* delta_rec(const Lane& L, int b) {
+    return L.sq + (size_t)(L.g.q_delta + b * kDeltaRows) * kRowWords + L.sslot;
+}
 B3D_FN uint32_t pair_key(int a, int b) { return a < b ? ((uint32_t)a << 16) | (uint32_t)b : ((uint32_t)b << 16) | (uint32_t)a; }
+/* Joint keys the pair loop keeps in registers (the rest it loads). */
+constexpr int kJointKeyRegs = 8;
 
 /* Shape pass: world pose, padded bounds and owning-body facts of every
  * shape (b3_shape_aabb plus the 0.02 pad, 08_contacts.inl:109-114).  The
@@ -618,19 +654,19 @@ B3D_FN void shape_pass(const Lane& L, int ns, float* bounds) {
             V3 lo, hi;
             shape_aabb(P[k], &lo, &hi);
             uint32_t* r = shape_rec(L, s);
-            st3(r, SS_P, P[k].p);
-            stq(r, SS_Q, P[k].q);
-            stf(r, SS_RADIUS, P[k].radius);
-            st3(r, SS_HALF, P[k].half);
-            sti(r, SS_TYPE, P[k].type);
-            sti(r, SS_BODY, b[k]);
-            sti(r, SS_BFLAGS, (btype[k] == kStatic ? kBodyStatic : 0) | (btype[k] == kDynamic ? kBodyDynamic : 0));
-            st3(r, SS_CENTER, center[k]);
+            rs3(r, SS_P, P[k].p);
+            rsf(r, SS_RADIUS, P[k].radius);
+            rsq(r, SS_Q, P[k].q);
+            rs3(r, SS_HALF, P[k].half);
+            rsu(r, SS_TYPE, (uint32_t)P[k].type);
+            rs3(r, SS_CENTER, center[k]);
+            rsu(r, SS_BODY, (uint32_t)b[k]);
 #pragma unroll
-            for (int f = 0; f < 4; f++) sti(r, SS_CATEGORY + f, (int)filt[k][f]);
-            stf(r, SS_FRICTION, mat[k][0]);
-            stf(r, SS_RESTITUTION, mat[k][1]);
-            stf(r, SS_ROLLING, mat[k][2]);
+            for (int f = 0; f < 4; f++) rsu(r, SS_CATEGORY + f, filt[k][f]);
+            rsu(r, SS_BFLAGS, (uint32_t)((btype[k] == kStatic ? kBodyStatic : 0) | (btype[k] == kDynamic ? kBodyDynamic : 0)));
+            rsf(r, SS_FRICTION, mat[k][0]);
+            rsf(r, SS_RESTITUTION, mat[k][1]);
+            rsf(r, SS_ROLLING, mat[k][2]);
             float* bd = bounds + s * 6 * kLanes;
             V3 l = sub(lo, pad), h = add(hi, pad);
             bd[0] = l.x;
@@ -645,11 +681,11 @@ B3D_FN void shape_pass(const Lane& L, int ns, float* bounds) {
 
 B3D_FN Posed posed_from(const uint32_t* r) {
     Posed P;
-    P.p = ld3(r, SS_P);
-    P.q = ldq(r, SS_Q);
-    P.radius = ldf(r, SS_RADIUS);
-    P.half = ld3(r, SS_HALF);
-    P.type = ldi(r, SS_TYPE);
+    P.p = r3(r, SS_P);
+    P.q = rq4(r, SS_Q);
+    P.radius = rf(r, SS_RADIUS);
+    P.half = r3(r, SS_HALF);
+    P.type = (int)ru(r, SS_TYPE);
     return P;
 }
 
@@ -740,14 +776,14 @@ struct PairShape {
 B3D_FN void pshape_load(const Lane& L, int s, PairShape* d) {
     const uint32_t* r = shape_rec(L, s);
     d->P = posed_from(r);
-    d->center = ld3(r, SS_CENTER);
-    d->body = ldi(r, SS_BODY);
-    d->bflags = ldi(r, SS_BFLAGS);
-    d->cat = ldu64(r, SS_CATEGORY);
-    d->mask = ldu64(r, SS_MASK);
-    d->friction = ldf(r, SS_FRICTION);
-    d->restitution = ldf(r, SS_RESTITUTION);
-    d->rolling = ldf(r, SS_ROLLING);
+    d->center = r3(r, SS_CENTER);
+    d->body = (int)ru(r, SS_BODY);
+    d->bflags = (int)ru(r, SS_BFLAGS);
+    d->cat = ru64(r, SS_CATEGORY);
+    d->mask = ru64(r, SS_MASK);
+    d->friction = rf(r, SS_FRICTION);
+    d->restitution = rf(r, SS_RESTITUTION);
+    d->rolling = rf(r, SS_ROLLING);
 }
 
 /* One old contact's warm-start data (the reference's B3Warm). */
@@ -795,47 +831,84 @@ B3D_FN void warm_apply(const OldWarm& o, NewContact* nc) {
  * shape bounds (LDS or scratch).
  *
  * First the bounds test of every pair i < j lists the overlapping pairs in
- * (i, j) order in scratch; then the list is walked with the next pair's
- * shape records in flight while the current pair is tested and collided.
- * When the old contact list is strictly sorted (every list the step writes
- * is), the warm-start lookup is a merge whose next old record is loaded as
- * soon as the previous one is consumed. */
+ * (i, j) order in scratch, each with the index of the old contact of the
+ * same shape pair when the old list is strictly sorted (every list the step
+ * writes is; the two sorted lists are merged).  Then the list is walked
+ * with the next pair's shape records and old contact in flight while the
+ * current pair is tested and collided. */
 B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int old_n, int sorted) {
     const Geometry& g = L.g;
     uint32_t* cand = L.scr + g.scr_cand * kLanes;
     int ncand = 0;
-    for (int i = 0; i < ns; i++) {
-        const float* bi = bounds + i * 6 * kLanes;
-        for (int j = i + 1; j < ns; j++) {
-            if (!overlaps(bi, bounds + j * 6 * kLanes)) continue;
-            sti(cand, ncand, (int)shape_key(i, j));
-            ncand++;
+    {
+        int op = 0;
+        uint32_t okey = sorted && old_n > 0 ? ldu(old_rec(L, 0), O_KEY) : 0xffffffffu;
+        for (int i = 0; i < ns; i++) {
+            const float* bi = bounds + i * 6 * kLanes;
+            for (int j0 = i + 1; j0 < ns; j0 += 4) {
+                bool ov[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) ov[k] = j0 + k < ns && overlaps(bi, bounds + (j0 + k) * 6 * kLanes);
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    if (!ov[k]) continue;
+                    uint32_t key = shape_key(i, j0 + k);
+                    int match = -1;
+                    if (sorted) {
+                        while (op < old_n && okey < key) {
+                            op++;
+                            okey = op < old_n ? ldu(old_rec(L, op), O_KEY) : 0xffffffffu;
+                        }
+                        if (op < old_n && okey == key) match = op;
+                    }
+                    sti(cand, 2 * ncand, (int)key);
+                    sti(cand, 2 * ncand + 1, match);
+                    ncand++;
+                }
+            }
         }
     }
     int cc = 0;
     int overflow = ldi(L.w, H_CONTACT_OVERFLOW);
     int dropped = ldi(L.w, H_CONTACTS_DROPPED);
-    int optr = 0;
-    OldWarm orec;
-    if (sorted && old_n > 0) old_load(L, 0, &orec);
+    /* the joint-connected body pairs, held in registers when there are few */
+    uint32_t jkey[kJointKeyRegs];
+#pragma unroll
+    for (int k = 0; k < kJointKeyRegs; k++) jkey[k] = k < nj ? ldu(joint_rec(L, k), JS_KEY) : 0xffffffffu;
     PairShape A, B, An, Bn;
+    OldWarm orec, orecn;
     uint32_t key = 0, key1 = 0;
+    int match = -1, match1 = -1;
     if (ncand > 0) {
         key = ldu(cand, 0);
+        match = ldi(cand, 1);
         pshape_load(L, (int)(key >> 16), &A);
         pshape_load(L, (int)(key & 0xffffu), &B);
+        if (match >= 0) old_load(L, match, &orec);
     }
-    if (ncand > 1) key1 = ldu(cand, 1);
+    if (ncand > 1) {
+        key1 = ldu(cand, 2);
+        match1 = ldi(cand, 3);
+    }
     for (int t = 0; t < ncand; t++) {
-        uint32_t key2 = t + 2 < ncand ? ldu(cand, t + 2) : 0u;
+        uint32_t key2 = 0;
+        int match2 = -1;
+        if (t + 2 < ncand) {
+            key2 = ldu(cand, 2 * (t + 2));
+            match2 = ldi(cand, 2 * (t + 2) + 1);
+        }
         if (t + 1 < ncand) {
             if ((key1 >> 16) != (key >> 16)) pshape_load(L, (int)(key1 >> 16), &An);
             else An = A;
             pshape_load(L, (int)(key1 & 0xffffu), &Bn);
+            if (match1 >= 0) old_load(L, match1, &orecn);
         }
         int i = (int)(key >> 16), j = (int)(key & 0xffffu);
+        uint32_t bkey = pair_key(A.body, B.body);
         int joined = 0;
-        for (int k = 0; k < nj; k++) joined |= ldu(joint_rec(L, k), JS_KEY) == pair_key(A.body, B.body);
+#pragma unroll
+        for (int k = 0; k < kJointKeyRegs; k++) joined |= jkey[k] == bkey;
+        for (int k = kJointKeyRegs; k < nj; k++) joined |= ldu(joint_rec(L, k), JS_KEY) == bkey;
         bool skip = A.body == B.body || (A.bflags & B.bflags & kBodyStatic) || (A.cat & B.mask) == 0
             || (B.cat & A.mask) == 0 || joined;
         Mani m;
@@ -864,17 +937,8 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
             nc.roll = zero3();
             /* warm start from the previous step's cache: every matching old
              * pair, the last one winning (08:154-170) */
-            uint32_t want = shape_key(i, j);
             if (sorted) {
-                while (optr < old_n && orec.key < want) {
-                    optr++;
-                    if (optr < old_n) old_load(L, optr, &orec);
-                }
-                if (optr < old_n && orec.key == want) {
-                    warm_apply(orec, &nc);
-                    optr++;
-                    if (optr < old_n) old_load(L, optr, &orec);
-                }
+                if (match >= 0) warm_apply(orec, &nc);
             } else {
                 for (int k = 0; k < old_n; k++) {
                     const uint32_t* o = old_rec(L, k);
@@ -923,8 +987,11 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
         }
         A = An;
         B = Bn;
+        orec = orecn;
         key = key1;
         key1 = key2;
+        match = match1;
+        match1 = match2;
     }
     sti(L.w, H_CONTACT_COUNT, cc);
     sti(L.w, H_CONTACT_OVERFLOW, overflow);
@@ -1012,9 +1079,11 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
                 imb[k] = ldf(w, bw(L, b[k], B_INV_MASS));
                 iwb[k] = ldm3(w, bw(L, b[k], B_INV_I_WORLD));
             }
-            dqa[k] = ldq(w, bw(L, a[k], B_DELTA_ROT));
-            dqb[k] = ldq(w, bw(L, b[k], B_DELTA_ROT));
-            dp[k] = sub(ld3(w, bw(L, b[k], B_DELTA_POS)), ld3(w, bw(L, a[k], B_DELTA_POS)));
+            const uint32_t* da = delta_rec(L, a[k]);
+            const uint32_t* db = delta_rec(L, b[k]);
+            dqa[k] = rq4(da, BD_DQ);
+            dqb[k] = rq4(db, BD_DQ);
+            dp[k] = sub(r3(db, BD_DP), r3(da, BD_DP));
             n[k] = ld3(w, cw(L, c, C_NORMAL));
             t1[k] = ld3(w, cw(L, c, C_TANGENT1));
 #pragma unroll
@@ -1342,8 +1411,8 @@ B3D_FN void warm_start_joints(const Lane& L) {
     const uint32_t* w = L.w;
     for (int i = 0; i < nj; i++) {
         int a = ldi(w, jw(L, i, J_BODY_A)), b = ldi(w, jw(L, i, J_BODY_B));
-        V3 ra = rot(ldq(w, bw(L, a, B_DELTA_ROT)), ld3(w, jw(L, i, J_FRAME_P_A)));
-        V3 rb = rot(ldq(w, bw(L, b, B_DELTA_ROT)), ld3(w, jw(L, i, J_FRAME_P_B)));
+        V3 ra = rot(rq4(delta_rec(L, a), BD_DQ), ld3(w, jw(L, i, J_FRAME_P_A)));
+        V3 rb = rot(rq4(delta_rec(L, b), BD_DQ), ld3(w, jw(L, i, J_FRAME_P_B)));
         V3 lin = ld3(w, jw(L, i, J_LINEAR_IMPULSE));
         V3 ang = ld3(w, jw(L, i, J_ANGULAR_IMPULSE));
         if (ldi(w, jw(L, i, J_TYPE)) == kJointRevolute) {
@@ -1408,9 +1477,11 @@ B3D_FN void contact_geometry(const Lane& L) {
             if (c >= cc) continue;
             const uint32_t* r = crec(L, c, hd[k].slot);
             n[k] = q3(r, R_N);
-            dqa[k] = ldq(w, bw(L, hd[k].a, B_DELTA_ROT));
-            dqb[k] = ldq(w, bw(L, hd[k].b, B_DELTA_ROT));
-            dp[k] = sub(ld3(w, bw(L, hd[k].b, B_DELTA_POS)), ld3(w, bw(L, hd[k].a, B_DELTA_POS)));
+            const uint32_t* da = delta_rec(L, hd[k].a);
+            const uint32_t* db = delta_rec(L, hd[k].b);
+            dqa[k] = rq4(da, BD_DQ);
+            dqb[k] = rq4(db, BD_DQ);
+            dp[k] = sub(r3(db, BD_DP), r3(da, BD_DP));
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) bs[k][p] = qf(r, R_BASE_SEP + p);
 #pragma unroll
@@ -1466,10 +1537,12 @@ B3D_FN void joint_geometry(const Lane& L) {
         for (int k = 0; k < kPrepChunk; k++) {
             int j = j0 + k;
             if (j >= nj) continue;
-            dqa[k] = ldq(w, bw(L, a[k], B_DELTA_ROT));
-            dqb[k] = ldq(w, bw(L, b[k], B_DELTA_ROT));
-            dpa[k] = ld3(w, bw(L, a[k], B_DELTA_POS));
-            dpb[k] = ld3(w, bw(L, b[k], B_DELTA_POS));
+            const uint32_t* da = delta_rec(L, a[k]);
+            const uint32_t* db = delta_rec(L, b[k]);
+            dqa[k] = rq4(da, BD_DQ);
+            dqb[k] = rq4(db, BD_DQ);
+            dpa[k] = r3(da, BD_DP);
+            dpb[k] = r3(db, BD_DP);
             fqa[k] = ldq(w, jw(L, j, J_FRAME_Q_A));
             fqb[k] = ldq(w, jw(L, j, J_FRAME_Q_B));
             fpa[k] = ld3(w, jw(L, j, J_FRAME_P_A));
@@ -2143,9 +2216,10 @@ B3D_FN void solve_joints(const Lane& L, float h, float inv_h, int use_bias) {
     }
 }
 
-/* Per-step body record (see BS_*): the velocity increments of gravity and
- * the applied force / torque and the damping factors of 09_step.inl:5-18,
- * whose inputs do not change during a step. */
+/* Per-step body records: the velocity increments of gravity and the
+ * applied force / torque and the damping factors of 09_step.inl:5-18, whose
+ * inputs do not change during a step (BS_*), and the body kind and the
+ * step's starting delta pose (BD_*). */
 B3D_FN void body_prepass(const Lane& L, float h) {
     uint32_t* w = L.w;
     V3 g = ld3(w, H_GRAVITY);
@@ -2154,12 +2228,15 @@ B3D_FN void body_prepass(const Lane& L, float h) {
         int type[kChunk];
         uint32_t flags[kChunk];
         float inv_mass[kChunk], lin_d[kChunk], ang_d[kChunk], gscale[kChunk];
-        V3 force[kChunk], torque[kChunk];
+        V3 force[kChunk], torque[kChunk], dp[kChunk];
         M3 iw[kChunk];
+        Q dq[kChunk];
 #pragma unroll
         for (int k = 0; k < kChunk; k++) {
             int b = b0 + k;
             if (b >= nb) continue;
+            dp[k] = ld3(w, bw(L, b, B_DELTA_POS));
+            dq[k] = ldq(w, bw(L, b, B_DELTA_ROT));
             type[k] = ldi(w, bw(L, b, B_TYPE));
             flags[k] = ldu(w, bw(L, b, B_FLAGS));
             inv_mass[k] = ldf(w, bw(L, b, B_INV_MASS));
@@ -2175,15 +2252,26 @@ B3D_FN void body_prepass(const Lane& L, float h) {
             int b = b0 + k;
             if (b >= nb) continue;
             uint32_t* r = body_rec(L, b);
+            uint32_t* d = delta_rec(L, b);
             int kind = (int)(flags[k] & 0xffu) | (type[k] == kDynamic ? kKindDynamic : 0)
                 | (type[k] == kStatic ? kKindStatic : 0);
-            sti(r, BS_KIND, kind);
+            uint32_t dbits = __builtin_bit_cast(uint32_t, dp[k].x) | __builtin_bit_cast(uint32_t, dp[k].y)
+                | __builtin_bit_cast(uint32_t, dp[k].z) | __builtin_bit_cast(uint32_t, dq[k].v.x)
+                | __builtin_bit_cast(uint32_t, dq[k].v.y) | __builtin_bit_cast(uint32_t, dq[k].v.z)
+                | (__builtin_bit_cast(uint32_t, dq[k].s) ^ 0x3f800000u);
+            uint32_t fbits = __builtin_bit_cast(uint32_t, force[k].x) | __builtin_bit_cast(uint32_t, force[k].y)
+                | __builtin_bit_cast(uint32_t, force[k].z) | __builtin_bit_cast(uint32_t, torque[k].x)
+                | __builtin_bit_cast(uint32_t, torque[k].y) | __builtin_bit_cast(uint32_t, torque[k].z);
+            kind |= (dbits ? kKindClearDelta : 0) | (fbits ? kKindClearForce : 0);
+            rs3(d, BD_DP, dp[k]);
+            rsu(d, BD_KIND, (uint32_t)kind);
+            rsq(d, BD_DQ, dq[k]);
             if (type[k] != kDynamic) continue;
             float gs = inv_mass[k] > 0.0f ? gscale[k] : 0.0f;
-            st3(r, BS_DV, add(scale(force[k], h * inv_mass[k]), scale(g, h * gs)));
-            st3(r, BS_DW, scale(mv(iw[k], torque[k]), h));
-            stf(r, BS_LD, 1.0f / (1.0f + h * lin_d[k]));
-            stf(r, BS_AD, 1.0f / (1.0f + h * ang_d[k]));
+            rs3(r, BS_DV, add(scale(force[k], h * inv_mass[k]), scale(g, h * gs)));
+            rsf(r, BS_LD, 1.0f / (1.0f + h * lin_d[k]));
+            rs3(r, BS_DW, scale(mv(iw[k], torque[k]), h));
+            rsf(r, BS_AD, 1.0f / (1.0f + h * ang_d[k]));
         }
     }
 }
@@ -2200,11 +2288,11 @@ B3D_FN void integrate_velocities(const Lane& L) {
             int b = b0 + k;
             if (b >= nb) continue;
             const uint32_t* r = body_rec(L, b);
-            kind[k] = ldi(r, BS_KIND);
-            dv[k] = ld3(r, BS_DV);
-            dw[k] = ld3(r, BS_DW);
-            ld[k] = ldf(r, BS_LD);
-            ad[k] = ldf(r, BS_AD);
+            kind[k] = (int)ru(delta_rec(L, b), BD_KIND);
+            dv[k] = r3(r, BS_DV);
+            dw[k] = r3(r, BS_DW);
+            ld[k] = rf(r, BS_LD);
+            ad[k] = rf(r, BS_AD);
         }
 #pragma unroll
         for (int k = 0; k < kChunk; k++) {
@@ -2232,9 +2320,10 @@ B3D_FN void integrate_positions(const Lane& L, float h, float inv_dt) {
         for (int k = 0; k < kChunk; k++) {
             int b = b0 + k;
             if (b >= nb) continue;
-            kind[k] = ldi(body_rec(L, b), BS_KIND);
-            dp[k] = ld3(w, bw(L, b, B_DELTA_POS));
-            dq[k] = ldq(w, bw(L, b, B_DELTA_ROT));
+            const uint32_t* d = delta_rec(L, b);
+            kind[k] = (int)ru(d, BD_KIND);
+            dp[k] = r3(d, BD_DP);
+            dq[k] = rq4(d, BD_DQ);
         }
 #pragma unroll
         for (int k = 0; k < kChunk; k++) {
@@ -2254,18 +2343,22 @@ B3D_FN void integrate_positions(const Lane& L, float h, float inv_dt) {
             if (w2 > max_ang2 && w2 > 0.0f) av = scale(av, rsqrt_scale(max_ang, w2));
             set_vlin(L, b, v);
             set_vang(L, b, av);
-            st3(w, bw(L, b, B_DELTA_POS), madd(dp[k], h, v));
-            stq(w, bw(L, b, B_DELTA_ROT), qintegrate(dq[k], scale(av, h)));
+            uint32_t* d = delta_rec(L, b);
+            rs3(d, BD_DP, madd(dp[k], h, v));
+            rsu(d, BD_KIND, (uint32_t)kind[k]);
+            rsq(d, BD_DQ, qintegrate(dq[k], scale(av, h)));
         }
     }
 }
 
-/* Commit the accumulated deltas and clear forces (09_step.inl:109-130). */
+/* Commit the accumulated deltas and clear forces (09_step.inl:109-130);
+ * delta pose, force and torque words already zero (identity) are left
+ * alone. */
 B3D_FN void finalize(const Lane& L) {
     uint32_t* w = L.w;
     int nb = body_count(L);
     for (int b0 = 0; b0 < nb; b0 += kChunk) {
-        int type[kChunk];
+        int type[kChunk], kind[kChunk];
         V3 center[kChunk], dp[kChunk], lc[kChunk], inv_i[kChunk];
         Q dq[kChunk], rq[kChunk];
 #pragma unroll
@@ -2274,8 +2367,10 @@ B3D_FN void finalize(const Lane& L) {
             if (b >= nb) continue;
             type[k] = ldi(w, bw(L, b, B_TYPE));
             center[k] = ld3(w, bw(L, b, B_CENTER));
-            dp[k] = ld3(w, bw(L, b, B_DELTA_POS));
-            dq[k] = ldq(w, bw(L, b, B_DELTA_ROT));
+            const uint32_t* d = delta_rec(L, b);
+            kind[k] = (int)ru(d, BD_KIND);
+            dp[k] = r3(d, BD_DP);
+            dq[k] = rq4(d, BD_DQ);
             rq[k] = ldq(w, bw(L, b, B_ROTATION));
             lc[k] = ld3(w, bw(L, b, B_LOCAL_CENTER));
             inv_i[k] = ld3(w, bw(L, b, B_INV_INERTIA));
@@ -2289,10 +2384,14 @@ B3D_FN void finalize(const Lane& L) {
             st3(w, bw(L, b, B_CENTER), c);
             stq(w, bw(L, b, B_ROTATION), r);
             st3(w, bw(L, b, B_POSITION), sub(c, rot(r, lc[k])));
-            st3(w, bw(L, b, B_DELTA_POS), zero3());
-            stq(w, bw(L, b, B_DELTA_ROT), qid());
-            st3(w, bw(L, b, B_FORCE), zero3());
-            st3(w, bw(L, b, B_TORQUE), zero3());
+            if (kind[k] & kKindClearDelta) {
+                st3(w, bw(L, b, B_DELTA_POS), zero3());
+                stq(w, bw(L, b, B_DELTA_ROT), qid());
+            }
+            if (kind[k] & kKindClearForce) {
+                st3(w, bw(L, b, B_FORCE), zero3());
+                st3(w, bw(L, b, B_TORQUE), zero3());
+            }
             if (type[k] == kDynamic) stm3(w, bw(L, b, B_INV_I_WORLD), world_inv_i(r, inv_i[k]));
         }
     }
@@ -2301,8 +2400,10 @@ B3D_FN void finalize(const Lane& L) {
 /* One world's b3_step (09_step.inl:148-264, default configuration).  Body
  * velocities are staged in the velocity rows after contact generation (which
  * uses the same rows for clip polygons) and written back at the end. */
-B3D_FN void step_world(const Lane& L, float dt, int substeps) {
+B3D_FN void step_world(const Lane& L0, float dt, int substeps) {
     if (!(dt > 0.0f)) return;
+    Lane L = L0;
+    L.sslot = wave_slot(L);
     int subs = substeps < 1 ? 1 : substeps;
     float h = dt / (float)subs;
     float inv_dt = 1.0f / dt;
