@@ -37,6 +37,20 @@ _engine = None
 _scenes = None
 
 
+def _torch_runtime_first():
+    """Initialise torch's HIP runtime before a library of this package loads
+    the system one.  PyTorch ships its own copy of the HIP runtime; when the
+    system runtime is loaded into the process first, calls through it fail
+    with hipErrorNoDevice once torch has initialised the GPU.  Without a GPU
+    (or without torch) this does nothing."""
+    try:
+        import torch
+    except ImportError:
+        return
+    if torch.cuda.is_available():
+        torch.cuda.init()
+
+
 def engine_lib():
     """The engine library, loaded once; raises if it has not been built."""
     global _engine
@@ -44,6 +58,7 @@ def engine_lib():
         if not os.path.exists(ENGINE_PATH):
             raise RuntimeError("%s is missing: run __graft_entry__.build()" % ENGINE_PATH)
         from .b3types import B3Batch
+        _torch_runtime_first()
         lib = C.CDLL(ENGINE_PATH)
         for name, res, args in ENGINE_SYMBOLS:
             fn = getattr(lib, name)

@@ -260,3 +260,61 @@ class EmuSig:
         out = np.zeros(self.count, dtype=self.dtype)
         emu().emu_download(self.tiles.ctypes.data, self.count, self.sig, out.ctypes.data)
         return out
+
+
+# ---- the hover environment (oracle and, where built, the reference task) ----
+
+HOVER_OBS = 3
+
+
+def hover_actions(n, steps, seed=5):
+    """Actions of a hover run: the three levels and the values at and just
+    below the level thresholds (hover_task.h:69)."""
+    rng = np.random.default_rng(seed)
+    vals = np.array([0.0, 1.0, 2.0, 0.49, 0.5, 1.49, 1.5, -1.0, 3.0], np.float32)
+    return rng.choice(vals, size=(steps, n)).astype(np.float32)
+
+
+def _hover_bind(lib, p):
+    getattr(lib, p + "_env_bytes").restype = C.c_size_t
+    getattr(lib, p + "_signature").restype = C.c_ulonglong
+    getattr(lib, p + "_init").argtypes = [_vp, _i, _f, _f, _f, _i, _i, C.c_uint32]
+    getattr(lib, p + "_reset").argtypes = [_vp, _i, _vp, _vp, _vp]
+    getattr(lib, p + "_step").argtypes = [_vp, _i, _vp, _vp, _vp, _vp]
+    getattr(lib, p + "_log").argtypes = [_vp, _i, _vp]
+    getattr(lib, p + "_world").argtypes = [_vp, _i, _vp]
+
+
+def hover_cpu_run(lib, prefix, n, actions, seed=1, config=(2.0, 10.0, 1.0 / 60.0, 4, 256)):
+    """Run the CPU hover envs of `lib` (`ohover` oracle or `rhover`
+    reference): init, reset, then one step per row of `actions`.  Returns
+    observations (steps+1, n, 3), rewards and terminals (steps+1, n), the
+    summed log and the final worlds' bytes."""
+    _hover_bind(lib, prefix)
+    f = lambda s: getattr(lib, prefix + s)
+    steps = len(actions)
+    envs = np.zeros(f("_env_bytes")() * n, np.uint8)
+    f("_init")(envs.ctypes.data, n, *config, seed)
+    obs = np.zeros((steps + 1, n, HOVER_OBS), np.float32)
+    rew = np.zeros((steps + 1, n), np.float32)
+    term = np.zeros((steps + 1, n), np.float32)
+    f("_reset")(envs.ctypes.data, n, obs[0].ctypes.data, rew[0].ctypes.data, term[0].ctypes.data)
+    for t in range(steps):
+        a = np.ascontiguousarray(actions[t], np.float32)
+        f("_step")(envs.ctypes.data, n, a.ctypes.data, obs[t + 1].ctypes.data, rew[t + 1].ctypes.data,
+                   term[t + 1].ctypes.data)
+    log = np.zeros(5, np.float32)
+    f("_log")(envs.ctypes.data, n, log.ctypes.data)
+    sig = f("_signature")()
+    from puffysics_amd.b3types import world_dtype
+    dt = world_dtype(sig)
+    worlds = np.zeros(n, dt)
+    for i in range(n):
+        f("_world")(envs.ctypes.data, i, worlds[i:i + 1].ctypes.data)
+    return obs, rew, term, log, worlds
+
+
+def hover_ref_lib():
+    """oracle/_ref/libhover_ref.so (the reference's hover task), or None."""
+    path = os.path.join(ROOT, "oracle", "_ref", "libhover_ref.so")
+    return C.CDLL(path) if os.path.exists(path) else None

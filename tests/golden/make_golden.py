@@ -22,7 +22,7 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "tests"))
 
-from b3test import ref_lib  # noqa: E402
+from b3test import hover_actions, hover_cpu_run, hover_ref_lib, ref_lib  # noqa: E402
 from puffysics_amd import scenes  # noqa: E402
 
 # scene -> (worlds, checkpoints in vector steps)
@@ -53,5 +53,29 @@ def main():
         print("%s: %d worlds, checkpoints %s, %d bytes" % (path, count, checkpoints, os.path.getsize(path)))
 
 
+# hover: envs, steps, observation checkpoints (every OBS_EVERY steps)
+HOVER = (32, 300)
+OBS_EVERY = 25
+
+
+def hover():
+    """The reference's hover task (oracle/_ref/libhover_ref.so) driven like
+    its PufferLib adapter: init with seed 1, reset, 300 steps of seeded
+    actions.  Rewards and terminals of every step, observations every 25
+    steps, the summed log and the final worlds."""
+    lib = hover_ref_lib()
+    if lib is None:
+        raise SystemExit("oracle/_ref/libhover_ref.so missing: run make -C oracle ref")
+    n, steps = HOVER
+    actions = hover_actions(n, steps)
+    obs, rew, term, log, worlds = hover_cpu_run(lib, "rhover", n, actions)
+    keep = np.arange(0, steps + 1, OBS_EVERY)
+    path = os.path.join(HERE, "hover.npz")
+    np.savez_compressed(path, actions=actions, rewards=rew, terminals=term, obs_steps=keep, observations=obs[keep],
+                        log=log, worlds=worlds.view(np.uint8).reshape(n, -1))
+    print("%s: %d envs, %d steps, %d episode ends, %d bytes" % (path, n, steps, int(term.sum()), os.path.getsize(path)))
+
+
 if __name__ == "__main__":
     main()
+    hover()
