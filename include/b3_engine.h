@@ -115,6 +115,35 @@ hipError_t b3_engine_device_view(const B3Engine* engine, void** tiles, size_t* w
 #define B3_ENGINE_KEEP_SOLVER_FIELDS 1u
 hipError_t b3_engine_set_options(B3Engine* engine, unsigned int options);
 
+/* ---- per-substep force laws ----
+ * The reference's optional force hook B3_USER_FORCES (01_config.inl:189-198,
+ * 09_step.inl:20-53) is a macro compiled into the step: once per substep,
+ * before the velocity update, it may add to each body's applied force and
+ * torque; that substep integrates the sums, and the applied values are
+ * restored for the next substep.  This library compiles its laws into the
+ * step kernel the same way, one entry point per law; each is
+ * b3_batch_step_gpu (same masks, fused restore, validation and errors) with
+ * the law in the hook. */
+
+/* Plummer-softened gravity between the bodies of each world
+ * (nbody_rigid.cuh:15-66; NbodyConfig, nbody.cuh:40-46).  For each pair
+ * i < j of bodies with nonzero masses, at least one of them dynamic,
+ *   r = c_j - c_i,  f = r * (gravity * m_i * m_j / (|r|^2 + softening^2)^1.5)
+ * is added to a dynamic i and subtracted from a dynamic j, where c is the
+ * body's current center (center + delta_pos, as the hook reads poses).
+ * `masses` is NULL or a device array [world][body] over the engine's body
+ * capacity of gravitational masses >= 0 (the world-major `masses` of
+ * b3_nbody_step_kernel, nbody_rigid.cuh:110-119); NULL uses 1 / inv_mass
+ * for dynamic bodies and 0 for the rest (b3_nbody_masses,
+ * nbody_rigid.cuh:14-33).  The law needs gravity >= 0 and softening > 0
+ * (nbody_cfg_ok, nbody.cuh:44-46), else hipErrorInvalidValue. */
+typedef struct B3GravityLaw {
+    float gravity;
+    float softening;
+} B3GravityLaw;
+hipError_t b3_batch_step_gravity_gpu(B3Engine* engine, float dt, int substeps, const unsigned char* step_mask,
+    const unsigned char* reset_mask, B3GravityLaw law, const float* masses, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1355,7 +1355,54 @@ static void o_solve_joints(OWorld* w, b3r h, b3r inv_h, int use_bias) {         
 /* Integration and the step driver: src/puffysics/09_step.inl           */
 /* ------------------------------------------------------------------ */
 
-static void o_integrate_velocities(OWorld* w, b3r h) {                                   /* :5-18, 41-53 */
+/* A force law in the B3_USER_FORCES hook (01_config.inl:189-198): it adds
+ * to the bodies' applied forces and torques of the world it is given. */
+typedef struct OForceLaw {
+    void (*apply)(const struct OForceLaw* law, OWorld* w, b3r h);
+    b3r gravity, softening;   /* o_gravity_law */
+    const float* masses;      /* o_gravity_law: this world's masses, or NULL */
+} OForceLaw;
+
+/* Plummer-softened gravity between the world's bodies (nbody_rigid.cuh:
+ * 15-66: b3_nbody_masses and b3_nbody_accumulate), with the sources at the
+ * current centers, center + delta_pos, as the hook reads poses
+ * (01_config.inl:189-192). */
+static void o_gravity_law(const OForceLaw* f, OWorld* w, b3r h) {
+    (void)h;
+    int n = w->h->body_count;
+    b3r masses[n > 0 ? n : 1];
+    for (int i = 0; i < n; i++) {                                                        /* :14-33 */
+        OBody* b = &w->bodies[i];
+        b3r one = 1.0f;
+        masses[i] = f->masses ? f->masses[i] : (b->type == B3_DYNAMIC && b->inv_mass > 0 ? one / b->inv_mass : 0);
+    }
+    b3r eps2 = f->softening * f->softening;                                              /* :35-66 */
+    for (int i = 0; i < n; i++) {
+        if (masses[i] == 0) continue;
+        OBody* a = &w->bodies[i];
+        for (int j = i + 1; j < n; j++) {
+            OBody* b = &w->bodies[j];
+            if (masses[j] == 0 || (a->type != B3_DYNAMIC && b->type != B3_DYNAMIC)) continue;
+            OV3 r = o_sub(o_add(b->center, b->delta_pos), o_add(a->center, a->delta_pos));
+            b3r q = o_dot(r, r) + eps2;
+            b3r one = 1.0f;
+            b3r inv = one / o_sqrt(q);
+            OV3 force = o_scale(r, f->gravity * masses[i] * masses[j] * inv * inv * inv);
+            if (a->type == B3_DYNAMIC) a->force = o_add(a->force, force);
+            if (b->type == B3_DYNAMIC) b->force = o_sub(b->force, force);
+        }
+    }
+}
+
+static void o_integrate_velocities(OWorld* w, b3r h, const OForceLaw* law) {             /* :5-18, 20-53 */
+    OV3 saved_force[law ? w->h->body_count + 1 : 1], saved_torque[law ? w->h->body_count + 1 : 1];
+    if (law) {                                                                           /* :25-31 */
+        for (int i = 0; i < w->h->body_count; i++) {
+            saved_force[i] = w->bodies[i].force;
+            saved_torque[i] = w->bodies[i].torque;
+        }
+        law->apply(law, w, h);
+    }
     OV3 g = w->h->gravity;
     for (int i = 0; i < w->h->body_count; i++) {
         OBody* b = &w->bodies[i];
@@ -1368,6 +1415,12 @@ static void o_integrate_velocities(OWorld* w, b3r h) {                          
         b->lin_vel = o_madd(dv, ld, b->lin_vel);
         OV3 dw = o_scale(o_mv(b->inv_i_world, b->torque), h);
         b->ang_vel = o_madd(dw, ad, b->ang_vel);
+    }
+    if (law) {                                                                           /* :33-38 */
+        for (int i = 0; i < w->h->body_count; i++) {
+            w->bodies[i].force = saved_force[i];
+            w->bodies[i].torque = saved_torque[i];
+        }
     }
 }
 
@@ -1411,7 +1464,7 @@ static void o_finalize(OWorld* w) {                                             
     }
 }
 
-static void o_step(OWorld* w, b3r dt, int substeps) {                                    /* :148-264 */
+static void o_step(OWorld* w, b3r dt, int substeps, const OForceLaw* law) {              /* :148-264 */
     if (dt <= 0.0f) return;
     int subs = substeps < 1 ? 1 : substeps;
     b3r one = 1.0f;
@@ -1435,7 +1488,7 @@ static void o_step(OWorld* w, b3r dt, int substeps) {                           
     o_warm_start_joints(w);
     /* b3_step_sub :167-181 */
     for (int s = 0; s < subs; s++) {
-        o_integrate_velocities(w, h);
+        o_integrate_velocities(w, h, law);
         o_solve_contacts(w, inv_h, w->h->contact_speed, 1);
         o_solve_joints(w, h, inv_h, 1);
         o_integrate_positions(w, h, inv_dt, w->h->max_linear_speed);
@@ -1458,7 +1511,15 @@ size_t ocpu_world_size(unsigned long long sig) {
 void ocpu_step(void* world, unsigned long long sig, float dt, int substeps) {
     OWorld w;
     if (!o_view(&w, world, sig)) return;
-    o_step(&w, dt, substeps);
+    o_step(&w, dt, substeps, NULL);
+}
+
+void ocpu_step_gravity(void* world, unsigned long long sig, float dt, int substeps, float gravity,
+        float softening, const float* masses) {
+    OWorld w;
+    if (!o_view(&w, world, sig)) return;
+    OForceLaw law = {o_gravity_law, gravity, softening, masses};
+    o_step(&w, dt, substeps, &law);
 }
 
 void ocpu_find_contacts(void* world, unsigned long long sig) {

@@ -24,6 +24,12 @@ extern "C" {
 size_t ocpu_world_size(unsigned long long sig);
 /* b3_step on one world (09_step.inl:262-264). */
 void ocpu_step(void* world, unsigned long long sig, float dt, int substeps);
+/* b3_step with a force law in the B3_USER_FORCES hook (01_config.inl:
+ * 189-198, 09_step.inl:20-53): Plummer-softened gravity between the
+ * world's bodies (nbody_rigid.cuh:15-66) at their current centers.
+ * `masses` is NULL (1 / inv_mass of dynamic bodies) or body_count floats. */
+void ocpu_step_gravity(void* world, unsigned long long sig, float dt, int substeps, float gravity,
+    float softening, const float* masses);
 /* b3_find_contacts alone (08_contacts.inl:64-173). */
 void ocpu_find_contacts(void* world, unsigned long long sig);
 /* b3_batch_step (b3_batch.cuh:39-48): 1 on success, 0 on invalid input. */

@@ -14,7 +14,8 @@ ENGINE_PATH = os.path.join(HERE, "libb3engine.so")
 SCENES_PATH = os.path.join(HERE, "libb3scenes.so")
 
 # (name, restype, argtypes) of every C-ABI entry point in include/b3_engine.h
-# and include/b3_workload.h.
+# and include/b3_workload.h; None and strings stand for the structs of
+# b3types.py passed by value (None: B3Batch).
 _vp, _i, _ull, _f, _sz = C.c_void_p, C.c_int, C.c_ulonglong, C.c_float, C.c_size_t
 ENGINE_SYMBOLS = [
     ("b3_engine_create", _i, [C.POINTER(C.c_void_p), None, _ull]),
@@ -29,6 +30,7 @@ ENGINE_SYMBOLS = [
     ("b3_batch_stats_gpu", _i, [_vp, _vp, _vp]),
     ("b3_engine_device_view", _i, [_vp, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]),
     ("b3_engine_set_options", _i, [_vp, C.c_uint]),
+    ("b3_batch_step_gravity_gpu", _i, [_vp, _f, _i, _vp, _vp, "B3GravityLaw", _vp, _vp]),
     ("b3w_masks_gpu", _i, [_i, _ull, _i, _i, _vp, _vp, _vp]),
     ("b3w_inputs_gpu", _i, [_vp, _i, _ull, _i, _vp, _vp]),
 ]
@@ -57,13 +59,14 @@ def engine_lib():
     if _engine is None:
         if not os.path.exists(ENGINE_PATH):
             raise RuntimeError("%s is missing: run __graft_entry__.build()" % ENGINE_PATH)
-        from .b3types import B3Batch
+        from . import b3types
         _torch_runtime_first()
         lib = C.CDLL(ENGINE_PATH)
         for name, res, args in ENGINE_SYMBOLS:
             fn = getattr(lib, name)
             fn.restype = res
-            fn.argtypes = [B3Batch if a is None else a for a in args]
+            fn.argtypes = [b3types.B3Batch if a is None else getattr(b3types, a) if isinstance(a, str) else a
+                           for a in args]
         _engine = lib
     return _engine
 

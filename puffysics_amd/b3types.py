@@ -108,6 +108,11 @@ class B3Batch(C.Structure):
     _fields_ = [("data", C.c_void_p), ("stride", C.c_size_t), ("world_offset", C.c_size_t), ("count", C.c_int)]
 
 
+class B3GravityLaw(C.Structure):
+    """Pairwise gravity law of b3_batch_step_gravity_gpu (NbodyConfig, nbody.cuh:40-46)."""
+    _fields_ = [("gravity", C.c_float), ("softening", C.c_float)]
+
+
 def signature(bodies, shapes, contacts, joints):
     """B3_CONFIG_SIGNATURE for a capacity set."""
     return bodies | (shapes << 16) | (contacts << 32) | (joints << 48)

@@ -76,30 +76,6 @@ __global__ __launch_bounds__(kXposeThreads) void b3k_download(const uint32_t* __
     }
 }
 
-/* ---- masked restore ---- */
-
-/* Restore the resetting worlds of this workgroup's tile from the snapshots,
- * which are kept as plain B3World structs (AoS): one world at a time, the 64
- * lanes read 64 consecutive snapshot words and write them to their rows of
- * the tile. */
-__device__ void restore_tile(uint32_t* live, const uint32_t* snap, const Geometry& g, int count,
-        const unsigned char* reset) {
-    int tile = blockIdx.x;
-    int w = tile * 64 + (int)threadIdx.x;
-    int want = w < count && reset[w] != 0;
-    uint64_t bits = __ballot(want);
-    uint32_t* lt = live + (size_t)tile * g.world_words * 64;
-    while (bits) {
-        int l = __builtin_ctzll(bits);
-        bits &= bits - 1;
-        const uint32_t* src = snap + (size_t)(tile * 64 + l) * g.world_words;
-        int lo[3], hi[3];
-        restore_ranges(g, (int)src[H_CONTACT_COUNT], lo, hi);
-        for (int r = 0; r < 3; r++)
-            for (int k = lo[r] + (int)threadIdx.x; k < hi[r]; k += 64) lt[(size_t)k * 64 + l] = src[k];
-    }
-}
-
 __global__ __launch_bounds__(64) void b3k_restore(uint32_t* live, const uint32_t* snap, Geometry g, int count,
         const unsigned char* reset) {
     restore_tile(live, snap, g, count, reset);
@@ -220,13 +196,6 @@ unsigned char* gather(const B3Batch& b, size_t world_bytes) {
         memcpy(buf + (size_t)i * world_bytes,
             (const unsigned char*)b.data + (size_t)i * b.stride + b.world_offset, world_bytes);
     return buf;
-}
-
-hipError_t on_device(const B3Engine* e) {
-    int dev = -1;
-    hipError_t err = hipGetDevice(&dev);
-    if (err != hipSuccess) return err;
-    return dev == e->device ? hipSuccess : hipErrorInvalidDevice;
 }
 
 /* Host AoS buffer -> staging -> tiles (dst). */

@@ -24,4 +24,38 @@ struct B3Engine {
     unsigned int options;    /* B3_ENGINE_* step options */
 };
 
+/* The engine's device is the current one. */
+inline hipError_t on_device(const B3Engine* e) {
+    int dev = -1;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    return dev == e->device ? hipSuccess : hipErrorInvalidDevice;
+}
+
+namespace b3d {
+
+/* Restore the resetting worlds of this workgroup's tile from the snapshots,
+ * which are kept as plain B3World structs (AoS): one world at a time, the 64
+ * lanes read 64 consecutive snapshot words and write them to their rows of
+ * the tile. */
+__device__ inline void restore_tile(uint32_t* live, const uint32_t* snap, const Geometry& g, int count,
+        const unsigned char* reset) {
+    int tile = blockIdx.x;
+    int w = tile * 64 + (int)threadIdx.x;
+    int want = w < count && reset[w] != 0;
+    uint64_t bits = __ballot(want);
+    uint32_t* lt = live + (size_t)tile * g.world_words * 64;
+    while (bits) {
+        int l = __builtin_ctzll(bits);
+        bits &= bits - 1;
+        const uint32_t* src = snap + (size_t)(tile * 64 + l) * g.world_words;
+        int lo[3], hi[3];
+        restore_ranges(g, (int)src[H_CONTACT_COUNT], lo, hi);
+        for (int r = 0; r < 3; r++)
+            for (int k = lo[r] + (int)threadIdx.x; k < hi[r]; k += 64) lt[(size_t)k * 64 + l] = src[k];
+    }
+}
+
+}  // namespace b3d
+
 #endif

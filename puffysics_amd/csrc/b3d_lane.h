@@ -2397,10 +2397,81 @@ B3D_FN void finalize(const Lane& L) {
     }
 }
 
-/* One world's b3_step (09_step.inl:148-264, default configuration).  Body
- * velocities are staged in the velocity rows after contact generation (which
- * uses the same rows for clip polygons) and written back at the end. */
-B3D_FN void step_world(const Lane& L0, float dt, int substeps) {
+/* ---- per-substep force laws: the B3_USER_FORCES hook ----
+ * 01_config.inl:189-198 and 09_step.inl:20-53: once per substep, before the
+ * velocity update, a force law may add to each body's applied force and
+ * torque; the velocity update uses the sums, and the applied force and
+ * torque are back to their own values for the next substep.  A law here is
+ * a type with `static constexpr bool kActive = true` and
+ *     B3D_FN void operator()(const ForceView& v) const;
+ * built once per world by the kernel that runs it (so it can hold that
+ * world's parameters and state).  The view reads the state of the substep
+ * as the reference's hook reads the world: start-of-step center, rotation
+ * and position with the current delta pose (current center = center +
+ * delta_pos, current rotation = delta_rot * rotation), current velocities,
+ * and any other world word through `L`. */
+struct ForceView {
+    Lane L;
+    float h;
+    B3D_MFN int body_count() const { return b3d::body_count(L); }
+    B3D_MFN int type(int b) const { return ldi(L.w, bw(L, b, B_TYPE)); }
+    B3D_MFN float inv_mass(int b) const { return ldf(L.w, bw(L, b, B_INV_MASS)); }
+    B3D_MFN V3 center(int b) const { return ld3(L.w, bw(L, b, B_CENTER)); }
+    B3D_MFN V3 position(int b) const { return ld3(L.w, bw(L, b, B_POSITION)); }
+    B3D_MFN Q rotation(int b) const { return ldq(L.w, bw(L, b, B_ROTATION)); }
+    B3D_MFN V3 delta_pos(int b) const { return r3(delta_rec(L, b), BD_DP); }
+    B3D_MFN Q delta_rot(int b) const { return rq4(delta_rec(L, b), BD_DQ); }
+    B3D_MFN V3 lin_vel(int b) const { return vlin(L, b); }
+    B3D_MFN V3 ang_vel(int b) const { return vang(L, b); }
+    /* The force and torque the velocity update of this substep uses. */
+    B3D_MFN V3 force(int b) const { return r3(body_rec(L, b), BS_DV); }
+    B3D_MFN V3 torque(int b) const { return r3(body_rec(L, b), BS_DW); }
+    B3D_MFN void set_force(int b, V3 f) const { rs3(body_rec(L, b), BS_DV, f); }
+    B3D_MFN void set_torque(int b, V3 t) const { rs3(body_rec(L, b), BS_DW, t); }
+};
+
+/* The law of a step without a hook (B3_HAS_USER_FORCES 0). */
+struct NoForces {
+    static constexpr bool kActive = false;
+    B3D_MFN void operator()(const ForceView&) const {}
+};
+
+/* b3_integrate_velocities with the hook (09_step.inl:5-18, 20-53): the
+ * body records' force and torque words take each body's applied force and
+ * torque, the law adds to them, and the update of 09_step.inl:5-18 runs on
+ * the sums; the world's own force and torque words are never touched. */
+template <class Law>
+B3D_FN void integrate_velocities_law(const Lane& L, float h, const Law& law) {
+    uint32_t* w = L.w;
+    int nb = body_count(L);
+    for (int b = 0; b < nb; b++) {
+        uint32_t* r = body_rec(L, b);
+        rs3(r, BS_DV, ld3(w, bw(L, b, B_FORCE)));
+        rs3(r, BS_DW, ld3(w, bw(L, b, B_TORQUE)));
+    }
+    ForceView v;
+    v.L = L;
+    v.h = h;
+    law(v);
+    V3 g = ld3(w, H_GRAVITY);
+    for (int b = 0; b < nb; b++) {
+        if (!(ru(delta_rec(L, b), BD_KIND) & kKindDynamic)) continue;
+        const uint32_t* r = body_rec(L, b);
+        float inv_mass = ldf(w, bw(L, b, B_INV_MASS));
+        float gs = inv_mass > 0.0f ? ldf(w, bw(L, b, B_GRAVITY_SCALE)) : 0.0f;
+        V3 dv = add(scale(r3(r, BS_DV), h * inv_mass), scale(g, h * gs));
+        V3 dw = scale(mv(ldm3(w, bw(L, b, B_INV_I_WORLD)), r3(r, BS_DW)), h);
+        set_vlin(L, b, madd(dv, rf(r, BS_LD), vlin(L, b)));
+        set_vang(L, b, madd(dw, rf(r, BS_AD), vang(L, b)));
+    }
+}
+
+/* One world's b3_step (09_step.inl:148-264, default configuration), with
+ * the force law `law` in the B3_USER_FORCES hook.  Body velocities are
+ * staged in the velocity rows after contact generation (which uses the
+ * same rows for clip polygons) and written back at the end. */
+template <class Law>
+B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
     if (!(dt > 0.0f)) return;
     Lane L = L0;
     L.sslot = wave_slot(L);
@@ -2424,7 +2495,10 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps) {
     warm_start_joints(L);
     joint_geometry(L);   /* the contacts' initial separations come from prepare_contacts */
     for (int s = 0; s < subs; s++) {
-        integrate_velocities(L);
+        if constexpr (Law::kActive)
+            integrate_velocities_law(L, h, law);
+        else
+            integrate_velocities(L);
         solve_contacts(L, inv_h, contact_speed, 1, cs, ss);
         solve_joints(L, h, inv_h, 1);
         integrate_positions(L, h, inv_dt);
@@ -2437,6 +2511,9 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps) {
     finalize(L);
     vel_store(L);
 }
+
+/* b3_step without a hook. */
+B3D_FN void step_world(const Lane& L, float dt, int substeps) { step_world(L, dt, substeps, NoForces()); }
 
 }  // namespace b3d
 

@@ -22,9 +22,12 @@
 #ifdef __HIPCC__
 #include <hip/hip_runtime.h>
 #define B3D_FN __host__ __device__ static inline __attribute__((always_inline))
+#define B3D_MFN __host__ __device__ inline __attribute__((always_inline))
 #else
 #define B3D_FN static inline __attribute__((always_inline))
+#define B3D_MFN inline __attribute__((always_inline))
 #endif
+/* B3D_FN for free functions, B3D_MFN for member functions. */
 
 namespace b3d {
 

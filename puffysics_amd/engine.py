@@ -14,7 +14,7 @@ import ctypes as C
 import numpy as np
 
 from . import _native
-from .b3types import B3StepStats, batch_of, world_dtype
+from .b3types import B3GravityLaw, B3StepStats, batch_of, world_dtype
 
 HIP_SUCCESS = 0
 HIP_ERROR_INVALID_VALUE = 1
@@ -66,6 +66,17 @@ def b3_batch_apply_gpu(engine, force=None, torque=None, linear_impulse=None, mas
     """Dense b3_apply_force / b3_apply_torque / b3_apply_linear_impulse (09_step.inl:132-146)."""
     return _native.engine_lib().b3_batch_apply_gpu(engine, _ptr(force), _ptr(torque), _ptr(linear_impulse),
                                                    _ptr(mask), _stream(stream))
+
+
+def b3_batch_step_gravity_gpu(engine, dt, substeps, gravity, softening, masses=None, step_mask=None,
+                              reset_mask=None, stream=None):
+    """b3_batch_step_gpu with Plummer-softened pairwise gravity between each
+    world's bodies in the per-substep force hook (B3_USER_FORCES,
+    01_config.inl:189-198; nbody_rigid.cuh:15-66).  `masses` is None or a
+    [worlds, max_bodies] float32 device tensor of gravitational masses."""
+    return _native.engine_lib().b3_batch_step_gravity_gpu(engine, dt, substeps, _ptr(step_mask), _ptr(reset_mask),
+                                                          B3GravityLaw(gravity, softening), _ptr(masses),
+                                                          _stream(stream))
 
 
 B3_ENGINE_KEEP_SOLVER_FIELDS = 1
@@ -129,6 +140,11 @@ class B3Engine:
 
     def step(self, dt, substeps, step_mask=None, reset_mask=None, stream=None):
         self._check("b3_batch_step_gpu", b3_batch_step_gpu(self._h, dt, substeps, step_mask, reset_mask, stream))
+
+    def step_gravity(self, dt, substeps, gravity, softening, masses=None, step_mask=None, reset_mask=None,
+                     stream=None):
+        self._check("b3_batch_step_gravity_gpu", b3_batch_step_gravity_gpu(
+            self._h, dt, substeps, gravity, softening, masses, step_mask, reset_mask, stream))
 
     def restore(self, reset=None, stream=None):
         self._check("b3_batch_restore_gpu", b3_batch_restore_gpu(self._h, reset, stream))

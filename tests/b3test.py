@@ -238,6 +238,35 @@ def oracle_step_batch(worlds, sig, dt, substeps, active=None):
                                None if act is None else act.ctypes.data)
 
 
+def oracle_step_gravity(worlds, sig, dt, substeps, gravity, softening, masses=None, active=None):
+    """b3_step with pairwise gravity in the force hook, world by world on
+    the oracle; `masses` is None or [count, max_bodies] float32."""
+    lib = oracle()
+    lib.ocpu_step_gravity.argtypes = [_vp, _ull, _f, _i, _f, _f, _vp]
+    m = None if masses is None else np.ascontiguousarray(masses, np.float32)
+    for k in range(len(worlds)):
+        if active is not None and not active[k]:
+            continue
+        lib.ocpu_step_gravity(worlds[k:k + 1].ctypes.data, sig, dt, substeps, gravity, softening,
+                              None if m is None else m[k].ctypes.data)
+
+
+def ref_gravity_lib(caps):
+    """The reference's b3_step with its B3_USER_FORCES hook running the
+    reference's pairwise gravity, for capacity set `caps` (0, 2, 4 or 5), or
+    None where the reference was not built."""
+    path = os.path.join(REF_DIR, "libb3ref_gravity_%d.so" % caps)
+    if not os.path.exists(path):
+        return None
+    key = "gravity_%d" % caps
+    if key not in _refs:
+        lib = C.CDLL(path)
+        lib.refg_sig.restype = C.c_ulonglong
+        lib.refg_step.argtypes = [_vp, _f, _i, _f, _f, _vp]
+        _refs[key] = lib
+    return _refs[key]
+
+
 class EmuSig:
     """Word-transposed tiles of any signature stepped by the host build of
     the lane code, without scene inputs."""
@@ -255,6 +284,15 @@ class EmuSig:
         act = None if active is None else np.ascontiguousarray(active, np.uint8)
         emu().emu_step(self.tiles.ctypes.data, self.count, self.sig, dt, substeps,
                        None if act is None else act.ctypes.data)
+
+    def step_gravity(self, dt, substeps, gravity, softening, masses=None, active=None):
+        lib = emu()
+        lib.emu_step_gravity.argtypes = [_vp, _i, _ull, _f, _i, _vp, _f, _f, _vp]
+        act = None if active is None else np.ascontiguousarray(active, np.uint8)
+        m = None if masses is None else np.ascontiguousarray(masses, np.float32)
+        lib.emu_step_gravity(self.tiles.ctypes.data, self.count, self.sig, dt, substeps,
+                             None if act is None else act.ctypes.data, gravity, softening,
+                             None if m is None else m.ctypes.data)
 
     def worlds(self):
         out = np.zeros(self.count, dtype=self.dtype)

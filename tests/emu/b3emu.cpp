@@ -14,6 +14,7 @@
 #include <string.h>
 #include <vector>
 
+#include "b3d_forces.h"
 #include "b3d_inputs.h"
 #include "b3d_lane.h"
 
@@ -91,6 +92,26 @@ void emu_step(uint32_t* tiles, int count, unsigned long long sig, float dt, int 
         if (step_mask && !step_mask[w]) continue;
         Lane L = lane_of(tiles, scratch.data(), vel.data(), g, w);
         step_world(L, dt, substeps);
+    }
+}
+
+/* emu_step with pairwise gravity in the force hook; `masses` is NULL or
+ * count * max_bodies floats. */
+void emu_step_gravity(uint32_t* tiles, int count, unsigned long long sig, float dt, int substeps,
+        const unsigned char* step_mask, float gravity, float softening, const float* masses) {
+    Geometry g;
+    size_t wb;
+    if (!geometry_of(sig, &g, &wb)) return;
+    int ntiles = (count + kLanes - 1) / kLanes;
+    std::vector<uint32_t> scratch((size_t)ntiles * g.tile_scr_words);
+    std::vector<float> vel((size_t)lds_rows(g) * kLanes);
+    for (int w = 0; w < count; w++) {
+        if (step_mask && !step_mask[w]) continue;
+        GravityLaw law;
+        law.gravity = gravity;
+        law.softening = softening;
+        law.masses = masses ? masses + (size_t)w * g.max_b : nullptr;
+        step_world(lane_of(tiles, scratch.data(), vel.data(), g, w), dt, substeps, law);
     }
 }
 
