@@ -226,6 +226,9 @@ constexpr int kKindClearDelta = 1 << 10, kKindClearForce = 1 << 11;
  * (pc | flags << 8). */
 constexpr int CH_AB = 0, CH_INFO = 1, kContactScr = 2;
 constexpr int CF_DYN_A = 1, CF_DYN_B = 2, CF_STATIC = 4, CF_RESTITUTION = 8, CF_ROLLING = 16;
+/* Per-lane step flags (scratch word scr_flags, written by the pair loop):
+ * some contact of the world has restitution. */
+constexpr int kLaneRestitution = 1;
 
 /* Packed contact records.  Past the per-lane words, a tile's scratch is
  * quad rows: 64 slots of 4 words (1 KB).  Contact c of a lane owns kCRows
@@ -247,14 +250,13 @@ constexpr int R_AB = 0, R_INFO = 1, R_FRICTION = 2, R_TWIST_MASS = 3,   /* row 0
               R_FI = 40, R_TWIST = 42, R_RESTITUTION = 43,              /* row 10 */
               R_ROLL = 44,                                              /* row 11 */
               R_REL_VEL = 48,                                           /* row 12: restitution only */
-              R_SEP = 52,                                               /* row 13: point separations */
-              R_BASE_SEP = 56,                                          /* row 14 */
-              R_NI = 60, R_TN = 61,                                     /* rows 15-16: point p at +2p */
-              kCRows = 17;
+              R_BASE_SEP = 52,                                          /* row 13: point base separations */
+              R_NI = 56, R_TN = 57,                                     /* rows 14-15: point p at +2p */
+              kCRows = 16;
 /* Point records: anchors, normal mass and twist lever.  A contact's
- * per-point values that change during the step (separation, accumulated
- * impulses) sit in whole rows of the contact record, so that each update
- * writes full quads. */
+ * per-point values that change during the step (the accumulated impulses)
+ * sit in whole rows of the contact record, so that each update writes full
+ * quads. */
 constexpr int PR_RA = 0, PR_NMASS = 3, PR_RB = 4, PR_LEVER = 7, kPRows = 2;
 /* Joint record in scratch: the joint-connection key, the head written by
  * prepare_joints (bodies a | b << 16 and JF_* flags), then everything that
@@ -278,7 +280,7 @@ struct Geometry {
     int max_b, max_s, max_c, max_j;
     int bo, so, co, jo;   /* word offsets of bodies, shapes, contacts, joints */
     int world_words;      /* words per world (sizeof(B3World) / 4) */
-    int scr_old, scr_sep, scr_joint, scr_bounds, scr_cand;
+    int scr_old, scr_sep, scr_joint, scr_bounds, scr_cand, scr_flags;
     int scr_words;        /* per-lane scratch words (a multiple of 4) */
     int q_ct, q_pt;       /* first quad row of the contact and point records */
     int q_body, q_delta, q_shape;  /* first quad row of the body, delta-pose and shape records */
@@ -304,7 +306,8 @@ B3D_FN bool geometry_of(unsigned long long sig, Geometry* g, size_t* world_bytes
     g->scr_joint = g->scr_sep + g->max_c * kContactScr;
     g->scr_bounds = g->scr_joint + g->max_j * kJointScr;
     g->scr_cand = g->scr_bounds + g->max_s * 6;
-    g->scr_words = (g->scr_cand + g->max_s * (g->max_s - 1) + 3) & ~3;
+    g->scr_flags = g->scr_cand + g->max_s * (g->max_s - 1);
+    g->scr_words = (g->scr_flags + 1 + 3) & ~3;
     g->q_ct = 0;
     g->q_pt = g->q_ct + g->max_c * kCRows;
     g->q_body = g->q_pt + g->max_c * kMaxManifold * kPRows;
@@ -365,6 +368,20 @@ B3D_FN int wave_slot(const Lane& L) {
     return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 #else
     return L.lane;
+#endif
+}
+
+/* `v` holds in some active lane of the wave (on the host: in this lane).
+ * Call where all of the tile's stepping lanes run: code that computes
+ * record slots (wave_slot) must run in every lane that owns the record, so
+ * a lane may only leave such code out when its whole wave does. */
+B3D_FN bool wave_any(const Lane& L, bool v) {
+#ifdef __HIP_DEVICE_COMPILE__
+    (void)L;
+    return __ballot(v) != 0;
+#else
+    (void)L;
+    return v;
 #endif
 }
 
@@ -869,6 +886,7 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
         }
     }
     int cc = 0;
+    int rest_any = 0;
     int overflow = ldi(L.w, H_CONTACT_OVERFLOW);
     int dropped = ldi(L.w, H_CONTACTS_DROPPED);
     /* the joint-connected body pairs, held in registers when there are few */
@@ -976,6 +994,7 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
             int info = (A.bflags & kBodyDynamic ? CF_DYN_A : 0) | (B.bflags & kBodyDynamic ? CF_DYN_B : 0)
                 | (!((A.bflags & B.bflags) & kBodyDynamic) ? CF_STATIC : 0) | (restitution != 0.0f ? CF_RESTITUTION : 0)
                 | (!(rolling <= 0.0f) ? CF_ROLLING : 0);
+            rest_any |= info & CF_RESTITUTION;
             uint32_t* hd = chead_rec(L, cc);
             sti(hd, CH_AB, A.body | (B.body << 16));
             sti(hd, CH_INFO, nc.count | (info << 8));
@@ -996,6 +1015,7 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
     sti(L.w, H_CONTACT_COUNT, cc);
     sti(L.w, H_CONTACT_OVERFLOW, overflow);
     sti(L.w, H_CONTACTS_DROPPED, dropped);
+    sti(L.scr + L.g.scr_flags * kLanes, 0, rest_any ? kLaneRestitution : 0);
 }
 
 /* Contact generation and warm start: b3_find_contacts (08_contacts.inl:
@@ -1024,16 +1044,33 @@ B3D_FN void find_contacts(const Lane& L) {
     }
 }
 
+/* b3_apply_impulse (08:184-192) on staged velocities: impulse s * p at
+ * lever r, dynamic bodies only. */
+B3D_FN void apply_impulse(const Lane& L, int b, float m, M3 i, V3 r, V3 p, float s) {
+    if (!is_dyn_flag(L, b)) return;
+    set_vlin(L, b, madd(vlin(L, b), s * m, p));
+    set_vang(L, b, add(vang(L, b), mv(i, scale(cross(r, p), s))));
+}
+
 /* b3_prepare_one_contact (08:234-291) for every new contact, two contacts
  * at a time: their heads, then their bodies and points, then the math.  The
  * prepared fields go to the world's contact rows and, with everything else
  * the solver reads, to the contact's packed record, whose point separations
- * start at the step's initial delta poses. */
+ * start at the step's initial delta poses.
+ *
+ * The warm start of the contacts (08:194-232) applies their impulses in
+ * contact order after all are prepared; preparation reads body velocities
+ * only for the relative normal velocities, which only restitution and the
+ * kept solver fields use.  A world with neither gets each contact's warm
+ * start right after its preparation, with the same impulses in the same
+ * order, and the function returns 1 (0: warm_start_contacts still to run). */
 constexpr int kPrepChunk = 2;
-B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
+B3D_FN int prepare_contacts(const Lane& L, Soft cs, Soft ss) {
     uint32_t* w = L.w;
     int cc = ldi(w, H_CONTACT_COUNT);
     const float inv_tau = 1.0f / kSpeculative;
+    const int keep = (L.opts & kKeepSolverFields) != 0;
+    const int fuse = !keep && !(ldi(L.scr + L.g.scr_flags * kLanes, 0) & kLaneRestitution);
     for (int c0 = 0; c0 < cc; c0 += kPrepChunk) {
         int a[kPrepChunk], b[kPrepChunk], pc[kPrepChunk], fl[kPrepChunk], slot[kPrepChunk];
         int pslot[kPrepChunk][kMaxManifold];
@@ -1050,8 +1087,7 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
         }
         float ima[kPrepChunk], imb[kPrepChunk];
         M3 iwa[kPrepChunk], iwb[kPrepChunk];
-        V3 n[kPrepChunk], t1[kPrepChunk], ra[kPrepChunk][kMaxManifold], rb[kPrepChunk][kMaxManifold], dp[kPrepChunk];
-        Q dqa[kPrepChunk], dqb[kPrepChunk];
+        V3 n[kPrepChunk], t1[kPrepChunk], ra[kPrepChunk][kMaxManifold], rb[kPrepChunk][kMaxManifold];
         float bs[kPrepChunk][kMaxManifold], ni[kPrepChunk][kMaxManifold];
         float fric[kPrepChunk], rest[kPrepChunk], roll_c[kPrepChunk], tw[kPrepChunk];
         V2 fi[kPrepChunk];
@@ -1079,11 +1115,6 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
                 imb[k] = ldf(w, bw(L, b[k], B_INV_MASS));
                 iwb[k] = ldm3(w, bw(L, b[k], B_INV_I_WORLD));
             }
-            const uint32_t* da = delta_rec(L, a[k]);
-            const uint32_t* db = delta_rec(L, b[k]);
-            dqa[k] = rq4(da, BD_DQ);
-            dqb[k] = rq4(db, BD_DQ);
-            dp[k] = sub(r3(db, BD_DP), r3(da, BD_DP));
             n[k] = ld3(w, cw(L, c, C_NORMAL));
             t1[k] = ld3(w, cw(L, c, C_TANGENT1));
 #pragma unroll
@@ -1104,19 +1135,24 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
             /* zero unless the body is dynamic (08:236-241) */
             float ma = ima[k], mb = imb[k];
             M3 ia = iwa[k], ib = iwb[k];
-            V3 va = vlin(L, a[k]), wa = vang(L, a[k]);
-            V3 vb = vlin(L, b[k]), wb = vang(L, b[k]);
+            const int need_rv = keep || (fl[k] & CF_RESTITUTION);
+            V3 va = zero3(), wa = zero3(), vb = zero3(), wb = zero3();
+            if (need_rv) {
+                va = vlin(L, a[k]);
+                wa = vang(L, a[k]);
+                vb = vlin(L, b[k]);
+                wb = vang(L, b[k]);
+            }
             /* tangent2 = tangent1 x normal as written by b3_contact_from_mani */
             V3 t2 = cross(t1[k], n[k]);
             V3 center_a = zero3(), center_b = zero3();
             float wsum = 0.0f;
-            float rel_vel[kMaxManifold], nmass[kMaxManifold], sep0[kMaxManifold], bsp[kMaxManifold],
+            float rel_vel[kMaxManifold], nmass[kMaxManifold], bsp[kMaxManifold],
                 nip[kMaxManifold];
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
                 rel_vel[p] = 0.0f;
                 nmass[p] = 0.0f;
-                sep0[p] = 0.0f;
                 bsp[p] = 0.0f;
                 nip[p] = 0.0f;
                 if (p >= pc[k]) continue;
@@ -1125,18 +1161,16 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
                 V3 rn_b = cross(rbp, n[k]);
                 float kn = ma + mb + dot(rn_a, mv(ia, rn_a)) + dot(rn_b, mv(ib, rn_b));
                 nmass[p] = kn > 0.0f ? 1.0f / kn : 0.0f;
-                V3 vra = add(va, cross(wa, rap));
-                V3 vrb = add(vb, cross(wb, rbp));
-                rel_vel[p] = dot(n[k], sub(vrb, vra));
+                if (need_rv) {
+                    V3 vra = add(va, cross(wa, rap));
+                    V3 vrb = add(vb, cross(wb, rbp));
+                    rel_vel[p] = dot(n[k], sub(vrb, vra));
+                }
                 float sep = bs[k][p] + dot(sub(rbp, rap), n[k]);
                 float weight = clampf(2.0f - sep * inv_tau, kMinFrictionW, 1.0f);
                 center_a = madd(center_a, weight, rap);
                 center_b = madd(center_b, weight, rbp);
                 wsum += weight;
-                /* the solver's separation at the initial delta poses (the
-                 * reference's per-row form, 08_contacts.inl:331-333) */
-                V3 ds = add(dp[k], sub(rot(dqb[k], rbp), rot(dqa[k], rap)));
-                sep0[p] = dot(ds, n[k]) + bs[k][p];
                 bsp[p] = bs[k][p];
                 nip[p] = ni[k][p];
             }
@@ -1211,7 +1245,6 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
             }
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
-                qsf(r, R_SEP + p, sep0[p]);
                 qsf(r, R_BASE_SEP + p, bsp[p]);
             }
 #pragma unroll
@@ -1226,8 +1259,25 @@ B3D_FN void prepare_contacts(const Lane& L, Soft cs, Soft ss) {
                     qsf(r, R_TN + 2 * p, 0.0f);
                 }
             }
+            if (fuse) {
+                /* warm_start_contacts' impulses for this contact */
+#pragma unroll
+                for (int p = 0; p < kMaxManifold; p++) {
+                    if (p >= pc[k]) continue;
+                    V3 P = scale(n[k], nip[p]);
+                    apply_impulse(L, a[k], ma, ia, ra[k][p], P, -1.0f);
+                    apply_impulse(L, b[k], mb, ib, rb[k][p], P, 1.0f);
+                }
+                V3 f = add(scale(t1[k], fi[k].x), scale(t2, fi[k].y));
+                apply_impulse(L, a[k], ma, ia, center_a, f, -1.0f);
+                apply_impulse(L, b[k], mb, ib, center_b, f, 1.0f);
+                V3 tr = add(scale(n[k], tw[k]), roll[k]);
+                if (is_dyn_flag(L, a[k])) set_vang(L, a[k], sub(vang(L, a[k]), mv(ia, tr)));
+                if (is_dyn_flag(L, b[k])) set_vang(L, b[k], add(vang(L, b[k]), mv(ib, tr)));
+            }
         }
     }
+    return fuse;
 }
 
 /* b3_prepare_joints (06_joints.inl:161-202), plus the hinge axis through
@@ -1335,16 +1385,11 @@ B3D_FN void prepare_joints(const Lane& L, float h) {
     }
 }
 
-/* b3_apply_impulse (08:184-192) on staged velocities. */
-B3D_FN void apply_impulse(const Lane& L, int b, float m, M3 i, V3 r, V3 p, float s) {
-    if (!is_dyn_flag(L, b)) return;
-    set_vlin(L, b, madd(vlin(L, b), s * m, p));
-    set_vang(L, b, add(vang(L, b), mv(i, scale(cross(r, p), s))));
-}
-
 /* b3_warm_start over contacts (08:194-232, 293-313), two contacts at a
- * time: heads, then records, then the impulses in contact order. */
-B3D_FN void warm_start_contacts(const Lane& L) {
+ * time: heads, then records, then the impulses in contact order.  Lanes
+ * whose warm start ran inside prepare_contacts (`done`) only take part in
+ * the record slots' ranks. */
+B3D_FN void warm_start_contacts(const Lane& L, int done) {
     int cc = ldi(L.w, H_CONTACT_COUNT);
     for (int c0 = 0; c0 < cc; c0 += kPrepChunk) {
         CHead hd[kPrepChunk];
@@ -1363,13 +1408,19 @@ B3D_FN void warm_start_contacts(const Lane& L) {
         for (int k = 0; k < kPrepChunk; k++) {
             int c = c0 + k;
             if (c >= cc) continue;
+            /* every lane with the point takes part in its slot's rank */
+            int ps[kMaxManifold];
+#pragma unroll
+            for (int p = 0; p < kMaxManifold; p++)
+                if (p < hd[k].pc) ps[p] = wave_slot(L);
+            if (done) continue;
             const uint32_t* r = crec(L, c, hd[k].slot);
             rec_masses(r, hd[k].flags, &ma[k], &ia[k], &mb[k], &ib[k]);
             n[k] = q3(r, R_N);
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
                 if (p >= hd[k].pc) continue;
-                const uint32_t* pr = prec(L, c, p, wave_slot(L));
+                const uint32_t* pr = prec(L, c, p, ps[p]);
                 ni[k][p] = qf(r, R_NI + 2 * p);
                 ra[k][p] = q3(pr, PR_RA);
                 rb[k][p] = q3(pr, PR_RB);
@@ -1385,7 +1436,7 @@ B3D_FN void warm_start_contacts(const Lane& L) {
 #pragma unroll
         for (int k = 0; k < kPrepChunk; k++) {
             int c = c0 + k;
-            if (c >= cc) continue;
+            if (c >= cc || done) continue;
             int a = hd[k].a, b = hd[k].b;
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
@@ -1456,65 +1507,9 @@ B3D_FN M3 point_k(float ma, float mb, M3 ia, M3 ib, V3 ra, V3 rb) {
  * state gives the same bits. */
 B3D_FN void joint_geometry(const Lane& L);
 
-/* Point separations of the current delta poses into the packed records. */
-B3D_FN void contact_geometry(const Lane& L) {
-    const uint32_t* w = L.w;
-    int cc = ldi(w, H_CONTACT_COUNT);
-    for (int c0 = 0; c0 < cc; c0 += kChunk) {
-        CHead hd[kChunk];
-#pragma unroll
-        for (int k = 0; k < kChunk; k++) {
-            int c = c0 + k;
-            if (c >= cc) continue;
-            hd[k] = rhead_load(L, c);
-        }
-        V3 n[kChunk], dp[kChunk], ra[kChunk][kMaxManifold], rb[kChunk][kMaxManifold];
-        Q dqa[kChunk], dqb[kChunk];
-        float bs[kChunk][kMaxManifold];
-#pragma unroll
-        for (int k = 0; k < kChunk; k++) {
-            int c = c0 + k;
-            if (c >= cc) continue;
-            const uint32_t* r = crec(L, c, hd[k].slot);
-            n[k] = q3(r, R_N);
-            const uint32_t* da = delta_rec(L, hd[k].a);
-            const uint32_t* db = delta_rec(L, hd[k].b);
-            dqa[k] = rq4(da, BD_DQ);
-            dqb[k] = rq4(db, BD_DQ);
-            dp[k] = sub(r3(db, BD_DP), r3(da, BD_DP));
-#pragma unroll
-            for (int p = 0; p < kMaxManifold; p++) bs[k][p] = qf(r, R_BASE_SEP + p);
-#pragma unroll
-            for (int p = 0; p < kMaxManifold; p++) {
-                if (p >= hd[k].pc) continue;
-                const uint32_t* pr = prec(L, c, p, wave_slot(L));
-                ra[k][p] = q3(pr, PR_RA);
-                rb[k][p] = q3(pr, PR_RB);
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < kChunk; k++) {
-            int c = c0 + k;
-            if (c >= cc) continue;
-            float sep[kMaxManifold];
-#pragma unroll
-            for (int p = 0; p < kMaxManifold; p++) {
-                sep[p] = 0.0f;
-                if (p >= hd[k].pc) continue;
-                V3 ds = add(dp[k], sub(rot(dqb[k], rb[k][p]), rot(dqa[k], ra[k][p])));
-                sep[p] = dot(ds, n[k]) + bs[k][p];
-            }
-            uint32_t* r = crec(L, c, hd[k].slot);
-#pragma unroll
-            for (int p = 0; p < kMaxManifold; p++) qsf(r, R_SEP + p, sep[p]);
-        }
-    }
-}
-
-B3D_FN void delta_geometry(const Lane& L) {
-    contact_geometry(L);
-    joint_geometry(L);
-}
+/* Geometry of the joints at new delta poses.  The contacts' separations
+ * are computed by each solve from the bodies' delta poses. */
+B3D_FN void delta_geometry(const Lane& L) { joint_geometry(L); }
 
 /* The joint rows' delta-pose geometry. */
 B3D_FN void joint_geometry(const Lane& L) {
@@ -1614,10 +1609,12 @@ B3D_FN void solve_rolling(V3 t1, V3 t2, float rolling, float total_n, M3 ia, M3 
 }
 
 /* The contact row as one solve needs it, loaded ahead of use. */
-struct CPoint { V3 ra, rb; float nmass, ni, tn, lever, sep; };
+struct CPoint { V3 ra, rb; float nmass, ni, tn, lever, base_sep; };
 struct CRow {
     int a, b, pc, flags, slot;
     V3 n;
+    V3 dpa, dpb;  /* the bodies' delta poses */
+    Q dqa, dqb;
     float ma, mb;
     M3 ia, ib;
     Soft soft;
@@ -1648,6 +1645,12 @@ B3D_FN void crow_load(const Lane& L, int c, CHead h, int relax, CRow* r) {
     r->twist_mass = h.twist_mass;
     r->n = q3(rc, R_N);
     r->rolling = qf(rc, R_ROLLING);
+    const uint32_t* da = delta_rec(L, h.a);
+    const uint32_t* db = delta_rec(L, h.b);
+    r->dpa = r3(da, BD_DP);
+    r->dqa = rq4(da, BD_DQ);
+    r->dpb = r3(db, BD_DP);
+    r->dqb = rq4(db, BD_DQ);
 #pragma unroll
     for (int p = 0; p < kMaxManifold; p++) {
         CPoint& q = r->pt[p];
@@ -1659,7 +1662,7 @@ B3D_FN void crow_load(const Lane& L, int c, CHead h, int relax, CRow* r) {
         q.nmass = qf(pr, PR_NMASS);
         q.rb = q3(pr, PR_RB);
         q.lever = relax ? qf(pr, PR_LEVER) : 0.0f;
-        q.sep = qf(rc, R_SEP + p);
+        q.base_sep = qf(rc, R_BASE_SEP + p);
         q.ni = qf(rc, R_NI + 2 * p);
         q.tn = qf(rc, R_TN + 2 * p);
     }
@@ -1692,7 +1695,9 @@ B3D_FN void crow_solve(const Lane& L, int c, CRow& r, float inv_h, float contact
     for (int p = 0; p < kMaxManifold; p++) {
         if (p >= r.pc) continue;
         CPoint& q = r.pt[p];
-        float sep = q.sep;
+        /* the point's separation at the current delta poses (08:331-333) */
+        V3 ds = add(sub(r.dpb, r.dpa), sub(rot(r.dqb, q.rb), rot(r.dqa, q.ra)));
+        float sep = dot(ds, n) + q.base_sep;
         float vbias = 0.0f, mscale = 1.0f, iscale = 0.0f;
         if (sep > 0.0f) {
             vbias = sep * inv_h;
@@ -2487,11 +2492,13 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
     float rest_threshold = ldf(L.w, H_RESTITUTION_THRESHOLD);
 
     find_contacts(L);
+    /* restitution runs in every lane of a wave where some world has it */
+    const bool rest_wave = wave_any(L, (ldi(L.scr + L.g.scr_flags * kLanes, 0) & kLaneRestitution) != 0);
     vel_load(L);
     body_prepass(L, h);
-    prepare_contacts(L, cs, ss);
+    int warm_done = prepare_contacts(L, cs, ss);
     prepare_joints(L, h);
-    warm_start_contacts(L);
+    if (wave_any(L, !warm_done)) warm_start_contacts(L, warm_done);
     warm_start_joints(L);
     joint_geometry(L);   /* the contacts' initial separations come from prepare_contacts */
     for (int s = 0; s < subs; s++) {
@@ -2505,7 +2512,7 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
         delta_geometry(L);
         solve_contacts(L, inv_h, contact_speed, 0, cs, ss);
         solve_joints(L, h, inv_h, 0);
-        apply_restitution(L, rest_threshold);
+        if (rest_wave) apply_restitution(L, rest_threshold);
     }
     contact_writeback(L);
     finalize(L);

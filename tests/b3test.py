@@ -159,6 +159,41 @@ def diff_words(a, b, sig):
     return np.argwhere(d)
 
 
+# ---- the contacts' prepared solver fields (written only with B3_ENGINE_KEEP_SOLVER_FIELDS) ----
+
+SOLVER_FIELDS = ("inv_mass_a", "inv_mass_b", "inv_i_a", "inv_i_b", "softness", "center_a", "center_b",
+                 "tangent_mass", "twist_mass", "rolling_mass")
+POINT_SOLVER_FIELDS = ("normal_mass", "rel_vel", "lever")
+
+
+def solver_field_words(worlds):
+    """Mask (world, word) of the prepared solver fields of live contacts."""
+    dt = worlds.dtype
+    nwords = dt.itemsize // 4
+    mask = np.zeros((len(worlds), nwords), bool)
+    c_dt = dt.fields["contacts"][0].base
+    c_off = dt.fields["contacts"][1]
+    p_dt = c_dt.fields["points"][0].base
+    p_off = c_dt.fields["points"][1]
+
+    def span(off, sub):
+        return off // 4, (off + sub.itemsize) // 4
+
+    for i, w in enumerate(worlds):
+        for c in range(int(w["contact_count"])):
+            base = c_off + c * c_dt.itemsize
+            for f in SOLVER_FIELDS:
+                a, b = span(base + c_dt.fields[f][1], c_dt.fields[f][0])
+                mask[i, a:b] = True
+            for p in range(int(w["contacts"][c]["point_count"])):
+                pb = base + p_off + p * p_dt.itemsize
+                for f in POINT_SOLVER_FIELDS:
+                    a, b = span(pb + p_dt.fields[f][1], p_dt.fields[f][0])
+                    mask[i, a:b] = True
+    return mask
+
+
+
 # ---- coverage worlds: features the five benchmark scenes do not reach ----
 
 def feature_worlds(count, seed=7, hinges=True):

@@ -70,3 +70,58 @@ def test_lane_code_single_joint_worlds():
         emu.step(1.0 / 60.0, 4)
     bad = diff_words(emu.worlds(), ref, CUSTOM_SIG)
     assert len(bad) == 0, bad[:10].tolist()
+
+
+@pytest.mark.parametrize("scene,count,steps", [(2, 70, 65), (4, 66, 12), (5, 130, 40)])
+def test_lane_code_default_options(scene, count, steps):
+    """Default options (prepared solver fields not written back, the warm
+    start fused into preparation where no contact has restitution): every
+    live word except those solver fields equals the oracle's."""
+    from b3test import emu, solver_field_words, live_word_mask, words
+    import ctypes as C
+    worlds = scenes.build(scene, count)
+    initial = clone(worlds)
+    lib = emu()
+    lib.emu_set_options.argtypes = [C.c_uint]
+    lib.emu_set_options(0)
+    try:
+        e = EmuBatch(scene, worlds)
+        e.run(0, steps)
+        got = e.worlds()
+    finally:
+        lib.emu_set_options(1)
+    ref = clone(worlds)
+    oracle_run(scene, ref, initial, 0, steps)
+    sig = scenes.SCENES[scene].sig
+    live = live_word_mask(ref, sig) & live_word_mask(got, sig)
+    diff = (words(got) != words(ref)) & live
+    solver = solver_field_words(ref)
+    assert not (diff & ~solver).any(), np.argwhere(diff & ~solver)[:10].tolist()
+    assert (diff & solver).any()   # the lean path really ran
+
+
+def test_lane_code_default_options_feature_worlds():
+    """The same on the coverage worlds, where some worlds have restitution
+    contacts (separate warm start) and some do not (fused)."""
+    import ctypes as C
+    from b3test import EmuSig, emu, feature_worlds, live_word_mask, oracle_step_batch, solver_field_words, words
+    from puffysics_amd.creation import CUSTOM_SIG
+    worlds = feature_worlds(40)
+    ref = clone(worlds)
+    lib = emu()
+    lib.emu_set_options.argtypes = [C.c_uint]
+    lib.emu_set_options(0)
+    try:
+        e = EmuSig(CUSTOM_SIG, worlds)
+        for t in range(40):
+            oracle_step_batch(ref, CUSTOM_SIG, 1.0 / 60.0, 4)
+            e.step(1.0 / 60.0, 4)
+        got = e.worlds()
+    finally:
+        lib.emu_set_options(1)
+    live = live_word_mask(ref, CUSTOM_SIG) & live_word_mask(got, CUSTOM_SIG)
+    diff = (words(got) != words(ref)) & live
+    assert not (diff & ~solver_field_words(ref)).any()
+    rest = ref["contacts"]["restitution"] > 0
+    has = np.array([rest[i, :ref["contact_count"][i]].any() for i in range(40)])
+    assert has.any() and not has.all()

@@ -13,7 +13,7 @@ the device result must be bit-identical to the oracle's.
 import numpy as np
 import pytest
 
-from b3test import clone, diff_words, oracle_run, words
+from b3test import clone, diff_words, oracle_run, solver_field_words, words
 from puffysics_amd import scenes
 
 torch = pytest.importorskip("torch")
@@ -278,38 +278,6 @@ def test_feature_worlds_with_hinges_one_step():
     assert_close_state(got, ref)
 
 
-SOLVER_FIELDS = ("inv_mass_a", "inv_mass_b", "inv_i_a", "inv_i_b", "softness", "center_a", "center_b",
-                 "tangent_mass", "twist_mass", "rolling_mass")
-POINT_SOLVER_FIELDS = ("normal_mass", "rel_vel", "lever")
-
-
-def solver_field_words(worlds):
-    """Mask (world, word) of the prepared solver fields of live contacts."""
-    dt = worlds.dtype
-    nwords = dt.itemsize // 4
-    mask = np.zeros((len(worlds), nwords), bool)
-    c_dt = dt.fields["contacts"][0].base
-    c_off = dt.fields["contacts"][1]
-    p_dt = c_dt.fields["points"][0].base
-    p_off = c_dt.fields["points"][1]
-
-    def span(off, sub):
-        return off // 4, (off + sub.itemsize) // 4
-
-    for i, w in enumerate(worlds):
-        for c in range(int(w["contact_count"])):
-            base = c_off + c * c_dt.itemsize
-            for f in SOLVER_FIELDS:
-                a, b = span(base + c_dt.fields[f][1], c_dt.fields[f][0])
-                mask[i, a:b] = True
-            for p in range(int(w["contacts"][c]["point_count"])):
-                pb = base + p_off + p * p_dt.itemsize
-                for f in POINT_SOLVER_FIELDS:
-                    a, b = span(pb + p_dt.fields[f][1], p_dt.fields[f][0])
-                    mask[i, a:b] = True
-    return mask
-
-
 def test_default_options_differ_only_in_solver_fields():
     """Without B3_ENGINE_KEEP_SOLVER_FIELDS the worlds evolve identically;
     only the prepared solver fields of the live contacts are not written."""
@@ -323,3 +291,31 @@ def test_default_options_differ_only_in_solver_fields():
     allowed = solver_field_words(a)
     assert len(bad) > 0   # the lean rows do hold stale values
     assert allowed[bad[:, 0], bad[:, 1]].all(), bad[~allowed[bad[:, 0], bad[:, 1]]][:10].tolist()
+
+
+def test_default_options_mixed_waves():
+    """Default options on the coverage worlds, where worlds with and without
+    restitution share waves: those without it warm-start inside
+    preparation, the others in the separate pass, and every wave computes
+    the packed records' slots over all of its lanes.  Every live word except
+    the prepared solver fields equals the oracle's, bit for bit, on the
+    hinge-free worlds."""
+    from b3test import feature_worlds, live_word_mask, oracle_step_batch
+    from puffysics_amd.creation import CUSTOM_SIG
+    from puffysics_amd.engine import B3Engine
+    worlds = feature_worlds(200, seed=3, hinges=False)
+    ref = clone(worlds)
+    eng = B3Engine(worlds, CUSTOM_SIG)
+    active = (np.arange(200) % 7 != 4).astype(np.uint8)
+    d_active = torch.from_numpy(active).cuda()
+    for t in range(40):
+        act = t % 2 == 1
+        oracle_step_batch(ref, CUSTOM_SIG, 1.0 / 60.0, 4, active if act else None)
+        eng.step(1.0 / 60.0, 4, d_active if act else None)
+    torch.cuda.synchronize()
+    got = eng.download()
+    live = live_word_mask(ref, CUSTOM_SIG) & live_word_mask(got, CUSTOM_SIG)
+    diff = (words(got) != words(ref)) & live & ~solver_field_words(ref)
+    assert not diff.any(), describe(np.argwhere(diff), got, ref, worlds)
+    rest = np.array([(ref["contacts"]["restitution"][i, :ref["contact_count"][i]] > 0).any() for i in range(200)])
+    assert rest.any() and not rest.all()
