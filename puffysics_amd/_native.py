@@ -31,6 +31,9 @@ ENGINE_SYMBOLS = [
     ("b3_engine_device_view", _i, [_vp, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]),
     ("b3_engine_set_options", _i, [_vp, C.c_uint]),
     ("b3_batch_step_gravity_gpu", _i, [_vp, _f, _i, _vp, _vp, "B3GravityLaw", _vp, _vp]),
+    ("b3_fluid_law_default", _i, [_vp]),
+    ("b3_fluid_state_words", _i, [_vp]),
+    ("b3_batch_step_fluid_gpu", _i, [_vp, _f, _i, _vp, _vp, _vp, _vp, _vp]),
     ("b3w_masks_gpu", _i, [_i, _ull, _i, _i, _vp, _vp, _vp]),
     ("b3w_inputs_gpu", _i, [_vp, _i, _ull, _i, _vp, _vp]),
 ]

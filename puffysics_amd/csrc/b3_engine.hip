@@ -249,6 +249,11 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
             return err;
         }
     }
+    err = b3i_forces_init(lds);
+    if (err != hipSuccess) {
+        free(e);
+        return err;
+    }
     if (e->tiles > 0) {
         size_t tiles_bytes = (size_t)e->tiles * e->tile_words * 4;
         if ((err = hipMalloc((void**)&e->live, tiles_bytes)) != hipSuccess

@@ -24,6 +24,9 @@ struct B3Engine {
     unsigned int options;    /* B3_ENGINE_* step options */
 };
 
+/* Set-up of the force-law kernels on the current device (b3_forces.hip). */
+hipError_t b3i_forces_init(size_t lds_bytes);
+
 /* The engine's device is the current one. */
 inline hipError_t on_device(const B3Engine* e) {
     int dev = -1;
