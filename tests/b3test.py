@@ -153,9 +153,16 @@ def words(worlds):
 
 
 def diff_words(a, b, sig):
-    """Indices (world, word) where two batches differ on live words."""
+    """Indices (world, word) where two batches differ on live words.  A word
+    that reads as a NaN float on both sides counts as equal: the sign and
+    payload of a NaN depend on operand order (the reference's capsule-box
+    manifold can produce a NaN normal, e.g. the bin scene's world 745 at
+    step 22, and the reference, the oracle and the engine then carry NaNs
+    with different bits)."""
     m = live_word_mask(a, sig) & live_word_mask(b, sig)
-    d = (words(a) != words(b)) & m
+    wa, wb = words(a), words(b)
+    both_nan = np.isnan(wa.view(np.float32)) & np.isnan(wb.view(np.float32))
+    d = (wa != wb) & m & ~both_nan
     return np.argwhere(d)
 
 

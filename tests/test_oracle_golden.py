@@ -88,3 +88,25 @@ def test_oracle_matches_reference_build_longer(scene):
     ref.ref_run(scene, a.ctypes.data, init.ctypes.data, count, scenes.SEED, 0, steps, sc.dt, sc.substeps, 4, None)
     oracle_run(scene, b, clone(init), 0, steps, threads=4)
     assert len(diff_words(a, b, sc.sig)) == 0
+
+
+@pytest.mark.skipif(ref_lib(4) is None, reason="reference CPU path not built here (no reference tree)")
+def test_reference_capsule_box_nan_is_reproduced():
+    """The reference's own step gives world 745 of the bin scene a contact
+    (capsule shape 15 against box shape 31) with a NaN normal at step 22,
+    and the oracle does the same: a NaN in the compared state is the
+    reference's result, which is why word comparisons treat NaN as equal to
+    NaN whatever its sign and payload."""
+    sc = scenes.SCENES[4]
+    count = 768
+    a = scenes.build(4, count)
+    init = clone(a)
+    b = clone(a)
+    ref = ref_lib(4)
+    ref.ref_run(4, a.ctypes.data, init.ctypes.data, count, scenes.SEED, 0, 23, sc.dt, sc.substeps, 4, None)
+    oracle_run(4, b, clone(init), 0, 23, threads=4)
+    for w in (a, b):
+        ct = w["contacts"][745, 12]
+        assert (int(ct["shape_a"]), int(ct["shape_b"])) == (15, 31)
+        assert np.isnan(ct["normal"]["x"]) and np.isnan(ct["normal"]["y"])
+    assert len(diff_words(a, b, sc.sig)) == 0
