@@ -134,6 +134,8 @@ def main():
     ap.add_argument("--worlds", type=int, default=0)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--art", action="store_true",
+                    help="step with articulation-aware contacts (B3_ENGINE_ART_CONTACTS); not the headline mode")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device 10 times with a plain copy kernel (for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
@@ -164,6 +166,9 @@ def main():
     log("building %d %s worlds" % (count, sc.name))
     worlds = scenes.build(args.scene, count)
     eng = B3Engine(worlds, sc.sig)
+    if args.art:
+        from puffysics_amd.engine import B3_ENGINE_ART_CONTACTS
+        eng.set_options(B3_ENGINE_ART_CONTACTS)
     stream = torch.cuda.current_stream()
     total = args.warmup + args.steps * args.repeats
     reset = torch.empty((total, count), dtype=torch.uint8, device="cuda")
@@ -218,10 +223,10 @@ def main():
     bytes_per_launch = float(per_world.mean()) * mean_stepped
     k_ms = kernel_ms[med]
     achieved = bytes_per_launch / (k_ms * 1e-3) / 1e9
-    traffic = load_traffic(sc.name, count)
+    traffic = None if args.art else load_traffic(sc.name, count)
     roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic,
-                "kernel": "b3k_step", "kernel_ms": round(k_ms, 4),
+                "kernel": "b3k_step_art" if args.art else "b3k_step", "kernel_ms": round(k_ms, 4),
                 "bytes_per_env_step": round(float(per_world.mean()), 1),
                 "mean_contacts_per_world": round(float(st["contact_count"].mean()), 2)}
     eng.close()
@@ -240,7 +245,8 @@ def main():
                sc.name, count, count, sc.name, sc.dt, sc.substeps,
                "2% reset / 90% step" if args.scene == 5 else "none"),
                "worlds": count, "scene": sc.name, "dt": sc.dt, "substeps": sc.substeps,
-               "repeats": args.repeats, "mean_stepped_worlds": round(mean_stepped, 1)},
+               "repeats": args.repeats, "mean_stepped_worlds": round(mean_stepped, 1),
+               "contacts": "articulated (B3_ENGINE_ART_CONTACTS)" if args.art else "independent-body (default)"},
            "roofline": roofline, "cpu_baseline": cpu}
     print(json.dumps(out), flush=True)
 

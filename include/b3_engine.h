@@ -19,8 +19,9 @@
  *   - masks are one byte per world in device memory, nonzero selects.
  *     NULL selects every world, except the reset mask of
  *     b3_batch_step_gpu, where NULL resets none;
- *   - b3_engine_create is the only call that allocates device memory, and
- *     b3_engine_destroy the only one that frees it.
+ *   - b3_engine_create is the only call that allocates device memory
+ *     (except b3_engine_set_options turning on B3_ENGINE_ART_CONTACTS),
+ *     and b3_engine_destroy the only one that frees it.
  */
 #ifndef PUFFYSICS_AMD_B3_ENGINE_H
 #define PUFFYSICS_AMD_B3_ENGINE_H
@@ -113,6 +114,19 @@ hipError_t b3_engine_device_view(const B3Engine* engine, void** tiles, size_t* w
  * worlds; every other field, and every body and joint, is the same either
  * way.  Set it to compare whole B3World structs with the reference. */
 #define B3_ENGINE_KEEP_SOLVER_FIELDS 1u
+/* B3_ENGINE_ART_CONTACTS: the step of the reference built with
+ * B3_ART_CONTACTS=1 (01_config.inl:176-187).  In a world with revolute
+ * joints and contacts whose joint tree builds (b3_art_bind, b3_art.cuh:
+ * 488-490), the contact warm start and sweeps apply impulses through the
+ * tree's Delassus operator (08_contacts.inl:194-232, 422-437); other
+ * worlds step as usual.  The contacts' solver fields are then always
+ * written back.  Turning it on allocates a workspace of
+ * 4 * count * (101 + 22) * max_bodies bytes (the one exception to
+ * b3_engine_create being the only allocating call); it is freed by
+ * b3_engine_destroy.  This mode costs far more per contact than the
+ * default, as in the reference.  The force-law entry points return
+ * hipErrorNotSupported while it is on. */
+#define B3_ENGINE_ART_CONTACTS 2u
 hipError_t b3_engine_set_options(B3Engine* engine, unsigned int options);
 
 /* ---- per-substep force laws ----

@@ -19,6 +19,7 @@
 #include <float.h>
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "b3cpu.h"
@@ -1706,7 +1707,24 @@ static void o_finalize(OWorld* w) {                                             
     }
 }
 
-static void o_step(OWorld* w, b3r dt, int substeps, const OForceLaw* law) {              /* :148-264 */
+#include "art.inc"
+
+/* b3_solve_contacts (08_contacts.inl:422-437): with articulated contacts on,
+ * a world with joints and contacts whose tree builds takes the articulated
+ * sweep. */
+static void o_solve_contacts_mode(OWorld* w, b3r inv_h, b3r contact_speed, int use_bias, int art_contacts) {
+    if (art_contacts && w->h->joint_count > 0 && w->h->contact_count > 0) {
+        OArt art;
+        if (o_art_bind(&art, w)) {
+            o_art_solve_contacts(&art, w, inv_h, contact_speed, use_bias);
+            o_art_free(&art);
+            return;
+        }
+    }
+    o_solve_contacts(w, inv_h, contact_speed, use_bias);
+}
+
+static void o_step(OWorld* w, b3r dt, int substeps, const OForceLaw* law, int art_contacts) {  /* :148-264 */
     if (dt <= 0.0f) return;
     int subs = substeps < 1 ? 1 : substeps;
     b3r one = 1.0f;
@@ -1723,7 +1741,16 @@ static void o_step(OWorld* w, b3r dt, int substeps, const OForceLaw* law) {     
         o_prepare_one_contact(c, &w->bodies[c->body_a], &w->bodies[c->body_b], cs, ss);
     }
     o_prepare_joints(w, h);
-    for (int i = 0; i < w->h->contact_count; i++) {
+    int warm_done = 0;                                                                   /* 08_contacts.inl:194-232 */
+    if (art_contacts && w->h->joint_count > 0 && w->h->contact_count > 0) {
+        OArt art;
+        if (o_art_bind(&art, w)) {
+            o_art_warm_start(&art, w);
+            o_art_free(&art);
+            warm_done = 1;
+        }
+    }
+    for (int i = 0; !warm_done && i < w->h->contact_count; i++) {
         OContact* c = &w->contacts[i];
         o_warm_one_contact(c, &w->bodies[c->body_a], &w->bodies[c->body_b]);
     }
@@ -1731,10 +1758,10 @@ static void o_step(OWorld* w, b3r dt, int substeps, const OForceLaw* law) {     
     /* b3_step_sub :167-181 */
     for (int s = 0; s < subs; s++) {
         o_integrate_velocities(w, h, law);
-        o_solve_contacts(w, inv_h, w->h->contact_speed, 1);
+        o_solve_contacts_mode(w, inv_h, w->h->contact_speed, 1, art_contacts);
         o_solve_joints(w, h, inv_h, 1);
         o_integrate_positions(w, h, inv_dt, w->h->max_linear_speed);
-        o_solve_contacts(w, inv_h, w->h->contact_speed, 0);
+        o_solve_contacts_mode(w, inv_h, w->h->contact_speed, 0, art_contacts);
         o_solve_joints(w, h, inv_h, 0);
         o_apply_restitution(w, w->h->restitution_threshold);
     }
@@ -1753,7 +1780,13 @@ size_t ocpu_world_size(unsigned long long sig) {
 void ocpu_step(void* world, unsigned long long sig, float dt, int substeps) {
     OWorld w;
     if (!o_view(&w, world, sig)) return;
-    o_step(&w, dt, substeps, NULL);
+    o_step(&w, dt, substeps, NULL, 0);
+}
+
+void ocpu_step_art(void* world, unsigned long long sig, float dt, int substeps) {
+    OWorld w;
+    if (!o_view(&w, world, sig)) return;
+    o_step(&w, dt, substeps, NULL, 1);
 }
 
 void ocpu_step_gravity(void* world, unsigned long long sig, float dt, int substeps, float gravity,
@@ -1761,14 +1794,14 @@ void ocpu_step_gravity(void* world, unsigned long long sig, float dt, int subste
     OWorld w;
     if (!o_view(&w, world, sig)) return;
     OForceLaw law = {o_gravity_law, gravity, softening, masses, NULL, NULL};
-    o_step(&w, dt, substeps, &law);
+    o_step(&w, dt, substeps, &law, 0);
 }
 
 void ocpu_step_fluid(void* world, unsigned long long sig, float dt, int substeps, const void* fluid, float* state) {
     OWorld w;
     if (!o_view(&w, world, sig)) return;
     OForceLaw law = {o_fluid_law, 0.0f, 0.0f, NULL, (const OFluid*)fluid, state};
-    o_step(&w, dt, substeps, &law);
+    o_step(&w, dt, substeps, &law, 0);
 }
 
 void ocpu_find_contacts(void* world, unsigned long long sig) {

@@ -36,6 +36,10 @@ void ocpu_step_gravity(void* world, unsigned long long sig, float dt, int subste
  * `state` is the world's 6 * max_bodies + 1 words: each body's previous
  * linear and angular velocity, then have_prev (int). */
 void ocpu_step_fluid(void* world, unsigned long long sig, float dt, int substeps, const void* fluid, float* state);
+/* b3_step built with B3_ART_CONTACTS=1 (01_config.inl:176-187): in a world
+ * with revolute joints the warm start and the contact sweeps use
+ * articulated responses (b3_art.cuh; 08_contacts.inl:194-232, 422-437). */
+void ocpu_step_art(void* world, unsigned long long sig, float dt, int substeps);
 /* b3_find_contacts alone (08_contacts.inl:64-173). */
 void ocpu_find_contacts(void* world, unsigned long long sig);
 /* b3_batch_step (b3_batch.cuh:39-48): 1 on success, 0 on invalid input. */

@@ -284,7 +284,7 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
 hipError_t b3_engine_destroy(B3Engine* e) {
     if (!e) return hipSuccess;
     hipError_t first = hipSuccess;
-    void* bufs[4] = {e->live, e->snap, e->scratch, e->staging};
+    void* bufs[5] = {e->live, e->snap, e->scratch, e->staging, e->art_ws};
     for (void* p : bufs) {
         if (!p) continue;
         hipError_t err = hipFree(p);
@@ -364,6 +364,7 @@ hipError_t b3_batch_step_gpu(B3Engine* e, float dt, int substeps, const unsigned
     hipError_t err = on_device(e);
     if (err != hipSuccess) return err;
     if (dt == 0.0f) return reset_mask ? b3_batch_restore_gpu(e, reset_mask, stream) : hipSuccess;
+    if (e->options & B3_ENGINE_ART_CONTACTS) return b3i_step_art(e, dt, substeps, step_mask, reset_mask, stream);
     b3k_step<<<e->tiles, 64, e->lds_bytes, stream>>>(e->live, e->snap, e->scratch, e->g, e->count, dt, substeps,
         step_mask, reset_mask, e->options);
     return hipGetLastError();
@@ -396,7 +397,12 @@ hipError_t b3_engine_device_view(const B3Engine* e, void** tiles, size_t* world_
 }
 
 hipError_t b3_engine_set_options(B3Engine* e, unsigned int options) {
-    if (!e || (options & ~B3_ENGINE_KEEP_SOLVER_FIELDS)) return hipErrorInvalidValue;
+    if (!e || (options & ~(B3_ENGINE_KEEP_SOLVER_FIELDS | B3_ENGINE_ART_CONTACTS))) return hipErrorInvalidValue;
+    if (options & B3_ENGINE_ART_CONTACTS) {
+        hipError_t err = on_device(e);
+        if (err == hipSuccess) err = b3i_art_init(e);
+        if (err != hipSuccess) return err;
+    }
     e->options = options;
     return hipSuccess;
 }

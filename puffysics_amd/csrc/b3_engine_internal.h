@@ -22,10 +22,15 @@ struct B3Engine {
     unsigned char* staging;  /* count * world_bytes, AoS, for up/download */
     size_t lds_bytes;
     unsigned int options;    /* B3_ENGINE_* step options */
+    float* art_ws;           /* articulated-contact workspace, allocated when that option is first set */
 };
 
 /* Set-up of the force-law kernels on the current device (b3_forces.hip). */
 hipError_t b3i_forces_init(size_t lds_bytes);
+/* The articulated-contact step (b3_art.hip): its workspace, then launches. */
+hipError_t b3i_art_init(B3Engine* e);
+hipError_t b3i_step_art(B3Engine* e, float dt, int substeps, const unsigned char* step_mask,
+    const unsigned char* reset_mask, hipStream_t stream);
 
 /* The engine's device is the current one. */
 inline hipError_t on_device(const B3Engine* e) {

@@ -96,6 +96,7 @@ hipError_t b3_batch_step_gravity_gpu(B3Engine* e, float dt, int substeps, const 
     /* nbody_cfg_ok (nbody.cuh:44-46): gravity >= 0 and softening > 0 */
     if (!e || !isfinite(dt) || dt < 0.0f || substeps < 1 || !(law.gravity >= 0.0f) || !(law.softening > 0.0f))
         return hipErrorInvalidValue;
+    if (e->options & B3_ENGINE_ART_CONTACTS) return hipErrorNotSupported;
     if (e->count == 0) return hipSuccess;
     hipError_t err = on_device(e);
     if (err != hipSuccess) return err;
@@ -128,6 +129,7 @@ hipError_t b3_batch_step_fluid_gpu(B3Engine* e, float dt, int substeps, const un
     if (!e || !law || !isfinite(dt) || dt < 0.0f || substeps < 1 || law->sphere_samples > kFluidTrig
             || law->box_face_samples > B3_FLUID_MAX_FACE_SAMPLES || law->capsule_rings > B3_FLUID_MAX_RINGS)
         return hipErrorInvalidValue;
+    if (e->options & B3_ENGINE_ART_CONTACTS) return hipErrorNotSupported;
     if (e->count == 0) return hipSuccess;
     if (!state) return hipErrorInvalidValue;
     hipError_t err = on_device(e);

@@ -95,6 +95,7 @@ def b3_batch_step_fluid_gpu(engine, dt, substeps, law, state, step_mask=None, re
 
 
 B3_ENGINE_KEEP_SOLVER_FIELDS = 1
+B3_ENGINE_ART_CONTACTS = 2
 
 
 class B3Engine:

@@ -271,6 +271,78 @@ def feature_worlds(count, seed=7, hinges=True):
     return w
 
 
+def passive_hinge_worlds(count, seed=5):
+    """Worlds of capacity set 16/16/32/8 for the articulated-contact path:
+    a ground box, a static post with a chain of three links on passive
+    hinges (no spring, motor or limit, so no atan2f on the path) swinging
+    into the ground and into each other, a second two-link chain hinged
+    between two dynamic bodies (a floating tree), and three free spheres or
+    boxes; every fifth world has no joints (the ordinary contact path)."""
+    from puffysics_amd import creation as cr
+    from puffysics_amd.b3types import B3_DYNAMIC, B3_STATIC
+    rng = np.random.default_rng(seed)
+    w = cr.new_worlds(count, gravity=(0.0, -9.81, 0.0))
+    for k in range(count):
+        g = cr.body(w, k, B3_STATIC, (0.0, -0.5, 0.0))
+        cr.box(w, k, g, (5.0, 0.5, 5.0), friction=float(rng.uniform(0.3, 0.9)))
+        if k % 5 != 4:
+            post = cr.body(w, k, B3_STATIC, (0.0, 1.2, 0.0))
+            prev, anchor = post, (0.0, 0.0, 0.0)
+            axis = tuple(rng.normal(size=3) * 0.2 + np.array([0.0, 0.0, 1.0]))
+            for i in range(3):
+                half = tuple(rng.uniform(0.06, 0.12, 3))
+                pos = (0.25 * (i + 1) + rng.uniform(-0.05, 0.05), 1.2 - 0.15 * i, rng.uniform(-0.1, 0.1))
+                b = cr.body(w, k, B3_DYNAMIC, pos, lin_vel=tuple(rng.uniform(-1, 1, 3)))
+                if i == 1:
+                    cr.capsule(w, k, b, 0.08, 0.06)
+                else:
+                    cr.box(w, k, b, half)
+                cr.finalize_mass(w, k, b)
+                local = (-0.125, 0.075, 0.0)
+                cr.revolute(w, k, prev, b, anchor, local, axis)
+                prev, anchor = b, (0.125, -0.075, 0.0)
+            a = cr.body(w, k, B3_DYNAMIC, (-0.6, 0.4, 0.2))
+            cr.box(w, k, a, (0.1, 0.1, 0.1))
+            cr.finalize_mass(w, k, a)
+            b = cr.body(w, k, B3_DYNAMIC, (-0.6, 0.7, 0.2), ang_vel=tuple(rng.uniform(-2, 2, 3)))
+            cr.sphere(w, k, b, 0.09)
+            cr.finalize_mass(w, k, b)
+            cr.revolute(w, k, a, b, (0.0, 0.15, 0.0), (0.0, -0.15, 0.0), (1.0, 0.0, 0.0))
+        for i in range(3):
+            p = (rng.uniform(-0.8, 0.8), rng.uniform(0.2, 1.0), rng.uniform(-0.8, 0.8))
+            b = cr.body(w, k, B3_DYNAMIC, p, lin_vel=tuple(rng.uniform(-1, 1, 3)))
+            if i % 2:
+                cr.sphere(w, k, b, rng.uniform(0.08, 0.15), restitution=float(rng.choice([0.0, 0.4])))
+            else:
+                cr.box(w, k, b, tuple(rng.uniform(0.06, 0.12, 3)))
+            cr.finalize_mass(w, k, b)
+    return w
+
+
+def oracle_step_art(worlds, sig, dt, substeps, active=None):
+    """b3_step built with articulated contacts, world by world on the oracle."""
+    lib = oracle()
+    lib.ocpu_step_art.argtypes = [_vp, _ull, _f, _i]
+    for k in range(len(worlds)):
+        if active is None or active[k]:
+            lib.ocpu_step_art(worlds[k:k + 1].ctypes.data, sig, dt, substeps)
+
+
+def ref_art_lib(caps):
+    """The reference's b3_step built with B3_ART_CONTACTS=1 for capacity set
+    `caps` (0, 3 or 5), or None where the reference was not built."""
+    path = os.path.join(REF_DIR, "libb3ref_art_%d.so" % caps)
+    if not os.path.exists(path):
+        return None
+    key = "art_%d" % caps
+    if key not in _refs:
+        lib = C.CDLL(path)
+        lib.refa_sig.restype = C.c_ulonglong
+        lib.refa_step.argtypes = [_vp, _f, _i]
+        _refs[key] = lib
+    return _refs[key]
+
+
 def oracle_step_batch(worlds, sig, dt, substeps, active=None):
     """b3_batch_step over a contiguous batch on the oracle."""
     lib = oracle()
@@ -349,6 +421,13 @@ class EmuSig:
         lib.emu_step_gravity(self.tiles.ctypes.data, self.count, self.sig, dt, substeps,
                              None if act is None else act.ctypes.data, gravity, softening,
                              None if m is None else m.ctypes.data)
+
+    def step_art(self, dt, substeps, active=None):
+        lib = emu()
+        lib.emu_step_art.argtypes = [_vp, _i, _ull, _f, _i, _vp]
+        act = None if active is None else np.ascontiguousarray(active, np.uint8)
+        lib.emu_step_art(self.tiles.ctypes.data, self.count, self.sig, dt, substeps,
+                         None if act is None else act.ctypes.data)
 
     def step_fluid(self, dt, substeps, law, state, active=None):
         lib = emu()

@@ -14,6 +14,7 @@
 #include <string.h>
 #include <vector>
 
+#include "b3d_art.h"
 #include "b3d_forces.h"
 #include "b3d_inputs.h"
 #include "b3d_lane.h"
@@ -138,6 +139,23 @@ void emu_step_fluid(uint32_t* tiles, int count, unsigned long long sig, float dt
         law.state = state + w * words;
         law.trig = trig.data();
         step_world(lane_of(tiles, scratch.data(), vel.data(), g, w), dt, substeps, law);
+    }
+}
+
+/* emu_step with articulated contacts (B3_ENGINE_ART_CONTACTS). */
+void emu_step_art(uint32_t* tiles, int count, unsigned long long sig, float dt, int substeps,
+        const unsigned char* step_mask) {
+    Geometry g;
+    size_t wb;
+    if (!geometry_of(sig, &g, &wb)) return;
+    int ntiles = (count + kLanes - 1) / kLanes;
+    std::vector<uint32_t> scratch((size_t)ntiles * g.tile_scr_words);
+    std::vector<float> vel((size_t)lds_rows(g) * kLanes);
+    std::vector<float> ws((size_t)ntiles * art_ws_words(g.max_b) * kLanes);
+    for (int w = 0; w < count; w++) {
+        if (step_mask && !step_mask[w]) continue;
+        float* lane_ws = ws.data() + (size_t)(w / kLanes) * art_ws_words(g.max_b) * kLanes + w % kLanes;
+        step_world_art(lane_of(tiles, scratch.data(), vel.data(), g, w), lane_ws, dt, substeps);
     }
 }
 

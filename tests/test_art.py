@@ -1,0 +1,215 @@
+"""Articulation-aware contacts: the step of the reference built with
+B3_ART_CONTACTS=1 (01_config.inl:176-187; b3_art.cuh; 08_contacts.inl:
+194-232, 422-437), behind B3_ENGINE_ART_CONTACTS.
+
+The oracle's articulated path (oracle/art.inc) is pinned against the
+reference's own build of it (oracle/_ref/libb3ref_art_*.so) bit for bit,
+and against closed forms of the Delassus operator: a link on one hinge
+responds at a point p along n with ((p - anchor) x n . u)^2 / I_axis, and a
+floating body with its independent-body mass.  The host build of the lane
+code and the device must then match the oracle: bit for bit on worlds whose
+hinges are passive (no atan2f on the path), within the single-step
+tolerance on the arm scene (motors and limits).
+"""
+import numpy as np
+import pytest
+
+import b3test as T
+from b3test import clone, diff_words
+from puffysics_amd import creation as cr
+from puffysics_amd import scenes
+from puffysics_amd.b3types import B3_DYNAMIC, B3_STATIC
+
+CUSTOM_SIG = cr.CUSTOM_SIG
+DT = 1.0 / 60.0
+
+
+def _arm_inputs(worlds, t):
+    scenes.apply_inputs(5, worlds, t)
+
+
+CASES = [("passive", 0, 40, None), ("features", 0, 20, None), ("arm", 5, 10, _arm_inputs), ("chain", 3, 10, None)]
+
+
+def _case_worlds(name, count):
+    if name == "passive":
+        return T.passive_hinge_worlds(count), CUSTOM_SIG
+    if name == "features":
+        return T.feature_worlds(count, hinges=True), CUSTOM_SIG
+    scene = {"arm": 5, "chain": 3}[name]
+    return scenes.build(scene, count), scenes.SCENES[scene].sig
+
+
+@pytest.mark.parametrize("name,caps,steps,inputs", CASES, ids=[c[0] for c in CASES])
+def test_oracle_matches_reference_art_build(name, caps, steps, inputs):
+    lib = T.ref_art_lib(caps)
+    if lib is None:
+        pytest.skip("reference not built (oracle/_ref)")
+    worlds, sig = _case_worlds(name, 8)
+    assert lib.refa_sig() == sig
+    a, b, plain = clone(worlds), clone(worlds), clone(worlds)
+    for t in range(steps):
+        if inputs:
+            for w in (a, b, plain):
+                inputs(w, t)
+        T.oracle_step_art(a, sig, DT, 4)
+        for k in range(len(b)):
+            lib.refa_step(b[k:k + 1].ctypes.data, DT, 4)
+        T.oracle_step_batch(plain, sig, DT, 4)
+    assert len(diff_words(a, b, sig)) == 0
+    changed = len(diff_words(a, plain, sig)) > 0
+    # the chain scene has no contacts, so the articulated path never runs
+    assert changed == (name != "chain")
+
+
+def test_worlds_without_joints_step_as_usual():
+    worlds = scenes.build(2, 6)
+    a, b = clone(worlds), clone(worlds)
+    for _ in range(20):
+        T.oracle_step_art(a, scenes.SCENES[2].sig, DT, 4)
+        T.oracle_step_batch(b, scenes.SCENES[2].sig, DT, 4)
+    assert len(diff_words(a, b, scenes.SCENES[2].sig)) == 0
+
+
+def _hinged_box_world():
+    """No gravity.  A box of half extent 0.1 (8 kg) hangs on a hinge about z
+    at the static post's origin (0, 0.2, 0), centred at (0.3, 0.1, 0), its
+    bottom face resting exactly on the ground; a free box rests on the
+    ground elsewhere."""
+    w = cr.new_worlds(1, gravity=(0.0, 0.0, 0.0))
+    g = cr.body(w, 0, B3_STATIC, (0.0, -0.5, 0.0))
+    cr.box(w, 0, g, (5.0, 0.5, 5.0))
+    post = cr.body(w, 0, B3_STATIC, (0.0, 0.2, 0.0))
+    link = cr.body(w, 0, B3_DYNAMIC, (0.3, 0.1, 0.0))
+    cr.box(w, 0, link, (0.1, 0.1, 0.1))
+    cr.finalize_mass(w, 0, link)
+    cr.revolute(w, 0, post, link, (0.0, 0.0, 0.0), (-0.3, 0.1, 0.0), (0.0, 0.0, 1.0))
+    free = cr.body(w, 0, B3_DYNAMIC, (-2.0, 0.1, 1.0))
+    cr.box(w, 0, free, (0.1, 0.1, 0.1))
+    cr.finalize_mass(w, 0, free)
+    return w, link, free
+
+
+def test_delassus_closed_forms():
+    """Normal masses written by the articulated sweep: for the hinged box,
+    1 / w with w = ((p - anchor) x n . z)^2 / (I_com,z + m d^2) = p_x^2 / I_axis;
+    for the free box, the independent-body mass 1 / (1/m + (r x n) . I^-1 (r x n))."""
+    w, link, free = _hinged_box_world()
+    T.oracle_step_art(w, CUSTOM_SIG, DT, 4)
+    m = 8.0
+    i_axis = m / 3.0 * (0.01 + 0.01) + m * (0.3 ** 2 + 0.1 ** 2)
+    i_com = m / 3.0 * 0.02
+    seen = {link: 0, free: 0}
+    for c in range(int(w["contact_count"][0])):
+        ct = w["contacts"][0, c]
+        b = int(ct["body_b"])
+        n = np.array([ct["normal"][a] for a in "xyz"], np.float64)
+        np.testing.assert_allclose(n, [0.0, 1.0, 0.0], atol=1e-6)
+        center = np.array([w["bodies"]["center"][0, b][a] for a in "xyz"], np.float64)
+        for p in range(int(ct["point_count"])):
+            rb = np.array([ct["points"][p]["r_b"][a] for a in "xyz"], np.float64)
+            got = float(ct["points"][p]["normal_mass"])
+            if b == link:
+                pw = center + rb - np.array([0.0, 0.2, 0.0])
+                wgt = np.cross(pw, n)[2] ** 2 / i_axis
+            else:
+                rn = np.cross(rb, n)
+                wgt = 1.0 / m + rn @ rn / i_com
+            np.testing.assert_allclose(got, 1.0 / wgt, rtol=1e-5)
+            seen[b] += 1
+    assert seen[link] >= 2 and seen[free] >= 2
+
+
+def test_lane_code_matches_oracle():
+    for name, steps in (("passive", 30), ("features", 15)):
+        worlds, sig = _case_worlds(name, 70)
+        ref = clone(worlds)
+        emu = T.EmuSig(sig, worlds)
+        active = (np.arange(70) % 4 != 1).astype(np.uint8)
+        for t in range(steps):
+            act = active if t % 2 else None
+            T.oracle_step_art(ref, sig, DT, 4, act)
+            emu.step_art(DT, 4, act)
+        assert len(diff_words(emu.worlds(), ref, sig)) == 0, name
+
+
+def test_art_option_is_validated_without_a_device():
+    from puffysics_amd import _native
+    lib = _native.engine_lib()
+    assert lib.b3_engine_set_options(None, 2) == 1
+    assert lib.b3_engine_set_options(None, 4) == 1
+
+
+# ---- device ----
+
+torch = pytest.importorskip("torch")
+
+
+def _dev(a):
+    return None if a is None else torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.mark.gpu
+def test_device_art_bit_exact_on_passive_hinges():
+    from puffysics_amd.engine import B3_ENGINE_ART_CONTACTS, B3Engine
+    worlds = T.passive_hinge_worlds(130)
+    ref = clone(worlds)
+    eng = B3Engine(worlds, CUSTOM_SIG)
+    eng.set_options(B3_ENGINE_ART_CONTACTS)
+    active = (np.arange(130) % 6 != 3).astype(np.uint8)
+    d_active = _dev(active)
+    for t in range(40):
+        act = t % 3 == 1
+        T.oracle_step_art(ref, CUSTOM_SIG, DT, 4, active if act else None)
+        eng.step(DT, 4, d_active if act else None)
+    torch.cuda.synchronize()
+    got = eng.download()
+    eng.close()
+    bad = diff_words(got, ref, CUSTOM_SIG)
+    assert len(bad) == 0, "%d differing words, first %s" % (len(bad), bad[:4].tolist())
+    assert ref["contact_count"].sum() > 0
+
+
+@pytest.mark.gpu
+def test_device_art_one_step_on_the_arm_scene():
+    from puffysics_amd.engine import B3_ENGINE_ART_CONTACTS, B3Engine
+    from test_gpu_parity import assert_close_state, contact_keys
+    sig = scenes.SCENES[5].sig
+    worlds = scenes.build(5, 128)
+    for t in range(3):
+        _arm_inputs(worlds, t)
+        T.oracle_step_art(worlds, sig, DT, 4)
+    ref = clone(worlds)
+    eng = B3Engine(worlds, sig)
+    eng.set_options(B3_ENGINE_ART_CONTACTS)
+    T.oracle_step_art(ref, sig, DT, 4)
+    eng.step(DT, 4)
+    torch.cuda.synchronize()
+    got = eng.download()
+    eng.close()
+    assert contact_keys(got) == contact_keys(ref)
+    assert_close_state(got, ref)
+
+
+@pytest.mark.gpu
+def test_device_art_rejects_force_laws_and_resets():
+    """Force-law entry points are not available with the option on; the
+    fused reset works as in the ordinary step."""
+    from puffysics_amd.engine import (B3_ENGINE_ART_CONTACTS, B3Engine, b3_batch_step_gravity_gpu,
+                                      fluid_law_default)
+    worlds = T.passive_hinge_worlds(64)
+    eng = B3Engine(worlds, CUSTOM_SIG)
+    eng.set_options(B3_ENGINE_ART_CONTACTS)
+    assert b3_batch_step_gravity_gpu(eng.handle, DT, 4, 1.0, 0.1) == 801   # hipErrorNotSupported
+    from puffysics_amd.engine import b3_batch_step_fluid_gpu
+    st = torch.zeros(64 * (6 * 16 + 1), dtype=torch.float32, device="cuda")
+    assert b3_batch_step_fluid_gpu(eng.handle, DT, 4, fluid_law_default(), st) == 801
+    for _ in range(5):
+        eng.step(DT, 4)
+    reset = np.zeros(64, np.uint8)
+    reset[::4] = 1
+    eng.step(DT, 4, _dev(1 - reset), _dev(reset))
+    torch.cuda.synchronize()
+    got = eng.download()
+    eng.close()
+    assert len(diff_words(got[::4], worlds[::4], CUSTOM_SIG)) == 0
