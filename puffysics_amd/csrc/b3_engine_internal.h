@@ -59,8 +59,21 @@ __device__ inline void restore_tile(uint32_t* live, const uint32_t* snap, const 
         const uint32_t* src = snap + (size_t)(tile * 64 + l) * g.world_words;
         int lo[3], hi[3];
         restore_ranges(g, (int)src[H_CONTACT_COUNT], lo, hi);
-        for (int r = 0; r < 3; r++)
-            for (int k = lo[r] + (int)threadIdx.x; k < hi[r]; k += 64) lt[(size_t)k * 64 + l] = src[k];
+        /* kRestoreBatch 256-byte snapshot reads in flight before their
+         * writes (the reads do not depend on the writes: the snapshots and
+         * the live tiles are separate allocations) */
+        constexpr int kRestoreBatch = 8;
+        for (int r = 0; r < 3; r++) {
+            for (int k0 = lo[r] + (int)threadIdx.x; k0 < hi[r]; k0 += 64 * kRestoreBatch) {
+                uint32_t v[kRestoreBatch];
+#pragma unroll
+                for (int i = 0; i < kRestoreBatch; i++)
+                    if (k0 + 64 * i < hi[r]) v[i] = src[k0 + 64 * i];
+#pragma unroll
+                for (int i = 0; i < kRestoreBatch; i++)
+                    if (k0 + 64 * i < hi[r]) lt[(size_t)(k0 + 64 * i) * 64 + l] = v[i];
+            }
+        }
     }
 }
 
