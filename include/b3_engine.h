@@ -121,13 +121,29 @@ hipError_t b3_engine_device_view(const B3Engine* engine, void** tiles, size_t* w
  * tree's Delassus operator (08_contacts.inl:194-232, 422-437); other
  * worlds step as usual.  The contacts' solver fields are then always
  * written back.  Turning it on allocates a workspace of
- * 4 * count * (101 + 22) * max_bodies bytes (the one exception to
+ * 4 * count * ((116 + 22) * max_bodies + 9) bytes (the one exception to
  * b3_engine_create being the only allocating call); it is freed by
  * b3_engine_destroy.  This mode costs far more per contact than the
  * default, as in the reference.  The force-law entry points return
  * hipErrorNotSupported while it is on. */
 #define B3_ENGINE_ART_CONTACTS 2u
 hipError_t b3_engine_set_options(B3Engine* engine, unsigned int options);
+
+/* b3_art_step (09_step.inl:266-323), which the reference defines only in
+ * its B3_ART_CONTACTS=1 build, over the masked batch: the reduced-
+ * coordinate integrator.  A world whose joints are all passive revolutes
+ * (no motor, spring, limit or fixed rotation) and whose bodies are neither
+ * kinematic nor axis-locked moves its joint trees by articulated-body
+ * dynamics and forward kinematics, solves loop-closing joints as 5x5
+ * blocks and its contacts with four articulated sweeps per solve
+ * (b3_art.cuh:990-1032, 1123-1279); any other world, or one without
+ * joints, takes b3_batch_step_gpu's step with articulated contacts.
+ * Masks, fused restore, validation and errors as b3_batch_step_gpu;
+ * hipErrorNotSupported unless B3_ENGINE_ART_CONTACTS is on (the
+ * workspace).  Results follow libm's sinf, cosf and atan2f (the joint
+ * angles), which the device's differ from in the last place. */
+hipError_t b3_batch_art_step_gpu(B3Engine* engine, float dt, int substeps, const unsigned char* step_mask,
+    const unsigned char* reset_mask, hipStream_t stream);
 
 /* ---- per-substep force laws ----
  * The reference's optional force hook B3_USER_FORCES (01_config.inl:189-198,

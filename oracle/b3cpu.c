@@ -1667,29 +1667,32 @@ static void o_integrate_velocities(OWorld* w, b3r h, const OForceLaw* law) {    
     }
 }
 
-static void o_integrate_positions(OWorld* w, b3r h, b3r inv_dt, b3r max_lin) {           /* :55-107 */
+/* b3_integrate_position_state (:55-93) on one body. */
+static void o_integrate_position_one(OBody* b, b3r h, b3r max_lin2, b3r max_ang2, b3r max_lin, b3r max_ang) {
+    if (b->type == B3_STATIC) return;
+    OV3 v = b->lin_vel, av = b->ang_vel;
+    if (b->flags & B3_LOCK_LIN_X) v.x = 0.0f;
+    if (b->flags & B3_LOCK_LIN_Y) v.y = 0.0f;
+    if (b->flags & B3_LOCK_LIN_Z) v.z = 0.0f;
+    if (b->flags & B3_LOCK_ANG_X) av.x = 0.0f;
+    if (b->flags & B3_LOCK_ANG_Y) av.y = 0.0f;
+    if (b->flags & B3_LOCK_ANG_Z) av.z = 0.0f;
+    b3r v2 = o_len2(v);
+    if (v2 > max_lin2 && v2 > 0.0f) v = o_scale(v, o_rsqrt_scale(max_lin, v2));
+    b3r w2 = o_len2(av);
+    if (w2 > max_ang2 && w2 > 0.0f) av = o_scale(av, o_rsqrt_scale(max_ang, w2));
+    b->lin_vel = v;
+    b->ang_vel = av;
+    b->delta_pos = o_madd(b->delta_pos, h, v);
+    b->delta_rot = o_qintegrate(b->delta_rot, o_scale(av, h));
+}
+
+static void o_integrate_positions(OWorld* w, b3r h, b3r inv_dt, b3r max_lin) {           /* :95-107 */
     b3r max_ang = B3_MAX_ROTATION * inv_dt;
     b3r max_lin2 = max_lin * max_lin;
     b3r max_ang2 = max_ang * max_ang;
-    for (int i = 0; i < w->h->body_count; i++) {
-        OBody* b = &w->bodies[i];
-        if (b->type == B3_STATIC) continue;
-        OV3 v = b->lin_vel, av = b->ang_vel;
-        if (b->flags & B3_LOCK_LIN_X) v.x = 0.0f;
-        if (b->flags & B3_LOCK_LIN_Y) v.y = 0.0f;
-        if (b->flags & B3_LOCK_LIN_Z) v.z = 0.0f;
-        if (b->flags & B3_LOCK_ANG_X) av.x = 0.0f;
-        if (b->flags & B3_LOCK_ANG_Y) av.y = 0.0f;
-        if (b->flags & B3_LOCK_ANG_Z) av.z = 0.0f;
-        b3r v2 = o_len2(v);
-        if (v2 > max_lin2 && v2 > 0.0f) v = o_scale(v, o_rsqrt_scale(max_lin, v2));
-        b3r w2 = o_len2(av);
-        if (w2 > max_ang2 && w2 > 0.0f) av = o_scale(av, o_rsqrt_scale(max_ang, w2));
-        b->lin_vel = v;
-        b->ang_vel = av;
-        b->delta_pos = o_madd(b->delta_pos, h, v);
-        b->delta_rot = o_qintegrate(b->delta_rot, o_scale(av, h));
-    }
+    for (int i = 0; i < w->h->body_count; i++)
+        o_integrate_position_one(&w->bodies[i], h, max_lin2, max_ang2, max_lin, max_ang);
 }
 
 static void o_finalize(OWorld* w) {                                                      /* :109-130 */
@@ -1716,12 +1719,30 @@ static void o_solve_contacts_mode(OWorld* w, b3r inv_h, b3r contact_speed, int u
     if (art_contacts && w->h->joint_count > 0 && w->h->contact_count > 0) {
         OArt art;
         if (o_art_bind(&art, w)) {
-            o_art_solve_contacts(&art, w, inv_h, contact_speed, use_bias);
+            o_art_solve_contacts(&art, w, inv_h, contact_speed, use_bias, 1);
             o_art_free(&art);
             return;
         }
     }
     o_solve_contacts(w, inv_h, contact_speed, use_bias);
+}
+
+/* The contacts' share of b3_warm_start (08_contacts.inl:194-232): the
+ * articulated sweep when that build option is on and the world has joints
+ * and contacts, the independent-body impulses otherwise. */
+static void o_warm_contacts(OWorld* w, int art_contacts) {
+    if (art_contacts && w->h->joint_count > 0 && w->h->contact_count > 0) {
+        OArt art;
+        if (o_art_bind(&art, w)) {
+            o_art_warm_start(&art, w);
+            o_art_free(&art);
+            return;
+        }
+    }
+    for (int i = 0; i < w->h->contact_count; i++) {
+        OContact* c = &w->contacts[i];
+        o_warm_one_contact(c, &w->bodies[c->body_a], &w->bodies[c->body_b]);
+    }
 }
 
 static void o_step(OWorld* w, b3r dt, int substeps, const OForceLaw* law, int art_contacts) {  /* :148-264 */
@@ -1741,19 +1762,7 @@ static void o_step(OWorld* w, b3r dt, int substeps, const OForceLaw* law, int ar
         o_prepare_one_contact(c, &w->bodies[c->body_a], &w->bodies[c->body_b], cs, ss);
     }
     o_prepare_joints(w, h);
-    int warm_done = 0;                                                                   /* 08_contacts.inl:194-232 */
-    if (art_contacts && w->h->joint_count > 0 && w->h->contact_count > 0) {
-        OArt art;
-        if (o_art_bind(&art, w)) {
-            o_art_warm_start(&art, w);
-            o_art_free(&art);
-            warm_done = 1;
-        }
-    }
-    for (int i = 0; !warm_done && i < w->h->contact_count; i++) {
-        OContact* c = &w->contacts[i];
-        o_warm_one_contact(c, &w->bodies[c->body_a], &w->bodies[c->body_b]);
-    }
+    o_warm_contacts(w, art_contacts);
     o_warm_start_joints(w);
     /* b3_step_sub :167-181 */
     for (int s = 0; s < subs; s++) {
@@ -1787,6 +1796,12 @@ void ocpu_step_art(void* world, unsigned long long sig, float dt, int substeps) 
     OWorld w;
     if (!o_view(&w, world, sig)) return;
     o_step(&w, dt, substeps, NULL, 1);
+}
+
+void ocpu_art_step(void* world, unsigned long long sig, float dt, int substeps) {
+    OWorld w;
+    if (!o_view(&w, world, sig)) return;
+    o_art_step(&w, dt, substeps);
 }
 
 void ocpu_step_gravity(void* world, unsigned long long sig, float dt, int substeps, float gravity,

@@ -40,6 +40,9 @@ void ocpu_step_fluid(void* world, unsigned long long sig, float dt, int substeps
  * with revolute joints the warm start and the contact sweeps use
  * articulated responses (b3_art.cuh; 08_contacts.inl:194-232, 422-437). */
 void ocpu_step_art(void* world, unsigned long long sig, float dt, int substeps);
+/* b3_art_step (09_step.inl:266-323): the reduced-coordinate integrator of
+ * passive revolute trees with loop cuts; other worlds take ocpu_step_art. */
+void ocpu_art_step(void* world, unsigned long long sig, float dt, int substeps);
 /* b3_find_contacts alone (08_contacts.inl:64-173). */
 void ocpu_find_contacts(void* world, unsigned long long sig);
 /* b3_batch_step (b3_batch.cuh:39-48): 1 on success, 0 on invalid input. */

@@ -26,6 +26,7 @@ ENGINE_SYMBOLS = [
     ("b3_engine_download", _i, [_vp, None]),
     ("b3_batch_restore_gpu", _i, [_vp, _vp, _vp]),
     ("b3_batch_step_gpu", _i, [_vp, _f, _i, _vp, _vp, _vp]),
+    ("b3_batch_art_step_gpu", _i, [_vp, _f, _i, _vp, _vp, _vp]),
     ("b3_batch_apply_gpu", _i, [_vp, _vp, _vp, _vp, _vp, _vp]),
     ("b3_batch_stats_gpu", _i, [_vp, _vp, _vp]),
     ("b3_engine_device_view", _i, [_vp, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]),

@@ -20,7 +20,14 @@
  * so it is built once per step; the reference rebuilds an identical one on
  * every call.  The joint angles and rates that b3_art_refresh also
  * computes (b3_art.cuh:563-568) feed only b3_art_step's integrator, never
- * the Delassus operator, and are left out here.
+ * the Delassus operator: art_refresh leaves them out, art_refresh_q (the
+ * integrator's) adds them.
+ *
+ * The second half is b3_art_step (09_step.inl:266-323), the reduced-
+ * coordinate integrator: passive revolute trees move by their joint angles
+ * (articulated-body dynamics, then forward kinematics), loop-closing joints
+ * ("cuts") are solved as 5x5 Delassus blocks, and contacts take four
+ * articulated sweeps per solve.
  */
 #ifndef PUFFYSICS_AMD_B3D_ART_H
 #define PUFFYSICS_AMD_B3D_ART_H
@@ -30,19 +37,25 @@
 namespace b3d {
 
 constexpr int kArtMaxDeg = 8;        /* B3_ART_MAX_DEG, b3_art.cuh:31-33 */
+constexpr int kArtMaxCuts = 8;       /* B3_ART_MAX_CUTS, :34-36 */
+constexpr int kArtCutIters = 4;      /* B3_ART_CUT_ITERS, :37-39 */
+constexpr int kArtContactIters = 4;  /* B3_ART_CONTACT_ITERS, :1281-1283 */
 constexpr float kArtDmin = 1.0e-8f;  /* B3_ART_DMIN, :40-42 */
 
-/* Link block words. */
+/* Link block words.  AL_C (bias acceleration), AL_Q / AL_QD (joint angle
+ * and rate) and the child-side joint frame AL_ANCHOR_B / AL_ROT_B serve the
+ * reduced integrator only. */
 constexpr int AL_PARENT = 0, AL_BODY = 1, AL_FIXED = 2, AL_FLOATING = 3, AL_ANCHOR_A = 4, AL_ROT_A = 7,
               AL_LC = 11, AL_ILOCAL = 14, AL_MASS = 17, AL_COM = 18, AL_POS = 21, AL_ROT = 24, AL_R = 28,
               AL_SW = 31, AL_SV = 34, AL_IWW = 37, AL_IA = 46, AL_U = 82, AL_PA = 88, AL_DINV = 94, AL_A = 95,
-              kArtLinkWords = 101;
+              AL_C = 101, AL_Q = 107, AL_QD = 108, AL_ANCHOR_B = 109, AL_ROT_B = 112, kArtLinkWords = 116;
 /* Search temporaries per body: degree, neighbours and joints, link of the
  * body, seen flag, queue, parent body and joint. */
 constexpr int kArtBodyTmp = 2 * kArtMaxDeg + 6;
 
-/* Words of one lane's workspace for a body capacity. */
-B3D_FN int art_ws_words(int max_b) { return max_b * (kArtLinkWords + kArtBodyTmp); }
+/* Words of one lane's workspace for a body capacity: the link blocks, the
+ * search temporaries, then the cut count and the cut joints. */
+B3D_FN int art_ws_words(int max_b) { return max_b * (kArtLinkWords + kArtBodyTmp) + 1 + kArtMaxCuts; }
 
 struct M6 { M3 ww, wv, vw, vv; };   /* spatial inertia, angular first (b3_art.cuh:54-59) */
 struct S6 { V3 w, v; };             /* motion or force: (angular, linear) */
@@ -70,6 +83,12 @@ struct ArtWs {
     /* search temporaries of body b */
     B3D_MFN int ti(int b, int f) const { return __builtin_bit_cast(int, p[(max_b * kArtLinkWords + b * kArtBodyTmp + f) * kLanes]); }
     B3D_MFN void tsi(int b, int f, int x) const { p[(max_b * kArtLinkWords + b * kArtBodyTmp + f) * kLanes] = __builtin_bit_cast(float, x); }
+    /* loop cuts: count, then joint indices */
+    B3D_MFN int cut_word(int k) const { return max_b * (kArtLinkWords + kArtBodyTmp) + k; }
+    B3D_MFN int n_cuts() const { return __builtin_bit_cast(int, p[cut_word(0) * kLanes]); }
+    B3D_MFN int cut(int c) const { return __builtin_bit_cast(int, p[cut_word(1 + c) * kLanes]); }
+    B3D_MFN void set_n_cuts(int n) const { p[cut_word(0) * kLanes] = __builtin_bit_cast(float, n); }
+    B3D_MFN void set_cut(int c, int j) const { p[cut_word(1 + c) * kLanes] = __builtin_bit_cast(float, j); }
 };
 constexpr int AT_DEG = 0, AT_ADJ_B = 1, AT_ADJ_J = 1 + kArtMaxDeg, AT_LINK = 1 + 2 * kArtMaxDeg, AT_SEEN = AT_LINK + 1,
               AT_QUEUE = AT_SEEN + 1, AT_PARENT_B = AT_QUEUE + 1, AT_PARENT_J = AT_PARENT_B + 1;
@@ -173,9 +192,10 @@ B3D_FN bool isolve(const M6& I, S6 rhs, S6* a) {
 
 /* b3_art_from_world (:340-486): the spanning forest of the revolute joints,
  * breadth first from the static bodies, then from dynamic ones; dynamic
- * bodies outside it float alone.  Cut joints (loops) take no part in the
- * contact path and are not recorded.  False when the tree cannot be built
- * (self-joint, a degree above kArtMaxDeg, more than 8 cuts, or no link). */
+ * bodies outside it float alone; joints that close a loop are recorded as
+ * cuts (used by the reduced integrator only).  False when the tree cannot
+ * be built (self-joint, a degree above kArtMaxDeg, more than kArtMaxCuts
+ * cuts, or no link). */
 B3D_FN bool art_build(const Lane& L, ArtWs& A) {
     const uint32_t* w = L.w;
     int nb = body_count(L);
@@ -202,7 +222,7 @@ B3D_FN bool art_build(const Lane& L, ArtWs& A) {
         A.tsi(b, AT_DEG, db + 1);
     }
     int n_cuts = 0;
-    int cuts[8];
+    A.set_n_cuts(0);
     for (int pass = 0; pass < 2; pass++) {
         for (int s = 0; s < nb; s++) {
             int is_static = ldi(w, bw(L, s, B_TYPE)) != kDynamic;
@@ -220,10 +240,11 @@ B3D_FN bool art_build(const Lane& L, ArtWs& A) {
                     if (A.ti(v, AT_SEEN)) {
                         if (A.ti(u, AT_PARENT_B) != v && A.ti(v, AT_PARENT_B) != u) {
                             int jk = A.ti(u, AT_ADJ_J + e), dup = 0;
-                            for (int c = 0; c < n_cuts; c++) dup |= cuts[c] == jk;
+                            for (int c = 0; c < n_cuts; c++) dup |= A.cut(c) == jk;
                             if (!dup) {
-                                if (n_cuts >= 8) return false;
-                                cuts[n_cuts++] = jk;
+                                if (n_cuts >= kArtMaxCuts) return false;
+                                A.set_cut(n_cuts++, jk);
+                                A.set_n_cuts(n_cuts);
                             }
                         }
                         continue;
@@ -252,6 +273,8 @@ B3D_FN bool art_build(const Lane& L, ArtWs& A) {
                     int side_b = ldi(w, jw(L, jk, J_BODY_B)) == b;
                     A.s3(li, AL_ANCHOR_A, ld3(w, jw(L, jk, side_b ? J_LOCAL_ANCHOR_A : J_LOCAL_ANCHOR_B)));
                     A.sq(li, AL_ROT_A, ldq(w, jw(L, jk, side_b ? J_LOCAL_ROT_A : J_LOCAL_ROT_B)));
+                    A.s3(li, AL_ANCHOR_B, ld3(w, jw(L, jk, side_b ? J_LOCAL_ANCHOR_B : J_LOCAL_ANCHOR_A)));
+                    A.sq(li, AL_ROT_B, ldq(w, jw(L, jk, side_b ? J_LOCAL_ROT_B : J_LOCAL_ROT_A)));
                 }
             }
         }
@@ -623,11 +646,14 @@ B3D_FN void art_friction(const Lane& L, const ArtWs& A, int c, const WContact& k
     st3(w, cw(L, c, C_ROLLING_IMPULSE), roll);
 }
 
-/* b3_art_solve_contacts with one iteration (08_contacts.inl:425-432;
- * b3_art.cuh:1220-1279). */
-B3D_FN void art_solve_contacts(const Lane& L, const ArtWs& A, float inv_h, float contact_speed, int use_bias) {
+/* b3_art_solve_contacts (b3_art.cuh:1220-1279): one iteration from the
+ * contact sweeps (08_contacts.inl:425-432), kArtContactIters from the
+ * reduced integrator; the normal masses are computed on the first. */
+B3D_FN void art_solve_contacts(const Lane& L, const ArtWs& A, float inv_h, float contact_speed, int use_bias,
+        int iters = 1) {
     uint32_t* w = L.w;
     int cc = ldi(w, H_CONTACT_COUNT);
+    for (int it = 0; it < iters; it++)
     for (int c = 0; c < cc; c++) {
         WContact k = wc_load(L, c);
         const uint32_t* da = delta_rec(L, k.a);
@@ -639,9 +665,14 @@ B3D_FN void art_solve_contacts(const Lane& L, const ArtWs& A, float inv_h, float
             V3 ra = ld3(w, pw(L, c, p, P_R_A)), rb = ld3(w, pw(L, c, p, P_R_B));
             ArtRow row;
             if (!art_make_row(A, k.a, k.b, ra, rb, k.n, &row)) continue;
-            float ww = art_response(L, A, row);
-            float nmass = ww > 0.0f ? 1.0f / ww : 0.0f;
-            stf(w, pw(L, c, p, P_NORMAL_MASS), nmass);
+            float nmass;
+            if (it == 0) {
+                float ww = art_response(L, A, row);
+                nmass = ww > 0.0f ? 1.0f / ww : 0.0f;
+                stf(w, pw(L, c, p, P_NORMAL_MASS), nmass);
+            } else {
+                nmass = ldf(w, pw(L, c, p, P_NORMAL_MASS));
+            }
             V3 ds = add(dp, sub(rot(dqb, rb), rot(dqa, ra)));
             float sep = dot(ds, k.n) + ldf(w, pw(L, c, p, P_BASE_SEP));
             float vbias = 0.0f, mscale = 1.0f, iscale = 0.0f;
@@ -929,50 +960,467 @@ B3D_FN void wrow_restitution(const Lane& L, float threshold) {
     }
 }
 
-/* One world's b3_step built with articulated contacts (09_step.inl:148-264
- * with 08_contacts.inl:194-232, 422-437).  Joints, integration and
- * finalize are the ordinary step's; the contacts live in the world rows.
- * `ws` is the lane's workspace. */
-B3D_FN void step_world_art(const Lane& L0, float* ws, float dt, int substeps) {
-    if (!(dt > 0.0f)) return;
-    Lane L = L0;
-    L.sslot = wave_slot(L);
-    int subs = substeps < 1 ? 1 : substeps;
-    float h = dt / (float)subs;
-    float inv_dt = 1.0f / dt;
-    float inv_h = (float)subs * inv_dt;
-    float hertz = minf(ldf(L.w, H_CONTACT_HERTZ), 0.25f * inv_h);
+/* The step's constants (b3_soft_step_params). */
+struct ArtParams {
+    int subs;
+    float h, inv_h, inv_dt, contact_speed, rest_threshold;
+    Soft cs, ss;
+};
+B3D_FN ArtParams art_params(const Lane& L, float dt, int substeps) {
+    ArtParams P;
+    P.subs = substeps < 1 ? 1 : substeps;
+    P.h = dt / (float)P.subs;
+    P.inv_dt = 1.0f / dt;
+    P.inv_h = (float)P.subs * P.inv_dt;
+    float hertz = minf(ldf(L.w, H_CONTACT_HERTZ), 0.25f * P.inv_h);
     float damping = ldf(L.w, H_CONTACT_DAMPING);
-    Soft cs = make_soft(hertz, damping, h);
-    Soft ss = make_soft(2.0f * hertz, 0.5f * damping, h);
-    float contact_speed = ldf(L.w, H_CONTACT_SPEED);
-    float rest_threshold = ldf(L.w, H_RESTITUTION_THRESHOLD);
+    P.cs = make_soft(hertz, damping, P.h);
+    P.ss = make_soft(2.0f * hertz, 0.5f * damping, P.h);
+    P.contact_speed = ldf(L.w, H_CONTACT_SPEED);
+    P.rest_threshold = ldf(L.w, H_RESTITUTION_THRESHOLD);
+    return P;
+}
 
+/* The opening both integrators share: contacts found and prepared in the
+ * world rows, velocities staged, per-step body records. */
+B3D_FN void art_open(const Lane& L, const ArtParams& P) {
     find_contacts(L);
     vel_load(L);
-    body_prepass(L, h);
-    wrow_prepare(L, cs, ss);
-    prepare_joints(L, h);
-    ArtWs A;
-    A.p = ws;
-    A.max_b = L.g.max_b;
-    A.n_links = 0;
-    bool art = ldi(L.w, H_JOINT_COUNT) > 0 && ldi(L.w, H_CONTACT_COUNT) > 0 && art_build(L, A);
+    body_prepass(L, P.h);
+    wrow_prepare(L, P.cs, P.ss);
+}
+
+/* The rest of b3_step with articulated contacts (09_step.inl:148-264 with
+ * 08_contacts.inl:194-232, 422-437).  Joints, integration and finalize are
+ * the ordinary step's.  `built` is 1 when the caller has already built the
+ * lane's tree, 0 when it has not tried. */
+B3D_FN void art_indep_rest(const Lane& L, ArtWs& A, const ArtParams& P, int built) {
+    prepare_joints(L, P.h);
+    bool art = ldi(L.w, H_JOINT_COUNT) > 0 && ldi(L.w, H_CONTACT_COUNT) > 0 && (built || art_build(L, A));
     if (art) art_warm_start(L, A);
     else wrow_warm(L);
     warm_start_joints(L);
     joint_geometry(L);
-    for (int s = 0; s < subs; s++) {
+    for (int s = 0; s < P.subs; s++) {
         integrate_velocities(L);
-        if (art) art_solve_contacts(L, A, inv_h, contact_speed, 1);
-        else wrow_solve(L, inv_h, contact_speed, 1);
-        solve_joints(L, h, inv_h, 1);
-        integrate_positions(L, h, inv_dt);
+        if (art) art_solve_contacts(L, A, P.inv_h, P.contact_speed, 1);
+        else wrow_solve(L, P.inv_h, P.contact_speed, 1);
+        solve_joints(L, P.h, P.inv_h, 1);
+        integrate_positions(L, P.h, P.inv_dt);
         delta_geometry(L);
-        if (art) art_solve_contacts(L, A, inv_h, contact_speed, 0);
-        else wrow_solve(L, inv_h, contact_speed, 0);
-        solve_joints(L, h, inv_h, 0);
-        wrow_restitution(L, rest_threshold);
+        if (art) art_solve_contacts(L, A, P.inv_h, P.contact_speed, 0);
+        else wrow_solve(L, P.inv_h, P.contact_speed, 0);
+        solve_joints(L, P.h, P.inv_h, 0);
+        wrow_restitution(L, P.rest_threshold);
+    }
+    finalize(L);
+    vel_store(L);
+}
+
+B3D_FN ArtWs art_ws_of(const Lane& L, float* ws) {
+    ArtWs A;
+    A.p = ws;
+    A.max_b = L.g.max_b;
+    A.n_links = 0;
+    return A;
+}
+
+/* One world's b3_step built with articulated contacts.  `ws` is the lane's
+ * workspace. */
+B3D_FN void step_world_art(const Lane& L0, float* ws, float dt, int substeps) {
+    if (!(dt > 0.0f)) return;
+    Lane L = L0;
+    L.sslot = wave_slot(L);
+    ArtParams P = art_params(L, dt, substeps);
+    art_open(L, P);
+    ArtWs A = art_ws_of(L, ws);
+    art_indep_rest(L, A, P, 0);
+}
+
+/* ---- the reduced-coordinate integrator (b3_art_step) ---- */
+
+B3D_FN Q qaxis_angle(V3 axis, float radians) {                           /* 03_math.inl:321-326 */
+    axis = norm(axis);
+    float h = 0.5f * radians;
+    float s = sinf(h);
+    return q4(s * axis.x, s * axis.y, s * axis.z, cosf(h));
+}
+
+/* art_refresh with each joint's rate about its axis and its angle, the
+ * twist of the child frame relative to the parent frame (b3_art.cuh:
+ * 499-507, 563-568). */
+B3D_FN void art_refresh_q(const Lane& L, const ArtWs& A) {
+    art_refresh(L, A);
+    for (int i = 0; i < A.n_links; i++) {
+        int p = A.gi(i, AL_PARENT);
+        float q = 0.0f, qd = 0.0f;
+        if (p >= 0) {
+            V3 wrel = sub(vang(L, A.gi(i, AL_BODY)), vang(L, A.gi(p, AL_BODY)));
+            qd = dot(wrel, A.g3(i, AL_SW));
+            Q qa = qmul(A.gq(p, AL_ROT), A.gq(i, AL_ROT_A));
+            Q qb = qmul(A.gq(i, AL_ROT), A.gq(i, AL_ROT_B));
+            if (qdot(qa, qb) < 0.0f) qb = qneg(qb);
+            q = twist(qinv_mul(qa, qb));
+        }
+        A.sf(i, AL_Q, q);
+        A.sf(i, AL_QD, qd);
+    }
+}
+
+/* Link accelerations under gravity, applied loads and velocity products
+ * with zero joint torques (b3_art_aba, :668-673: the refresh, the full
+ * b3_art_seed_bias, :572-605, and both sweeps, :607-666). */
+B3D_FN void art_aba(const Lane& L, const ArtWs& A) {
+    art_refresh_q(L, A);
+    V3 g = ld3(L.w, H_GRAVITY);
+    for (int i = 0; i < A.n_links; i++) {
+        M6 I = art_inertia(A, i);
+        A.sI(i, AL_IA, I);
+        S6 pa = s6zero(), c = s6zero();
+        if (!A.gi(i, AL_FIXED)) {
+            int b = A.gi(i, AL_BODY);
+            S6 v;
+            v.w = vang(L, b);
+            v.v = vlin(L, b);
+            S6 ext;
+            ext.v = add(ld3(L.w, bw(L, b, B_FORCE)),
+                scale(g, A.gf(i, AL_MASS) * ldf(L.w, bw(L, b, B_GRAVITY_SCALE))));
+            ext.w = ld3(L.w, bw(L, b, B_TORQUE));
+            S6 Iw = imul(I, v);
+            pa.w = sub(cross(v.w, Iw.w), ext.w);
+            pa.v = sub(cross(v.w, Iw.v), ext.v);
+            int p = A.gi(i, AL_PARENT);
+            if (p >= 0) {
+                float qd = A.gf(i, AL_QD);
+                V3 wp = vang(L, A.gi(p, AL_BODY));
+                c.w = cross(v.w, scale(A.g3(i, AL_SW), qd));
+                c.v = add(cross(v.w, scale(A.g3(i, AL_SV), qd)), cross(wp, cross(wp, A.g3(i, AL_R))));
+            }
+        }
+        A.s6(i, AL_PA, pa);
+        A.s6(i, AL_C, c);
+    }
+    for (int i = A.n_links - 1; i >= 0; i--) {
+        int p = A.gi(i, AL_PARENT);
+        if (p < 0) continue;
+        S6 S;
+        S.w = A.g3(i, AL_SW);
+        S.v = A.g3(i, AL_SV);
+        M6 IA = A.gI(i, AL_IA);
+        S6 U = imul(IA, S);
+        A.s6(i, AL_U, U);
+        float D = sdot(S, U);
+        if (D < kArtDmin) D = kArtDmin;
+        float Dinv = 1.0f / D;
+        A.sf(i, AL_DINV, Dinv);
+        S6 pA = A.g6(i, AL_PA);
+        float u = 0.0f - sdot(S, pA);
+        M6 IAp = irank1(IA, U, Dinv);
+        S6 Ic = imul(IA, A.g6(i, AL_C));
+        pA.w = add(add(pA.w, Ic.w), scale(U.w, u * Dinv));
+        pA.v = add(add(pA.v, Ic.v), scale(U.v, u * Dinv));
+        if (!A.gi(p, AL_FIXED)) {
+            V3 r = A.g3(i, AL_R);
+            A.sI(p, AL_IA, iadd(A.gI(p, AL_IA), ishift(IAp, r)));
+            S6 pp = A.g6(p, AL_PA);
+            pp.w = add(pp.w, add(pA.w, cross(r, pA.v)));
+            pp.v = add(pp.v, pA.v);
+            A.s6(p, AL_PA, pp);
+        }
+    }
+    for (int i = 0; i < A.n_links; i++) {
+        int p = A.gi(i, AL_PARENT);
+        if (p < 0) {
+            S6 a = s6zero();
+            if (!A.gi(i, AL_FIXED) && A.gi(i, AL_FLOATING)) {
+                S6 pA = A.g6(i, AL_PA), rhs;
+                rhs.w = neg(pA.w);
+                rhs.v = neg(pA.v);
+                if (!isolve(A.gI(i, AL_IA), rhs, &a)) a = s6zero();
+            }
+            A.s6(i, AL_A, a);
+            continue;
+        }
+        S6 ap = A.g6(p, AL_A), rhs, c = A.g6(i, AL_C);
+        V3 r = A.g3(i, AL_R);
+        rhs.w = ap.w;
+        rhs.v = add(ap.v, cross(ap.w, r));
+        rhs.w = add(rhs.w, c.w);
+        rhs.v = add(rhs.v, c.v);
+        S6 S;
+        S.w = A.g3(i, AL_SW);
+        S.v = A.g3(i, AL_SV);
+        float u = 0.0f - sdot(S, A.g6(i, AL_PA));
+        u -= sdot(S, imul(A.gI(i, AL_IA), rhs));
+        float qdd = A.gf(i, AL_DINV) * u;
+        S6 a;
+        a.w = add(rhs.w, scale(S.w, qdd));
+        a.v = add(rhs.v, scale(S.v, qdd));
+        A.s6(i, AL_A, a);
+    }
+}
+
+/* b3_art_integrate_vel (:990-1000). */
+B3D_FN void art_integrate_vel(const Lane& L, const ArtWs& A, float h) {
+    art_aba(L, A);
+    for (int i = 0; i < A.n_links; i++) {
+        if (A.gi(i, AL_FIXED)) continue;
+        int b = A.gi(i, AL_BODY);
+        S6 a = A.g6(i, AL_A);
+        set_vlin(L, b, madd(vlin(L, b), h, a.v));
+        set_vang(L, b, madd(vang(L, b), h, a.w));
+    }
+}
+
+/* Link i's pose from its parent's and its joint angle q (b3_art_fk_link,
+ * :509-525). */
+B3D_FN void art_fk_link(const ArtWs& A, int i, float q) {
+    int p = A.gi(i, AL_PARENT);
+    Q rz = qaxis_angle(v3(0.0f, 0.0f, 1.0f), q);
+    Q rp = A.gq(p, AL_ROT);
+    Q rq = qnorm(qmul(rp, qmul(A.gq(i, AL_ROT_A), qmul(rz, qconj(A.gq(i, AL_ROT_B))))));
+    V3 anchor = xf(A.g3(p, AL_POS), rp, A.g3(i, AL_ANCHOR_A));
+    V3 com = add(anchor, rot(rq, sub(A.g3(i, AL_LC), A.g3(i, AL_ANCHOR_B))));
+    A.sq(i, AL_ROT, rq);
+    A.s3(i, AL_COM, com);
+    A.s3(i, AL_POS, sub(com, rot(rq, A.g3(i, AL_LC))));
+}
+
+/* Roots move as free bodies (b3_integrate_position_state, 09_step.inl:
+ * 55-93, without axis locks: locked worlds never get here); joints advance
+ * by h qd, the rate clamped to the rotation limit, and the tree's poses
+ * follow, written to the delta records (b3_art_integrate_pos, :1002-1032;
+ * b3_art_write_delta, :981-988). */
+B3D_FN void art_integrate_pos(const Lane& L, const ArtWs& A, float h, float inv_dt) {
+    float max_lin = ldf(L.w, H_MAX_LINEAR_SPEED);
+    float max_ang = kMaxRotation * inv_dt;
+    float max_lin2 = max_lin * max_lin;
+    float max_ang2 = max_ang * max_ang;
+    art_refresh_q(L, A);
+    for (int i = 0; i < A.n_links; i++) {
+        int p = A.gi(i, AL_PARENT);
+        int b = A.gi(i, AL_BODY);
+        if (p < 0) {
+            if (A.gi(i, AL_FIXED)) continue;
+            V3 v = vlin(L, b), av = vang(L, b);
+            float v2 = len2(v);
+            if (v2 > max_lin2 && v2 > 0.0f) v = scale(v, rsqrt_scale(max_lin, v2));
+            float w2 = len2(av);
+            if (w2 > max_ang2 && w2 > 0.0f) av = scale(av, rsqrt_scale(max_ang, w2));
+            set_vlin(L, b, v);
+            set_vang(L, b, av);
+            uint32_t* d = delta_rec(L, b);
+            V3 dp = madd(r3(d, BD_DP), h, v);
+            Q dq = qintegrate(rq4(d, BD_DQ), scale(av, h));
+            rs3(d, BD_DP, dp);
+            rsq(d, BD_DQ, dq);
+            Q rq = qnorm(qmul(dq, ldq(L.w, bw(L, b, B_ROTATION))));
+            V3 com = add(ld3(L.w, bw(L, b, B_CENTER)), dp);
+            A.sq(i, AL_ROT, rq);
+            A.s3(i, AL_COM, com);
+            A.s3(i, AL_POS, sub(com, rot(rq, A.g3(i, AL_LC))));
+            continue;
+        }
+        float qd = A.gf(i, AL_QD);
+        if (qd * qd > max_ang2 && max_ang2 > 0.0f) qd = copysignf(max_ang, qd);
+        art_fk_link(A, i, A.gf(i, AL_Q) + h * qd);
+        if (A.gi(i, AL_FIXED)) continue;
+        uint32_t* d = delta_rec(L, b);
+        rs3(d, BD_DP, sub(A.g3(i, AL_COM), ld3(L.w, bw(L, b, B_CENTER))));
+        rsq(d, BD_DQ, qnorm(qmul(A.gq(i, AL_ROT), qconj(ldq(L.w, bw(L, b, B_ROTATION))))));
+    }
+}
+
+/* The velocity along a row (b3_art_row_eval without accelerations,
+ * :688-720); the link velocities are the bodies'. */
+B3D_FN float art_row_vel(const Lane& L, const ArtWs& A, const ArtRow& row) {
+    float y = 0.0f;
+    int ba = row.link_a >= 0 ? A.gi(row.link_a, AL_BODY) : -1;
+    int bb = row.link_b >= 0 ? A.gi(row.link_b, AL_BODY) : -1;
+    if (row.torque == 1) {
+        if (ba >= 0) y += dot(vang(L, ba), row.n);
+        if (bb >= 0) y -= dot(vang(L, bb), row.n);
+        return y;
+    }
+    if (ba >= 0) y += dot(add(vlin(L, ba), cross(vang(L, ba), row.ra)), row.n);
+    if (bb >= 0) y -= dot(add(vlin(L, bb), cross(vang(L, bb), row.rb)), row.n);
+    return y;
+}
+
+/* The five rows of cut c, three linear and two angular, with their errors
+ * (b3_art_cut_rows, :1123-1175); false when a side has no link. */
+B3D_FN bool art_cut_rows(const Lane& L, const ArtWs& A, int c, ArtRow rows[5], float err[5]) {
+    const uint32_t* w = L.w;
+    int jk = A.cut(c);
+    int la = art_link_of(A, ldi(w, jw(L, jk, J_BODY_A))), lb = art_link_of(A, ldi(w, jw(L, jk, J_BODY_B)));
+    if (la < 0 || lb < 0) return false;
+    Q rla = A.gq(la, AL_ROT), rlb = A.gq(lb, AL_ROT);
+    V3 pa = xf(A.g3(la, AL_POS), rla, ld3(w, jw(L, jk, J_LOCAL_ANCHOR_A)));
+    V3 pb = xf(A.g3(lb, AL_POS), rlb, ld3(w, jw(L, jk, J_LOCAL_ANCHOR_B)));
+    V3 ra = sub(pa, A.g3(la, AL_COM)), rb = sub(pb, A.g3(lb, AL_COM)), d = sub(pb, pa);
+    for (int k = 0; k < 3; k++) {
+        V3 ax = v3(k == 0 ? 1.0f : 0.0f, k == 1 ? 1.0f : 0.0f, k == 2 ? 1.0f : 0.0f);
+        rows[k].link_a = la;
+        rows[k].link_b = lb;
+        rows[k].torque = 0;
+        rows[k].ra = ra;
+        rows[k].rb = rb;
+        rows[k].n = ax;
+        err[k] = dot(d, ax);
+    }
+    Q qa = qmul(rla, ldq(w, jw(L, jk, J_LOCAL_ROT_A))), qb = qmul(rlb, ldq(w, jw(L, jk, J_LOCAL_ROT_B)));
+    if (qdot(qa, qb) < 0.0f) qb = qneg(qb);
+    Q rel = qinv_mul(qa, qb);
+    for (int k = 3; k < 5; k++) {
+        rows[k].link_a = la;
+        rows[k].link_b = lb;
+        rows[k].torque = 1;
+        rows[k].ra = zero3();
+        rows[k].rb = zero3();
+        rows[k].n = rot(qa, k == 3 ? v3(1.0f, 0.0f, 0.0f) : v3(0.0f, 1.0f, 0.0f));
+    }
+    err[3] = 2.0f * rel.v.x;
+    err[4] = 2.0f * rel.v.y;
+    return true;
+}
+
+/* x = D^-1 b for a 5x5 block by Gauss-Jordan with partial pivoting
+ * (b3_solve_n, :869-923); false if a pivot is below 1e-12. */
+B3D_FN bool solve5(const float* D, const float* b, float* x) {
+    float M[5][6];
+    for (int r = 0; r < 5; r++) {
+        for (int c = 0; c < 5; c++) M[r][c] = D[r * 5 + c];
+        M[r][5] = b[r];
+    }
+    for (int k = 0; k < 5; k++) {
+        int piv = k;
+        float best = fabsf(M[k][k]);
+        for (int r = k + 1; r < 5; r++) {
+            float v = fabsf(M[r][k]);
+            if (v > best) {
+                best = v;
+                piv = r;
+            }
+        }
+        if (best < 1.0e-12f) return false;
+        if (piv != k) {
+            for (int c = k; c < 6; c++) {
+                float t = M[k][c];
+                M[k][c] = M[piv][c];
+                M[piv][c] = t;
+            }
+        }
+        float inv = 1.0f / M[k][k];
+        for (int c = k; c < 6; c++) M[k][c] *= inv;
+        for (int r = 0; r < 5; r++) {
+            if (r == k) continue;
+            float s = M[r][k];
+            for (int c = k; c < 6; c++) M[r][c] -= s * M[k][c];
+        }
+    }
+    for (int r = 0; r < 5; r++) x[r] = M[r][5];
+    return true;
+}
+
+/* Each cut's five rows solved together against its 5x5 Delassus block,
+ * Baumgarte-biased by 0.2 / h of the joint error on the biased pass
+ * (b3_art_solve_cuts, :1177-1218, with b3_art_delassus_matrix, :925-940,
+ * and b3_art_apply_impulses, :942-959). */
+B3D_FN void art_solve_cuts(const Lane& L, const ArtWs& A, float inv_h, int use_bias, int iters) {
+    int nc = A.n_cuts();
+    if (nc < 1) return;
+    art_refresh(L, A);
+    for (int it = 0; it < iters; it++) {
+        for (int c = 0; c < nc; c++) {
+            ArtRow rows[5];
+            float err[5];
+            if (!art_cut_rows(L, A, c, rows, err)) continue;
+            art_refresh(L, A);
+            float rhs[5];
+            for (int k = 0; k < 5; k++) {
+                float vbias = 0.0f;
+                if (use_bias) vbias = 0.2f * inv_h * err[k];
+                rhs[k] = art_row_vel(L, A, rows[k]) - vbias;
+            }
+            float D[25], x[5], y[5];
+            for (int k = 0; k < 5; k++) x[k] = 0.0f;
+            for (int col = 0; col < 5; col++) {
+                x[col] = 1.0f;
+                art_delassus(L, A, rows, x, y, 5);
+                for (int r = 0; r < 5; r++) D[r * 5 + col] = y[r];
+                x[col] = 0.0f;
+            }
+            for (int k = 0; k < 5; k++) D[k * 5 + k] += 1.0e-8f;
+            float lam[5];
+            if (!solve5(D, rhs, lam)) {
+                for (int k = 0; k < 5; k++) {
+                    float ww = D[k * 5 + k];
+                    lam[k] = ww > 1.0e-10f ? rhs[k] / ww : 0.0f;
+                }
+            }
+            int any = 0;
+            for (int k = 0; k < 5; k++) {
+                x[k] = -lam[k];
+                any |= lam[k] != 0.0f;
+            }
+            if (!any) continue;
+            art_delassus(L, A, rows, x, y, 5);
+            for (int i = 0; i < A.n_links; i++) {
+                if (A.gi(i, AL_FIXED)) continue;
+                int b = A.gi(i, AL_BODY);
+                S6 a = A.g6(i, AL_A);
+                set_vlin(L, b, add(vlin(L, b), a.v));
+                set_vang(L, b, add(vang(L, b), a.w));
+            }
+        }
+    }
+}
+
+/* What the reduced integrator cannot honour sends a world to the ordinary
+ * step (09_step.inl:271-291): a weld, a motor, spring or limit, a joint
+ * with fixed rotation, a kinematic body or an axis lock. */
+B3D_FN bool art_reduced_supported(const Lane& L) {
+    const uint32_t* w = L.w;
+    int nj = clampi(ldi(w, H_JOINT_COUNT), 0, L.g.max_j);
+    for (int j = 0; j < nj; j++) {
+        if (ldi(w, jw(L, j, J_FIXED_ROTATION)) || ldi(w, jw(L, j, J_ENABLE_SPRING)) || ldi(w, jw(L, j, J_ENABLE_LIMIT))
+                || ldi(w, jw(L, j, J_TYPE)) != kJointRevolute || ldi(w, jw(L, j, J_ENABLE_MOTOR)))
+            return false;
+    }
+    int nb = body_count(L);
+    for (int b = 0; b < nb; b++) {
+        if (ldi(w, bw(L, b, B_TYPE)) == kKinematic || (ldu(w, bw(L, b, B_FLAGS)) & 0x3fu)) return false;
+    }
+    return true;
+}
+
+/* One world's b3_art_step (09_step.inl:266-323): worlds it cannot take, and
+ * worlds without joints or whose tree does not build, take the step with
+ * articulated contacts.  The opening is shared so that every stepping lane
+ * ranks its records together. */
+B3D_FN void step_world_art_reduced(const Lane& L0, float* ws, float dt, int substeps) {
+    if (!(dt > 0.0f)) return;
+    Lane L = L0;
+    L.sslot = wave_slot(L);
+    ArtParams P = art_params(L, dt, substeps);
+    bool supported = art_reduced_supported(L);
+    art_open(L, P);
+    ArtWs A = art_ws_of(L, ws);
+    if (!(supported && ldi(L.w, H_JOINT_COUNT) > 0 && art_build(L, A))) {
+        art_indep_rest(L, A, P, 0);
+        return;
+    }
+    /* b3_warm_start: this world's tree builds, so the articulated branch
+     * runs whenever there are contacts */
+    if (ldi(L.w, H_CONTACT_COUNT) > 0) art_warm_start(L, A);
+    for (int s = 0; s < P.subs; s++) {
+        art_integrate_vel(L, A, P.h);
+        art_solve_contacts(L, A, P.inv_h, P.contact_speed, 1, kArtContactIters);
+        art_solve_cuts(L, A, P.inv_h, 1, kArtCutIters);
+        art_integrate_pos(L, A, P.h, P.inv_dt);
+        art_solve_contacts(L, A, P.inv_h, P.contact_speed, 0, kArtContactIters);
+        art_solve_cuts(L, A, P.inv_h, 0, kArtCutIters);
+        wrow_restitution(L, P.rest_threshold);
     }
     finalize(L);
     vel_store(L);

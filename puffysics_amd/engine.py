@@ -57,6 +57,14 @@ def b3_batch_step_gpu(engine, dt, substeps, step_mask=None, reset_mask=None, str
                                                   _stream(stream))
 
 
+def b3_batch_art_step_gpu(engine, dt, substeps, step_mask=None, reset_mask=None, stream=None):
+    """b3_art_step, the reduced-coordinate integrator (09_step.inl:266-323),
+    over the masked batch with the fused restore; the engine needs
+    B3_ENGINE_ART_CONTACTS."""
+    return _native.engine_lib().b3_batch_art_step_gpu(engine, dt, substeps, _ptr(step_mask), _ptr(reset_mask),
+                                                      _stream(stream))
+
+
 def b3_batch_restore_gpu(engine, reset=None, stream=None):
     """Masked snapshot restore (b3_batch_restore_gpu, b3_batch.cuh:91-99)."""
     return _native.engine_lib().b3_batch_restore_gpu(engine, _ptr(reset), _stream(stream))
@@ -156,6 +164,10 @@ class B3Engine:
 
     def step(self, dt, substeps, step_mask=None, reset_mask=None, stream=None):
         self._check("b3_batch_step_gpu", b3_batch_step_gpu(self._h, dt, substeps, step_mask, reset_mask, stream))
+
+    def art_step(self, dt, substeps, step_mask=None, reset_mask=None, stream=None):
+        self._check("b3_batch_art_step_gpu", b3_batch_art_step_gpu(self._h, dt, substeps, step_mask, reset_mask,
+                                                                   stream))
 
     def step_gravity(self, dt, substeps, gravity, softening, masses=None, step_mask=None, reset_mask=None,
                      stream=None):

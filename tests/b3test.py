@@ -319,6 +319,75 @@ def passive_hinge_worlds(count, seed=5):
     return w
 
 
+def reduced_tree_worlds(count, seed=11):
+    """Worlds of capacity set 16/16/32/8 for the reduced-coordinate
+    integrator, every joint passive and revolute with coincident anchors:
+    a ground box; a static post carrying a hanging chain of three links
+    whose hinge axes lean off z and whose tip swings into a free box on the
+    ground, and a four-bar loop (three links and four hinges, so one hinge
+    is a loop cut); a floating two-link tree dropped on the ground; a free
+    sphere.  Every fourth world puts a motor on its last joint, which sends
+    it to the articulated-contact step instead.
+
+    The reference's reduced integrator gains energy on fast swings (a chain
+    released horizontally diverges within a second), so the scene starts
+    near rest: the oracle follows the reference either way, but the tests
+    want finite states to compare."""
+    from puffysics_amd import creation as cr
+    from puffysics_amd.b3types import B3_DYNAMIC, B3_STATIC
+    rng = np.random.default_rng(seed)
+    w = cr.new_worlds(count, gravity=(0.0, -9.81, 0.0))
+    for k in range(count):
+        g = cr.body(w, k, B3_STATIC, (0.0, -0.5, 0.0))
+        cr.box(w, k, g, (5.0, 0.5, 5.0), friction=float(rng.uniform(0.3, 0.9)))
+        post = cr.body(w, k, B3_STATIC, (0.0, 1.0, 0.0))
+        prev = post
+        for i in range(3):
+            b = cr.body(w, k, B3_DYNAMIC, (0.0, 0.85 - 0.3 * i, 0.0),
+                        ang_vel=(0.0, 0.0, float(rng.uniform(-0.8, 0.8))))
+            if i == 1:
+                cr.capsule(w, k, b, 0.1, 0.04)
+            else:
+                cr.box(w, k, b, (0.04, 0.15, 0.04))
+            cr.finalize_mass(w, k, b)
+            axis = tuple(rng.normal(size=3) * 0.15 + np.array([0.0, 0.0, 1.0]))
+            anchor = (0.0, 0.0, 0.0) if prev == post else (0.0, -0.15, 0.0)
+            cr.revolute(w, k, prev, b, anchor, (0.0, 0.15, 0.0), axis)
+            prev = b
+        tip = cr.body(w, k, B3_DYNAMIC, (float(rng.uniform(0.1, 0.16)), 0.06, 0.0))
+        cr.box(w, k, tip, (0.06, 0.06, 0.06))
+        cr.finalize_mass(w, k, tip)
+        x0 = float(rng.uniform(-1.2, -0.8))
+        la = cr.body(w, k, B3_DYNAMIC, (x0, 0.8, 0.5))
+        cr.box(w, k, la, (0.03, 0.2, 0.03))
+        cr.finalize_mass(w, k, la)
+        lb = cr.body(w, k, B3_DYNAMIC, (x0 + 0.2, 0.6, 0.5))
+        cr.box(w, k, lb, (0.2, 0.03, 0.03))
+        cr.finalize_mass(w, k, lb)
+        lc = cr.body(w, k, B3_DYNAMIC, (x0 + 0.4, 0.8, 0.5), ang_vel=(0.0, 0.0, float(rng.uniform(-1, 1))))
+        cr.box(w, k, lc, (0.03, 0.2, 0.03))
+        cr.finalize_mass(w, k, lc)
+        z = (0.0, 0.0, 1.0)
+        cr.revolute(w, k, post, la, (x0, 0.0, 0.5), (0.0, 0.2, 0.0), z)
+        cr.revolute(w, k, la, lb, (0.0, -0.2, 0.0), (-0.2, 0.0, 0.0), z)
+        cr.revolute(w, k, lb, lc, (0.2, 0.0, 0.0), (0.0, -0.2, 0.0), z)
+        cr.revolute(w, k, lc, post, (0.0, 0.2, 0.0), (x0 + 0.4, 0.0, 0.5), z)
+        fa = cr.body(w, k, B3_DYNAMIC, (0.8, 0.3, -0.8), lin_vel=tuple(rng.uniform(-0.5, 0.5, 3)))
+        cr.box(w, k, fa, (0.08, 0.08, 0.08))
+        cr.finalize_mass(w, k, fa)
+        fb = cr.body(w, k, B3_DYNAMIC, (0.8, 0.6, -0.8), ang_vel=tuple(rng.uniform(-1, 1, 3)))
+        cr.sphere(w, k, fb, 0.07)
+        cr.finalize_mass(w, k, fb)
+        cr.revolute(w, k, fa, fb, (0.0, 0.15, 0.0), (0.0, -0.15, 0.0), (1.0, 0.0, 0.0))
+        s = cr.body(w, k, B3_DYNAMIC, (float(rng.uniform(-0.4, 0.4)), 0.3, float(rng.uniform(-0.5, -0.2))),
+                    lin_vel=tuple(rng.uniform(-1, 1, 3)))
+        cr.sphere(w, k, s, float(rng.uniform(0.06, 0.1)), restitution=float(rng.choice([0.0, 0.4])))
+        cr.finalize_mass(w, k, s)
+        if k % 4 == 3:
+            cr.joint_motor(w, k, 7, 1.0, 5.0)
+    return w
+
+
 def oracle_step_art(worlds, sig, dt, substeps, active=None):
     """b3_step built with articulated contacts, world by world on the oracle."""
     lib = oracle()
@@ -328,9 +397,63 @@ def oracle_step_art(worlds, sig, dt, substeps, active=None):
             lib.ocpu_step_art(worlds[k:k + 1].ctypes.data, sig, dt, substeps)
 
 
+def oracle_art_step(worlds, sig, dt, substeps, active=None):
+    """b3_art_step, the reduced-coordinate integrator, world by world on the oracle."""
+    lib = oracle()
+    lib.ocpu_art_step.argtypes = [_vp, _ull, _f, _i]
+    for k in range(len(worlds)):
+        if active is None or active[k]:
+            lib.ocpu_art_step(worlds[k:k + 1].ctypes.data, sig, dt, substeps)
+
+
+ORACLE_ULP_PATH = os.path.join(ROOT, "oracle", "liboracle_ulp.so")
+_oracle_ulp = None
+
+
+def ulp_spread(worlds, sig, dt, substeps, runs=24, entry="ocpu_art_step"):
+    """Largest deviation, per body-state entry (body_state layout), of the
+    oracle with its sinf, cosf and atan2f results moved by one ulp at random
+    (oracle/ulp_envelope.c) from the plain oracle, over `runs` seeds, for one
+    step of `worlds` through `entry`: the envelope of a faithful
+    implementation whose libm differs from glibc's in the last place."""
+    global _oracle_ulp
+    if _oracle_ulp is None:
+        lib = C.CDLL(ORACLE_ULP_PATH)
+        lib.oulp_seed.argtypes = [_ull]
+        _oracle_ulp = lib
+    lib = _oracle_ulp
+    fn = getattr(lib, entry)
+    fn.argtypes = [_vp, _ull, _f, _i]
+    exact = clone(worlds)
+    ofn = getattr(oracle(), entry)
+    ofn.argtypes = [_vp, _ull, _f, _i]
+    for k in range(len(exact)):
+        ofn(exact[k:k + 1].ctypes.data, sig, dt, substeps)
+    ref = body_state(exact)
+    spread = np.zeros_like(ref)
+    for seed in range(runs):
+        lib.oulp_seed(seed + 1)
+        w = clone(worlds)
+        for k in range(len(w)):
+            fn(w[k:k + 1].ctypes.data, sig, dt, substeps)
+        spread = np.maximum(spread, np.abs(body_state(w) - ref))
+    return spread
+
+
+def body_state(worlds):
+    """Per body: position, center, linear and angular velocity, rotation
+    (x, y, z, s), as float64 [world, body, 16]."""
+    b = worlds["bodies"]
+    cols = []
+    for f in ("position", "center", "lin_vel", "ang_vel"):
+        cols += [b[f][a] for a in "xyz"]
+    cols += [b["rotation"]["v"][a] for a in "xyz"] + [b["rotation"]["s"]]
+    return np.stack(cols, axis=-1).astype(np.float64)
+
+
 def ref_art_lib(caps):
     """The reference's b3_step built with B3_ART_CONTACTS=1 for capacity set
-    `caps` (0, 3 or 5), or None where the reference was not built."""
+    `caps` (0, 2, 3 or 5), or None where the reference was not built."""
     path = os.path.join(REF_DIR, "libb3ref_art_%d.so" % caps)
     if not os.path.exists(path):
         return None
@@ -339,6 +462,7 @@ def ref_art_lib(caps):
         lib = C.CDLL(path)
         lib.refa_sig.restype = C.c_ulonglong
         lib.refa_step.argtypes = [_vp, _f, _i]
+        lib.refa_art_step.argtypes = [_vp, _f, _i]
         _refs[key] = lib
     return _refs[key]
 
@@ -427,6 +551,13 @@ class EmuSig:
         lib.emu_step_art.argtypes = [_vp, _i, _ull, _f, _i, _vp]
         act = None if active is None else np.ascontiguousarray(active, np.uint8)
         lib.emu_step_art(self.tiles.ctypes.data, self.count, self.sig, dt, substeps,
+                         None if act is None else act.ctypes.data)
+
+    def art_step(self, dt, substeps, active=None):
+        lib = emu()
+        lib.emu_art_step.argtypes = [_vp, _i, _ull, _f, _i, _vp]
+        act = None if active is None else np.ascontiguousarray(active, np.uint8)
+        lib.emu_art_step(self.tiles.ctypes.data, self.count, self.sig, dt, substeps,
                          None if act is None else act.ctypes.data)
 
     def step_fluid(self, dt, substeps, law, state, active=None):

@@ -159,6 +159,23 @@ void emu_step_art(uint32_t* tiles, int count, unsigned long long sig, float dt, 
     }
 }
 
+/* emu_step_art with the reduced-coordinate integrator (b3_art_step). */
+void emu_art_step(uint32_t* tiles, int count, unsigned long long sig, float dt, int substeps,
+        const unsigned char* step_mask) {
+    Geometry g;
+    size_t wb;
+    if (!geometry_of(sig, &g, &wb)) return;
+    int ntiles = (count + kLanes - 1) / kLanes;
+    std::vector<uint32_t> scratch((size_t)ntiles * g.tile_scr_words);
+    std::vector<float> vel((size_t)lds_rows(g) * kLanes);
+    std::vector<float> ws((size_t)ntiles * art_ws_words(g.max_b) * kLanes);
+    for (int w = 0; w < count; w++) {
+        if (step_mask && !step_mask[w]) continue;
+        float* lane_ws = ws.data() + (size_t)(w / kLanes) * art_ws_words(g.max_b) * kLanes + w % kLanes;
+        step_world_art_reduced(lane_of(tiles, scratch.data(), vel.data(), g, w), lane_ws, dt, substeps);
+    }
+}
+
 void emu_inputs(uint32_t* tiles, int count, unsigned long long sig, int scene, unsigned long long seed, int step,
         const unsigned char* step_mask) {
     Geometry g;
