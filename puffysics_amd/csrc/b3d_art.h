@@ -44,11 +44,16 @@ constexpr float kArtDmin = 1.0e-8f;  /* B3_ART_DMIN, :40-42 */
 
 /* Link block words.  AL_C (bias acceleration), AL_Q / AL_QD (joint angle
  * and rate) and the child-side joint frame AL_ANCHOR_B / AL_ROT_B serve the
- * reduced integrator only. */
+ * reduced integrator only.  AL_IA, AL_U, AL_DINV, AL_IC and AL_GJ are the
+ * pose-only half of the Delassus operator (art_pose_pass). */
 constexpr int AL_PARENT = 0, AL_BODY = 1, AL_FIXED = 2, AL_FLOATING = 3, AL_ANCHOR_A = 4, AL_ROT_A = 7,
               AL_LC = 11, AL_ILOCAL = 14, AL_MASS = 17, AL_COM = 18, AL_POS = 21, AL_ROT = 24, AL_R = 28,
               AL_SW = 31, AL_SV = 34, AL_IWW = 37, AL_IA = 46, AL_U = 82, AL_PA = 88, AL_DINV = 94, AL_A = 95,
-              AL_C = 101, AL_Q = 107, AL_QD = 108, AL_ANCHOR_B = 109, AL_ROT_B = 112, kArtLinkWords = 116;
+              AL_C = 101, AL_Q = 107, AL_QD = 108, AL_ANCHOR_B = 109, AL_ROT_B = 112, AL_IC = 116, AL_GJ = 122,
+              kArtLinkWords = 171;
+/* A floating root's elimination record (AL_GJ + ...): pivot rows, reciprocal
+ * pivots, the other rows' multipliers [k][r], and whether it completed. */
+constexpr int GJ_PIV = 0, GJ_INV = 6, GJ_MUL = 12, GJ_OK = 48;
 /* Search temporaries per body: degree, neighbours and joints, link of the
  * body, seen flag, queue, parent body and joint. */
 constexpr int kArtBodyTmp = 2 * kArtMaxDeg + 6;
@@ -187,6 +192,81 @@ B3D_FN bool isolve(const M6& I, S6 rhs, S6* a) {
     }
     a->w = v3(M[0][6], M[1][6], M[2][6]);
     a->v = v3(M[3][6], M[4][6], M[5][6]);
+    return true;
+}
+
+/* The same elimination split in two: isolve_record runs it on I alone and
+ * keeps what the right-hand side's column sees (row swaps, reciprocal
+ * pivots, multipliers); isolve_replay applies those to a right-hand side.
+ * Together they give isolve's result bit for bit: the column's operations
+ * and their order are unchanged. */
+B3D_FN void isolve_record(const ArtWs& A, int li, const M6& I) {
+    float M[6][6];
+    V3 cn[3] = {I.ww.cx, I.ww.cy, I.ww.cz}, cf[3] = {I.vw.cx, I.vw.cy, I.vw.cz};
+    V3 dn[3] = {I.wv.cx, I.wv.cy, I.wv.cz}, df[3] = {I.vv.cx, I.vv.cy, I.vv.cz};
+    for (int c = 0; c < 3; c++) {
+        M[0][c] = cn[c].x; M[1][c] = cn[c].y; M[2][c] = cn[c].z;
+        M[3][c] = cf[c].x; M[4][c] = cf[c].y; M[5][c] = cf[c].z;
+        M[0][3 + c] = dn[c].x; M[1][3 + c] = dn[c].y; M[2][3 + c] = dn[c].z;
+        M[3][3 + c] = df[c].x; M[4][3 + c] = df[c].y; M[5][3 + c] = df[c].z;
+    }
+    const int g = AL_GJ;
+    for (int k = 0; k < 6; k++) {
+        int piv = k;
+        float best = fabsf(M[k][k]);
+        for (int r = k + 1; r < 6; r++) {
+            float v = fabsf(M[r][k]);
+            if (v > best) {
+                best = v;
+                piv = r;
+            }
+        }
+        if (best < 1.0e-12f) {
+            A.si(li, g + GJ_OK, 0);
+            return;
+        }
+        A.si(li, g + GJ_PIV + k, piv);
+        if (piv != k) {
+            for (int c = k; c < 6; c++) {
+                float t = M[k][c];
+                M[k][c] = M[piv][c];
+                M[piv][c] = t;
+            }
+        }
+        float inv = 1.0f / M[k][k];
+        A.sf(li, g + GJ_INV + k, inv);
+        for (int c = k; c < 6; c++) M[k][c] *= inv;
+        for (int r = 0; r < 6; r++) {
+            if (r == k) continue;
+            float sr = M[r][k];
+            A.sf(li, g + GJ_MUL + k * 6 + r, sr);
+            for (int c = k; c < 6; c++) M[r][c] -= sr * M[k][c];
+        }
+    }
+    A.si(li, g + GJ_OK, 1);
+}
+B3D_FN bool isolve_replay(const ArtWs& A, int li, S6 rhs, S6* a) {
+    const int g = AL_GJ;
+    if (!A.gi(li, g + GJ_OK)) {
+        *a = s6zero();
+        return false;
+    }
+    float b[6] = {rhs.w.x, rhs.w.y, rhs.w.z, rhs.v.x, rhs.v.y, rhs.v.z};
+    for (int k = 0; k < 6; k++) {
+        int piv = A.gi(li, g + GJ_PIV + k);
+        if (piv != k) {
+            float t = b[k];
+            b[k] = b[piv];
+            b[piv] = t;
+        }
+        b[k] *= A.gf(li, g + GJ_INV + k);
+        for (int r = 0; r < 6; r++) {
+            if (r == k) continue;
+            b[r] -= A.gf(li, g + GJ_MUL + k * 6 + r) * b[k];
+        }
+    }
+    a->w = v3(b[0], b[1], b[2]);
+    a->v = v3(b[3], b[4], b[5]);
     return true;
 }
 
@@ -359,14 +439,47 @@ B3D_FN S6 art_wrench(V3 r, V3 n, float x, int torque) {                 /* :675-
     return f;
 }
 
-/* y = J M^-1 J^T x for n rows (b3_art_delassus_apply, :722-749, with the
- * zero link velocities and joint rates it sets, b3_art_seed_bias's linear
- * form, :572-605, and the two sweeps, :607-666); the accelerations stay
- * in the links' AL_A words. */
-B3D_FN void art_delassus(const Lane& L, const ArtWs& A, const ArtRow* rows, const float* x, float* y, int n) {
+/* The pose-only half of b3_art_delassus_apply (:722-749): the refresh, the
+ * links' own inertias (b3_art_seed_bias's linear form, :572-605) and, of the
+ * backward sweep (:607-633), the articulated inertias, U = I^A S, 1/D, the
+ * zero-bias term I^A c (c = 0) and each floating root's elimination.  None
+ * of it depends on the impulses, and nothing a sweep does between two
+ * operator calls changes the poses it is built from (only velocities), so a
+ * pass runs it once and art_delassus reuses it for every call: the values
+ * are the ones each call of the reference recomputes. */
+B3D_FN void art_pose_pass(const Lane& L, const ArtWs& A) {
     art_refresh(L, A);
+    for (int i = 0; i < A.n_links; i++) A.sI(i, AL_IA, art_inertia(A, i));
+    for (int i = A.n_links - 1; i >= 0; i--) {
+        int p = A.gi(i, AL_PARENT);
+        if (p < 0) {
+            if (!A.gi(i, AL_FIXED) && A.gi(i, AL_FLOATING)) isolve_record(A, i, A.gI(i, AL_IA));
+            continue;
+        }
+        S6 S;
+        S.w = A.g3(i, AL_SW);
+        S.v = A.g3(i, AL_SV);
+        M6 IA = A.gI(i, AL_IA);
+        S6 U = imul(IA, S);
+        A.s6(i, AL_U, U);
+        float D = sdot(S, U);
+        if (D < kArtDmin) D = kArtDmin;
+        float Dinv = 1.0f / D;
+        A.sf(i, AL_DINV, Dinv);
+        A.s6(i, AL_IC, imul(IA, s6zero()));
+        if (!A.gi(p, AL_FIXED))
+            A.sI(p, AL_IA, iadd(A.gI(p, AL_IA), ishift(irank1(IA, U, Dinv), A.g3(i, AL_R))));
+    }
+}
+
+/* y = J M^-1 J^T x for n rows: the impulse half of b3_art_delassus_apply
+ * (:722-749) on the last art_pose_pass, with the zero link velocities and
+ * joint rates it sets (the row wrenches, the bias-force half of the
+ * backward sweep, the forward sweep :635-666); the accelerations stay in
+ * the links' AL_A words. */
+B3D_FN void art_delassus(const Lane& L, const ArtWs& A, const ArtRow* rows, const float* x, float* y, int n) {
+    (void)L;
     for (int i = 0; i < A.n_links; i++) {
-        A.sI(i, AL_IA, art_inertia(A, i));
         S6 pa;
         pa.w = sub(zero3(), zero3());
         pa.v = pa.w;
@@ -389,36 +502,29 @@ B3D_FN void art_delassus(const Lane& L, const ArtWs& A, const ArtRow* rows, cons
             A.s6(row.link_b, AL_PA, pa);
         }
     }
-    /* backward sweep (:607-633), with zero bias accelerations and torques */
+    /* backward sweep, bias forces only (zero joint torques) */
     for (int i = A.n_links - 1; i >= 0; i--) {
         int p = A.gi(i, AL_PARENT);
         if (p < 0) continue;
         S6 S;
         S.w = A.g3(i, AL_SW);
         S.v = A.g3(i, AL_SV);
-        M6 IA = A.gI(i, AL_IA);
-        S6 U = imul(IA, S);
-        A.s6(i, AL_U, U);
-        float D = sdot(S, U);
-        if (D < kArtDmin) D = kArtDmin;
-        float Dinv = 1.0f / D;
-        A.sf(i, AL_DINV, Dinv);
+        S6 U = A.g6(i, AL_U);
+        float Dinv = A.gf(i, AL_DINV);
         S6 pA = A.g6(i, AL_PA);
         float u = 0.0f - sdot(S, pA);
-        M6 IAp = irank1(IA, U, Dinv);
-        S6 Ic = imul(IA, s6zero());
+        S6 Ic = A.g6(i, AL_IC);
         pA.w = add(add(pA.w, Ic.w), scale(U.w, u * Dinv));
         pA.v = add(add(pA.v, Ic.v), scale(U.v, u * Dinv));
         if (!A.gi(p, AL_FIXED)) {
             V3 r = A.g3(i, AL_R);
-            A.sI(p, AL_IA, iadd(A.gI(p, AL_IA), ishift(IAp, r)));
             S6 pp = A.g6(p, AL_PA);
             pp.w = add(pp.w, add(pA.w, cross(r, pA.v)));
             pp.v = add(pp.v, pA.v);
             A.s6(p, AL_PA, pp);
         }
     }
-    /* forward sweep (:635-666) */
+    /* forward sweep */
     for (int i = 0; i < A.n_links; i++) {
         int p = A.gi(i, AL_PARENT);
         if (p < 0) {
@@ -427,7 +533,7 @@ B3D_FN void art_delassus(const Lane& L, const ArtWs& A, const ArtRow* rows, cons
                 S6 pA = A.g6(i, AL_PA), rhs;
                 rhs.w = neg(pA.w);
                 rhs.v = neg(pA.v);
-                if (!isolve(A.gI(i, AL_IA), rhs, &a)) a = s6zero();
+                if (!isolve_replay(A, i, rhs, &a)) a = s6zero();
             }
             A.s6(i, AL_A, a);
             continue;
@@ -653,6 +759,7 @@ B3D_FN void art_solve_contacts(const Lane& L, const ArtWs& A, float inv_h, float
         int iters = 1) {
     uint32_t* w = L.w;
     int cc = ldi(w, H_CONTACT_COUNT);
+    if (cc > 0) art_pose_pass(L, A);
     for (int it = 0; it < iters; it++)
     for (int c = 0; c < cc; c++) {
         WContact k = wc_load(L, c);
@@ -702,6 +809,7 @@ B3D_FN void art_solve_contacts(const Lane& L, const ArtWs& A, float inv_h, float
 B3D_FN void art_warm_start(const Lane& L, const ArtWs& A) {
     uint32_t* w = L.w;
     int cc = ldi(w, H_CONTACT_COUNT);
+    if (cc > 0) art_pose_pass(L, A);
     for (int c = 0; c < cc; c++) {
         WContact k = wc_load(L, c);
         ArtRow row;
@@ -1329,13 +1437,15 @@ B3D_FN bool solve5(const float* D, const float* b, float* x) {
 B3D_FN void art_solve_cuts(const Lane& L, const ArtWs& A, float inv_h, int use_bias, int iters) {
     int nc = A.n_cuts();
     if (nc < 1) return;
-    art_refresh(L, A);
+    /* the reference refreshes again before each cut's rows are evaluated;
+     * the poses are unchanged within the pass and the velocities are read
+     * from the bodies */
+    art_pose_pass(L, A);
     for (int it = 0; it < iters; it++) {
         for (int c = 0; c < nc; c++) {
             ArtRow rows[5];
             float err[5];
             if (!art_cut_rows(L, A, c, rows, err)) continue;
-            art_refresh(L, A);
             float rhs[5];
             for (int k = 0; k < 5; k++) {
                 float vbias = 0.0f;
