@@ -28,7 +28,7 @@ __global__ __launch_bounds__(64) void b3k_step_art(uint32_t* live, const uint32_
         const unsigned char* reset_mask, unsigned int opts) {
     extern __shared__ float vel_rows[];
     if (reset_mask) {
-        restore_tile(live, snap, g, count, reset_mask);
+        restore_tile(live, snap, g, count, reset_mask, blockIdx.x, 0, 1);
         __syncthreads();
     }
     int tile = blockIdx.x;

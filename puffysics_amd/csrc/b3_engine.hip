@@ -11,8 +11,9 @@
  *   b3k_upload / b3k_download  AoS <-> tiles, transposed through LDS in
  *                              64 x 64 word blocks (both sides coalesced)
  *   b3k_restore                masked restore from the snapshots (plain
- *                              B3World structs); the wave copies one
- *                              resetting world at a time with all 64 lanes
+ *                              B3World structs); four waves per tile, each
+ *                              copying every fourth 512-word chunk of the
+ *                              tile's resetting worlds with all 64 lanes
  *   b3k_step                   optional fused restore, then one b3_step per
  *                              selected lane; LDS holds the lane's clip
  *                              polygons, then its body velocities
@@ -76,9 +77,14 @@ __global__ __launch_bounds__(kXposeThreads) void b3k_download(const uint32_t* __
     }
 }
 
+/* kRestoreSlices waves per tile share its restores chunk by chunk: a tile
+ * with several resetting worlds is then not one wave's long chain of
+ * dependent rounds. */
+constexpr int kRestoreSlices = 4;
 __global__ __launch_bounds__(64) void b3k_restore(uint32_t* live, const uint32_t* snap, Geometry g, int count,
         const unsigned char* reset) {
-    restore_tile(live, snap, g, count, reset);
+    restore_tile(live, snap, g, count, reset, blockIdx.x / kRestoreSlices, blockIdx.x % kRestoreSlices,
+        kRestoreSlices);
 }
 
 /* ---- the step ---- */
@@ -88,7 +94,7 @@ __global__ __launch_bounds__(64) void b3k_step(uint32_t* live, const uint32_t* s
         const unsigned char* reset_mask, unsigned int opts) {
     extern __shared__ float vel_rows[];
     if (reset_mask) {
-        restore_tile(live, snap, g, count, reset_mask);
+        restore_tile(live, snap, g, count, reset_mask, blockIdx.x, 0, 1);
         __syncthreads();
     }
     int tile = blockIdx.x;
@@ -353,7 +359,7 @@ hipError_t b3_batch_restore_gpu(B3Engine* e, const unsigned char* reset, hipStre
         b3k_upload<<<grid, kXposeThreads, 0, stream>>>(e->snap, e->live, e->count, e->g.world_words);
         return hipGetLastError();
     }
-    b3k_restore<<<e->tiles, 64, 0, stream>>>(e->live, e->snap, e->g, e->count, reset);
+    b3k_restore<<<e->tiles * kRestoreSlices, 64, 0, stream>>>(e->live, e->snap, e->g, e->count, reset);
     return hipGetLastError();
 }
 

@@ -42,13 +42,15 @@ inline hipError_t on_device(const B3Engine* e) {
 
 namespace b3d {
 
-/* Restore the resetting worlds of this workgroup's tile from the snapshots,
- * which are kept as plain B3World structs (AoS): one world at a time, the 64
- * lanes read 64 consecutive snapshot words and write them to their rows of
- * the tile. */
+/* Restore the resetting worlds of tile `tile` from the snapshots, which are
+ * kept as plain B3World structs (AoS): one world at a time, the 64 lanes
+ * read 64 consecutive snapshot words and write them to their rows of the
+ * tile.  A world's copy is cut into chunks of kRestoreChunk words; this
+ * wave copies chunk k of every resetting world when k % nslices == slice,
+ * so nslices waves share a tile's restores. */
+constexpr int kRestoreBatch = 8, kRestoreChunk = 64 * kRestoreBatch;
 __device__ inline void restore_tile(uint32_t* live, const uint32_t* snap, const Geometry& g, int count,
-        const unsigned char* reset) {
-    int tile = blockIdx.x;
+        const unsigned char* reset, int tile, int slice, int nslices) {
     int w = tile * 64 + (int)threadIdx.x;
     int want = w < count && reset[w] != 0;
     uint64_t bits = __ballot(want);
@@ -59,12 +61,14 @@ __device__ inline void restore_tile(uint32_t* live, const uint32_t* snap, const 
         const uint32_t* src = snap + (size_t)(tile * 64 + l) * g.world_words;
         int lo[3], hi[3];
         restore_ranges(g, (int)src[H_CONTACT_COUNT], lo, hi);
-        /* kRestoreBatch 256-byte snapshot reads in flight before their
-         * writes (the reads do not depend on the writes: the snapshots and
-         * the live tiles are separate allocations) */
-        constexpr int kRestoreBatch = 8;
+        int chunk = 0;
         for (int r = 0; r < 3; r++) {
-            for (int k0 = lo[r] + (int)threadIdx.x; k0 < hi[r]; k0 += 64 * kRestoreBatch) {
+            for (int c0 = lo[r]; c0 < hi[r]; c0 += kRestoreChunk, chunk++) {
+                if (chunk % nslices != slice) continue;
+                /* kRestoreBatch 256-byte snapshot reads in flight before
+                 * their writes (the reads do not depend on the writes: the
+                 * snapshots and the live tiles are separate allocations) */
+                int k0 = c0 + (int)threadIdx.x;
                 uint32_t v[kRestoreBatch];
 #pragma unroll
                 for (int i = 0; i < kRestoreBatch; i++)

@@ -29,7 +29,7 @@ __global__ __launch_bounds__(64) void b3k_step_gravity(uint32_t* live, const uin
         const unsigned char* reset_mask, unsigned int opts, B3GravityLaw law, const float* masses) {
     extern __shared__ float vel_rows[];
     if (reset_mask) {
-        restore_tile(live, snap, g, count, reset_mask);
+        restore_tile(live, snap, g, count, reset_mask, blockIdx.x, 0, 1);
         __syncthreads();
     }
     int tile = blockIdx.x;
@@ -56,7 +56,7 @@ __global__ __launch_bounds__(64) void b3k_step_fluid(uint32_t* live, const uint3
     int w = tile * 64 + lane;
     size_t words = (size_t)6 * g.max_b + 1;
     if (reset_mask) {
-        restore_tile(live, snap, g, count, reset_mask);
+        restore_tile(live, snap, g, count, reset_mask, blockIdx.x, 0, 1);
         /* a restored world starts without previous velocities (b3_fluid_state_reset, ambient.h:69-74) */
         if (w < count && reset_mask[w]) state[w * words + 6 * g.max_b] = 0.0f;
         __syncthreads();
