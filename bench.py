@@ -10,9 +10,11 @@ on the device before the timed region; the worlds stay resident in HBM.
 
 Prints one JSON line with the throughput, the roofline of the step kernel
 (algorithmic bytes per launch / its event-timed average duration, against
-8 TB/s) and a CPU baseline: the reference's own CPU path compiled from its
-sources (oracle/_ref) when present, else the oracle, on a bounded sample of
-the same workload with one thread per physical core.
+8 TB/s; with the committed counter summary of the workload, also its HBM
+traffic and its VALU issue rate against the fp32 vector rate) and a CPU
+baseline: the reference's own CPU path compiled from its sources
+(oracle/_ref) when present, else the oracle, on a bounded sample of the
+same workload with one thread per physical core.
 """
 import argparse
 import ctypes as C
@@ -26,6 +28,9 @@ sys.path.insert(0, ROOT)
 
 METRIC = "physics env-steps/sec at 4096 and 65536 worlds, 1 MI355X; % HBM/VALU roofline"
 HBM_PEAK_GBS = 8000.0
+# fp32 vector issue rate: 256 CUs x 4 SIMDs x 16 lanes x 2.4 GHz (an FMA would count twice; the
+# step is built without contraction)
+VALU_PEAK_TLANE = 39.32
 VALU_FP32_PEAK_TFLOPS = 157.3
 
 # Algorithmic bytes of one env-step, per item: the minimal persistent-state
@@ -115,13 +120,14 @@ def cpu_baseline(scene, seconds_target, threads_limit):
                       "%.1f s" % (count, nsteps, 9 + nsteps, nthreads, el)}
 
 
-def load_traffic(scene, worlds):
-    """HBM bytes per step launch from a committed rocprofv3 counter summary, if any."""
+def load_counters(scene, worlds):
+    """Per-launch counter figures of the step kernel from a committed rocprofv3
+    summary (HBM bytes, VALU instructions), or {}."""
     path = os.path.join(ROOT, "profiles", "b3k_step_%s%d_traffic.json" % (scene, worlds))
     if not os.path.exists(path):
-        return None
+        return {}
     with open(path) as f:
-        return json.load(f).get("bytes_per_launch")
+        return json.load(f)
 
 
 def main():
@@ -223,12 +229,21 @@ def main():
     bytes_per_launch = float(per_world.mean()) * mean_stepped
     k_ms = kernel_ms[med]
     achieved = bytes_per_launch / (k_ms * 1e-3) / 1e9
-    traffic = None if args.art else load_traffic(sc.name, count)
+    counters = {} if args.art else load_counters(sc.name, count)
+    traffic = counters.get("bytes_per_launch")
+    valu = None
+    if counters.get("valu_insts_per_launch"):
+        # wave64 VALU instructions x 64 lanes over the measured launch time,
+        # against the fp32 vector issue rate
+        lane_ops = counters["valu_insts_per_launch"] * 64
+        rate = lane_ops / (k_ms * 1e-3) / 1e12
+        valu = {"achieved": round(rate, 3), "peak": VALU_PEAK_TLANE, "unit": "T lane-ops/s",
+                "frac": round(rate / VALU_PEAK_TLANE, 4), "insts_per_launch": counters["valu_insts_per_launch"]}
     roofline = {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic,
                 "kernel": "b3k_step_art" if args.art else "b3k_step", "kernel_ms": round(k_ms, 4),
                 "bytes_per_env_step": round(float(per_world.mean()), 1),
-                "mean_contacts_per_world": round(float(st["contact_count"].mean()), 2)}
+                "mean_contacts_per_world": round(float(st["contact_count"].mean()), 2), "valu": valu}
     eng.close()
     del worlds
 
