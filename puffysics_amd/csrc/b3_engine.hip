@@ -17,6 +17,9 @@
  *   b3k_step                   optional fused restore, then one b3_step per
  *                              selected lane; LDS holds the lane's clip
  *                              polygons, then its body velocities
+ *   b3k_step_shared            the same for batches of at most one tile per
+ *                              CU, with the narrowphase split over four
+ *                              waves per tile
  *   b3k_apply                  dense force / torque / impulse inputs
  *   b3k_stats                  per-world B3StepStats
  */
@@ -102,6 +105,37 @@ __global__ __launch_bounds__(64) void b3k_step(uint32_t* live, const uint32_t* s
     int w = tile * 64 + lane;
     if (w >= count || (step_mask && !step_mask[w])) return;
     step_world(lane_view(live, scratch, vel_rows, g, tile, lane, opts), dt, substeps);
+}
+
+/* The step with the narrowphase shared by kTileWaves waves per tile (small
+ * batches, whose one wave per tile would leave most CUs idle): wave 0 steps
+ * its lanes' worlds as b3k_step does; the other waves wait for its
+ * candidate lists, collide their share of the pairs into the stage, and
+ * end.  Every wave sees the same stepping lanes, so all of them reach both
+ * barriers of the shared phase or none does. */
+__global__ __launch_bounds__(64 * kTileWaves) void b3k_step_shared(uint32_t* live, const uint32_t* snap,
+        uint32_t* scratch, uint32_t* stage, size_t stage_tile_words, Geometry g, int count, float dt, int substeps,
+        const unsigned char* step_mask, const unsigned char* reset_mask, unsigned int opts) {
+    extern __shared__ float lds[];
+    int wave = (int)(threadIdx.x >> 6), lane = (int)(threadIdx.x & 63u);
+    int tile = blockIdx.x;
+    if (reset_mask) {
+        restore_tile(live, snap, g, count, reset_mask, tile, wave, kTileWaves);
+        __syncthreads();
+    }
+    int w = tile * 64 + lane;
+    bool stepping = w < count && (!step_mask || step_mask[w]);
+    if (!(dt > 0.0f) || __ballot(stepping) == 0) return;
+    if (!stepping) return;
+    PairStage S;
+    S.p = stage + (size_t)tile * stage_tile_words + lane;
+    S.clip = (wave == 0 ? lds : lds + (size_t)lds_rows(g) * kLanes + (size_t)(wave - 1) * kClipWords * kLanes) + lane;
+    S.wave = wave;
+    S.waves = kTileWaves;
+    Lane L = lane_view(live, scratch, lds, g, tile, lane, opts);
+    L.stage = &S;
+    if (wave == 0) step_world(L, dt, substeps);
+    else pair_helper(L, S);
 }
 
 /* ---- inputs and stats ---- */
@@ -269,6 +303,28 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
             (void)b3_engine_destroy(e);
             return err;
         }
+        /* A batch of at most one tile per CU shares each tile's narrowphase
+         * among kTileWaves waves (b3k_step_shared). */
+        int cus = 0;
+        size_t shared_lds = lds + (size_t)(kTileWaves - 1) * kClipWords * kLanes * sizeof(float);
+        if ((err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device)) != hipSuccess) {
+            (void)b3_engine_destroy(e);
+            return err;
+        }
+        if (e->tiles <= cus && shared_lds <= 160u * 1024u) {
+            size_t max_cand = (size_t)g.max_s * (size_t)(g.max_s - 1) / 2;
+            e->stage_tile_words = (1 + max_cand * kManiWords) * kLanes;
+            e->lds_shared_bytes = shared_lds;
+            if (shared_lds > 64u * 1024u)
+                err = hipFuncSetAttribute((const void*)b3k_step_shared, hipFuncAttributeMaxDynamicSharedMemorySize,
+                    (int)shared_lds);
+            if (err == hipSuccess)
+                err = hipMalloc((void**)&e->pair_stage, (size_t)e->tiles * e->stage_tile_words * sizeof(uint32_t));
+            if (err != hipSuccess) {
+                (void)b3_engine_destroy(e);
+                return err;
+            }
+        }
         unsigned char* host = gather(worlds, world_bytes);
         if (!host) {
             (void)b3_engine_destroy(e);
@@ -290,7 +346,7 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
 hipError_t b3_engine_destroy(B3Engine* e) {
     if (!e) return hipSuccess;
     hipError_t first = hipSuccess;
-    void* bufs[5] = {e->live, e->snap, e->scratch, e->staging, e->art_ws};
+    void* bufs[6] = {e->live, e->snap, e->scratch, e->staging, e->art_ws, e->pair_stage};
     for (void* p : bufs) {
         if (!p) continue;
         hipError_t err = hipFree(p);
@@ -371,6 +427,11 @@ hipError_t b3_batch_step_gpu(B3Engine* e, float dt, int substeps, const unsigned
     if (err != hipSuccess) return err;
     if (dt == 0.0f) return reset_mask ? b3_batch_restore_gpu(e, reset_mask, stream) : hipSuccess;
     if (e->options & B3_ENGINE_ART_CONTACTS) return b3i_step_art(e, dt, substeps, step_mask, reset_mask, stream);
+    if (e->pair_stage && !(e->options & B3_ENGINE_ONE_WAVE_PER_TILE)) {
+        b3k_step_shared<<<e->tiles, 64 * kTileWaves, e->lds_shared_bytes, stream>>>(e->live, e->snap, e->scratch,
+            e->pair_stage, e->stage_tile_words, e->g, e->count, dt, substeps, step_mask, reset_mask, e->options);
+        return hipGetLastError();
+    }
     b3k_step<<<e->tiles, 64, e->lds_bytes, stream>>>(e->live, e->snap, e->scratch, e->g, e->count, dt, substeps,
         step_mask, reset_mask, e->options);
     return hipGetLastError();
@@ -403,7 +464,8 @@ hipError_t b3_engine_device_view(const B3Engine* e, void** tiles, size_t* world_
 }
 
 hipError_t b3_engine_set_options(B3Engine* e, unsigned int options) {
-    if (!e || (options & ~(B3_ENGINE_KEEP_SOLVER_FIELDS | B3_ENGINE_ART_CONTACTS))) return hipErrorInvalidValue;
+    if (!e || (options & ~(B3_ENGINE_KEEP_SOLVER_FIELDS | B3_ENGINE_ART_CONTACTS | B3_ENGINE_ONE_WAVE_PER_TILE)))
+        return hipErrorInvalidValue;
     if (options & B3_ENGINE_ART_CONTACTS) {
         hipError_t err = on_device(e);
         if (err == hipSuccess) err = b3i_art_init(e);

@@ -23,7 +23,13 @@ struct B3Engine {
     size_t lds_bytes;
     unsigned int options;    /* B3_ENGINE_* step options */
     float* art_ws;           /* articulated-contact workspace, allocated when that option is first set */
+    uint32_t* pair_stage;    /* small batches: the tile's waves share the narrowphase (b3d::PairStage) */
+    size_t stage_tile_words;
+    size_t lds_shared_bytes; /* LDS of a workgroup of kTileWaves waves */
 };
+
+/* Waves per tile when the narrowphase is shared. */
+constexpr int kTileWaves = 4;
 
 /* Set-up of the force-law kernels on the current device (b3_forces.hip). */
 hipError_t b3i_forces_init(size_t lds_bytes);
@@ -51,7 +57,8 @@ namespace b3d {
 constexpr int kRestoreBatch = 8, kRestoreChunk = 64 * kRestoreBatch;
 __device__ inline void restore_tile(uint32_t* live, const uint32_t* snap, const Geometry& g, int count,
         const unsigned char* reset, int tile, int slice, int nslices) {
-    int w = tile * 64 + (int)threadIdx.x;
+    int lane = (int)(threadIdx.x & 63u);
+    int w = tile * 64 + lane;
     int want = w < count && reset[w] != 0;
     uint64_t bits = __ballot(want);
     uint32_t* lt = live + (size_t)tile * g.world_words * 64;
@@ -68,7 +75,7 @@ __device__ inline void restore_tile(uint32_t* live, const uint32_t* snap, const 
                 /* kRestoreBatch 256-byte snapshot reads in flight before
                  * their writes (the reads do not depend on the writes: the
                  * snapshots and the live tiles are separate allocations) */
-                int k0 = c0 + (int)threadIdx.x;
+                int k0 = c0 + lane;
                 uint32_t v[kRestoreBatch];
 #pragma unroll
                 for (int i = 0; i < kRestoreBatch; i++)

@@ -319,6 +319,18 @@ B3D_FN bool geometry_of(unsigned long long sig, Geometry* g, size_t* world_bytes
     return true;
 }
 
+/* Manifolds of a tile's candidate pairs, computed by the tile's waves
+ * together (small batches, where one wave per tile leaves CUs idle): the
+ * lane's candidate count at word 0, then kManiWords words per candidate
+ * (count, normal, then per point p_a, p_b, separation, feature), word k of a
+ * lane at p[k * kLanes]. */
+constexpr int kManiWords = 4 + 8 * kMaxManifold;
+struct PairStage {
+    uint32_t* p;   /* lane base */
+    float* clip;   /* this wave's clip rows (lane base) */
+    int wave, waves;
+};
+
 /* Per-lane view of one world. */
 struct Lane {
     uint32_t* w;    /* live tile + lane */
@@ -330,6 +342,7 @@ struct Lane {
     int sslot;          /* rank among the tile's stepping lanes: the slot of
                            the body, delta-pose and shape records */
     unsigned int opts;  /* kKeepSolverFields */
+    const PairStage* stage;  /* non-null: the tile's waves share the narrowphase */
     Geometry g;
 };
 
@@ -348,6 +361,7 @@ B3D_FN Lane lane_view(uint32_t* live, uint32_t* scratch, float* vel_rows, const 
         unsigned int opts = 0) {
     Lane L;
     L.opts = opts;
+    L.stage = nullptr;
     L.sslot = lane;
     L.w = live + (size_t)tile * g.world_words * kLanes + lane;
     L.scr = scratch ? scratch + (size_t)tile * g.tile_scr_words + lane : nullptr;
@@ -384,6 +398,13 @@ B3D_FN bool wave_any(const Lane& L, bool v) {
     return v;
 #endif
 }
+
+/* Workgroup barrier (a no-op in a host build, where no stage is used). */
+#ifdef __HIP_DEVICE_COMPILE__
+#define B3D_BARRIER() __syncthreads()
+#else
+#define B3D_BARRIER() ((void)0)
+#endif
 
 /* Shape bounds stay in the LDS rows during contact generation when the
  * rows of kClipWords + 6 max_s words fit in this many words per lane;
@@ -853,6 +874,92 @@ B3D_FN void warm_apply(const OldWarm& o, NewContact* nc) {
  * writes is; the two sorted lists are merged).  Then the list is walked
  * with the next pair's shape records and old contact in flight while the
  * current pair is tested and collided. */
+B3D_FN void mani_store(const PairStage& S, int t, const Mani& m) {
+    uint32_t* r = S.p + (size_t)(1 + t * kManiWords) * kLanes;
+    sti(r, 0, m.count);
+    if (m.count <= 0) return;
+    st3(r, 1, m.normal);
+#pragma unroll
+    for (int p = 0; p < kMaxManifold; p++) {
+        if (p >= m.count) continue;
+        st3(r, 4 + 8 * p, m.p_a[p]);
+        st3(r, 7 + 8 * p, m.p_b[p]);
+        stf(r, 10 + 8 * p, m.sep[p]);
+        sti(r, 11 + 8 * p, (int)m.feature[p]);
+    }
+}
+B3D_FN void mani_load(const PairStage& S, int t, Mani* m) {
+    const uint32_t* r = S.p + (size_t)(1 + t * kManiWords) * kLanes;
+    m->count = ldi(r, 0);
+    if (m->count <= 0) return;
+    m->normal = ld3(r, 1);
+#pragma unroll
+    for (int p = 0; p < kMaxManifold; p++) {
+        if (p >= m->count) continue;
+        m->p_a[p] = ld3(r, 4 + 8 * p);
+        m->p_b[p] = ld3(r, 7 + 8 * p);
+        m->sep[p] = ldf(r, 10 + 8 * p);
+        m->feature[p] = ldu(r, 11 + 8 * p);
+    }
+}
+
+/* Whether candidate pair (A, B) is filtered out before the narrowphase
+ * (08:127-139): one body, both static, category / mask, or joined by a
+ * joint that does not collide its bodies. */
+B3D_FN bool pair_skipped(const Lane& L, const PairShape& A, const PairShape& B, const uint32_t* jkey, int nj) {
+    uint32_t bkey = pair_key(A.body, B.body);
+    int joined = 0;
+#pragma unroll
+    for (int k = 0; k < kJointKeyRegs; k++) joined |= jkey[k] == bkey;
+    for (int k = kJointKeyRegs; k < nj; k++) joined |= ldu(joint_rec(L, k), JS_KEY) == bkey;
+    return A.body == B.body || (A.bflags & B.bflags & kBodyStatic) || (A.cat & B.mask) == 0
+        || (B.cat & A.mask) == 0 || joined;
+}
+
+/* This wave's share of the tile's narrowphase: candidates t = wave, wave +
+ * waves, ..., each manifold (empty when filtered) to the stage; the next
+ * share's shapes are in flight during a collision. */
+B3D_FN void pair_share(const Lane& L, const PairStage& S, int ncand, int nj) {
+    const uint32_t* cand = L.scr + L.g.scr_cand * kLanes;
+    uint32_t jkey[kJointKeyRegs];
+#pragma unroll
+    for (int k = 0; k < kJointKeyRegs; k++) jkey[k] = k < nj ? ldu(joint_rec(L, k), JS_KEY) : 0xffffffffu;
+    PairShape A, B, An, Bn;
+    int t = S.wave;
+    if (t < ncand) {
+        uint32_t key = ldu(cand, 2 * t);
+        pshape_load(L, (int)(key >> 16), &A);
+        pshape_load(L, (int)(key & 0xffffu), &B);
+    }
+    for (; t < ncand; t += S.waves) {
+        int tn = t + S.waves;
+        if (tn < ncand) {
+            uint32_t kn = ldu(cand, 2 * tn);
+            pshape_load(L, (int)(kn >> 16), &An);
+            pshape_load(L, (int)(kn & 0xffffu), &Bn);
+        }
+        Mani m;
+        m.count = 0;
+        if (!pair_skipped(L, A, B, jkey, nj)) collide_pair(&m, A.P, B.P, S.clip);
+        mani_store(S, t, m);
+        A = An;
+        B = Bn;
+    }
+}
+
+/* A helper wave of a staged tile: waits for wave 0's candidate lists, runs
+ * its share of the narrowphase, and signals.  Runs in the tile's stepping
+ * lanes, like wave 0, so its record slots are wave 0's. */
+B3D_FN void pair_helper(const Lane& L0, const PairStage& S) {
+    Lane L = L0;
+    L.sslot = wave_slot(L);
+    B3D_BARRIER();
+    int ncand = ldi(S.p, 0);
+    int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
+    pair_share(L, S, ncand, nj);
+    B3D_BARRIER();
+}
+
 B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int old_n, int sorted) {
     const Geometry& g = L.g;
     uint32_t* cand = L.scr + g.scr_cand * kLanes;
@@ -884,6 +991,14 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
                 }
             }
         }
+    }
+    if (L.stage) {
+        /* the tile's waves split the narrowphase; wave 0 then appends the
+         * manifolds in candidate order as below */
+        sti(L.stage->p, 0, ncand);
+        B3D_BARRIER();
+        pair_share(L, *L.stage, ncand, nj);
+        B3D_BARRIER();
     }
     int cc = 0;
     int rest_any = 0;
@@ -922,16 +1037,10 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
             if (match1 >= 0) old_load(L, match1, &orecn);
         }
         int i = (int)(key >> 16), j = (int)(key & 0xffffu);
-        uint32_t bkey = pair_key(A.body, B.body);
-        int joined = 0;
-#pragma unroll
-        for (int k = 0; k < kJointKeyRegs; k++) joined |= jkey[k] == bkey;
-        for (int k = kJointKeyRegs; k < nj; k++) joined |= ldu(joint_rec(L, k), JS_KEY) == bkey;
-        bool skip = A.body == B.body || (A.bflags & B.bflags & kBodyStatic) || (A.cat & B.mask) == 0
-            || (B.cat & A.mask) == 0 || joined;
         Mani m;
         m.count = 0;
-        if (!skip) collide_pair(&m, A.P, B.P, L.vel);
+        if (L.stage) mani_load(*L.stage, t, &m);
+        else if (!pair_skipped(L, A, B, jkey, nj)) collide_pair(&m, A.P, B.P, L.vel);
         if (m.count > 0 && cc >= g.max_c) {
             overflow = 1;
             dropped++;

@@ -104,6 +104,7 @@ def b3_batch_step_fluid_gpu(engine, dt, substeps, law, state, step_mask=None, re
 
 B3_ENGINE_KEEP_SOLVER_FIELDS = 1
 B3_ENGINE_ART_CONTACTS = 2
+B3_ENGINE_ONE_WAVE_PER_TILE = 4
 
 
 class B3Engine:

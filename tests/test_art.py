@@ -148,7 +148,7 @@ def test_art_option_is_validated_without_a_device():
     from puffysics_amd import _native
     lib = _native.engine_lib()
     assert lib.b3_engine_set_options(None, 2) == 1
-    assert lib.b3_engine_set_options(None, 4) == 1
+    assert lib.b3_engine_set_options(None, 8) == 1
 
 
 # ---- the reduced-coordinate integrator (b3_art_step) ----

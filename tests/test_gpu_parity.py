@@ -293,6 +293,32 @@ def test_default_options_differ_only_in_solver_fields():
     assert allowed[bad[:, 0], bad[:, 1]].all(), bad[~allowed[bad[:, 0], bad[:, 1]]][:10].tolist()
 
 
+@pytest.mark.parametrize("scene,count,steps", [(2, 256, 40), (4, 192, 10), (5, 256, 30)])
+def test_shared_narrowphase_matches_one_wave_per_tile(scene, count, steps):
+    """Batches of at most one tile per CU split the narrowphase over four
+    waves per tile; the worlds equal those of the one-wave launch word for
+    word, through masks, resets (restored by four waves) and the fused
+    reset."""
+    from puffysics_amd.engine import B3_ENGINE_KEEP_SOLVER_FIELDS, B3_ENGINE_ONE_WAVE_PER_TILE
+    worlds = scenes.build(scene, count)
+    shared = _engine(worlds, scene)
+    one = _engine(worlds, scene, keep=False)
+    one.set_options(B3_ENGINE_KEEP_SOLVER_FIELDS | B3_ENGINE_ONE_WAVE_PER_TILE)
+    gpu_run(shared, scene, 0, steps)
+    gpu_run(one, scene, 0, steps)
+    sc = scenes.SCENES[scene]
+    reset = torch.from_numpy((np.arange(count) % 7 == 3).astype(np.uint8)).cuda()
+    for eng in (shared, one):
+        eng.step(sc.dt, sc.substeps, None, reset)
+    torch.cuda.synchronize()
+    a, b = shared.download(), one.download()
+    shared.close()
+    one.close()
+    bad = diff_words(a, b, sc.sig)
+    assert len(bad) == 0, "%d differing words, first %s" % (len(bad), bad[:4].tolist())
+    assert a["contact_count"].sum() > 0
+
+
 def test_default_options_mixed_waves():
     """Default options on the coverage worlds, where worlds with and without
     restitution share waves: those without it warm-start inside
