@@ -132,6 +132,7 @@ __global__ __launch_bounds__(64 * kTileWaves) void b3k_step_shared(uint32_t* liv
     S.clip = (wave == 0 ? lds : lds + (size_t)lds_rows(g) * kLanes + (size_t)(wave - 1) * kClipWords * kLanes) + lane;
     S.wave = wave;
     S.waves = kTileWaves;
+    S.lds_bounds = 1;
     Lane L = lane_view(live, scratch, lds, g, tile, lane, opts);
     L.stage = &S;
     if (wave == 0) step_world(L, dt, substeps);
@@ -307,6 +308,11 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
          * among kTileWaves waves (b3k_step_shared). */
         int cus = 0;
         size_t shared_lds = lds + (size_t)(kTileWaves - 1) * kClipWords * kLanes * sizeof(float);
+        /* wave 0's shape bounds and old contact keys stay in LDS during
+         * candidate search (the helpers' clip rows, and the velocity rows,
+         * are only used after it) */
+        size_t bounds_lds = (size_t)(kClipWords + 6 * g.max_s + g.max_c) * kLanes * sizeof(float);
+        if (bounds_lds > shared_lds) shared_lds = bounds_lds;
         if ((err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device)) != hipSuccess) {
             (void)b3_engine_destroy(e);
             return err;

@@ -326,9 +326,10 @@ B3D_FN bool geometry_of(unsigned long long sig, Geometry* g, size_t* world_bytes
  * lane at p[k * kLanes]. */
 constexpr int kManiWords = 4 + 8 * kMaxManifold;
 struct PairStage {
-    uint32_t* p;   /* lane base */
-    float* clip;   /* this wave's clip rows (lane base) */
+    uint32_t* p;     /* lane base */
+    float* clip;     /* this wave's clip rows (lane base) */
     int wave, waves;
+    int lds_bounds;  /* the workgroup's LDS also holds wave 0's shape bounds */
 };
 
 /* Per-lane view of one world. */
@@ -733,6 +734,16 @@ B3D_FN uint32_t shape_key(int i, int j) { return ((uint32_t)i << 16) | (uint32_t
 /* Copy the contacts' warm-start data into the old-cache scratch
  * (08_contacts.inl:65-91); returns whether their shape pairs are strictly
  * increasing, as every list the step itself writes is. */
+/* With a shared narrowphase the workgroup's LDS also holds the old contacts'
+ * keys, after wave 0's clip rows and shape bounds, for the candidate search
+ * to merge against. */
+B3D_FN bool lds_old_keys(const Lane& L) { return L.stage && L.stage->lds_bounds; }
+B3D_FN float* old_key_rows(const Lane& L) { return L.vel + (kClipWords + 6 * L.g.max_s) * kLanes; }
+B3D_FN uint32_t old_key(const Lane& L, int k) {
+    if (lds_old_keys(L)) return __builtin_bit_cast(uint32_t, old_key_rows(L)[k * kLanes]);
+    return ldu(old_rec(L, k), O_KEY);
+}
+
 B3D_FN int save_old(const Lane& L, int old_n) {
     int sorted = 1;
     uint32_t prev = 0;
@@ -770,6 +781,7 @@ B3D_FN int save_old(const Lane& L, int old_n) {
             sti(o, O_SHAPE_B, sb[q]);
             sti(o, O_POINT_COUNT, pc[q]);
             sti(o, O_KEY, (int)key);
+            if (lds_old_keys(L)) old_key_rows(L)[k * kLanes] = __builtin_bit_cast(float, key);
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
                 if (p >= pc[q]) continue;
@@ -888,14 +900,14 @@ B3D_FN void mani_store(const PairStage& S, int t, const Mani& m) {
         sti(r, 11 + 8 * p, (int)m.feature[p]);
     }
 }
+/* All words of a staged manifold, requested at once (those past its point
+ * count are stale and go unused), so that the load can run ahead. */
 B3D_FN void mani_load(const PairStage& S, int t, Mani* m) {
     const uint32_t* r = S.p + (size_t)(1 + t * kManiWords) * kLanes;
     m->count = ldi(r, 0);
-    if (m->count <= 0) return;
     m->normal = ld3(r, 1);
 #pragma unroll
     for (int p = 0; p < kMaxManifold; p++) {
-        if (p >= m->count) continue;
         m->p_a[p] = ld3(r, 4 + 8 * p);
         m->p_b[p] = ld3(r, 7 + 8 * p);
         m->sep[p] = ldf(r, 10 + 8 * p);
@@ -966,7 +978,7 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
     int ncand = 0;
     {
         int op = 0;
-        uint32_t okey = sorted && old_n > 0 ? ldu(old_rec(L, 0), O_KEY) : 0xffffffffu;
+        uint32_t okey = sorted && old_n > 0 ? old_key(L, 0) : 0xffffffffu;
         for (int i = 0; i < ns; i++) {
             const float* bi = bounds + i * 6 * kLanes;
             for (int j0 = i + 1; j0 < ns; j0 += 4) {
@@ -981,7 +993,7 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
                     if (sorted) {
                         while (op < old_n && okey < key) {
                             op++;
-                            okey = op < old_n ? ldu(old_rec(L, op), O_KEY) : 0xffffffffu;
+                            okey = op < old_n ? old_key(L, op) : 0xffffffffu;
                         }
                         if (op < old_n && okey == key) match = op;
                     }
@@ -1010,6 +1022,7 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
     for (int k = 0; k < kJointKeyRegs; k++) jkey[k] = k < nj ? ldu(joint_rec(L, k), JS_KEY) : 0xffffffffu;
     PairShape A, B, An, Bn;
     OldWarm orec, orecn;
+    Mani ms, msn;   /* staged manifolds of candidates t and t + 1 */
     uint32_t key = 0, key1 = 0;
     int match = -1, match1 = -1;
     if (ncand > 0) {
@@ -1018,6 +1031,7 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
         pshape_load(L, (int)(key >> 16), &A);
         pshape_load(L, (int)(key & 0xffffu), &B);
         if (match >= 0) old_load(L, match, &orec);
+        if (L.stage) mani_load(*L.stage, 0, &ms);
     }
     if (ncand > 1) {
         key1 = ldu(cand, 2);
@@ -1035,11 +1049,12 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
             else An = A;
             pshape_load(L, (int)(key1 & 0xffffu), &Bn);
             if (match1 >= 0) old_load(L, match1, &orecn);
+            if (L.stage) mani_load(*L.stage, t + 1, &msn);
         }
         int i = (int)(key >> 16), j = (int)(key & 0xffffu);
         Mani m;
         m.count = 0;
-        if (L.stage) mani_load(*L.stage, t, &m);
+        if (L.stage) m = ms;
         else if (!pair_skipped(L, A, B, jkey, nj)) collide_pair(&m, A.P, B.P, L.vel);
         if (m.count > 0 && cc >= g.max_c) {
             overflow = 1;
@@ -1116,6 +1131,7 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
         A = An;
         B = Bn;
         orec = orecn;
+        ms = msn;
         key = key1;
         key1 = key2;
         match = match1;
@@ -1142,7 +1158,7 @@ B3D_FN void find_contacts(const Lane& L) {
             key = pair_key(ldi(L.w, jw(L, j, J_BODY_A)), ldi(L.w, jw(L, j, J_BODY_B)));
         sti(joint_rec(L, j), JS_KEY, (int)key);
     }
-    if (bounds_in_lds(g)) {
+    if (bounds_in_lds(g) || (L.stage && L.stage->lds_bounds)) {
         float* bounds = L.vel + kClipWords * kLanes;
         shape_pass(L, ns, bounds);
         find_pairs(L, bounds, ns, nj, old_n, sorted);
