@@ -226,6 +226,10 @@ constexpr int kKindClearDelta = 1 << 10, kKindClearForce = 1 << 11;
  * (pc | flags << 8). */
 constexpr int CH_AB = 0, CH_INFO = 1, kContactScr = 2;
 constexpr int CF_DYN_A = 1, CF_DYN_B = 2, CF_STATIC = 4, CF_RESTITUTION = 8, CF_ROLLING = 16;
+/* Packed records only: the body is static and its delta pose is exactly zero
+ * and the identity for the whole step (nothing moves a static body), so the
+ * sweeps use those values instead of loading its delta record. */
+constexpr int CF_FIXED_A = 32, CF_FIXED_B = 64;
 /* Per-lane step flags (scratch word scr_flags, written by the pair loop):
  * some contact of the world has restitution. */
 constexpr int kLaneRestitution = 1;
@@ -1210,6 +1214,18 @@ B3D_FN int prepare_contacts(const Lane& L, Soft cs, Soft ss) {
             pc[k] = hd.pc;
             fl[k] = hd.flags;
         }
+        int fixed[kPrepChunk];
+#pragma unroll
+        for (int k = 0; k < kPrepChunk; k++) {
+            int c = c0 + k;
+            fixed[k] = 0;
+            if (c >= cc) continue;
+            /* a static body whose delta pose is untouched (no kKindClearDelta) */
+            if (!(fl[k] & CF_DYN_A) && (ru(delta_rec(L, a[k]), BD_KIND) & (kKindStatic | kKindClearDelta)) == kKindStatic)
+                fixed[k] |= CF_FIXED_A;
+            if (!(fl[k] & CF_DYN_B) && (ru(delta_rec(L, b[k]), BD_KIND) & (kKindStatic | kKindClearDelta)) == kKindStatic)
+                fixed[k] |= CF_FIXED_B;
+        }
         float ima[kPrepChunk], imb[kPrepChunk];
         M3 iwa[kPrepChunk], iwb[kPrepChunk];
         V3 n[kPrepChunk], t1[kPrepChunk], ra[kPrepChunk][kMaxManifold], rb[kPrepChunk][kMaxManifold];
@@ -1347,7 +1363,7 @@ B3D_FN int prepare_contacts(const Lane& L, Soft cs, Soft ss) {
             }
             /* the packed record */
             qsu(r, R_AB, (uint32_t)(a[k] | (b[k] << 16)));
-            qsu(r, R_INFO, (uint32_t)(pc[k] | (fl[k] << 8)));
+            qsu(r, R_INFO, (uint32_t)(pc[k] | ((fl[k] | fixed[k]) << 8)));
             qsf(r, R_FRICTION, fric[k]);
             qsf(r, R_TWIST_MASS, twist_mass);
             qs3(r, R_N, n[k]);
@@ -1770,12 +1786,22 @@ B3D_FN void crow_load(const Lane& L, int c, CHead h, int relax, CRow* r) {
     r->twist_mass = h.twist_mass;
     r->n = q3(rc, R_N);
     r->rolling = qf(rc, R_ROLLING);
-    const uint32_t* da = delta_rec(L, h.a);
-    const uint32_t* db = delta_rec(L, h.b);
-    r->dpa = r3(da, BD_DP);
-    r->dqa = rq4(da, BD_DQ);
-    r->dpb = r3(db, BD_DP);
-    r->dqb = rq4(db, BD_DQ);
+    if (h.flags & CF_FIXED_A) {
+        r->dpa = zero3();
+        r->dqa = qid();
+    } else {
+        const uint32_t* da = delta_rec(L, h.a);
+        r->dpa = r3(da, BD_DP);
+        r->dqa = rq4(da, BD_DQ);
+    }
+    if (h.flags & CF_FIXED_B) {
+        r->dpb = zero3();
+        r->dqb = qid();
+    } else {
+        const uint32_t* db = delta_rec(L, h.b);
+        r->dpb = r3(db, BD_DP);
+        r->dqb = rq4(db, BD_DQ);
+    }
 #pragma unroll
     for (int p = 0; p < kMaxManifold; p++) {
         CPoint& q = r->pt[p];
