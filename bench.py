@@ -244,6 +244,10 @@ def main():
                 "kernel": "b3k_step_art" if args.art else "b3k_step", "kernel_ms": round(k_ms, 4),
                 "bytes_per_env_step": round(float(per_world.mean()), 1),
                 "mean_contacts_per_world": round(float(st["contact_count"].mean()), 2), "valu": valu}
+    if traffic:
+        # the measured HBM bytes of a launch over the same launch time
+        roofline["traffic_gbs"] = round(traffic / (k_ms * 1e-3) / 1e9, 1)
+        roofline["traffic_frac"] = round(traffic / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
     eng.close()
     del worlds
 
