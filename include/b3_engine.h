@@ -129,11 +129,13 @@ hipError_t b3_engine_device_view(const B3Engine* engine, void** tiles, size_t* w
 #define B3_ENGINE_ART_CONTACTS 2u
 /* B3_ENGINE_ONE_WAVE_PER_TILE: no counterpart in the reference (a launch
  * choice).  A batch of at most one 64-world tile per CU normally runs with
- * four waves per tile that share the narrowphase (its pairs are
- * independent) while one wave steps, and allocates a staging buffer for
- * that at creation of 4 * tiles * 64 * (1 + 36 * max_shapes * (max_shapes
- * - 1) / 2) bytes.  This option launches one wave per tile as for larger
- * batches.  Results are identical either way. */
+ * four waves per tile: they share the narrowphase (its pairs are
+ * independent) and the contact sweeps (contacts on disjoint dynamic bodies,
+ * level by level, keeping every body's updates in contact order), while one
+ * wave does the rest.  That allocates at creation a staging buffer of
+ * 4 * tiles * 64 * (1 + max(36 * max_shapes * (max_shapes - 1) / 2,
+ * 3 * max_contacts)) bytes.  This option launches one wave per tile as for
+ * larger batches.  Results are identical either way. */
 #define B3_ENGINE_ONE_WAVE_PER_TILE 4u
 hipError_t b3_engine_set_options(B3Engine* engine, unsigned int options);
 

@@ -107,12 +107,13 @@ __global__ __launch_bounds__(64) void b3k_step(uint32_t* live, const uint32_t* s
     step_world(lane_view(live, scratch, vel_rows, g, tile, lane, opts), dt, substeps);
 }
 
-/* The step with the narrowphase shared by kTileWaves waves per tile (small
- * batches, whose one wave per tile would leave most CUs idle): wave 0 steps
- * its lanes' worlds as b3k_step does; the other waves wait for its
- * candidate lists, collide their share of the pairs into the stage, and
- * end.  Every wave sees the same stepping lanes, so all of them reach both
- * barriers of the shared phase or none does. */
+/* The step with the narrowphase and the contact sweeps shared by
+ * kTileWaves waves per tile (small batches, whose one wave per tile would
+ * leave most CUs idle): wave 0 steps its lanes' worlds as b3k_step does;
+ * the other waves wait for its candidate lists, collide their share of the
+ * pairs into the stage, then solve their share of each level of every
+ * contact sweep.  Every wave sees the same stepping lanes and computes the
+ * same level count, so all of them reach the same barriers or none does. */
 __global__ __launch_bounds__(64 * kTileWaves) void b3k_step_shared(uint32_t* live, const uint32_t* snap,
         uint32_t* scratch, uint32_t* stage, size_t stage_tile_words, Geometry g, int count, float dt, int substeps,
         const unsigned char* step_mask, const unsigned char* reset_mask, unsigned int opts) {
@@ -135,8 +136,12 @@ __global__ __launch_bounds__(64 * kTileWaves) void b3k_step_shared(uint32_t* liv
     S.lds_bounds = 1;
     Lane L = lane_view(live, scratch, lds, g, tile, lane, opts);
     L.stage = &S;
-    if (wave == 0) step_world(L, dt, substeps);
-    else pair_helper(L, S);
+    if (wave == 0) {
+        step_world(L, dt, substeps);
+    } else {
+        pair_helper(L, S);
+        sweep_helper(L, dt, substeps);
+    }
 }
 
 /* ---- inputs and stats ---- */
@@ -313,13 +318,18 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
          * are only used after it) */
         size_t bounds_lds = (size_t)(kClipWords + 6 * g.max_s + g.max_c) * kLanes * sizeof(float);
         if (bounds_lds > shared_lds) shared_lds = bounds_lds;
+        /* and, past wave 0's rows, the contact levels of the shared sweeps */
+        size_t sched_lds = (size_t)(lds_rows(g) + sched_words(g)) * kLanes * sizeof(float);
+        if (sched_lds > shared_lds) shared_lds = sched_lds;
         if ((err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device)) != hipSuccess) {
             (void)b3_engine_destroy(e);
             return err;
         }
         if (e->tiles <= cus && shared_lds <= 160u * 1024u) {
             size_t max_cand = (size_t)g.max_s * (size_t)(g.max_s - 1) / 2;
-            e->stage_tile_words = (1 + max_cand * kManiWords) * kLanes;
+            size_t stage_words = max_cand * kManiWords;
+            if ((size_t)stage_sched_words(g) > stage_words) stage_words = (size_t)stage_sched_words(g);
+            e->stage_tile_words = (1 + stage_words) * kLanes;
             e->lds_shared_bytes = shared_lds;
             if (shared_lds > 64u * 1024u)
                 err = hipFuncSetAttribute((const void*)b3k_step_shared, hipFuncAttributeMaxDynamicSharedMemorySize,

@@ -603,6 +603,15 @@ B3D_FN CHead rhead_load(const Lane& L, int c) {
     h.twist_mass = qf(r, R_TWIST_MASS);
     return h;
 }
+/* The head of contact c's packed record in a known slot. */
+B3D_FN CHead rhead_at(const Lane& L, int c, int slot) {
+    const uint32_t* r = crec(L, c, slot);
+    CHead h = head_of(qu(r, R_AB), qu(r, R_INFO));
+    h.slot = slot;
+    h.friction = qf(r, R_FRICTION);
+    h.twist_mass = qf(r, R_TWIST_MASS);
+    return h;
+}
 /* Inverse masses and world inertias of a record's bodies: exact zeros for a
  * body that is not dynamic (08:236-241), which are therefore not stored. */
 B3D_FN void rec_masses(const uint32_t* r, int flags, float* ma, M3* ia, float* mb, M3* ib) {
@@ -1193,6 +1202,42 @@ B3D_FN void apply_impulse(const Lane& L, int b, float m, M3 i, V3 r, V3 p, float
  * kept solver fields use.  A world with neither gets each contact's warm
  * start right after its preparation, with the same impulses in the same
  * order, and the function returns 1 (0: warm_start_contacts still to run). */
+/* Contact levels for the shared sweeps (shared-narrowphase launches only).
+ * A contact's solve reads and writes the velocities of its dynamic bodies
+ * and nothing else a sweep changes, so two contacts with no dynamic body in
+ * common give the same results in either order.  Level 1 + the highest
+ * level among earlier contacts on the same dynamic bodies keeps every
+ * body's sequence of updates in contact order; contacts of one level are
+ * solved by the tile's waves together.
+ * Per lane in the workgroup's LDS, past wave 0's rows: the lane's level
+ * count, each body's last level, each contact's level, and P: per level
+ * its contact count, then (prefix) its first entry, then (after the fill)
+ * one past its last.  In the stage (free once the manifolds are appended):
+ * each contact's record slots (slot | point p's slot << 6 + 6p), then the
+ * entries in level order, two words each (contact, slots). */
+B3D_FN float* sched_rows(const Lane& L) { return L.vel + lds_rows(L.g) * kLanes; }
+B3D_FN int sched_words(const Geometry& g) { return 2 + g.max_b + 2 * g.max_c; }
+B3D_FN int sch_get(const Lane& L, int k) { return __builtin_bit_cast(int, sched_rows(L)[k * kLanes]); }
+B3D_FN void sch_set(const Lane& L, int k, int v) { sched_rows(L)[k * kLanes] = __builtin_bit_cast(float, v); }
+B3D_FN int sch_last(const Lane& L, int b) { return 1 + b; }
+B3D_FN int sch_level(const Lane& L, int c) { return 1 + L.g.max_b + c; }
+B3D_FN int sch_p(const Lane& L, int lev) { return 1 + L.g.max_b + L.g.max_c + lev; }
+/* stage words of the schedule */
+B3D_FN int stage_sched_words(const Geometry& g) { return 3 * g.max_c; }
+B3D_FN uint32_t* sch_slots(const Lane& L, int c) { return L.stage->p + (size_t)(1 + c) * kLanes; }
+B3D_FN uint32_t* sch_entry(const Lane& L, int i) { return L.stage->p + (size_t)(1 + L.g.max_c + 2 * i) * kLanes; }
+
+/* The largest level count among the tile's stepping lanes (every wave of
+ * the tile gets the same value). */
+B3D_FN int tile_levels(const Lane& L) {
+    int v = sch_get(L, 0), m = 0;
+    for (int bit = 15; bit >= 0; bit--) {
+        int cand = m | (1 << bit);
+        if (wave_any(L, v >= cand)) m = cand;
+    }
+    return m;
+}
+
 constexpr int kPrepChunk = 2;
 B3D_FN int prepare_contacts(const Lane& L, Soft cs, Soft ss) {
     uint32_t* w = L.w;
@@ -1200,6 +1245,11 @@ B3D_FN int prepare_contacts(const Lane& L, Soft cs, Soft ss) {
     const float inv_tau = 1.0f / kSpeculative;
     const int keep = (L.opts & kKeepSolverFields) != 0;
     const int fuse = !keep && !(ldi(L.scr + L.g.scr_flags * kLanes, 0) & kLaneRestitution);
+    if (L.stage) {
+        sch_set(L, 0, 0);
+        for (int b = 0; b < body_count(L); b++) sch_set(L, sch_last(L, b), 0);
+        for (int lev = 0; lev <= clampi(cc, 0, L.g.max_c); lev++) sch_set(L, sch_p(L, lev), 0);
+    }
     for (int c0 = 0; c0 < cc; c0 += kPrepChunk) {
         int a[kPrepChunk], b[kPrepChunk], pc[kPrepChunk], fl[kPrepChunk], slot[kPrepChunk];
         int pslot[kPrepChunk][kMaxManifold];
@@ -1364,6 +1414,21 @@ B3D_FN int prepare_contacts(const Lane& L, Soft cs, Soft ss) {
             /* the packed record */
             qsu(r, R_AB, (uint32_t)(a[k] | (b[k] << 16)));
             qsu(r, R_INFO, (uint32_t)(pc[k] | ((fl[k] | fixed[k]) << 8)));
+            if (L.stage) {
+                int la = (fl[k] & CF_DYN_A) ? sch_get(L, sch_last(L, a[k])) : 0;
+                int lb = (fl[k] & CF_DYN_B) ? sch_get(L, sch_last(L, b[k])) : 0;
+                int lev = (la > lb ? la : lb) + 1;
+                if (fl[k] & CF_DYN_A) sch_set(L, sch_last(L, a[k]), lev);
+                if (fl[k] & CF_DYN_B) sch_set(L, sch_last(L, b[k]), lev);
+                sch_set(L, sch_level(L, c), lev);
+                sch_set(L, sch_p(L, lev), sch_get(L, sch_p(L, lev)) + 1);
+                int packed = slot[k];
+#pragma unroll
+                for (int p = 0; p < kMaxManifold; p++)
+                    if (p < pc[k]) packed |= pslot[k][p] << (6 + 6 * p);
+                sti(sch_slots(L, c), 0, packed);
+                if (lev > sch_get(L, 0)) sch_set(L, 0, lev);
+            }
             qsf(r, R_FRICTION, fric[k]);
             qsf(r, R_TWIST_MASS, twist_mass);
             qs3(r, R_N, n[k]);
@@ -1416,6 +1481,23 @@ B3D_FN int prepare_contacts(const Lane& L, Soft cs, Soft ss) {
                 if (is_dyn_flag(L, a[k])) set_vang(L, a[k], sub(vang(L, a[k]), mv(ia, tr)));
                 if (is_dyn_flag(L, b[k])) set_vang(L, b[k], add(vang(L, b[k]), mv(ib, tr)));
             }
+        }
+    }
+    if (L.stage) {
+        /* counting sort of the contacts by level (contact order within one) */
+        int nlev = sch_get(L, 0), run = 0;
+        for (int lev = 1; lev <= nlev; lev++) {
+            int n = sch_get(L, sch_p(L, lev));
+            sch_set(L, sch_p(L, lev), run);
+            run += n;
+        }
+        for (int c = 0; c < cc; c++) {
+            int lev = sch_get(L, sch_level(L, c));
+            int at = sch_get(L, sch_p(L, lev));
+            sch_set(L, sch_p(L, lev), at + 1);
+            uint32_t* e = sch_entry(L, at);
+            sti(e, 0, c);
+            sti(e, 1, ldi(sch_slots(L, c), 0));
         }
     }
     return fuse;
@@ -1775,7 +1857,7 @@ B3D_FN void crow_masses(const Lane& L, int c, CRow* r, Soft cs, Soft ss) {
 
 /* Normal, points and friction data of a row: loaded one contact ahead.
  * Call where exactly the lanes with a contact c run. */
-B3D_FN void crow_load(const Lane& L, int c, CHead h, int relax, CRow* r) {
+B3D_FN void crow_load(const Lane& L, int c, CHead h, int relax, CRow* r, const int* ps = nullptr) {
     const uint32_t* rc = crec(L, c, h.slot);
     r->a = h.a;
     r->b = h.b;
@@ -1808,7 +1890,7 @@ B3D_FN void crow_load(const Lane& L, int c, CHead h, int relax, CRow* r) {
         q.ni = 0.0f;
         q.tn = 0.0f;
         if (p >= h.pc) continue;
-        const uint32_t* pr = prec(L, c, p, wave_slot(L));
+        const uint32_t* pr = prec(L, c, p, ps ? ps[p] : wave_slot(L));
         q.ra = q3(pr, PR_RA);
         q.nmass = qf(pr, PR_NMASS);
         q.rb = q3(pr, PR_RB);
@@ -1961,6 +2043,39 @@ B3D_FN void solve_contacts(const Lane& L, float inv_h, float contact_speed, int 
         crow_solve(L, c, cur, inv_h, contact_speed, use_bias);
         cur = nxt;
         h1 = h2;
+    }
+}
+
+/* One sweep of a shared-narrowphase tile: level by level, each of the
+ * tile's waves solving every waves-th contact of the level (in contact
+ * order), a workgroup barrier after each level and one before the first,
+ * which also publishes wave 0's velocity updates since the last sweep.
+ * Every wave runs 1 + nlev barriers (nlev from tile_levels). */
+B3D_FN void solve_contacts_leveled(const Lane& L, float inv_h, float contact_speed, int use_bias, Soft cs, Soft ss,
+        int nlev) {
+    const PairStage& S = *L.stage;
+    int relax = !use_bias;
+    int mine = sch_get(L, 0);
+    B3D_BARRIER();
+    int first = 0;
+    for (int lev = 1; lev <= nlev; lev++) {
+        if (lev <= mine) {
+            int end = sch_get(L, sch_p(L, lev));
+            for (int i = first + S.wave; i < end; i += S.waves) {
+                const uint32_t* en = sch_entry(L, i);
+                int c = ldi(en, 0), e = ldi(en, 1);
+                int ps[kMaxManifold];
+#pragma unroll
+                for (int p = 0; p < kMaxManifold; p++) ps[p] = (e >> (6 + 6 * p)) & 63;
+                CHead h = rhead_at(L, c, e & 63);
+                CRow r;
+                crow_load(L, c, h, relax, &r, ps);
+                crow_masses(L, c, &r, cs, ss);
+                crow_solve(L, c, r, inv_h, contact_speed, use_bias);
+            }
+            first = end;
+        }
+        B3D_BARRIER();
     }
 }
 
@@ -2652,16 +2767,24 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
     if (wave_any(L, !warm_done)) warm_start_contacts(L, warm_done);
     warm_start_joints(L);
     joint_geometry(L);   /* the contacts' initial separations come from prepare_contacts */
+    int nlev = 0;
+    if (L.stage) {
+        /* the helper waves join here for the contact sweeps */
+        B3D_BARRIER();
+        nlev = tile_levels(L);
+    }
     for (int s = 0; s < subs; s++) {
         if constexpr (Law::kActive)
             integrate_velocities_law(L, h, law);
         else
             integrate_velocities(L);
-        solve_contacts(L, inv_h, contact_speed, 1, cs, ss);
+        if (L.stage) solve_contacts_leveled(L, inv_h, contact_speed, 1, cs, ss, nlev);
+        else solve_contacts(L, inv_h, contact_speed, 1, cs, ss);
         solve_joints(L, h, inv_h, 1);
         integrate_positions(L, h, inv_dt);
         delta_geometry(L);
-        solve_contacts(L, inv_h, contact_speed, 0, cs, ss);
+        if (L.stage) solve_contacts_leveled(L, inv_h, contact_speed, 0, cs, ss, nlev);
+        else solve_contacts(L, inv_h, contact_speed, 0, cs, ss);
         solve_joints(L, h, inv_h, 0);
         if (rest_wave) apply_restitution(L, rest_threshold);
     }
@@ -2672,6 +2795,30 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
 
 /* b3_step without a hook. */
 B3D_FN void step_world(const Lane& L, float dt, int substeps) { step_world(L, dt, substeps, NoForces()); }
+
+/* A helper wave of a shared-narrowphase tile after its narrowphase share:
+ * its part of every contact sweep, in step with wave 0 (the same barriers:
+ * one where wave 0 starts the substeps, then each sweep's).  Runs in the
+ * tile's stepping lanes, so its body and delta record slots are wave 0's. */
+B3D_FN void sweep_helper(const Lane& L0, float dt, int substeps) {
+    Lane L = L0;
+    L.sslot = wave_slot(L);
+    int subs = substeps < 1 ? 1 : substeps;
+    float h = dt / (float)subs;
+    float inv_dt = 1.0f / dt;
+    float inv_h = (float)subs * inv_dt;
+    float hertz = minf(ldf(L.w, H_CONTACT_HERTZ), 0.25f * inv_h);
+    float damping = ldf(L.w, H_CONTACT_DAMPING);
+    Soft cs = make_soft(hertz, damping, h);
+    Soft ss = make_soft(2.0f * hertz, 0.5f * damping, h);
+    float contact_speed = ldf(L.w, H_CONTACT_SPEED);
+    B3D_BARRIER();
+    int nlev = tile_levels(L);
+    for (int s = 0; s < subs; s++) {
+        solve_contacts_leveled(L, inv_h, contact_speed, 1, cs, ss, nlev);
+        solve_contacts_leveled(L, inv_h, contact_speed, 0, cs, ss, nlev);
+    }
+}
 
 }  // namespace b3d
 
