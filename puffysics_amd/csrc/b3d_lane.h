@@ -2061,9 +2061,20 @@ B3D_FN void solve_contacts_leveled(const Lane& L, float inv_h, float contact_spe
     for (int lev = 1; lev <= nlev; lev++) {
         if (lev <= mine) {
             int end = sch_get(L, sch_p(L, lev));
+            /* the entry of the next contact is in flight during a solve */
+            int cn = 0, en = 0;
+            if (first + S.wave < end) {
+                const uint32_t* ep = sch_entry(L, first + S.wave);
+                cn = ldi(ep, 0);
+                en = ldi(ep, 1);
+            }
             for (int i = first + S.wave; i < end; i += S.waves) {
-                const uint32_t* en = sch_entry(L, i);
-                int c = ldi(en, 0), e = ldi(en, 1);
+                int c = cn, e = en;
+                if (i + S.waves < end) {
+                    const uint32_t* ep = sch_entry(L, i + S.waves);
+                    cn = ldi(ep, 0);
+                    en = ldi(ep, 1);
+                }
                 int ps[kMaxManifold];
 #pragma unroll
                 for (int p = 0; p < kMaxManifold; p++) ps[p] = (e >> (6 + 6 * p)) & 63;
