@@ -1244,13 +1244,11 @@ B3D_FN int prepare_contacts(const Lane& L, Soft cs, Soft ss) {
     int cc = ldi(w, H_CONTACT_COUNT);
     const float inv_tau = 1.0f / kSpeculative;
     const int keep = (L.opts & kKeepSolverFields) != 0;
-    const int fuse = !keep && !(ldi(L.scr + L.g.scr_flags * kLanes, 0) & kLaneRestitution);
-    if (L.stage) {
-        sch_set(L, 0, 0);
-        for (int b = 0; b < body_count(L); b++) sch_set(L, sch_last(L, b), 0);
-        for (int lev = 0; lev <= clampi(cc, 0, L.g.max_c); lev++) sch_set(L, sch_p(L, lev), 0);
-    }
-    for (int c0 = 0; c0 < cc; c0 += kPrepChunk) {
+    /* a shared tile prepares its contacts in parallel (every waves-th chunk
+     * per wave) and warm-starts them afterwards, level by level */
+    const int fuse = !L.stage && !keep && !(ldi(L.scr + L.g.scr_flags * kLanes, 0) & kLaneRestitution);
+    const int first = L.stage ? L.stage->wave : 0, stride = L.stage ? L.stage->waves : 1;
+    for (int c0 = first * kPrepChunk; c0 < cc; c0 += stride * kPrepChunk) {
         int a[kPrepChunk], b[kPrepChunk], pc[kPrepChunk], fl[kPrepChunk], slot[kPrepChunk];
         int pslot[kPrepChunk][kMaxManifold];
 #pragma unroll
@@ -1415,19 +1413,11 @@ B3D_FN int prepare_contacts(const Lane& L, Soft cs, Soft ss) {
             qsu(r, R_AB, (uint32_t)(a[k] | (b[k] << 16)));
             qsu(r, R_INFO, (uint32_t)(pc[k] | ((fl[k] | fixed[k]) << 8)));
             if (L.stage) {
-                int la = (fl[k] & CF_DYN_A) ? sch_get(L, sch_last(L, a[k])) : 0;
-                int lb = (fl[k] & CF_DYN_B) ? sch_get(L, sch_last(L, b[k])) : 0;
-                int lev = (la > lb ? la : lb) + 1;
-                if (fl[k] & CF_DYN_A) sch_set(L, sch_last(L, a[k]), lev);
-                if (fl[k] & CF_DYN_B) sch_set(L, sch_last(L, b[k]), lev);
-                sch_set(L, sch_level(L, c), lev);
-                sch_set(L, sch_p(L, lev), sch_get(L, sch_p(L, lev)) + 1);
                 int packed = slot[k];
 #pragma unroll
                 for (int p = 0; p < kMaxManifold; p++)
                     if (p < pc[k]) packed |= pslot[k][p] << (6 + 6 * p);
                 sti(sch_slots(L, c), 0, packed);
-                if (lev > sch_get(L, 0)) sch_set(L, 0, lev);
             }
             qsf(r, R_FRICTION, fric[k]);
             qsf(r, R_TWIST_MASS, twist_mass);
@@ -1483,24 +1473,44 @@ B3D_FN int prepare_contacts(const Lane& L, Soft cs, Soft ss) {
             }
         }
     }
-    if (L.stage) {
-        /* counting sort of the contacts by level (contact order within one) */
-        int nlev = sch_get(L, 0), run = 0;
-        for (int lev = 1; lev <= nlev; lev++) {
-            int n = sch_get(L, sch_p(L, lev));
-            sch_set(L, sch_p(L, lev), run);
-            run += n;
-        }
-        for (int c = 0; c < cc; c++) {
-            int lev = sch_get(L, sch_level(L, c));
-            int at = sch_get(L, sch_p(L, lev));
-            sch_set(L, sch_p(L, lev), at + 1);
-            uint32_t* e = sch_entry(L, at);
-            sti(e, 0, c);
-            sti(e, 1, ldi(sch_slots(L, c), 0));
-        }
-    }
     return fuse;
+}
+
+/* A shared tile's contact levels (wave 0, after the parallel preparation):
+ * each contact's level from its dynamic bodies' last levels, in contact
+ * order, then a counting sort of the contacts by level into the entries. */
+B3D_FN void sched_build(const Lane& L) {
+    int cc = clampi(ldi(L.w, H_CONTACT_COUNT), 0, L.g.max_c);
+    int nb = body_count(L);
+    for (int b = 0; b < nb; b++) sch_set(L, sch_last(L, b), 0);
+    for (int lev = 0; lev <= cc; lev++) sch_set(L, sch_p(L, lev), 0);
+    int nlev = 0;
+    for (int c = 0; c < cc; c++) {
+        CHead hd = chead_load(L, c);
+        int la = (hd.flags & CF_DYN_A) ? sch_get(L, sch_last(L, hd.a)) : 0;
+        int lb = (hd.flags & CF_DYN_B) ? sch_get(L, sch_last(L, hd.b)) : 0;
+        int lev = (la > lb ? la : lb) + 1;
+        if (hd.flags & CF_DYN_A) sch_set(L, sch_last(L, hd.a), lev);
+        if (hd.flags & CF_DYN_B) sch_set(L, sch_last(L, hd.b), lev);
+        sch_set(L, sch_level(L, c), lev);
+        sch_set(L, sch_p(L, lev), sch_get(L, sch_p(L, lev)) + 1);
+        if (lev > nlev) nlev = lev;
+    }
+    sch_set(L, 0, nlev);
+    int run = 0;
+    for (int lev = 1; lev <= nlev; lev++) {
+        int n = sch_get(L, sch_p(L, lev));
+        sch_set(L, sch_p(L, lev), run);
+        run += n;
+    }
+    for (int c = 0; c < cc; c++) {
+        int lev = sch_get(L, sch_level(L, c));
+        int at = sch_get(L, sch_p(L, lev));
+        sch_set(L, sch_p(L, lev), at + 1);
+        uint32_t* e = sch_entry(L, at);
+        sti(e, 0, c);
+        sti(e, 1, ldi(sch_slots(L, c), 0));
+    }
 }
 
 /* b3_prepare_joints (06_joints.inl:161-202), plus the hinge axis through
@@ -2083,6 +2093,52 @@ B3D_FN void solve_contacts_leveled(const Lane& L, float inv_h, float contact_spe
                 crow_load(L, c, h, relax, &r, ps);
                 crow_masses(L, c, &r, cs, ss);
                 crow_solve(L, c, r, inv_h, contact_speed, use_bias);
+            }
+            first = end;
+        }
+        B3D_BARRIER();
+    }
+}
+
+/* b3_warm_start (08:194-232) for a shared tile: each contact's impulses
+ * as warm_start_contacts applies them, level by level like the sweeps
+ * (1 + nlev barriers). */
+B3D_FN void warm_contacts_leveled(const Lane& L, int nlev) {
+    const PairStage& S = *L.stage;
+    int mine = sch_get(L, 0);
+    B3D_BARRIER();
+    int first = 0;
+    for (int lev = 1; lev <= nlev; lev++) {
+        if (lev <= mine) {
+            int end = sch_get(L, sch_p(L, lev));
+            for (int i = first + S.wave; i < end; i += S.waves) {
+                const uint32_t* en = sch_entry(L, i);
+                int c = ldi(en, 0), e = ldi(en, 1);
+                CHead h = rhead_at(L, c, e & 63);
+                const uint32_t* r = crec(L, c, h.slot);
+                float ma, mb;
+                M3 ia, ib;
+                rec_masses(r, h.flags, &ma, &ia, &mb, &ib);
+                V3 n = q3(r, R_N);
+#pragma unroll
+                for (int p = 0; p < kMaxManifold; p++) {
+                    if (p >= h.pc) continue;
+                    const uint32_t* pr = prec(L, c, p, (e >> (6 + 6 * p)) & 63);
+                    V3 P = scale(n, qf(r, R_NI + 2 * p));
+                    apply_impulse(L, h.a, ma, ia, q3(pr, PR_RA), P, -1.0f);
+                    apply_impulse(L, h.b, mb, ib, q3(pr, PR_RB), P, 1.0f);
+                }
+                V3 t1 = q3(r, R_T1);
+                V2 fi;
+                fi.x = qf(r, R_FI);
+                fi.y = qf(r, R_FI + 1);
+                V3 t2 = cross(t1, n);
+                V3 f = add(scale(t1, fi.x), scale(t2, fi.y));
+                apply_impulse(L, h.a, ma, ia, q3(r, R_CA), f, -1.0f);
+                apply_impulse(L, h.b, mb, ib, q3(r, R_CB), f, 1.0f);
+                V3 tr = add(scale(n, qf(r, R_TWIST)), q3(r, R_ROLL));
+                if (is_dyn_flag(L, h.a)) set_vang(L, h.a, sub(vang(L, h.a), mv(ia, tr)));
+                if (is_dyn_flag(L, h.b)) set_vang(L, h.b, add(vang(L, h.b), mv(ib, tr)));
             }
             first = end;
         }
@@ -2773,17 +2829,26 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
     const bool rest_wave = wave_any(L, (ldi(L.scr + L.g.scr_flags * kLanes, 0) & kLaneRestitution) != 0);
     vel_load(L);
     body_prepass(L, h);
-    int warm_done = prepare_contacts(L, cs, ss);
-    prepare_joints(L, h);
-    if (wave_any(L, !warm_done)) warm_start_contacts(L, warm_done);
-    warm_start_joints(L);
-    joint_geometry(L);   /* the contacts' initial separations come from prepare_contacts */
     int nlev = 0;
     if (L.stage) {
-        /* the helper waves join here for the contact sweeps */
+        /* the tile's waves prepare the contacts together; wave 0 levels
+         * them; all warm-start them level by level (the helper waves meet
+         * wave 0 at each barrier, sweep_helper) */
+        B3D_BARRIER();
+        prepare_contacts(L, cs, ss);
+        B3D_BARRIER();
+        sched_build(L);
+        prepare_joints(L, h);
         B3D_BARRIER();
         nlev = tile_levels(L);
+        warm_contacts_leveled(L, nlev);
+    } else {
+        int warm_done = prepare_contacts(L, cs, ss);
+        prepare_joints(L, h);
+        if (wave_any(L, !warm_done)) warm_start_contacts(L, warm_done);
     }
+    warm_start_joints(L);
+    joint_geometry(L);   /* the contacts' initial separations come from prepare_contacts */
     for (int s = 0; s < subs; s++) {
         if constexpr (Law::kActive)
             integrate_velocities_law(L, h, law);
@@ -2808,9 +2873,10 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
 B3D_FN void step_world(const Lane& L, float dt, int substeps) { step_world(L, dt, substeps, NoForces()); }
 
 /* A helper wave of a shared-narrowphase tile after its narrowphase share:
- * its part of every contact sweep, in step with wave 0 (the same barriers:
- * one where wave 0 starts the substeps, then each sweep's).  Runs in the
- * tile's stepping lanes, so its body and delta record slots are wave 0's. */
+ * its share of the contact preparation, of the level-by-level warm start
+ * and of every contact sweep, in step with wave 0 (the same barriers, in
+ * the same order, as step_world's shared path).  Runs in the tile's
+ * stepping lanes, so its body and delta record slots are wave 0's. */
 B3D_FN void sweep_helper(const Lane& L0, float dt, int substeps) {
     Lane L = L0;
     L.sslot = wave_slot(L);
@@ -2823,8 +2889,12 @@ B3D_FN void sweep_helper(const Lane& L0, float dt, int substeps) {
     Soft cs = make_soft(hertz, damping, h);
     Soft ss = make_soft(2.0f * hertz, 0.5f * damping, h);
     float contact_speed = ldf(L.w, H_CONTACT_SPEED);
-    B3D_BARRIER();
+    B3D_BARRIER();                 /* wave 0 has staged velocities and body records */
+    prepare_contacts(L, cs, ss);
+    B3D_BARRIER();                 /* all contacts prepared */
+    B3D_BARRIER();                 /* wave 0 has levelled them */
     int nlev = tile_levels(L);
+    warm_contacts_leveled(L, nlev);
     for (int s = 0; s < subs; s++) {
         solve_contacts_leveled(L, inv_h, contact_speed, 1, cs, ss, nlev);
         solve_contacts_leveled(L, inv_h, contact_speed, 0, cs, ss, nlev);
