@@ -121,7 +121,7 @@ hipError_t b3_engine_device_view(const B3Engine* engine, void** tiles, size_t* w
  * tree's Delassus operator (08_contacts.inl:194-232, 422-437); other
  * worlds step as usual.  The contacts' solver fields are then always
  * written back.  Turning it on allocates a workspace of
- * 4 * count * ((171 + 22) * max_bodies + 9) bytes (the one exception to
+ * 4 * count * ((171 + 22) * max_bodies + 209) bytes (the one exception to
  * b3_engine_create being the only allocating call); it is freed by
  * b3_engine_destroy.  This mode costs far more per contact than the
  * default, as in the reference.  The force-law entry points return

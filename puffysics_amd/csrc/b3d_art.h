@@ -60,7 +60,7 @@ constexpr int kArtBodyTmp = 2 * kArtMaxDeg + 6;
 
 /* Words of one lane's workspace for a body capacity: the link blocks, the
  * search temporaries, then the cut count and the cut joints. */
-B3D_FN int art_ws_words(int max_b) { return max_b * (kArtLinkWords + kArtBodyTmp) + 1 + kArtMaxCuts; }
+B3D_FN int art_ws_words(int max_b) { return max_b * (kArtLinkWords + kArtBodyTmp) + 1 + kArtMaxCuts * (1 + 25); }
 
 struct M6 { M3 ww, wv, vw, vv; };   /* spatial inertia, angular first (b3_art.cuh:54-59) */
 struct S6 { V3 w, v; };             /* motion or force: (angular, linear) */
@@ -94,6 +94,9 @@ struct ArtWs {
     B3D_MFN int cut(int c) const { return __builtin_bit_cast(int, p[cut_word(1 + c) * kLanes]); }
     B3D_MFN void set_n_cuts(int n) const { p[cut_word(0) * kLanes] = __builtin_bit_cast(float, n); }
     B3D_MFN void set_cut(int c, int j) const { p[cut_word(1 + c) * kLanes] = __builtin_bit_cast(float, j); }
+    /* each cut's regularised 5x5 Delassus block, for the iterations of one pass */
+    B3D_MFN float gd(int c, int k) const { return p[cut_word(1 + kArtMaxCuts + c * 25 + k) * kLanes]; }
+    B3D_MFN void sd(int c, int k, float v) const { p[cut_word(1 + kArtMaxCuts + c * 25 + k) * kLanes] = v; }
 };
 constexpr int AT_DEG = 0, AT_ADJ_B = 1, AT_ADJ_J = 1 + kArtMaxDeg, AT_LINK = 1 + 2 * kArtMaxDeg, AT_SEEN = AT_LINK + 1,
               AT_QUEUE = AT_SEEN + 1, AT_PARENT_B = AT_QUEUE + 1, AT_PARENT_J = AT_PARENT_B + 1;
@@ -1452,15 +1455,22 @@ B3D_FN void art_solve_cuts(const Lane& L, const ArtWs& A, float inv_h, int use_b
                 if (use_bias) vbias = 0.2f * inv_h * err[k];
                 rhs[k] = art_row_vel(L, A, rows[k]) - vbias;
             }
+            /* the block depends only on the poses, which the pass does not
+             * change: built on the first iteration, the same bits reused */
             float D[25], x[5], y[5];
-            for (int k = 0; k < 5; k++) x[k] = 0.0f;
-            for (int col = 0; col < 5; col++) {
-                x[col] = 1.0f;
-                art_delassus(L, A, rows, x, y, 5);
-                for (int r = 0; r < 5; r++) D[r * 5 + col] = y[r];
-                x[col] = 0.0f;
+            if (it == 0) {
+                for (int k = 0; k < 5; k++) x[k] = 0.0f;
+                for (int col = 0; col < 5; col++) {
+                    x[col] = 1.0f;
+                    art_delassus(L, A, rows, x, y, 5);
+                    for (int r = 0; r < 5; r++) D[r * 5 + col] = y[r];
+                    x[col] = 0.0f;
+                }
+                for (int k = 0; k < 5; k++) D[k * 5 + k] += 1.0e-8f;
+                for (int k = 0; k < 25; k++) A.sd(c, k, D[k]);
+            } else {
+                for (int k = 0; k < 25; k++) D[k] = A.gd(c, k);
             }
-            for (int k = 0; k < 5; k++) D[k * 5 + k] += 1.0e-8f;
             float lam[5];
             if (!solve5(D, rhs, lam)) {
                 for (int k = 0; k < 5; k++) {
