@@ -94,16 +94,17 @@ class EmuBatch:
         self.snap = w.view(np.uint32).copy()   # snapshots stay plain B3World structs
         emu().emu_upload(w.ctypes.data, self.count, self.sc.sig, self.tiles.ctypes.data)
 
-    def run(self, t0, nsteps, seed=scenes.SEED):
+    def run(self, t0, nsteps, seed=scenes.SEED, shared=False):
         e = emu()
+        step = e.emu_step_shared if shared else e.emu_step
+        step.argtypes = [_vp, _i, _ull, _f, _i, _vp]
         for t in range(t0, t0 + nsteps):
             reset, stepm = scenes.masks(self.scene, self.count, t, seed)
             if reset.any():
                 e.emu_restore(self.tiles.ctypes.data, self.snap.ctypes.data, self.count, self.sc.sig,
                               reset.ctypes.data)
             e.emu_inputs(self.tiles.ctypes.data, self.count, self.sc.sig, self.scene, seed, t, stepm.ctypes.data)
-            e.emu_step(self.tiles.ctypes.data, self.count, self.sc.sig, self.sc.dt, self.sc.substeps,
-                       stepm.ctypes.data)
+            step(self.tiles.ctypes.data, self.count, self.sc.sig, self.sc.dt, self.sc.substeps, stepm.ctypes.data)
 
     def worlds(self):
         out = np.zeros(self.count, dtype=self.dtype)
@@ -536,6 +537,13 @@ class EmuSig:
         act = None if active is None else np.ascontiguousarray(active, np.uint8)
         emu().emu_step(self.tiles.ctypes.data, self.count, self.sig, dt, substeps,
                        None if act is None else act.ctypes.data)
+
+    def step_shared(self, dt, substeps, active=None):
+        lib = emu()
+        lib.emu_step_shared.argtypes = [_vp, _i, _ull, _f, _i, _vp]
+        act = None if active is None else np.ascontiguousarray(active, np.uint8)
+        lib.emu_step_shared(self.tiles.ctypes.data, self.count, self.sig, dt, substeps,
+                            None if act is None else act.ctypes.data)
 
     def step_gravity(self, dt, substeps, gravity, softening, masses=None, active=None):
         lib = emu()

@@ -96,6 +96,41 @@ void emu_step(uint32_t* tiles, int count, unsigned long long sig, float dt, int 
     }
 }
 
+/* emu_step through the shared-tile path of b3k_step_shared with a single
+ * wave per tile: the staged narrowphase, the parallel preparation's
+ * staging, the contact levels, and the level-by-level warm start and
+ * sweeps (with one wave, a level's contacts in level order rather than
+ * contact order, which must not change any result). */
+void emu_step_shared(uint32_t* tiles, int count, unsigned long long sig, float dt, int substeps,
+        const unsigned char* step_mask) {
+    Geometry g;
+    size_t wb;
+    if (!geometry_of(sig, &g, &wb)) return;
+    int ntiles = (count + kLanes - 1) / kLanes;
+    std::vector<uint32_t> scratch((size_t)ntiles * g.tile_scr_words);
+    int rows = lds_rows(g) + 3 * kClipWords;
+    if (kClipWords + 6 * g.max_s + g.max_c > rows) rows = kClipWords + 6 * g.max_s + g.max_c;
+    if (lds_rows(g) + sched_words(g) > rows) rows = lds_rows(g) + sched_words(g);
+    std::vector<float> lds((size_t)rows * kLanes);
+    size_t max_cand = (size_t)g.max_s * (size_t)(g.max_s - 1) / 2;
+    size_t words = max_cand * kManiWords;
+    if ((size_t)stage_sched_words(g) > words) words = (size_t)stage_sched_words(g);
+    size_t stage_tile = (1 + words) * kLanes;
+    std::vector<uint32_t> stage((size_t)ntiles * stage_tile);
+    for (int w = 0; w < count; w++) {
+        if (step_mask && !step_mask[w]) continue;
+        Lane L = lane_of(tiles, scratch.data(), lds.data(), g, w);
+        PairStage S;
+        S.p = stage.data() + (size_t)(w / kLanes) * stage_tile + w % kLanes;
+        S.clip = lds.data() + w % kLanes;
+        S.wave = 0;
+        S.waves = 1;
+        S.lds_bounds = 1;
+        L.stage = &S;
+        step_world(L, dt, substeps);
+    }
+}
+
 /* emu_step with pairwise gravity in the force hook; `masses` is NULL or
  * count * max_bodies floats. */
 void emu_step_gravity(uint32_t* tiles, int count, unsigned long long sig, float dt, int substeps,

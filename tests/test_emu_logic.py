@@ -125,3 +125,35 @@ def test_lane_code_default_options_feature_worlds():
     rest = ref["contacts"]["restitution"] > 0
     has = np.array([rest[i, :ref["contact_count"][i]].any() for i in range(40)])
     assert has.any() and not has.all()
+
+
+@pytest.mark.parametrize("scene,count,steps", [(1, 70, 80), (2, 70, 65), (4, 66, 12), (5, 130, 40)])
+def test_shared_tile_path_on_the_host(scene, count, steps):
+    """The shared-tile path of small batches (staged narrowphase, staged
+    preparation, contact levels, level-by-level warm start and sweeps), run
+    on the host with one wave per tile: a level's contacts are then solved
+    in level order instead of contact order, which a correct levelling does
+    not change, so the worlds equal the oracle's word for word."""
+    worlds = scenes.build(scene, count)
+    initial = clone(worlds)
+    e = EmuBatch(scene, worlds)
+    e.run(0, steps, shared=True)
+    ref = clone(worlds)
+    oracle_run(scene, ref, initial, 0, steps)
+    bad = diff_words(e.worlds(), ref, scenes.SCENES[scene].sig)
+    assert len(bad) == 0, "%d differing words, first %s" % (len(bad), bad[:4].tolist())
+
+
+def test_shared_tile_path_on_the_host_feature_worlds():
+    """The same on the coverage worlds (restitution, rolling, kinematic and
+    locked bodies, welds and hinges)."""
+    from b3test import EmuSig, feature_worlds, oracle_step_batch
+    from puffysics_amd.creation import CUSTOM_SIG
+    worlds = feature_worlds(40, hinges=True)
+    ref = clone(worlds)
+    emu_ = EmuSig(CUSTOM_SIG, worlds)
+    for _ in range(15):
+        oracle_step_batch(ref, CUSTOM_SIG, 1.0 / 60.0, 4)
+        emu_.step_shared(1.0 / 60.0, 4)
+    bad = diff_words(emu_.worlds(), ref, CUSTOM_SIG)
+    assert len(bad) == 0, "%d differing words, first %s" % (len(bad), bad[:4].tolist())
