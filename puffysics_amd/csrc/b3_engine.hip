@@ -325,7 +325,7 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
             (void)b3_engine_destroy(e);
             return err;
         }
-        if (e->tiles <= cus && shared_lds <= 160u * 1024u) {
+        if (e->tiles <= cus && shared_lds <= 160u * 1024u && kClipWords + hit_words(g) + 2 <= lds_rows(g)) {
             size_t max_cand = (size_t)g.max_s * (size_t)(g.max_s - 1) / 2;
             size_t stage_words = max_cand * kManiWords;
             if ((size_t)stage_sched_words(g) > stage_words) stage_words = (size_t)stage_sched_words(g);

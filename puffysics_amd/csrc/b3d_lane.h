@@ -941,6 +941,21 @@ B3D_FN bool pair_skipped(const Lane& L, const PairShape& A, const PairShape& B, 
         || (B.cat & A.mask) == 0 || joined;
 }
 
+/* Which candidates of a shared tile produced a manifold: one bit per
+ * candidate, then a restitution flag and whether the old contacts were
+ * sorted, in wave 0's LDS rows past its clip rows (the shape bounds there
+ * are dead once the candidates are listed; the helpers' clip rows start
+ * past all of wave 0's rows). */
+B3D_FN int hit_words(const Geometry& g) { return (g.max_s * (g.max_s - 1) / 2 + 31) / 32; }
+B3D_FN float* hit_rows(const Lane& L) { return L.vel + kClipWords * kLanes; }
+B3D_FN void lds_or(float* p, uint32_t bits) {
+#ifdef __HIP_DEVICE_COMPILE__
+    atomicOr(reinterpret_cast<unsigned int*>(p), bits);
+#else
+    *p = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, *p) | bits);
+#endif
+}
+
 /* This wave's share of the tile's narrowphase: candidates t = wave, wave +
  * waves, ..., each manifold (empty when filtered) to the stage; the next
  * share's shapes are in flight during a collision. */
@@ -967,9 +982,113 @@ B3D_FN void pair_share(const Lane& L, const PairStage& S, int ncand, int nj) {
         m.count = 0;
         if (!pair_skipped(L, A, B, jkey, nj)) collide_pair(&m, A.P, B.P, S.clip);
         mani_store(S, t, m);
+        if (m.count > 0) lds_or(hit_rows(L) + (t >> 5) * kLanes, 1u << (t & 31));
         A = An;
         B = Bn;
     }
+}
+
+/* Contact cc of the step from candidate pair (i, j)'s manifold m: its
+ * anchors and base separations, the warm start from the matching old
+ * contact, the world's contact row and the head for prepare_contacts
+ * (08:140-170, b3_contact_from_mani 08:5-39).  Returns the CF_* flags. */
+B3D_FN int write_new_contact(const Lane& L, int cc, int i, int j, const PairShape& A, const PairShape& B,
+        const Mani& m, int sorted, int match, const OldWarm& orec, int old_n) {
+    NewContact nc;
+    nc.count = m.count;
+    nc.normal = m.normal;
+    nc.t1 = perp(m.normal);
+    nc.t2 = cross(nc.t1, m.normal);
+#pragma unroll
+    for (int p = 0; p < kMaxManifold; p++) {
+        if (p >= m.count) continue;
+        nc.r_a[p] = sub(m.p_a[p], A.center);
+        nc.r_b[p] = sub(m.p_b[p], B.center);
+        nc.base_sep[p] = m.sep[p] - dot(sub(nc.r_b[p], nc.r_a[p]), m.normal);
+        nc.feature[p] = m.feature[p];
+        nc.ni[p] = 0.0f;
+    }
+    nc.fi = V2{0.0f, 0.0f};
+    nc.twist = 0.0f;
+    nc.roll = zero3();
+    /* warm start from the previous step's cache: every matching old
+     * pair, the last one winning (08:154-170) */
+    if (sorted) {
+        if (match >= 0) warm_apply(orec, &nc);
+    } else {
+        for (int k = 0; k < old_n; k++) {
+            const uint32_t* o = old_rec(L, k);
+            if (ldi(o, O_SHAPE_A) == i && ldi(o, O_SHAPE_B) == j) {
+                OldWarm ow;
+                old_load(L, k, &ow);
+                warm_apply(ow, &nc);
+            }
+        }
+    }
+    uint32_t* w = L.w;
+    sti(w, cw(L, cc, C_SHAPE_A), i);
+    sti(w, cw(L, cc, C_SHAPE_B), j);
+    sti(w, cw(L, cc, C_BODY_A), A.body);
+    sti(w, cw(L, cc, C_BODY_B), B.body);
+    sti(w, cw(L, cc, C_POINT_COUNT), nc.count);
+    sti(w, cw(L, cc, C_STATIC), !((A.bflags & B.bflags) & kBodyDynamic));
+    st3(w, cw(L, cc, C_NORMAL), nc.normal);
+    st3(w, cw(L, cc, C_TANGENT1), nc.t1);
+    st3(w, cw(L, cc, C_TANGENT2), nc.t2);
+#pragma unroll
+    for (int p = 0; p < kMaxManifold; p++) {
+        if (p >= nc.count) continue;
+        st3(w, pw(L, cc, p, P_R_A), nc.r_a[p]);
+        st3(w, pw(L, cc, p, P_R_B), nc.r_b[p]);
+        stf(w, pw(L, cc, p, P_BASE_SEP), nc.base_sep[p]);
+        stf(w, pw(L, cc, p, P_NORMAL_IMPULSE), nc.ni[p]);
+        sti(w, pw(L, cc, p, P_FEATURE), (int)nc.feature[p]);
+    }
+    float restitution = A.restitution > B.restitution ? A.restitution : B.restitution;
+    float rolling = maxf(A.rolling, B.rolling);
+    stf(w, cw(L, cc, C_FRICTION), sqrtf(A.friction * B.friction));
+    stf(w, cw(L, cc, C_RESTITUTION), restitution);
+    stf(w, cw(L, cc, C_ROLLING), rolling);
+    int info = (A.bflags & kBodyDynamic ? CF_DYN_A : 0) | (B.bflags & kBodyDynamic ? CF_DYN_B : 0)
+        | (!((A.bflags & B.bflags) & kBodyDynamic) ? CF_STATIC : 0) | (restitution != 0.0f ? CF_RESTITUTION : 0)
+        | (!(rolling <= 0.0f) ? CF_ROLLING : 0);
+    uint32_t* hd = chead_rec(L, cc);
+    sti(hd, CH_AB, A.body | (B.body << 16));
+    sti(hd, CH_INFO, nc.count | (info << 8));
+    stf(w, cw(L, cc, C_TWIST_IMPULSE), nc.twist);
+    stf(w, cw(L, cc, C_FRICTION_IMPULSE), nc.fi.x);
+    stf(w, cw(L, cc, C_FRICTION_IMPULSE + 1), nc.fi.y);
+    st3(w, cw(L, cc, C_ROLLING_IMPULSE), nc.roll);
+    return info;
+}
+
+/* This wave's share of writing the new contacts: candidate t with a
+ * manifold becomes contact number (candidates below t with one), as the
+ * sequential append would number it; those past the capacity are dropped
+ * (the header is wave 0's). */
+B3D_FN void append_share(const Lane& L, const PairStage& S, int ncand, int old_n, int sorted) {
+    const uint32_t* cand = L.scr + L.g.scr_cand * kLanes;
+    const float* hit = hit_rows(L);
+    int acc = 0, word = 0, rest = 0;
+    for (int t = S.wave; t < ncand; t += S.waves) {
+        while (word < (t >> 5)) acc += __builtin_popcount(__builtin_bit_cast(uint32_t, hit[word++ * kLanes]));
+        uint32_t bits = __builtin_bit_cast(uint32_t, hit[(t >> 5) * kLanes]);
+        if (!((bits >> (t & 31)) & 1u)) continue;
+        int idx = acc + __builtin_popcount(bits & ((1u << (t & 31)) - 1u));
+        if (idx >= L.g.max_c) continue;
+        uint32_t key = ldu(cand, 2 * t);
+        int match = ldi(cand, 2 * t + 1);
+        int i = (int)(key >> 16), j = (int)(key & 0xffffu);
+        PairShape A, B;
+        pshape_load(L, i, &A);
+        pshape_load(L, j, &B);
+        OldWarm orec;
+        if (sorted && match >= 0) old_load(L, match, &orec);
+        Mani m;
+        mani_load(S, t, &m);
+        rest |= write_new_contact(L, idx, i, j, A, B, m, sorted, match, orec, old_n) & CF_RESTITUTION;
+    }
+    if (rest) lds_or(const_cast<float*>(hit) + hit_words(L.g) * kLanes, 1u);
 }
 
 /* A helper wave of a staged tile: waits for wave 0's candidate lists, runs
@@ -981,7 +1100,11 @@ B3D_FN void pair_helper(const Lane& L0, const PairStage& S) {
     B3D_BARRIER();
     int ncand = ldi(S.p, 0);
     int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
+    int old_n = clampi(ldi(L.w, H_CONTACT_COUNT), 0, L.g.max_c);
+    int sorted = __builtin_bit_cast(int, hit_rows(L)[(hit_words(L.g) + 1) * kLanes]);
     pair_share(L, S, ncand, nj);
+    B3D_BARRIER();
+    append_share(L, S, ncand, old_n, sorted);
     B3D_BARRIER();
 }
 
@@ -1018,12 +1141,27 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
         }
     }
     if (L.stage) {
-        /* the tile's waves split the narrowphase; wave 0 then appends the
-         * manifolds in candidate order as below */
-        sti(L.stage->p, 0, ncand);
+        /* the tile's waves split the narrowphase, then write the new
+         * contacts at the places the candidate order gives them */
+        const PairStage& S = *L.stage;
+        sti(S.p, 0, ncand);
+        float* hit = hit_rows(L);
+        for (int k = 0; k <= hit_words(g); k++) hit[k * kLanes] = 0.0f;
+        hit[(hit_words(g) + 1) * kLanes] = __builtin_bit_cast(float, sorted);
         B3D_BARRIER();
-        pair_share(L, *L.stage, ncand, nj);
+        pair_share(L, S, ncand, nj);
         B3D_BARRIER();
+        append_share(L, S, ncand, old_n, sorted);
+        B3D_BARRIER();
+        int total = 0;
+        for (int k = 0; k < hit_words(g); k++) total += __builtin_popcount(__builtin_bit_cast(uint32_t, hit[k * kLanes]));
+        int cc = total < g.max_c ? total : g.max_c;
+        int rest = __builtin_bit_cast(uint32_t, hit[hit_words(g) * kLanes]) != 0;
+        sti(L.w, H_CONTACT_COUNT, cc);
+        sti(L.w, H_CONTACT_OVERFLOW, ldi(L.w, H_CONTACT_OVERFLOW) | (total > g.max_c ? 1 : 0));
+        sti(L.w, H_CONTACTS_DROPPED, ldi(L.w, H_CONTACTS_DROPPED) + (total - cc));
+        sti(L.scr + L.g.scr_flags * kLanes, 0, rest ? kLaneRestitution : 0);
+        return;
     }
     int cc = 0;
     int rest_any = 0;
@@ -1073,72 +1211,7 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
             overflow = 1;
             dropped++;
         } else if (m.count > 0) {
-            NewContact nc;
-            nc.count = m.count;
-            nc.normal = m.normal;
-            nc.t1 = perp(m.normal);
-            nc.t2 = cross(nc.t1, m.normal);
-#pragma unroll
-            for (int p = 0; p < kMaxManifold; p++) {
-                if (p >= m.count) continue;
-                nc.r_a[p] = sub(m.p_a[p], A.center);
-                nc.r_b[p] = sub(m.p_b[p], B.center);
-                nc.base_sep[p] = m.sep[p] - dot(sub(nc.r_b[p], nc.r_a[p]), m.normal);
-                nc.feature[p] = m.feature[p];
-                nc.ni[p] = 0.0f;
-            }
-            nc.fi = V2{0.0f, 0.0f};
-            nc.twist = 0.0f;
-            nc.roll = zero3();
-            /* warm start from the previous step's cache: every matching old
-             * pair, the last one winning (08:154-170) */
-            if (sorted) {
-                if (match >= 0) warm_apply(orec, &nc);
-            } else {
-                for (int k = 0; k < old_n; k++) {
-                    const uint32_t* o = old_rec(L, k);
-                    if (ldi(o, O_SHAPE_A) == i && ldi(o, O_SHAPE_B) == j) {
-                        OldWarm ow;
-                        old_load(L, k, &ow);
-                        warm_apply(ow, &nc);
-                    }
-                }
-            }
-            uint32_t* w = L.w;
-            sti(w, cw(L, cc, C_SHAPE_A), i);
-            sti(w, cw(L, cc, C_SHAPE_B), j);
-            sti(w, cw(L, cc, C_BODY_A), A.body);
-            sti(w, cw(L, cc, C_BODY_B), B.body);
-            sti(w, cw(L, cc, C_POINT_COUNT), nc.count);
-            sti(w, cw(L, cc, C_STATIC), !((A.bflags & B.bflags) & kBodyDynamic));
-            st3(w, cw(L, cc, C_NORMAL), nc.normal);
-            st3(w, cw(L, cc, C_TANGENT1), nc.t1);
-            st3(w, cw(L, cc, C_TANGENT2), nc.t2);
-#pragma unroll
-            for (int p = 0; p < kMaxManifold; p++) {
-                if (p >= nc.count) continue;
-                st3(w, pw(L, cc, p, P_R_A), nc.r_a[p]);
-                st3(w, pw(L, cc, p, P_R_B), nc.r_b[p]);
-                stf(w, pw(L, cc, p, P_BASE_SEP), nc.base_sep[p]);
-                stf(w, pw(L, cc, p, P_NORMAL_IMPULSE), nc.ni[p]);
-                sti(w, pw(L, cc, p, P_FEATURE), (int)nc.feature[p]);
-            }
-            float restitution = A.restitution > B.restitution ? A.restitution : B.restitution;
-            float rolling = maxf(A.rolling, B.rolling);
-            stf(w, cw(L, cc, C_FRICTION), sqrtf(A.friction * B.friction));
-            stf(w, cw(L, cc, C_RESTITUTION), restitution);
-            stf(w, cw(L, cc, C_ROLLING), rolling);
-            int info = (A.bflags & kBodyDynamic ? CF_DYN_A : 0) | (B.bflags & kBodyDynamic ? CF_DYN_B : 0)
-                | (!((A.bflags & B.bflags) & kBodyDynamic) ? CF_STATIC : 0) | (restitution != 0.0f ? CF_RESTITUTION : 0)
-                | (!(rolling <= 0.0f) ? CF_ROLLING : 0);
-            rest_any |= info & CF_RESTITUTION;
-            uint32_t* hd = chead_rec(L, cc);
-            sti(hd, CH_AB, A.body | (B.body << 16));
-            sti(hd, CH_INFO, nc.count | (info << 8));
-            stf(w, cw(L, cc, C_TWIST_IMPULSE), nc.twist);
-            stf(w, cw(L, cc, C_FRICTION_IMPULSE), nc.fi.x);
-            stf(w, cw(L, cc, C_FRICTION_IMPULSE + 1), nc.fi.y);
-            st3(w, cw(L, cc, C_ROLLING_IMPULSE), nc.roll);
+            rest_any |= write_new_contact(L, cc, i, j, A, B, m, sorted, match, orec, old_n) & CF_RESTITUTION;
             cc++;
         }
         A = An;

@@ -112,6 +112,7 @@ void emu_step_shared(uint32_t* tiles, int count, unsigned long long sig, float d
     if (kClipWords + 6 * g.max_s + g.max_c > rows) rows = kClipWords + 6 * g.max_s + g.max_c;
     if (lds_rows(g) + sched_words(g) > rows) rows = lds_rows(g) + sched_words(g);
     std::vector<float> lds((size_t)rows * kLanes);
+    if (kClipWords + hit_words(g) + 2 > lds_rows(g)) return;
     size_t max_cand = (size_t)g.max_s * (size_t)(g.max_s - 1) / 2;
     size_t words = max_cand * kManiWords;
     if ((size_t)stage_sched_words(g) > words) words = (size_t)stage_sched_words(g);
