@@ -114,6 +114,7 @@ __global__ __launch_bounds__(64) void b3k_step(uint32_t* live, const uint32_t* s
  * pairs into the stage, then solve their share of each level of every
  * contact sweep.  Every wave sees the same stepping lanes and computes the
  * same level count, so all of them reach the same barriers or none does. */
+template <bool Masks>
 __global__ __launch_bounds__(64 * kTileWaves) void b3k_step_shared(uint32_t* live, const uint32_t* snap,
         uint32_t* scratch, uint32_t* stage, size_t stage_tile_words, Geometry g, int count, float dt, int substeps,
         const unsigned char* step_mask, const unsigned char* reset_mask, unsigned int opts) {
@@ -137,9 +138,9 @@ __global__ __launch_bounds__(64 * kTileWaves) void b3k_step_shared(uint32_t* liv
     Lane L = lane_view(live, scratch, lds, g, tile, lane, opts);
     L.stage = &S;
     if (wave == 0) {
-        step_world(L, dt, substeps);
+        step_world<Masks>(L, dt, substeps);
     } else {
-        pair_helper(L, S);
+        pair_helper<Masks>(L, S);
         sweep_helper(L, dt, substeps);
     }
 }
@@ -312,11 +313,12 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
         /* A batch of at most one tile per CU shares each tile's narrowphase
          * among kTileWaves waves (b3k_step_shared). */
         int cus = 0;
-        size_t shared_lds = lds + (size_t)(kTileWaves - 1) * kClipWords * kLanes * sizeof(float);
-        /* wave 0's shape bounds and old contact keys stay in LDS during
-         * candidate search (the helpers' clip rows, and the velocity rows,
-         * are only used after it) */
-        size_t bounds_lds = (size_t)(kClipWords + 6 * g.max_s + g.max_c) * kLanes * sizeof(float);
+        /* wave 0's rows and the helpers' clip rows, then the old contact
+         * keys, the overlap masks and the hit bits of the candidates */
+        size_t shared_lds = (size_t)shared_lds_words(g) * kLanes * sizeof(float);
+        /* wave 0's shape bounds stay in LDS until the overlap masks are
+         * built (the helpers' clip rows are only used after them) */
+        size_t bounds_lds = (size_t)(kClipWords + 6 * g.max_s) * kLanes * sizeof(float);
         if (bounds_lds > shared_lds) shared_lds = bounds_lds;
         /* and, past wave 0's rows, the contact levels of the shared sweeps */
         size_t sched_lds = (size_t)(lds_rows(g) + sched_words(g)) * kLanes * sizeof(float);
@@ -325,15 +327,19 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
             (void)b3_engine_destroy(e);
             return err;
         }
-        if (e->tiles <= cus && shared_lds <= 160u * 1024u && kClipWords + hit_words(g) + 2 <= lds_rows(g)) {
+        if (e->tiles <= cus && shared_lds <= 160u * 1024u) {
             size_t max_cand = (size_t)g.max_s * (size_t)(g.max_s - 1) / 2;
             size_t stage_words = max_cand * kManiWords;
             if ((size_t)stage_sched_words(g) > stage_words) stage_words = (size_t)stage_sched_words(g);
             e->stage_tile_words = (1 + stage_words) * kLanes;
             e->lds_shared_bytes = shared_lds;
+            e->shared_masks = shared_masks(g);
+            /* the attribute is per kernel and shared by every engine: set
+             * it to the most any launch takes */
             if (shared_lds > 64u * 1024u)
-                err = hipFuncSetAttribute((const void*)b3k_step_shared, hipFuncAttributeMaxDynamicSharedMemorySize,
-                    (int)shared_lds);
+                err = hipFuncSetAttribute(e->shared_masks ? (const void*)b3k_step_shared<true>
+                    : (const void*)b3k_step_shared<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                    (int)(160u * 1024u));
             if (err == hipSuccess)
                 err = hipMalloc((void**)&e->pair_stage, (size_t)e->tiles * e->stage_tile_words * sizeof(uint32_t));
             if (err != hipSuccess) {
@@ -444,8 +450,14 @@ hipError_t b3_batch_step_gpu(B3Engine* e, float dt, int substeps, const unsigned
     if (dt == 0.0f) return reset_mask ? b3_batch_restore_gpu(e, reset_mask, stream) : hipSuccess;
     if (e->options & B3_ENGINE_ART_CONTACTS) return b3i_step_art(e, dt, substeps, step_mask, reset_mask, stream);
     if (e->pair_stage && !(e->options & B3_ENGINE_ONE_WAVE_PER_TILE)) {
-        b3k_step_shared<<<e->tiles, 64 * kTileWaves, e->lds_shared_bytes, stream>>>(e->live, e->snap, e->scratch,
-            e->pair_stage, e->stage_tile_words, e->g, e->count, dt, substeps, step_mask, reset_mask, e->options);
+        if (e->shared_masks)
+            b3k_step_shared<true><<<e->tiles, 64 * kTileWaves, e->lds_shared_bytes, stream>>>(e->live, e->snap,
+                e->scratch, e->pair_stage, e->stage_tile_words, e->g, e->count, dt, substeps, step_mask, reset_mask,
+                e->options);
+        else
+            b3k_step_shared<false><<<e->tiles, 64 * kTileWaves, e->lds_shared_bytes, stream>>>(e->live, e->snap,
+                e->scratch, e->pair_stage, e->stage_tile_words, e->g, e->count, dt, substeps, step_mask, reset_mask,
+                e->options);
         return hipGetLastError();
     }
     b3k_step<<<e->tiles, 64, e->lds_bytes, stream>>>(e->live, e->snap, e->scratch, e->g, e->count, dt, substeps,

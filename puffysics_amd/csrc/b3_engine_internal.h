@@ -26,6 +26,7 @@ struct B3Engine {
     uint32_t* pair_stage;    /* small batches: the tile's waves share the narrowphase (b3d::PairStage) */
     size_t stage_tile_words;
     size_t lds_shared_bytes; /* LDS of a workgroup of kTileWaves waves */
+    bool shared_masks;       /* ... which also split the candidate search (b3d::shared_masks) */
 };
 
 /* Waves per tile when the narrowphase is shared. */

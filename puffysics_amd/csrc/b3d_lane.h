@@ -751,7 +751,18 @@ B3D_FN uint32_t shape_key(int i, int j) { return ((uint32_t)i << 16) | (uint32_t
  * keys, after wave 0's clip rows and shape bounds, for the candidate search
  * to merge against. */
 B3D_FN bool lds_old_keys(const Lane& L) { return L.stage && L.stage->lds_bounds; }
-B3D_FN float* old_key_rows(const Lane& L) { return L.vel + (kClipWords + 6 * L.g.max_s) * kLanes; }
+/* A shared tile's LDS, per lane: wave 0's rows (clip rows, then shape
+ * bounds, later velocities) and the helpers' clip rows, then, past both
+ * and past the shape bounds, the old contact keys, the bound-overlap masks
+ * of the shape pairs and the candidates' hit bits, which the waves use
+ * while colliding in their clip rows. */
+B3D_FN int shared_keys_word(const Geometry& g) {
+    int a = lds_rows(g) + 3 * kClipWords, b = kClipWords + 6 * g.max_s;
+    return a > b ? a : b;
+}
+B3D_FN int shared_masks_word(const Geometry& g) { return shared_keys_word(g) + g.max_c; }
+B3D_FN int shared_hits_word(const Geometry& g) { return shared_masks_word(g) + 2 * g.max_s; }
+B3D_FN float* old_key_rows(const Lane& L) { return L.vel + shared_keys_word(L.g) * kLanes; }
 B3D_FN uint32_t old_key(const Lane& L, int k) {
     if (lds_old_keys(L)) return __builtin_bit_cast(uint32_t, old_key_rows(L)[k * kLanes]);
     return ldu(old_rec(L, k), O_KEY);
@@ -943,11 +954,11 @@ B3D_FN bool pair_skipped(const Lane& L, const PairShape& A, const PairShape& B, 
 
 /* Which candidates of a shared tile produced a manifold: one bit per
  * candidate, then a restitution flag and whether the old contacts were
- * sorted, in wave 0's LDS rows past its clip rows (the shape bounds there
- * are dead once the candidates are listed; the helpers' clip rows start
- * past all of wave 0's rows). */
+ * sorted. */
 B3D_FN int hit_words(const Geometry& g) { return (g.max_s * (g.max_s - 1) / 2 + 31) / 32; }
-B3D_FN float* hit_rows(const Lane& L) { return L.vel + kClipWords * kLanes; }
+B3D_FN float* hit_rows(const Lane& L) { return L.vel + shared_hits_word(L.g) * kLanes; }
+/* Words of a shared tile's LDS per lane. */
+B3D_FN int shared_lds_words(const Geometry& g) { return shared_hits_word(g) + hit_words(g) + 2; }
 B3D_FN void lds_or(float* p, uint32_t bits) {
 #ifdef __HIP_DEVICE_COMPILE__
     atomicOr(reinterpret_cast<unsigned int*>(p), bits);
@@ -956,27 +967,102 @@ B3D_FN void lds_or(float* p, uint32_t bits) {
 #endif
 }
 
+/* Bound-overlap masks of a shared tile's shape pairs (bit j of row i:
+ * shapes i < j overlap; at most 64 shapes), rows i = wave, wave + waves. */
+B3D_FN uint64_t overlap_mask(const Lane& L, int i) {
+    const float* r = L.vel + (shared_masks_word(L.g) + 2 * i) * kLanes;
+    return (uint64_t)__builtin_bit_cast(uint32_t, r[0]) | ((uint64_t)__builtin_bit_cast(uint32_t, r[kLanes]) << 32);
+}
+B3D_FN void overlap_rows(const Lane& L, const float* bounds, int ns, const PairStage& S) {
+    for (int i = S.wave; i < ns; i += S.waves) {
+        const float* bi = bounds + i * 6 * kLanes;
+        uint64_t m = 0;
+        for (int j = i + 1; j < ns; j++)
+            if (overlaps(bi, bounds + j * 6 * kLanes)) m |= 1ull << j;
+        float* r = L.vel + (shared_masks_word(L.g) + 2 * i) * kLanes;
+        r[0] = __builtin_bit_cast(float, (uint32_t)m);
+        r[kLanes] = __builtin_bit_cast(float, (uint32_t)(m >> 32));
+    }
+}
+/* Candidate t of the masks in (i, j) order; row and acc (candidates in
+ * rows before it) carry the walk over increasing t. */
+B3D_FN void mask_candidate(const Lane& L, int t, int* row, int* acc, int* i, int* j) {
+    uint64_t m = overlap_mask(L, *row);
+    int c = __builtin_popcountll(m);
+    while (t >= *acc + c) {
+        *acc += c;
+        *row += 1;
+        m = overlap_mask(L, *row);
+        c = __builtin_popcountll(m);
+    }
+    for (int k = t - *acc; k > 0; k--) m &= m - 1;
+    *i = *row;
+    *j = __builtin_ctzll(m);
+}
+/* The old contact whose shape key equals key (the first at or past it in
+ * the sorted keys: the merge of the sequential search), or -1. */
+B3D_FN int old_match(const Lane& L, int old_n, uint32_t key) {
+    int lo = 0, hi = old_n;
+    while (lo < hi) {
+        int mid = (lo + hi) >> 1;
+        if (old_key(L, mid) < key) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo < old_n && old_key(L, lo) == key ? lo : -1;
+}
+
+/* Whether a shared tile's waves also split the candidate search through
+ * the overlap masks; with few shapes wave 0 lists the candidates alone,
+ * which costs less than the masks' extra barrier.  The shared launches are
+ * specialised on it (template argument Masks of step_world, find_pairs and
+ * pair_helper), as the masks' code costs the other variant registers. */
+constexpr int kMaskMinShapes = 12;
+B3D_FN bool shared_masks(const Geometry& g) { return g.max_s >= kMaskMinShapes && g.max_s <= 64; }
+B3D_FN int mask_candidates(const Lane& L, int ns) {
+    int n = 0;
+    for (int i = 0; i < ns; i++) n += __builtin_popcountll(overlap_mask(L, i));
+    return n;
+}
+/* Candidate t's shapes: from the masks (listing it, with its old-contact
+ * match, in the candidate rows), or from wave 0's list. */
+B3D_FN void share_candidate(const Lane& L, bool masks, int t, int* row, int* acc, int* i, int* j, int old_n,
+        int sorted) {
+    uint32_t* cand = L.scr + L.g.scr_cand * kLanes;
+    if (masks) {
+        mask_candidate(L, t, row, acc, i, j);
+        uint32_t key = shape_key(*i, *j);
+        sti(cand, 2 * t, (int)key);
+        sti(cand, 2 * t + 1, sorted ? old_match(L, old_n, key) : -1);
+    } else {
+        uint32_t key = ldu(cand, 2 * t);
+        *i = (int)(key >> 16);
+        *j = (int)(key & 0xffffu);
+    }
+}
+
 /* This wave's share of the tile's narrowphase: candidates t = wave, wave +
- * waves, ..., each manifold (empty when filtered) to the stage; the next
+ * waves, ..., each collided (empty when filtered) into the stage; the next
  * share's shapes are in flight during a collision. */
-B3D_FN void pair_share(const Lane& L, const PairStage& S, int ncand, int nj) {
-    const uint32_t* cand = L.scr + L.g.scr_cand * kLanes;
+B3D_FN void pair_share(const Lane& L, const PairStage& S, bool masks, int ncand, int nj, int old_n, int sorted) {
     uint32_t jkey[kJointKeyRegs];
 #pragma unroll
     for (int k = 0; k < kJointKeyRegs; k++) jkey[k] = k < nj ? ldu(joint_rec(L, k), JS_KEY) : 0xffffffffu;
+    int row = 0, acc = 0, i = 0, j = 0, in = 0, jn = 0;
     PairShape A, B, An, Bn;
     int t = S.wave;
     if (t < ncand) {
-        uint32_t key = ldu(cand, 2 * t);
-        pshape_load(L, (int)(key >> 16), &A);
-        pshape_load(L, (int)(key & 0xffffu), &B);
+        share_candidate(L, masks, t, &row, &acc, &i, &j, old_n, sorted);
+        pshape_load(L, i, &A);
+        pshape_load(L, j, &B);
+        An = A;
+        Bn = B;
     }
     for (; t < ncand; t += S.waves) {
         int tn = t + S.waves;
         if (tn < ncand) {
-            uint32_t kn = ldu(cand, 2 * tn);
-            pshape_load(L, (int)(kn >> 16), &An);
-            pshape_load(L, (int)(kn & 0xffffu), &Bn);
+            share_candidate(L, masks, tn, &row, &acc, &in, &jn, old_n, sorted);
+            pshape_load(L, in, &An);
+            pshape_load(L, jn, &Bn);
         }
         Mani m;
         m.count = 0;
@@ -985,6 +1071,8 @@ B3D_FN void pair_share(const Lane& L, const PairStage& S, int ncand, int nj) {
         if (m.count > 0) lds_or(hit_rows(L) + (t >> 5) * kLanes, 1u << (t & 31));
         A = An;
         B = Bn;
+        i = in;
+        j = jn;
     }
 }
 
@@ -1094,25 +1182,49 @@ B3D_FN void append_share(const Lane& L, const PairStage& S, int ncand, int old_n
 /* A helper wave of a staged tile: waits for wave 0's candidate lists, runs
  * its share of the narrowphase, and signals.  Runs in the tile's stepping
  * lanes, like wave 0, so its record slots are wave 0's. */
+template <bool Masks>
 B3D_FN void pair_helper(const Lane& L0, const PairStage& S) {
     Lane L = L0;
     L.sslot = wave_slot(L);
-    B3D_BARRIER();
-    int ncand = ldi(S.p, 0);
+    int ns = clampi(ldi(L.w, H_SHAPE_COUNT), 0, L.g.max_s);
     int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
     int old_n = clampi(ldi(L.w, H_CONTACT_COUNT), 0, L.g.max_c);
+    constexpr bool masks = Masks;
+    B3D_BARRIER();                 /* wave 0's shape bounds and old keys (or its candidates) */
+    int ncand;
+    if (masks) {
+        overlap_rows(L, L.vel + kClipWords * kLanes, ns, S);
+        B3D_BARRIER();             /* the overlap masks are complete */
+        ncand = mask_candidates(L, ns);
+    } else {
+        ncand = ldi(S.p, 0);
+    }
     int sorted = __builtin_bit_cast(int, hit_rows(L)[(hit_words(L.g) + 1) * kLanes]);
-    pair_share(L, S, ncand, nj);
-    B3D_BARRIER();
+    pair_share(L, S, masks, ncand, nj, old_n, sorted);
+    B3D_BARRIER();                 /* every manifold is staged */
     append_share(L, S, ncand, old_n, sorted);
-    B3D_BARRIER();
+    B3D_BARRIER();                 /* every new contact is written */
 }
 
+template <bool Masks>
 B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int old_n, int sorted) {
     const Geometry& g = L.g;
     uint32_t* cand = L.scr + g.scr_cand * kLanes;
     int ncand = 0;
-    {
+    bool masks = Masks && L.stage;
+    if (L.stage) {
+        float* hit = hit_rows(L);
+        for (int k = 0; k <= hit_words(g); k++) hit[k * kLanes] = 0.0f;
+        hit[(hit_words(g) + 1) * kLanes] = __builtin_bit_cast(float, sorted);
+    }
+    if (masks) {
+        /* the tile's waves test the bound pairs, then list the candidates
+         * in the same order as below */
+        B3D_BARRIER();
+        overlap_rows(L, bounds, ns, *L.stage);
+        B3D_BARRIER();
+        ncand = mask_candidates(L, ns);
+    } else {
         int op = 0;
         uint32_t okey = sorted && old_n > 0 ? old_key(L, 0) : 0xffffffffu;
         for (int i = 0; i < ns; i++) {
@@ -1139,17 +1251,17 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
                 }
             }
         }
+        if (L.stage) {
+            sti(L.stage->p, 0, ncand);
+            B3D_BARRIER();
+        }
     }
     if (L.stage) {
         /* the tile's waves split the narrowphase, then write the new
          * contacts at the places the candidate order gives them */
         const PairStage& S = *L.stage;
-        sti(S.p, 0, ncand);
-        float* hit = hit_rows(L);
-        for (int k = 0; k <= hit_words(g); k++) hit[k * kLanes] = 0.0f;
-        hit[(hit_words(g) + 1) * kLanes] = __builtin_bit_cast(float, sorted);
-        B3D_BARRIER();
-        pair_share(L, S, ncand, nj);
+        const float* hit = hit_rows(L);
+        pair_share(L, S, masks, ncand, nj, old_n, sorted);
         B3D_BARRIER();
         append_share(L, S, ncand, old_n, sorted);
         B3D_BARRIER();
@@ -1231,6 +1343,7 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
 
 /* Contact generation and warm start: b3_find_contacts (08_contacts.inl:
  * 64-173).  The prepared fields are filled in by prepare_contacts. */
+template <bool Masks = false>
 B3D_FN void find_contacts(const Lane& L) {
     const Geometry& g = L.g;
     int old_n = clampi(ldi(L.w, H_CONTACT_COUNT), 0, g.max_c);
@@ -1247,11 +1360,11 @@ B3D_FN void find_contacts(const Lane& L) {
     if (bounds_in_lds(g) || (L.stage && L.stage->lds_bounds)) {
         float* bounds = L.vel + kClipWords * kLanes;
         shape_pass(L, ns, bounds);
-        find_pairs(L, bounds, ns, nj, old_n, sorted);
+        find_pairs<Masks>(L, bounds, ns, nj, old_n, sorted);
     } else {
         float* bounds = (float*)(L.scr + g.scr_bounds * kLanes);
         shape_pass(L, ns, bounds);
-        find_pairs(L, bounds, ns, nj, old_n, sorted);
+        find_pairs<Masks>(L, bounds, ns, nj, old_n, sorted);
     }
 }
 
@@ -2881,7 +2994,7 @@ B3D_FN void integrate_velocities_law(const Lane& L, float h, const Law& law) {
  * the force law `law` in the B3_USER_FORCES hook.  Body velocities are
  * staged in the velocity rows after contact generation (which uses the
  * same rows for clip polygons) and written back at the end. */
-template <class Law>
+template <bool Masks = false, class Law>
 B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
     if (!(dt > 0.0f)) return;
     Lane L = L0;
@@ -2897,7 +3010,7 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
     float contact_speed = ldf(L.w, H_CONTACT_SPEED);
     float rest_threshold = ldf(L.w, H_RESTITUTION_THRESHOLD);
 
-    find_contacts(L);
+    find_contacts<Masks>(L);
     /* restitution runs in every lane of a wave where some world has it */
     const bool rest_wave = wave_any(L, (ldi(L.scr + L.g.scr_flags * kLanes, 0) & kLaneRestitution) != 0);
     vel_load(L);
@@ -2943,7 +3056,8 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
 }
 
 /* b3_step without a hook. */
-B3D_FN void step_world(const Lane& L, float dt, int substeps) { step_world(L, dt, substeps, NoForces()); }
+template <bool Masks = false>
+B3D_FN void step_world(const Lane& L, float dt, int substeps) { step_world<Masks>(L, dt, substeps, NoForces()); }
 
 /* A helper wave of a shared-narrowphase tile after its narrowphase share:
  * its share of the contact preparation, of the level-by-level warm start

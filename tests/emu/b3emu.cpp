@@ -108,11 +108,10 @@ void emu_step_shared(uint32_t* tiles, int count, unsigned long long sig, float d
     if (!geometry_of(sig, &g, &wb)) return;
     int ntiles = (count + kLanes - 1) / kLanes;
     std::vector<uint32_t> scratch((size_t)ntiles * g.tile_scr_words);
-    int rows = lds_rows(g) + 3 * kClipWords;
-    if (kClipWords + 6 * g.max_s + g.max_c > rows) rows = kClipWords + 6 * g.max_s + g.max_c;
+    int rows = shared_lds_words(g);
+    if (kClipWords + 6 * g.max_s > rows) rows = kClipWords + 6 * g.max_s;
     if (lds_rows(g) + sched_words(g) > rows) rows = lds_rows(g) + sched_words(g);
     std::vector<float> lds((size_t)rows * kLanes);
-    if (kClipWords + hit_words(g) + 2 > lds_rows(g)) return;
     size_t max_cand = (size_t)g.max_s * (size_t)(g.max_s - 1) / 2;
     size_t words = max_cand * kManiWords;
     if ((size_t)stage_sched_words(g) > words) words = (size_t)stage_sched_words(g);
@@ -128,7 +127,8 @@ void emu_step_shared(uint32_t* tiles, int count, unsigned long long sig, float d
         S.waves = 1;
         S.lds_bounds = 1;
         L.stage = &S;
-        step_world(L, dt, substeps);
+        if (shared_masks(g)) step_world<true>(L, dt, substeps);
+        else step_world<false>(L, dt, substeps);
     }
 }
 
