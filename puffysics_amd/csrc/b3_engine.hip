@@ -17,9 +17,11 @@
  *   b3k_step                   optional fused restore, then one b3_step per
  *                              selected lane; LDS holds the lane's clip
  *                              polygons, then its body velocities
- *   b3k_step_shared            the same for batches of at most one tile per
- *                              CU, with the narrowphase split over four
- *                              waves per tile
+ *   b3k_step_shared<Masks>     the same for batches of at most one tile per
+ *                              CU, with the narrowphase, the contact writes,
+ *                              preparation and contact sweeps split over
+ *                              four waves per tile (Masks: the candidate
+ *                              search too, for 12 shapes or more)
  *   b3k_apply                  dense force / torque / impulse inputs
  *   b3k_stats                  per-world B3StepStats
  */
@@ -110,9 +112,11 @@ __global__ __launch_bounds__(64) void b3k_step(uint32_t* live, const uint32_t* s
 /* The step with the narrowphase and the contact sweeps shared by
  * kTileWaves waves per tile (small batches, whose one wave per tile would
  * leave most CUs idle): wave 0 steps its lanes' worlds as b3k_step does;
- * the other waves wait for its candidate lists, collide their share of the
- * pairs into the stage, then solve their share of each level of every
- * contact sweep.  Every wave sees the same stepping lanes and computes the
+ * the other waves wait for its shape bounds (Masks: test their rows of the
+ * bound pairs, then list their share of the candidates) or its candidate
+ * lists, collide their share of the pairs into the stage, write their share
+ * of the new contacts, prepare their share of them, then solve their share
+ * of each level of every contact sweep.  Every wave sees the same stepping lanes and computes the
  * same level count, so all of them reach the same barriers or none does. */
 template <bool Masks>
 __global__ __launch_bounds__(64 * kTileWaves) void b3k_step_shared(uint32_t* live, const uint32_t* snap,
