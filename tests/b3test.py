@@ -94,10 +94,17 @@ class EmuBatch:
         self.snap = w.view(np.uint32).copy()   # snapshots stay plain B3World structs
         emu().emu_upload(w.ctypes.data, self.count, self.sc.sig, self.tiles.ctypes.data)
 
-    def run(self, t0, nsteps, seed=scenes.SEED, shared=False):
+    def run(self, t0, nsteps, seed=scenes.SEED, shared=False, masks=-1):
+        """`shared`: the shared-tile path with one wave per tile; `masks`
+        -1 picks its candidate search by shape capacity as the engine does,
+        0 / 1 force wave 0's list / the overlap masks."""
         e = emu()
-        step = e.emu_step_shared if shared else e.emu_step
-        step.argtypes = [_vp, _i, _ull, _f, _i, _vp]
+        if shared:
+            e.emu_step_shared.argtypes = [_vp, _i, _ull, _f, _i, _vp, _i]
+            step = lambda *a: e.emu_step_shared(*a, masks)
+        else:
+            step = e.emu_step
+            step.argtypes = [_vp, _i, _ull, _f, _i, _vp]
         for t in range(t0, t0 + nsteps):
             reset, stepm = scenes.masks(self.scene, self.count, t, seed)
             if reset.any():
@@ -538,12 +545,12 @@ class EmuSig:
         emu().emu_step(self.tiles.ctypes.data, self.count, self.sig, dt, substeps,
                        None if act is None else act.ctypes.data)
 
-    def step_shared(self, dt, substeps, active=None):
+    def step_shared(self, dt, substeps, active=None, masks=-1):
         lib = emu()
-        lib.emu_step_shared.argtypes = [_vp, _i, _ull, _f, _i, _vp]
+        lib.emu_step_shared.argtypes = [_vp, _i, _ull, _f, _i, _vp, _i]
         act = None if active is None else np.ascontiguousarray(active, np.uint8)
         lib.emu_step_shared(self.tiles.ctypes.data, self.count, self.sig, dt, substeps,
-                            None if act is None else act.ctypes.data)
+                            None if act is None else act.ctypes.data, masks)
 
     def step_gravity(self, dt, substeps, gravity, softening, masses=None, active=None):
         lib = emu()

@@ -102,7 +102,7 @@ void emu_step(uint32_t* tiles, int count, unsigned long long sig, float dt, int 
  * sweeps (with one wave, a level's contacts in level order rather than
  * contact order, which must not change any result). */
 void emu_step_shared(uint32_t* tiles, int count, unsigned long long sig, float dt, int substeps,
-        const unsigned char* step_mask) {
+        const unsigned char* step_mask, int masks) {
     Geometry g;
     size_t wb;
     if (!geometry_of(sig, &g, &wb)) return;
@@ -127,7 +127,7 @@ void emu_step_shared(uint32_t* tiles, int count, unsigned long long sig, float d
         S.waves = 1;
         S.lds_bounds = 1;
         L.stage = &S;
-        if (shared_masks(g)) step_world<true>(L, dt, substeps);
+        if (masks < 0 ? shared_masks(g) : (masks > 0 && g.max_s <= 64)) step_world<true>(L, dt, substeps);
         else step_world<false>(L, dt, substeps);
     }
 }

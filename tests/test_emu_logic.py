@@ -144,7 +144,24 @@ def test_shared_tile_path_on_the_host(scene, count, steps):
     assert len(bad) == 0, "%d differing words, first %s" % (len(bad), bad[:4].tolist())
 
 
-def test_shared_tile_path_on_the_host_feature_worlds():
+@pytest.mark.parametrize("scene,count,steps,masks", [(2, 70, 65, 1), (4, 66, 12, 0), (5, 130, 40, 0)])
+def test_shared_candidate_search_variants_on_the_host(scene, count, steps, masks):
+    """Both candidate searches of the shared path on the scenes where the
+    engine picks the other one: the overlap masks walked in (i, j) order
+    with a binary search for the old contacts (masks=1), and wave 0's
+    merged list (masks=0), each equal to the oracle word for word."""
+    worlds = scenes.build(scene, count)
+    initial = clone(worlds)
+    e = EmuBatch(scene, worlds)
+    e.run(0, steps, shared=True, masks=masks)
+    ref = clone(worlds)
+    oracle_run(scene, ref, initial, 0, steps)
+    bad = diff_words(e.worlds(), ref, scenes.SCENES[scene].sig)
+    assert len(bad) == 0, "%d differing words, first %s" % (len(bad), bad[:4].tolist())
+
+
+@pytest.mark.parametrize("masks", [-1, 0])
+def test_shared_tile_path_on_the_host_feature_worlds(masks):
     """The same on the coverage worlds (restitution, rolling, kinematic and
     locked bodies, welds and hinges)."""
     from b3test import EmuSig, feature_worlds, oracle_step_batch
@@ -154,6 +171,6 @@ def test_shared_tile_path_on_the_host_feature_worlds():
     emu_ = EmuSig(CUSTOM_SIG, worlds)
     for _ in range(15):
         oracle_step_batch(ref, CUSTOM_SIG, 1.0 / 60.0, 4)
-        emu_.step_shared(1.0 / 60.0, 4)
+        emu_.step_shared(1.0 / 60.0, 4, masks=masks)
     bad = diff_words(emu_.worlds(), ref, CUSTOM_SIG)
     assert len(bad) == 0, "%d differing words, first %s" % (len(bad), bad[:4].tolist())
