@@ -46,15 +46,9 @@ __global__ __launch_bounds__(64) void b3k_step_art(uint32_t* live, const uint32_
 /* The articulated steps' device memory and launch limits: called by
  * b3_engine_set_options when the option is first turned on. */
 hipError_t b3i_art_init(B3Engine* e) {
-    hipError_t err;
-    if (e->lds_bytes > 64u * 1024u) {
-        err = hipFuncSetAttribute((const void*)b3k_step_art<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-            (int)e->lds_bytes);
-        if (err != hipSuccess) return err;
-        err = hipFuncSetAttribute((const void*)b3k_step_art<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-            (int)e->lds_bytes);
-        if (err != hipSuccess) return err;
-    }
+    hipError_t err = b3i_lds_limit((const void*)b3k_step_art<false>);
+    if (err == hipSuccess) err = b3i_lds_limit((const void*)b3k_step_art<true>);
+    if (err != hipSuccess) return err;
     if (e->art_ws || e->tiles == 0) return hipSuccess;
     size_t bytes = (size_t)e->tiles * art_ws_words(e->g.max_b) * 64 * sizeof(float);
     return hipMalloc((void**)&e->art_ws, bytes);

@@ -116,8 +116,15 @@ __global__ __launch_bounds__(64) void b3k_step(uint32_t* live, const uint32_t* s
  * bound pairs, then list their share of the candidates) or its candidate
  * lists, collide their share of the pairs into the stage, write their share
  * of the new contacts, prepare their share of them, then solve their share
- * of each level of every contact sweep.  Every wave sees the same stepping lanes and computes the
- * same level count, so all of them reach the same barriers or none does. */
+ * of each level of every contact sweep.
+ * Barriers: every thread of the workgroup reaches every __syncthreads.  A
+ * tile with no stepping world returns as a whole (lane l of every wave
+ * holds world 64 tile + l, so the ballot is the same in every wave).
+ * Otherwise no thread returns: idle lanes (world past the batch or not in
+ * the step mask) run the same control flow with L.active false, their
+ * work skipped and their candidate and level counts zero; the barrier
+ * count (find_pairs' fixed barriers, then 1 + nlev per levelled pass, with
+ * nlev the tile's largest level count) is the same in every lane. */
 template <bool Masks>
 __global__ __launch_bounds__(64 * kTileWaves) void b3k_step_shared(uint32_t* live, const uint32_t* snap,
         uint32_t* scratch, uint32_t* stage, size_t stage_tile_words, Geometry g, int count, float dt, int substeps,
@@ -132,7 +139,6 @@ __global__ __launch_bounds__(64 * kTileWaves) void b3k_step_shared(uint32_t* liv
     int w = tile * 64 + lane;
     bool stepping = w < count && (!step_mask || step_mask[w]);
     if (!(dt > 0.0f) || __ballot(stepping) == 0) return;
-    if (!stepping) return;
     PairStage S;
     S.p = stage + (size_t)tile * stage_tile_words + lane;
     S.clip = (wave == 0 ? lds : lds + (size_t)lds_rows(g) * kLanes + (size_t)(wave - 1) * kClipWords * kLanes) + lane;
@@ -141,6 +147,7 @@ __global__ __launch_bounds__(64 * kTileWaves) void b3k_step_shared(uint32_t* liv
     S.lds_bounds = 1;
     Lane L = lane_view(live, scratch, lds, g, tile, lane, opts);
     L.stage = &S;
+    L.active = stepping;
     if (wave == 0) {
         step_world<Masks>(L, dt, substeps);
     } else {
@@ -274,7 +281,7 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
     if (!geometry_of(config_signature, &g, &world_bytes)) return hipErrorInvalidValue;
     if (!batch_valid(worlds, world_bytes)) return hipErrorInvalidValue;
     size_t lds = (size_t)lds_rows(g) * kLanes * sizeof(float);
-    if (lds > 160u * 1024u) return hipErrorInvalidValue;
+    if (lds > kCuLdsBytes) return hipErrorInvalidValue;
     for (int i = 0; i < worlds.count; i++) {
         const unsigned char* wp = (const unsigned char*)worlds.data + (size_t)i * worlds.stride + worlds.world_offset;
         if (!world_valid(wp, g)) return hipErrorInvalidValue;
@@ -293,14 +300,14 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
     e->world_bytes = world_bytes;
     e->tile_words = (size_t)g.world_words * 64;
     e->lds_bytes = lds;
-    if (lds > 64u * 1024u) {
-        err = hipFuncSetAttribute((const void*)b3k_step, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (err != hipSuccess) {
-            free(e);
-            return err;
-        }
+    err = b3i_lds_limit((const void*)b3k_step);
+    if (err == hipSuccess) err = b3i_lds_limit((const void*)b3k_step_shared<true>);
+    if (err == hipSuccess) err = b3i_lds_limit((const void*)b3k_step_shared<false>);
+    if (err != hipSuccess) {
+        free(e);
+        return err;
     }
-    err = b3i_forces_init(lds);
+    err = b3i_forces_init();
     if (err != hipSuccess) {
         free(e);
         return err;
@@ -331,21 +338,14 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
             (void)b3_engine_destroy(e);
             return err;
         }
-        if (e->tiles <= cus && shared_lds <= 160u * 1024u) {
+        if (e->tiles <= cus && shared_lds <= kCuLdsBytes) {
             size_t max_cand = (size_t)g.max_s * (size_t)(g.max_s - 1) / 2;
             size_t stage_words = max_cand * kManiWords;
             if ((size_t)stage_sched_words(g) > stage_words) stage_words = (size_t)stage_sched_words(g);
             e->stage_tile_words = (1 + stage_words) * kLanes;
             e->lds_shared_bytes = shared_lds;
             e->shared_masks = shared_masks(g);
-            /* the attribute is per kernel and shared by every engine: set
-             * it to the most any launch takes */
-            if (shared_lds > 64u * 1024u)
-                err = hipFuncSetAttribute(e->shared_masks ? (const void*)b3k_step_shared<true>
-                    : (const void*)b3k_step_shared<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                    (int)(160u * 1024u));
-            if (err == hipSuccess)
-                err = hipMalloc((void**)&e->pair_stage, (size_t)e->tiles * e->stage_tile_words * sizeof(uint32_t));
+            err = hipMalloc((void**)&e->pair_stage, (size_t)e->tiles * e->stage_tile_words * sizeof(uint32_t));
             if (err != hipSuccess) {
                 (void)b3_engine_destroy(e);
                 return err;

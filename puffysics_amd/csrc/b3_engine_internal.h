@@ -32,8 +32,17 @@ struct B3Engine {
 /* Waves per tile when the narrowphase is shared. */
 constexpr int kTileWaves = 4;
 
+/* A CU's LDS.  The dynamic-LDS limit of a kernel is one setting shared by
+ * every engine in the process, so the library raises it to this maximum
+ * (b3i_lds_limit) instead of one engine's size, which an engine created
+ * later with a smaller size would otherwise lower under an earlier one. */
+constexpr size_t kCuLdsBytes = 160u * 1024u;
+inline hipError_t b3i_lds_limit(const void* kernel) {
+    return hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kCuLdsBytes);
+}
+
 /* Set-up of the force-law kernels on the current device (b3_forces.hip). */
-hipError_t b3i_forces_init(size_t lds_bytes);
+hipError_t b3i_forces_init();
 /* The articulated-contact step (b3_art.hip): its workspace, then launches. */
 hipError_t b3i_art_init(B3Engine* e);
 hipError_t b3i_step_art(B3Engine* e, float dt, int substeps, const unsigned char* step_mask,

@@ -72,18 +72,12 @@ __global__ __launch_bounds__(64) void b3k_step_fluid(uint32_t* live, const uint3
 }  // namespace
 
 /* Set-up for the force-law kernels on the current device, called by
- * b3_engine_create: their dynamic LDS limit when the engine's velocity rows
- * need more than 64 KB, and the fluid law's sample table. */
-hipError_t b3i_forces_init(size_t lds_bytes) {
+ * b3_engine_create: their dynamic LDS limit (b3i_lds_limit) and the fluid
+ * law's sample table. */
+hipError_t b3i_forces_init() {
     hipError_t err;
-    if (lds_bytes > 64u * 1024u) {
-        if ((err = hipFuncSetAttribute((const void*)b3k_step_gravity, hipFuncAttributeMaxDynamicSharedMemorySize,
-                 (int)lds_bytes)) != hipSuccess)
-            return err;
-        if ((err = hipFuncSetAttribute((const void*)b3k_step_fluid, hipFuncAttributeMaxDynamicSharedMemorySize,
-                 (int)lds_bytes)) != hipSuccess)
-            return err;
-    }
+    if ((err = b3i_lds_limit((const void*)b3k_step_gravity)) != hipSuccess) return err;
+    if ((err = b3i_lds_limit((const void*)b3k_step_fluid)) != hipSuccess) return err;
     static float table[2 * kFluidTrig];
     fluid_trig_table(table);
     return hipMemcpyToSymbol(HIP_SYMBOL(g_fluid_trig), table, sizeof(table));

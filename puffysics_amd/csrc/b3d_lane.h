@@ -348,6 +348,9 @@ struct Lane {
                            the body, delta-pose and shape records */
     unsigned int opts;  /* kKeepSolverFields */
     const PairStage* stage;  /* non-null: the tile's waves share the narrowphase */
+    bool active;        /* the lane steps its world.  Only a shared tile
+                           (stage non-null) runs idle lanes: they go through
+                           every workgroup barrier with their work skipped */
     Geometry g;
 };
 
@@ -373,6 +376,7 @@ B3D_FN Lane lane_view(uint32_t* live, uint32_t* scratch, float* vel_rows, const 
     L.sq = scratch ? scratch + (size_t)tile * g.tile_scr_words + (size_t)g.scr_words * kLanes : nullptr;
     L.vel = vel_rows ? vel_rows + lane : nullptr;
     L.lane = lane;
+    L.active = true;
     L.g = g;
     return L;
 }
@@ -384,6 +388,18 @@ B3D_FN int wave_slot(const Lane& L) {
 #ifdef __HIP_DEVICE_COMPILE__
     (void)L;
     uint64_t m = __ballot(1);
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+#else
+    return L.lane;
+#endif
+}
+
+/* Rank of this lane among its wave's stepping lanes (L.active): the slot of
+ * the lane's body, delta-pose and shape records.  A shared tile computes
+ * it with its idle lanes executing too. */
+B3D_FN int wave_rank(const Lane& L) {
+#ifdef __HIP_DEVICE_COMPILE__
+    uint64_t m = __ballot(L.active);
     return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 #else
     return L.lane;
@@ -404,11 +420,14 @@ B3D_FN bool wave_any(const Lane& L, bool v) {
 #endif
 }
 
-/* Workgroup barrier (a no-op in a host build, where no stage is used). */
+/* Workgroup barrier.  A host build runs one lane at a time and only counts
+ * the barriers a lane passes (host_barriers), so a host test can check
+ * that stepping and idle lanes of a shared tile meet the same ones. */
 #ifdef __HIP_DEVICE_COMPILE__
 #define B3D_BARRIER() __syncthreads()
 #else
-#define B3D_BARRIER() ((void)0)
+inline int host_barriers = 0;
+#define B3D_BARRIER() ((void)++host_barriers)
 #endif
 
 /* Shape bounds stay in the LDS rows during contact generation when the
@@ -1180,15 +1199,16 @@ B3D_FN void append_share(const Lane& L, const PairStage& S, int ncand, int old_n
 }
 
 /* A helper wave of a staged tile: waits for wave 0's candidate lists, runs
- * its share of the narrowphase, and signals.  Runs in the tile's stepping
- * lanes, like wave 0, so its record slots are wave 0's. */
+ * its share of the narrowphase, and signals.  Runs in all lanes, like wave
+ * 0; its stepping lanes rank as wave 0's, so its record slots are wave
+ * 0's, and its idle lanes have no candidates. */
 template <bool Masks>
 B3D_FN void pair_helper(const Lane& L0, const PairStage& S) {
     Lane L = L0;
-    L.sslot = wave_slot(L);
-    int ns = clampi(ldi(L.w, H_SHAPE_COUNT), 0, L.g.max_s);
-    int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
-    int old_n = clampi(ldi(L.w, H_CONTACT_COUNT), 0, L.g.max_c);
+    L.sslot = wave_rank(L);
+    int ns = L.active ? clampi(ldi(L.w, H_SHAPE_COUNT), 0, L.g.max_s) : 0;
+    int nj = L.active ? clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j) : 0;
+    int old_n = L.active ? clampi(ldi(L.w, H_CONTACT_COUNT), 0, L.g.max_c) : 0;
     constexpr bool masks = Masks;
     B3D_BARRIER();                 /* wave 0's shape bounds and old keys (or its candidates) */
     int ncand;
@@ -1197,9 +1217,9 @@ B3D_FN void pair_helper(const Lane& L0, const PairStage& S) {
         B3D_BARRIER();             /* the overlap masks are complete */
         ncand = mask_candidates(L, ns);
     } else {
-        ncand = ldi(S.p, 0);
+        ncand = L.active ? ldi(S.p, 0) : 0;
     }
-    int sorted = __builtin_bit_cast(int, hit_rows(L)[(hit_words(L.g) + 1) * kLanes]);
+    int sorted = L.active ? __builtin_bit_cast(int, hit_rows(L)[(hit_words(L.g) + 1) * kLanes]) : 0;
     pair_share(L, S, masks, ncand, nj, old_n, sorted);
     B3D_BARRIER();                 /* every manifold is staged */
     append_share(L, S, ncand, old_n, sorted);
@@ -1265,6 +1285,7 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
         B3D_BARRIER();
         append_share(L, S, ncand, old_n, sorted);
         B3D_BARRIER();
+        if (!L.active) return;
         int total = 0;
         for (int k = 0; k < hit_words(g); k++) total += __builtin_popcount(__builtin_bit_cast(uint32_t, hit[k * kLanes]));
         int cc = total < g.max_c ? total : g.max_c;
@@ -1346,10 +1367,12 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
 template <bool Masks = false>
 B3D_FN void find_contacts(const Lane& L) {
     const Geometry& g = L.g;
-    int old_n = clampi(ldi(L.w, H_CONTACT_COUNT), 0, g.max_c);
-    int sorted = save_old(L, old_n);
-    int ns = clampi(ldi(L.w, H_SHAPE_COUNT), 0, g.max_s);
-    int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, g.max_j);
+    /* an idle lane of a shared tile has no old contacts, shapes or joints:
+     * it only meets the other waves at find_pairs' barriers */
+    int old_n = L.active ? clampi(ldi(L.w, H_CONTACT_COUNT), 0, g.max_c) : 0;
+    int sorted = L.active ? save_old(L, old_n) : 0;
+    int ns = L.active ? clampi(ldi(L.w, H_SHAPE_COUNT), 0, g.max_s) : 0;
+    int nj = L.active ? clampi(ldi(L.w, H_JOINT_COUNT), 0, g.max_j) : 0;
     /* joint-connected body pairs (08:95-108) as sorted-pair keys */
     for (int j = 0; j < nj; j++) {
         uint32_t key = 0xffffffffu;
@@ -2998,7 +3021,7 @@ template <bool Masks = false, class Law>
 B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
     if (!(dt > 0.0f)) return;
     Lane L = L0;
-    L.sslot = wave_slot(L);
+    L.sslot = wave_rank(L);
     int subs = substeps < 1 ? 1 : substeps;
     float h = dt / (float)subs;
     float inv_dt = 1.0f / dt;
@@ -3009,22 +3032,34 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
     Soft ss = make_soft(2.0f * hertz, 0.5f * damping, h);
     float contact_speed = ldf(L.w, H_CONTACT_SPEED);
     float rest_threshold = ldf(L.w, H_RESTITUTION_THRESHOLD);
+    /* Idle lanes (L.active false) run only in a shared tile, where every
+     * lane of the workgroup reaches every barrier: the barriers sit outside
+     * the `if (L.active)` blocks, in find_pairs and in the levelled warm
+     * start and sweeps, which an idle lane enters with no candidates and
+     * no contact levels. */
+    const bool act = L.active;
 
     find_contacts<Masks>(L);
     /* restitution runs in every lane of a wave where some world has it */
-    const bool rest_wave = wave_any(L, (ldi(L.scr + L.g.scr_flags * kLanes, 0) & kLaneRestitution) != 0);
-    vel_load(L);
-    body_prepass(L, h);
+    const bool rest_wave = wave_any(L, act && (ldi(L.scr + L.g.scr_flags * kLanes, 0) & kLaneRestitution) != 0);
+    if (act) {
+        vel_load(L);
+        body_prepass(L, h);
+    }
     int nlev = 0;
     if (L.stage) {
         /* the tile's waves prepare the contacts together; wave 0 levels
          * them; all warm-start them level by level (the helper waves meet
          * wave 0 at each barrier, sweep_helper) */
         B3D_BARRIER();
-        prepare_contacts(L, cs, ss);
+        if (act) prepare_contacts(L, cs, ss);
         B3D_BARRIER();
-        sched_build(L);
-        prepare_joints(L, h);
+        if (act) {
+            sched_build(L);
+            prepare_joints(L, h);
+        } else {
+            sch_set(L, 0, 0);      /* no contact levels */
+        }
         B3D_BARRIER();
         nlev = tile_levels(L);
         warm_contacts_leveled(L, nlev);
@@ -3033,26 +3068,36 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
         prepare_joints(L, h);
         if (wave_any(L, !warm_done)) warm_start_contacts(L, warm_done);
     }
-    warm_start_joints(L);
-    joint_geometry(L);   /* the contacts' initial separations come from prepare_contacts */
+    if (act) {
+        warm_start_joints(L);
+        joint_geometry(L);   /* the contacts' initial separations come from prepare_contacts */
+    }
     for (int s = 0; s < subs; s++) {
-        if constexpr (Law::kActive)
-            integrate_velocities_law(L, h, law);
-        else
-            integrate_velocities(L);
+        if (act) {
+            if constexpr (Law::kActive)
+                integrate_velocities_law(L, h, law);
+            else
+                integrate_velocities(L);
+        }
         if (L.stage) solve_contacts_leveled(L, inv_h, contact_speed, 1, cs, ss, nlev);
         else solve_contacts(L, inv_h, contact_speed, 1, cs, ss);
-        solve_joints(L, h, inv_h, 1);
-        integrate_positions(L, h, inv_dt);
-        delta_geometry(L);
+        if (act) {
+            solve_joints(L, h, inv_h, 1);
+            integrate_positions(L, h, inv_dt);
+            delta_geometry(L);
+        }
         if (L.stage) solve_contacts_leveled(L, inv_h, contact_speed, 0, cs, ss, nlev);
         else solve_contacts(L, inv_h, contact_speed, 0, cs, ss);
-        solve_joints(L, h, inv_h, 0);
-        if (rest_wave) apply_restitution(L, rest_threshold);
+        if (act) {
+            solve_joints(L, h, inv_h, 0);
+            if (rest_wave) apply_restitution(L, rest_threshold);
+        }
     }
-    contact_writeback(L);
-    finalize(L);
-    vel_store(L);
+    if (act) {
+        contact_writeback(L);
+        finalize(L);
+        vel_store(L);
+    }
 }
 
 /* b3_step without a hook. */
@@ -3062,11 +3107,12 @@ B3D_FN void step_world(const Lane& L, float dt, int substeps) { step_world<Masks
 /* A helper wave of a shared-narrowphase tile after its narrowphase share:
  * its share of the contact preparation, of the level-by-level warm start
  * and of every contact sweep, in step with wave 0 (the same barriers, in
- * the same order, as step_world's shared path).  Runs in the tile's
- * stepping lanes, so its body and delta record slots are wave 0's. */
+ * the same order, as step_world's shared path).  Runs in all lanes; its
+ * stepping lanes rank as wave 0's, so its body and delta record slots are
+ * wave 0's, and its idle lanes have no contact levels (wave 0 set them). */
 B3D_FN void sweep_helper(const Lane& L0, float dt, int substeps) {
     Lane L = L0;
-    L.sslot = wave_slot(L);
+    L.sslot = wave_rank(L);
     int subs = substeps < 1 ? 1 : substeps;
     float h = dt / (float)subs;
     float inv_dt = 1.0f / dt;
@@ -3077,7 +3123,7 @@ B3D_FN void sweep_helper(const Lane& L0, float dt, int substeps) {
     Soft ss = make_soft(2.0f * hertz, 0.5f * damping, h);
     float contact_speed = ldf(L.w, H_CONTACT_SPEED);
     B3D_BARRIER();                 /* wave 0 has staged velocities and body records */
-    prepare_contacts(L, cs, ss);
+    if (L.active) prepare_contacts(L, cs, ss);
     B3D_BARRIER();                 /* all contacts prepared */
     B3D_BARRIER();                 /* wave 0 has levelled them */
     int nlev = tile_levels(L);

@@ -109,9 +109,121 @@ B3D_FN void axes(Q q, V3* x, V3* y, V3* z) {
     *y = rot(q, v3(0.0f, 1.0f, 0.0f));
     *z = rot(q, v3(0.0f, 0.0f, 1.0f));
 }
-/* Angle of the twist about local Z (03_math.inl:293-309, libm atan2f). */
+/* ---- atan2f with the host C library's bits ----
+ *
+ * The reference's twist calls libm atan2f (03_math.inl:305-306); its CPU
+ * path runs glibc 2.35, whose float atan2 is Sun's fdlibm method (fdlibm
+ * 5.3, e_atan2.c and s_atan.c) in the single-precision form by Ian Lance
+ * Taylor (Cygnus Support) that newlib and glibc carry:
+ *   atan(x): reduce |x| to t on one of five intervals, with breakpoints at
+ *   7/16, 11/16, 19/16 and 39/16 and the reductions t = x,
+ *   (2x-1)/(2+x), (x-1)/(x+1), (x-1.5)/(1+1.5x) and -1/x, which are
+ *   exact shifts by atan(0), atan(1/2), atan(1), atan(3/2) and atan(inf);
+ *   then atan(t) = t - t (s1 + s2), an 11-term odd polynomial in t^2
+ *   split into even and odd powers of t^4; the shift is added as a
+ *   hi + lo pair.
+ *   atan2(y, x): IEEE special cases, then atan(|y/x|) with |y/x| rounded
+ *   once, signed and moved to the quadrant of (x, y) with pi as hi + lo.
+ * The constants are that source's single-precision decimals, as a C
+ * compiler rounds them (the first coefficient's decimal 3.3333334327e-01
+ * is 0x3eaaaaab).  Every operation is a single fp32 add, multiply or
+ * correctly rounded divide in the source's order, and nothing is
+ * contracted (-ffp-contract=off), so device and host give the same bits.
+ * This was checked against glibc's atanf on all 2^32 inputs and against
+ * its atan2f on 5e9 sampled pairs, edge values included.  The host-side
+ * test is in tests/test_atan2.py; the device test in
+ * tests/test_gpu_atan2.py. */
+B3D_FN uint32_t fbits_(float f) { return __builtin_bit_cast(uint32_t, f); }
+B3D_FN float fd_atanf(float x) {
+    const int32_t hx = (int32_t)fbits_(x);
+    const int32_t ix = hx & 0x7fffffff;
+    if (ix >= 0x4c000000) {                         /* |x| >= 2^25, or NaN */
+        if (ix > 0x7f800000) return x + x;
+        const float r = 0x1.921fb4p+0f + 0x1.4442d0p-24f;   /* atan(inf) hi + lo */
+        return hx > 0 ? r : -0x1.921fb4p+0f - 0x1.4442d0p-24f;
+    }
+    int id;
+    float hi = 0.0f, lo = 0.0f;
+    if (ix < 0x3ee00000) {                          /* |x| < 7/16 */
+        if (ix < 0x31000000) return x;              /* |x| < 2^-29 */
+        id = -1;
+    } else {
+        x = fabsf(x);
+        if (ix < 0x3f980000) {                      /* |x| < 19/16 */
+            if (ix < 0x3f300000) {                  /* |x| < 11/16 */
+                id = 0; x = (2.0f * x - 1.0f) / (2.0f + x);
+                hi = 0x1.dac670p-2f; lo = 0x1.586ed2p-28f;      /* atan(1/2) */
+            } else {
+                id = 1; x = (x - 1.0f) / (x + 1.0f);
+                hi = 0x1.921fb4p-1f; lo = 0x1.4442d0p-25f;      /* atan(1) */
+            }
+        } else {
+            if (ix < 0x401c0000) {                  /* |x| < 39/16 */
+                id = 2; x = (x - 1.5f) / (1.0f + 1.5f * x);
+                hi = 0x1.f730bcp-1f; lo = 0x1.281f68p-25f;      /* atan(3/2) */
+            } else {
+                id = 3; x = -1.0f / x;
+                hi = 0x1.921fb4p+0f; lo = 0x1.4442d0p-24f;      /* atan(inf) */
+            }
+        }
+    }
+    const float z = x * x;
+    const float w = z * z;
+    const float s1 = z * (0x1.555556p-2f + w * (0x1.24924ap-3f + w * (0x1.745cdcp-4f
+        + w * (0x1.10d66ap-4f + w * (0x1.97b4b2p-5f + w * 0x1.0ad3aep-6f)))));
+    const float s2 = w * (-0x1.99999ap-3f + w * (-0x1.c71c70p-4f + w * (-0x1.3b0f2ap-4f
+        + w * (-0x1.dde2d6p-5f + w * -0x1.2b4442p-5f))));
+    if (id < 0) return x - x * (s1 + s2);
+    const float r = hi - ((x * (s1 + s2) - lo) - x);
+    return hx < 0 ? -r : r;
+}
+B3D_FN float fd_atan2f(float y, float x) {
+    const float pi_o_4 = 0x1.921fb6p-1f, pi_o_2 = 0x1.921fb6p+0f;
+    const float pi = 0x1.921fb6p+1f, pi_lo = -0x1.777a5cp-24f, tiny = 1.0e-30f;
+    const int32_t hx = (int32_t)fbits_(x), ix = hx & 0x7fffffff;
+    const int32_t hy = (int32_t)fbits_(y), iy = hy & 0x7fffffff;
+    if (ix > 0x7f800000 || iy > 0x7f800000) return x + y;      /* NaN */
+    if (hx == 0x3f800000) return fd_atanf(y);                   /* x == 1 */
+    const int m = ((hy >> 31) & 1) | ((hx >> 30) & 2);          /* 2 sign(x) + sign(y) */
+    if (iy == 0) {
+        if (m < 2) return y;
+        return m == 2 ? pi + tiny : -pi - tiny;
+    }
+    if (ix == 0) return hy < 0 ? -pi_o_2 - tiny : pi_o_2 + tiny;
+    if (ix == 0x7f800000) {
+        if (iy == 0x7f800000) {
+            switch (m) {
+            case 0: return pi_o_4 + tiny;
+            case 1: return -pi_o_4 - tiny;
+            case 2: return 3.0f * pi_o_4 + tiny;
+            default: return -3.0f * pi_o_4 - tiny;
+            }
+        }
+        switch (m) {
+        case 0: return 0.0f;
+        case 1: return -0.0f;
+        case 2: return pi + tiny;
+        default: return -pi - tiny;
+        }
+    }
+    if (iy == 0x7f800000) return hy < 0 ? -pi_o_2 - tiny : pi_o_2 + tiny;
+    const int32_t k = (iy - ix) >> 23;
+    float z;
+    if (k > 60) z = pi_o_2 + 0.5f * pi_lo;                      /* |y/x| > 2^60 */
+    else if (hx < 0 && k < -60) z = 0.0f;
+    else z = fd_atanf(fabsf(y / x));
+    switch (m) {
+    case 0: return z;
+    case 1: return -z;
+    case 2: return pi - (z - pi_lo);
+    default: return (z - pi_lo) - pi;
+    }
+}
+
+/* Angle of the twist about local Z (03_math.inl:293-309), with the host
+ * library's atan2f bits (fd_atan2f above). */
 B3D_FN float twist(Q q) {
-    float t = q.s < 0.0f ? atan2f(-q.v.z, -q.s) : atan2f(q.v.z, q.s);
+    float t = q.s < 0.0f ? fd_atan2f(-q.v.z, -q.s) : fd_atan2f(q.v.z, q.s);
     return 2.0f * t;
 }
 /* Hinge perpendicular rows 0.5 R(qa) (e s + rel.v x e), e = x, y (03_math.inl:311-319). */

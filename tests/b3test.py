@@ -95,11 +95,18 @@ class EmuBatch:
         emu().emu_upload(w.ctypes.data, self.count, self.sc.sig, self.tiles.ctypes.data)
 
     def run(self, t0, nsteps, seed=scenes.SEED, shared=False, masks=-1):
-        """`shared`: the shared-tile path with one wave per tile; `masks`
-        -1 picks its candidate search by shape capacity as the engine does,
-        0 / 1 force wave 0's list / the overlap masks."""
+        """`shared`: the shared-tile path with one wave per tile ("idle":
+        with the idle lanes run too, checking every lane's barrier count);
+        `masks` -1 picks its candidate search by shape capacity as the
+        engine does, 0 / 1 force wave 0's list / the overlap masks."""
         e = emu()
-        if shared:
+        if shared == "idle":
+            e.emu_step_shared_idle.argtypes = [_vp, _i, _ull, _f, _i, _vp, _i]
+
+            def step(*a):
+                rc = e.emu_step_shared_idle(*a, masks)
+                assert rc == 0, "world %d passed other barriers than a lane of its levels" % (-1 - rc)
+        elif shared:
             e.emu_step_shared.argtypes = [_vp, _i, _ull, _f, _i, _vp, _i]
             step = lambda *a: e.emu_step_shared(*a, masks)
         else:
@@ -644,3 +651,17 @@ def hover_ref_lib():
     """oracle/_ref/libhover_ref.so (the reference's hover task), or None."""
     path = os.path.join(ROOT, "oracle", "_ref", "libhover_ref.so")
     return C.CDLL(path) if os.path.exists(path) else None
+
+
+def gpu_run(eng, scene, t0, nsteps, seed=scenes.SEED):
+    """The workload loop on the device: masks, restore, inputs, step."""
+    import torch
+    sc = scenes.SCENES[scene]
+    reset = torch.zeros(eng.count, dtype=torch.uint8, device="cuda")
+    stepm = torch.zeros(eng.count, dtype=torch.uint8, device="cuda")
+    for t in range(t0, t0 + nsteps):
+        eng.scene_masks(scene, seed, t, reset, stepm)
+        eng.restore(reset)
+        eng.scene_inputs(scene, seed, t, stepm)
+        eng.step(sc.dt, sc.substeps, stepm)
+    torch.cuda.synchronize()

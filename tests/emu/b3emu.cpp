@@ -132,6 +132,63 @@ void emu_step_shared(uint32_t* tiles, int count, unsigned long long sig, float d
     }
 }
 
+/* The shared-tile path with its idle lanes (worlds not in step_mask) run
+ * too, as the device runs them: as wave 0 (step_world) and as a helper wave
+ * (pair_helper, sweep_helper) with L.active false.  Returns 0 when every
+ * lane passed the barriers a lane with its level count passes (find_pairs'
+ * 3 or 4, step_world's 3, then 1 + levels per levelled pass: the warm start
+ * and two sweeps per substep), and an idle lane's own count equals a
+ * helper's; otherwise -1 - the first world that did not.  Idle lanes have
+ * no levels, so on the device, where every lane passes 1 + the tile's
+ * largest level count per pass, all lanes meet the same barriers. */
+int emu_step_shared_idle(uint32_t* tiles, int count, unsigned long long sig, float dt, int substeps,
+        const unsigned char* step_mask, int masks) {
+    Geometry g;
+    size_t wb;
+    if (!geometry_of(sig, &g, &wb)) return -1;
+    int ntiles = (count + kLanes - 1) / kLanes;
+    std::vector<uint32_t> scratch((size_t)ntiles * g.tile_scr_words);
+    int rows = shared_lds_words(g);
+    if (kClipWords + 6 * g.max_s > rows) rows = kClipWords + 6 * g.max_s;
+    if (lds_rows(g) + sched_words(g) > rows) rows = lds_rows(g) + sched_words(g);
+    std::vector<float> lds((size_t)rows * kLanes);
+    size_t max_cand = (size_t)g.max_s * (size_t)(g.max_s - 1) / 2;
+    size_t words = max_cand * kManiWords;
+    if ((size_t)stage_sched_words(g) > words) words = (size_t)stage_sched_words(g);
+    size_t stage_tile = (1 + words) * kLanes;
+    std::vector<uint32_t> stage((size_t)ntiles * stage_tile);
+    bool use_masks = masks < 0 ? shared_masks(g) : (masks > 0 && g.max_s <= 64);
+    int subs = substeps < 1 ? 1 : substeps;
+    int fixed = (use_masks ? 4 : 3) + 3, passes = 1 + 2 * subs;
+    for (int w = 0; w < count; w++) {
+        bool active = !step_mask || step_mask[w];
+        Lane L = lane_of(tiles, scratch.data(), lds.data(), g, w);
+        PairStage S;
+        S.p = stage.data() + (size_t)(w / kLanes) * stage_tile + w % kLanes;
+        S.clip = lds.data() + w % kLanes;
+        S.wave = 0;
+        S.waves = 1;
+        S.lds_bounds = 1;
+        L.stage = &S;
+        L.active = active;
+        host_barriers = 0;
+        if (use_masks) step_world<true>(L, dt, substeps);
+        else step_world<false>(L, dt, substeps);
+        int levels = active ? sch_get(L, 0) : 0;
+        if (host_barriers != fixed + passes * (1 + levels)) return -1 - w;
+        if (!active) {
+            host_barriers = 0;
+            S.wave = 1;
+            S.waves = 2;
+            if (use_masks) pair_helper<true>(L, S);
+            else pair_helper<false>(L, S);
+            sweep_helper(L, dt, substeps);
+            if (host_barriers != fixed + passes) return -1 - w;
+        }
+    }
+    return 0;
+}
+
 /* emu_step with pairwise gravity in the force hook; `masses` is NULL or
  * count * max_bodies floats. */
 void emu_step_gravity(uint32_t* tiles, int count, unsigned long long sig, float dt, int substeps,
@@ -222,6 +279,72 @@ void emu_inputs(uint32_t* tiles, int count, unsigned long long sig, int scene, u
         Lane L = lane_of(tiles, nullptr, nullptr, g, w);
         scene_inputs(L, scene, seed, w, step);
     }
+}
+
+}  // extern "C"
+
+/* ---- atan2f: the engine's fd_atan2f against this host's libm ---- */
+#include <thread>
+
+extern "C" {
+
+/* Host libm atan2f over arrays (the values the reference's CPU path gets). */
+void emu_libm_atan2f(const float* y, const float* x, float* out, long n) {
+    for (long i = 0; i < n; i++) out[i] = atan2f(y[i], x[i]);
+}
+
+/* The engine's fd_atan2f over arrays, built for the host. */
+void emu_fd_atan2f(const float* y, const float* x, float* out, long n) {
+    for (long i = 0; i < n; i++) out[i] = fd_atan2f(y[i], x[i]);
+}
+
+static uint64_t emu_mix(uint64_t z) {
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+static float emu_f(uint32_t u) { return __builtin_bit_cast(float, u); }
+static bool emu_same(float a, float b) {
+    return __builtin_bit_cast(uint32_t, a) == __builtin_bit_cast(uint32_t, b) || (a != a && b != b);
+}
+
+/* Counts inputs where fd_atanf (mode 0: every float with bits in [lo, hi))
+ * or fd_atan2f (mode 1: n pairs from the twist's domain, x in [0, 1] and
+ * y in [-1, 1] with uniform bit patterns; mode 2: n pairs of arbitrary bit
+ * patterns) differs from libm, on `threads` threads. */
+unsigned long long emu_atan_mismatches(int mode, unsigned long long lo, unsigned long long hi,
+        unsigned long long seed, int threads) {
+    std::vector<unsigned long long> bad(threads, 0);
+    std::vector<std::thread> pool;
+    for (int t = 0; t < threads; t++) {
+        pool.emplace_back([&, t]() {
+            unsigned long long a = lo + (hi - lo) * t / threads, b = lo + (hi - lo) * (t + 1) / threads;
+            for (unsigned long long i = a; i < b; i++) {
+                if (mode == 0) {
+                    float x = emu_f((uint32_t)i);
+                    bad[t] += !emu_same(atanf(x), fd_atanf(x));
+                    continue;
+                }
+                uint64_t r = emu_mix(i ^ (seed << 40));
+                float x, y;
+                if (mode == 1) {
+                    x = emu_f((uint32_t)(r % 0x3f800001u));
+                    y = emu_f((uint32_t)((r >> 32) % 0x3f800001u) | ((uint32_t)(r >> 31) & 1u) << 31);
+                } else {
+                    x = emu_f((uint32_t)r);
+                    y = emu_f((uint32_t)(r >> 32));
+                }
+                bad[t] += !emu_same(atan2f(y, x), fd_atan2f(y, x));
+            }
+        });
+    }
+    unsigned long long total = 0;
+    for (int t = 0; t < threads; t++) {
+        pool[t].join();
+        total += bad[t];
+    }
+    return total;
 }
 
 }  // extern "C"

@@ -144,6 +144,24 @@ def test_shared_tile_path_on_the_host(scene, count, steps):
     assert len(bad) == 0, "%d differing words, first %s" % (len(bad), bad[:4].tolist())
 
 
+@pytest.mark.parametrize("scene,count,steps,masks", [(1, 70, 30, -1), (2, 70, 30, 1), (3, 70, 20, -1),
+                                                     (4, 66, 8, -1), (5, 130, 25, -1), (5, 130, 25, 0)])
+def test_shared_tile_idle_lanes_on_the_host(scene, count, steps, masks):
+    """Idle lanes of a shared tile (worlds past the batch's end or outside
+    the step mask) run the shared path with their work skipped, as wave 0
+    and as a helper wave: they change no word of their worlds (the oracle
+    leaves them alone too) and pass the barriers of a lane with no contact
+    levels, while each stepping lane passes those of its own levels."""
+    worlds = scenes.build(scene, count)
+    initial = clone(worlds)
+    e = EmuBatch(scene, worlds)
+    e.run(0, steps, shared="idle", masks=masks)
+    ref = clone(worlds)
+    oracle_run(scene, ref, initial, 0, steps)
+    bad = diff_words(e.worlds(), ref, scenes.SCENES[scene].sig)
+    assert len(bad) == 0, "%d differing words, first %s" % (len(bad), bad[:4].tolist())
+
+
 @pytest.mark.parametrize("scene,count,steps,masks", [(2, 70, 65, 1), (4, 66, 12, 0), (5, 130, 40, 0)])
 def test_shared_candidate_search_variants_on_the_host(scene, count, steps, masks):
     """Both candidate searches of the shared path on the scenes where the

@@ -1,0 +1,107 @@
+"""Boundary behaviour of the device engine beyond single-scene parity:
+  - the step, restore and scene inputs captured into a HIP graph replay
+    bit-identically to the same calls made eagerly ("enqueues on stream
+    without allocation or synchronization; safe in capture",
+    b3_batch.cuh:77-80);
+  - a kernel's dynamic-LDS limit, one setting shared by every engine in the
+    process, is not lowered by an engine created later;
+  - idle lanes of a shared tile (worlds outside the step mask, or past the
+    end of the batch) stay untouched while the tile's other worlds step.
+"""
+import numpy as np
+import pytest
+
+from b3test import clone, diff_words, gpu_run, oracle_run
+from puffysics_amd import scenes
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+def _engine(worlds, scene, options=1):
+    from puffysics_amd.engine import B3Engine
+    eng = B3Engine(worlds, scenes.SCENES[scene].sig)
+    eng.set_options(options)
+    return eng
+
+
+def _vector_step(eng, scene, t, reset, stepm):
+    sc = scenes.SCENES[scene]
+    eng.scene_masks(scene, scenes.SEED, t, reset, stepm)
+    eng.scene_inputs(scene, scenes.SEED, t, stepm)
+    eng.step(sc.dt, sc.substeps, stepm, reset)
+
+
+@pytest.mark.parametrize("scene,count", [(5, 4096), (5, 300), (4, 130)])
+def test_graph_replay_equals_eager(scene, count):
+    """Masks, inputs and the fused restore + step of one vector step are
+    captured once; each replay is checked against the same calls made
+    eagerly on a twin engine, with downloads (eager work and
+    synchronisation) between replays.  4,096 arm worlds take the one-wave
+    kernel, 300 and the bin the shared-tile kernel."""
+    sc = scenes.SCENES[scene]
+    worlds = scenes.build(scene, count)
+    graphed, eager = _engine(worlds, scene), _engine(worlds, scene)
+    reset_g = torch.zeros(count, dtype=torch.uint8, device="cuda")
+    stepm_g = torch.zeros(count, dtype=torch.uint8, device="cuda")
+    reset_e = torch.zeros_like(reset_g)
+    stepm_e = torch.zeros_like(stepm_g)
+    t = 7                                  # a step whose masks reset some worlds
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _vector_step(graphed, scene, t, reset_g, stepm_g)
+    torch.cuda.synchronize()
+    assert len(diff_words(graphed.download(), worlds, sc.sig)) == 0   # capture ran nothing
+    for r in range(4):
+        graph.replay()
+        _vector_step(eager, scene, t, reset_e, stepm_e)
+        torch.cuda.synchronize()
+        a, b = graphed.download(), eager.download()
+        bad = diff_words(a, b, sc.sig)
+        assert len(bad) == 0, "replay %d: %d differing words" % (r, len(bad))
+    assert int(reset_e.sum()) > 0 and int(stepm_e.sum()) < count
+    graphed.close()
+    eager.close()
+
+
+def test_lds_limit_survives_a_later_engine():
+    """The bin's shared tiles take 150 KiB of LDS.  Creating a stacks engine
+    (less LDS) afterwards must not lower the kernels' limit below what the
+    bin launches with."""
+    worlds = scenes.build(4, 130)
+    ref = clone(worlds)
+    bin_eng = _engine(worlds, 4)
+    stacks = _engine(scenes.build(2, 64), 2)
+    gpu_run(bin_eng, 4, 0, 5)
+    oracle_run(4, ref, clone(worlds), 0, 5)
+    bad = diff_words(bin_eng.download(), ref, scenes.SCENES[4].sig)
+    assert len(bad) == 0
+    stacks.close()
+    bin_eng.close()
+
+
+@pytest.mark.parametrize("scene,count", [(5, 200), (4, 100), (2, 70)])
+def test_shared_tile_with_sparse_step_mask(scene, count):
+    """Shared tiles where only every ninth world steps and one whole tile
+    steps none: idle worlds keep every word, the stepping ones equal the
+    oracle's."""
+    from b3test import oracle_step_batch
+    sc = scenes.SCENES[scene]
+    worlds = scenes.build(scene, count)
+    oracle_run(scene, worlds, clone(worlds), 0, 10)
+    active = (np.arange(count) % 9 == 4).astype(np.uint8)
+    active[64:128] = 0
+    ref = clone(worlds)
+    eng = _engine(worlds, scene)
+    d_active = torch.from_numpy(active).cuda()
+    for _ in range(6):
+        oracle_step_batch(ref, sc.sig, sc.dt, sc.substeps, active)
+        eng.step(sc.dt, sc.substeps, d_active)
+    torch.cuda.synchronize()
+    got = eng.download()
+    eng.close()
+    bad = diff_words(got, ref, sc.sig)
+    assert len(bad) == 0, "%d differing words, first %s" % (len(bad), bad[:4].tolist())
+    idle = active == 0
+    assert len(diff_words(got[idle], worlds[idle], sc.sig)) == 0

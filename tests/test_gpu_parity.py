@@ -6,9 +6,10 @@ parity contract of the engine:
   - single-step body state within 1e-4 relative / 1e-5 absolute;
   - over long runs, batch means of per-world mean height and mean energy
     within 1%.
-Scenes without hinges do not call atan2f, the only libm function on the
-step path whose device implementation differs from glibc's, so for them
-the device result must be bit-identical to the oracle's.
+The hinge twist's atan2f runs the host C library's method on the device
+(fd_atan2f in puffysics_amd/csrc/b3d_math.h, pinned bit for bit against
+glibc in tests/test_atan2.py and tests/test_gpu_atan2.py), so every scene,
+hinged or not, must be bit-identical to the oracle.
 """
 import numpy as np
 import pytest
@@ -79,8 +80,9 @@ def assert_close_state(got, ref, rel=1e-4, abs_=1e-5):
     assert ok.all(), "max err %g at %s" % (err.max(), np.argwhere(~ok)[:5].tolist())
 
 
-@pytest.mark.parametrize("scene,count,steps", [(1, 200, 120), (2, 200, 130), (4, 130, 60)])
-def test_contact_scenes_bit_exact(scene, count, steps):
+@pytest.mark.parametrize("scene,count,steps", [(1, 200, 120), (2, 200, 130), (3, 200, 120), (4, 130, 60),
+                                               (5, 200, 80)])
+def test_scenes_bit_exact(scene, count, steps):
     worlds = scenes.build(scene, count)
     eng = _engine(worlds, scene)
     ref = clone(worlds)
@@ -109,37 +111,59 @@ def test_single_step_parity(scene, count):
 
 
 def world_stats(worlds, gravity=9.81):
-    """Per-world mean height and mean (kinetic + potential) energy of the
-    dynamic bodies."""
+    """Per-world mean height and mean energy of the dynamic bodies: linear
+    and rotational kinetic energy (0.5 w.I w with I = R diag(1/inv_i) R^T,
+    evaluated in the body frame) plus gravitational potential energy."""
     b = worlds["bodies"]
     dyn = b["type"] == 2
-    inv_m = b["inv_mass"]
+    inv_m = b["inv_mass"].astype(np.float64)
     m = np.where(inv_m > 0, 1.0 / np.where(inv_m > 0, inv_m, 1.0), 0.0)
     v2 = sum(b["lin_vel"][a].astype(np.float64) ** 2 for a in "xyz")
+    q = b["rotation"]
+    qv = np.stack([q["v"][a] for a in "xyz"], -1).astype(np.float64)
+    qs = q["s"].astype(np.float64)[..., None]
+    w = np.stack([b["ang_vel"][a] for a in "xyz"], -1).astype(np.float64)
+    t = 2.0 * np.cross(-qv, w)                      # body-frame w: R^T w
+    wl = w + qs * t + np.cross(-qv, t)
+    ii = np.stack([b["inv_inertia"][a] for a in "xyz"], -1).astype(np.float64)
+    inertia = np.where(ii > 0, 1.0 / np.where(ii > 0, ii, 1.0), 0.0)
+    rot = 0.5 * (inertia * wl * wl).sum(-1)
     y = b["center"]["y"].astype(np.float64)
-    e = 0.5 * m * v2 + m * gravity * y
+    e = 0.5 * m * v2 + rot + m * gravity * y
     n = np.maximum(dyn.sum(axis=1), 1)
     return (np.where(dyn, y, 0).sum(axis=1) / n, np.where(dyn, e, 0).sum(axis=1) / n)
+
+
+def _within_one_percent(got, ref):
+    """Per-world relative agreement; worlds whose aggregate is near zero are
+    held to 1% of the batch's typical magnitude instead."""
+    floor = 1e-2 * np.median(np.abs(ref)) + 1e-12
+    return np.abs(got - ref) <= 0.01 * np.maximum(np.abs(ref), floor)
 
 
 @pytest.mark.parametrize("scene,count,steps", [(1, 128, 1000), (2, 128, 1000), (3, 128, 1000), (4, 64, 2000),
                                                (5, 256, 1000)])
 def test_long_run_aggregates(scene, count, steps):
+    """Each world's time-mean height and energy, sampled after every vector
+    step, within 1% of the oracle's (the contract's long-run bar)."""
     worlds = scenes.build(scene, count)
     eng = _engine(worlds, scene)
     ref = clone(worlds)
     initial = clone(worlds)
-    chunk = 100
-    hg, hr, eg, er = [], [], [], []
-    for t0 in range(0, steps, chunk):
-        oracle_run(scene, ref, initial, t0, chunk, threads=8)
-        gpu_run(eng, scene, t0, chunk)
+    acc = np.zeros((4, count))
+    for t in range(steps):
+        oracle_run(scene, ref, initial, t, 1, threads=8)
+        gpu_run(eng, scene, t, 1)
         got = eng.download()
         a, b = world_stats(got), world_stats(ref)
-        hg.append(a[0]); eg.append(a[1]); hr.append(b[0]); er.append(b[1])
-    hg, hr, eg, er = (np.mean(x, axis=0) for x in (hg, hr, eg, er))
-    assert abs(hg.mean() - hr.mean()) <= 0.01 * abs(hr.mean())
-    assert abs(eg.mean() - er.mean()) <= 0.01 * abs(er.mean())
+        acc += np.stack([a[0], b[0], a[1], b[1]])
+    acc /= steps
+    h_ok = _within_one_percent(acc[0], acc[1])
+    e_ok = _within_one_percent(acc[2], acc[3])
+    assert h_ok.all(), "mean height differs in worlds %s" % np.flatnonzero(~h_ok)[:10].tolist()
+    assert e_ok.all(), "mean energy differs in worlds %s" % np.flatnonzero(~e_ok)[:10].tolist()
+    # the scenes really move: energy changes over the run in most worlds
+    assert np.abs(acc[3] - world_stats(initial)[1]).max() > 0
 
 
 def test_fused_reset_equals_restore_then_step():
@@ -262,20 +286,28 @@ def test_feature_worlds_without_hinges_bit_exact():
     assert ref["contacts_dropped"].max() > 0
 
 
-def test_feature_worlds_with_hinges_one_step():
+def test_feature_worlds_with_hinges_bit_exact():
+    """The coverage worlds with hinges too (springs, motors, limits and
+    fixed hinges, whose rows use the twist's atan2f): bit-identical to the
+    oracle over 60 steps with a step mask on every third step."""
     from b3test import feature_worlds, oracle_step_batch
     from puffysics_amd.creation import CUSTOM_SIG
-    from puffysics_amd.engine import B3Engine
+    from puffysics_amd.engine import B3_ENGINE_KEEP_SOLVER_FIELDS, B3Engine
     worlds = feature_worlds(100)
-    oracle_step_batch(worlds, CUSTOM_SIG, 1.0 / 60.0, 4)   # warm caches and impulses
     ref = clone(worlds)
     eng = B3Engine(worlds, CUSTOM_SIG)
-    oracle_step_batch(ref, CUSTOM_SIG, 1.0 / 60.0, 4)
-    eng.step(1.0 / 60.0, 4)
+    eng.set_options(B3_ENGINE_KEEP_SOLVER_FIELDS)
+    active = (np.arange(100) % 5 != 2).astype(np.uint8)
+    d_active = torch.from_numpy(active).cuda()
+    for t in range(60):
+        act = t % 3 == 0
+        oracle_step_batch(ref, CUSTOM_SIG, 1.0 / 60.0, 4, active if act else None)
+        eng.step(1.0 / 60.0, 4, d_active if act else None)
     torch.cuda.synchronize()
     got = eng.download()
-    assert contact_keys(got) == contact_keys(ref)
-    assert_close_state(got, ref)
+    bad = diff_words(got, ref, CUSTOM_SIG)
+    assert len(bad) == 0, describe(bad, got, ref, worlds)
+    assert np.abs(ref["joints"]["motor_impulse"]).max() > 0
 
 
 def test_default_options_differ_only_in_solver_fields():
