@@ -60,7 +60,8 @@ def test_graph_replay_equals_eager(scene, count):
         a, b = graphed.download(), eager.download()
         bad = diff_words(a, b, sc.sig)
         assert len(bad) == 0, "replay %d: %d differing words" % (r, len(bad))
-    assert int(reset_e.sum()) > 0 and int(stepm_e.sum()) < count
+    if scene == 5:                         # the arm scene's masks reset and skip worlds
+        assert int(reset_e.sum()) > 0 and int(stepm_e.sum()) < count
     graphed.close()
     eager.close()
 

@@ -136,9 +136,13 @@ def world_stats(worlds, gravity=9.81):
 
 def _within_one_percent(got, ref):
     """Per-world relative agreement; worlds whose aggregate is near zero are
-    held to 1% of the batch's typical magnitude instead."""
-    floor = 1e-2 * np.median(np.abs(ref)) + 1e-12
-    return np.abs(got - ref) <= 0.01 * np.maximum(np.abs(ref), floor)
+    held to 1% of the batch's typical magnitude instead.  A world whose
+    aggregate is NaN on both sides agrees: the reference's own capsule-box
+    manifold can produce a NaN normal (the arm scene's world 62 carries NaNs
+    from step 547 until its reset at step 555), and the engine reproduces
+    it."""
+    floor = 1e-2 * np.nanmedian(np.abs(ref)) + 1e-12
+    return (np.abs(got - ref) <= 0.01 * np.maximum(np.abs(ref), floor)) | (np.isnan(got) & np.isnan(ref))
 
 
 @pytest.mark.parametrize("scene,count,steps", [(1, 128, 1000), (2, 128, 1000), (3, 128, 1000), (4, 64, 2000),
@@ -163,7 +167,7 @@ def test_long_run_aggregates(scene, count, steps):
     assert h_ok.all(), "mean height differs in worlds %s" % np.flatnonzero(~h_ok)[:10].tolist()
     assert e_ok.all(), "mean energy differs in worlds %s" % np.flatnonzero(~e_ok)[:10].tolist()
     # the scenes really move: energy changes over the run in most worlds
-    assert np.abs(acc[3] - world_stats(initial)[1]).max() > 0
+    assert np.nanmax(np.abs(acc[3] - world_stats(initial)[1])) > 0
 
 
 def test_fused_reset_equals_restore_then_step():
