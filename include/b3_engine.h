@@ -155,6 +155,42 @@ hipError_t b3_engine_set_options(B3Engine* engine, unsigned int options);
 hipError_t b3_batch_art_step_gpu(B3Engine* engine, float dt, int substeps, const unsigned char* step_mask,
     const unsigned char* reset_mask, hipStream_t stream);
 
+/* The step without allocation.  No counterpart in the reference as a
+ * separate entry point: it is for callers that cannot allocate device
+ * memory at all, such as code under HIP graph capture, tight serving loops
+ * and harnesses that forbid hipMalloc, and that hold their worlds in their
+ * own device memory.  The reference's b3_batch_step_gpu (b3_batch.cuh:
+ * 81-89) steps such worlds without allocating because its kernel keeps all
+ * scratch per thread; this engine's step needs per-step scratch, which
+ * b3_batch_step_gpu takes from the engine (allocated by b3_engine_create)
+ * and this entry point from a fixed device array of the library.
+ *
+ * Steps the device-resident B3World structs viewed by `worlds` (a B3Batch
+ * over device memory, as b3_batch_valid accepts, with data, stride and
+ * world_offset multiples of 4) whose capacities are `config_signature`, in
+ * place: the worlds selected by `active` (device bytes, nonzero selects,
+ * NULL selects all) that are structurally valid (counts within the
+ * capacities, every body and shape index in range; others are left as they
+ * are).  The results equal b3_batch_step_gpu's on an engine with default
+ * options.  dt must be finite and >= 0, substeps >= 1; an empty batch or
+ * dt == 0 is a no-op.  Enqueues on `stream`; calls no allocating routine.
+ *
+ * Limit: the array holds 256 MiB, and a call needs
+ *   ceil(count / 64) * 64 * (sizeof(B3World) + scratch per world) + count
+ * bytes of it.  The per-step scratch per world is about the size of the
+ * world (34.3 KB beside a 37.3 KB world of 17 bodies, 17 shapes, 64
+ * contacts and 4 joints; 2.4 KB beside 3.5 KB for 2 bodies, 2 shapes, 4
+ * contacts and 2 joints), so a call takes at most about 3,700 worlds of the
+ * first kind and 45,000 of the second.  A larger batch returns
+ * hipErrorOutOfMemory without launching;
+ * split it over several calls.  All calls on one GPU share that GPU's
+ * array: two calls that overlap in time on one GPU (different streams, or
+ * host threads) race and corrupt each other's worlds; calls in one stream
+ * are ordered and safe.  The array keeps the last call's contents; nothing
+ * in it needs clearing between calls. */
+hipError_t b3_batch_step_worlds_gpu(B3Batch worlds, unsigned long long config_signature, float dt, int substeps,
+    const unsigned char* active, hipStream_t stream);
+
 /* ---- per-substep force laws ----
  * The reference's optional force hook B3_USER_FORCES (01_config.inl:189-198,
  * 09_step.inl:20-53) is a macro compiled into the step: once per substep,

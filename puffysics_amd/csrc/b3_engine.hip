@@ -10,6 +10,8 @@
  * Kernels:
  *   b3k_upload / b3k_download  AoS <-> tiles, transposed through LDS in
  *                              64 x 64 word blocks (both sides coalesced)
+ *   b3k_step_select            b3_batch_step_worlds_gpu's worlds to step:
+ *                              selected and structurally valid
  *   b3k_restore                masked restore from the snapshots (plain
  *                              B3World structs); four waves per tile, each
  *                              copying every fourth 512-word chunk of the
@@ -27,8 +29,11 @@
  */
 #include <hip/hip_runtime.h>
 
+#include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+
+#include <mutex>
 
 #include "b3_engine.h"
 #include "b3_engine_internal.h"
@@ -43,9 +48,11 @@ constexpr int kXposeThreads = 256;
 /* ---- AoS <-> tile transposes ---- */
 
 /* One workgroup per (tile, 64-word block): reads 64 worlds x 64 words with
- * each world's block contiguous, writes 64 rows of 64 lanes. */
+ * each world's block contiguous, writes 64 rows of 64 lanes.  World w's
+ * words start at aos[w * stride + offset] (stride, offset in words: a
+ * B3Batch over device memory; world_words and 0 for packed worlds). */
 __global__ __launch_bounds__(kXposeThreads) void b3k_upload(const uint32_t* __restrict__ aos,
-        uint32_t* __restrict__ tiles, int count, int world_words) {
+        uint32_t* __restrict__ tiles, int count, int world_words, size_t stride, size_t offset) {
     __shared__ uint32_t blk[64][65];
     int tile = blockIdx.y;
     int k0 = blockIdx.x * 64;
@@ -53,7 +60,7 @@ __global__ __launch_bounds__(kXposeThreads) void b3k_upload(const uint32_t* __re
         int l = e >> 6, kk = e & 63;
         int w = tile * 64 + l;
         uint32_t v = 0;
-        if (w < count && k0 + kk < world_words) v = aos[(size_t)w * world_words + k0 + kk];
+        if (w < count && k0 + kk < world_words) v = aos[(size_t)w * stride + offset + k0 + kk];
         blk[l][kk] = v;
     }
     __syncthreads();
@@ -65,7 +72,8 @@ __global__ __launch_bounds__(kXposeThreads) void b3k_upload(const uint32_t* __re
 }
 
 __global__ __launch_bounds__(kXposeThreads) void b3k_download(const uint32_t* __restrict__ tiles,
-        uint32_t* __restrict__ aos, int count, int world_words) {
+        uint32_t* __restrict__ aos, int count, int world_words, size_t stride, size_t offset,
+        const unsigned char* only) {
     __shared__ uint32_t blk[64][65];
     int tile = blockIdx.y;
     int k0 = blockIdx.x * 64;
@@ -78,7 +86,8 @@ __global__ __launch_bounds__(kXposeThreads) void b3k_download(const uint32_t* __
     for (int e = threadIdx.x; e < 64 * 64; e += kXposeThreads) {
         int l = e >> 6, kk = e & 63;
         int w = tile * 64 + l;
-        if (w < count && k0 + kk < world_words) aos[(size_t)w * world_words + k0 + kk] = blk[l][kk];
+        if (w < count && k0 + kk < world_words && (!only || only[w]))
+            aos[(size_t)w * stride + offset + k0 + kk] = blk[l][kk];
     }
 }
 
@@ -219,31 +228,53 @@ int host_word(const unsigned char* world, int k) {
     return v;
 }
 
-/* Structural checks that keep every index the kernels follow in range. */
-bool world_valid(const unsigned char* wp, const Geometry& g) {
-    int nb = host_word(wp, H_BODY_COUNT), ns = host_word(wp, H_SHAPE_COUNT);
-    int nc = host_word(wp, H_CONTACT_COUNT), nj = host_word(wp, H_JOINT_COUNT);
+/* Structural checks that keep every index the kernels follow in range:
+ * counts within the capacities, and every body and shape index a shape,
+ * joint or contact holds below the world's counts.  `word(k)` reads word k
+ * of the world. */
+template <class Word>
+B3D_FN bool world_ok(const Word& word, const Geometry& g) {
+    int nb = word(H_BODY_COUNT), ns = word(H_SHAPE_COUNT);
+    int nc = word(H_CONTACT_COUNT), nj = word(H_JOINT_COUNT);
     if (nb < 0 || nb > g.max_b || ns < 0 || ns > g.max_s || nc < 0 || nc > g.max_c || nj < 0 || nj > g.max_j)
         return false;
     for (int s = 0; s < ns; s++) {
-        int b = host_word(wp, g.so + s * kShapeWords + S_BODY);
+        int b = word(g.so + s * kShapeWords + S_BODY);
         if (b < 0 || b >= nb) return false;
     }
     for (int j = 0; j < nj; j++) {
-        int a = host_word(wp, g.jo + j * kJointWords + J_BODY_A);
-        int b = host_word(wp, g.jo + j * kJointWords + J_BODY_B);
+        int a = word(g.jo + j * kJointWords + J_BODY_A);
+        int b = word(g.jo + j * kJointWords + J_BODY_B);
         if (a < 0 || a >= nb || b < 0 || b >= nb) return false;
     }
     for (int c = 0; c < nc; c++) {
         int base = g.co + c * kContactWords;
-        int sa = host_word(wp, base + C_SHAPE_A), sb = host_word(wp, base + C_SHAPE_B);
-        int ba = host_word(wp, base + C_BODY_A), bb = host_word(wp, base + C_BODY_B);
-        int pc = host_word(wp, base + C_POINT_COUNT);
+        int sa = word(base + C_SHAPE_A), sb = word(base + C_SHAPE_B);
+        int ba = word(base + C_BODY_A), bb = word(base + C_BODY_B);
+        int pc = word(base + C_POINT_COUNT);
         if (sa < 0 || sa >= ns || sb < 0 || sb >= ns || ba < 0 || ba >= nb || bb < 0 || bb >= nb || pc < 0
                 || pc > kMaxManifold)
             return false;
     }
     return true;
+}
+bool world_valid(const unsigned char* wp, const Geometry& g) {
+    return world_ok([wp](int k) { return host_word(wp, k); }, g);
+}
+
+/* The worlds b3_batch_step_worlds_gpu steps: selected by `active` (NULL:
+ * all) and structurally valid (world_ok on the uploaded tile), so that a
+ * corrupt caller world is left as it is rather than followed out of
+ * range. */
+__global__ __launch_bounds__(64) void b3k_step_select(const uint32_t* tiles, Geometry g, int count,
+        const unsigned char* active, unsigned char* mask) {
+    int tile = blockIdx.x;
+    int lane = threadIdx.x;
+    int w = tile * 64 + lane;
+    if (w >= count) return;
+    const uint32_t* p = tiles + (size_t)tile * g.world_words * 64 + lane;
+    bool on = !active || active[w];
+    mask[w] = on && world_ok([p](int k) { return ldi(p, k); }, g) ? 1 : 0;
 }
 
 /* Gather the batch's worlds into one contiguous host buffer. */
@@ -263,10 +294,52 @@ hipError_t put_worlds(B3Engine* e, const unsigned char* host, uint32_t* dst) {
     hipError_t err = hipMemcpy(e->staging, host, bytes, hipMemcpyHostToDevice);
     if (err != hipSuccess) return err;
     dim3 grid((unsigned)((e->g.world_words + 63) / 64), (unsigned)e->tiles);
-    b3k_upload<<<grid, kXposeThreads>>>((const uint32_t*)e->staging, dst, e->count, e->g.world_words);
+    b3k_upload<<<grid, kXposeThreads>>>((const uint32_t*)e->staging, dst, e->count, e->g.world_words,
+        (size_t)e->g.world_words, 0);
     err = hipGetLastError();
     if (err != hipSuccess) return err;
     return hipDeviceSynchronize();
+}
+
+/* ---- the step without allocation ----
+ * b3_batch_step_worlds_gpu steps device-resident B3World structs in place
+ * through the kernels of b3_batch_step_gpu, staging the batch as tiles in a
+ * fixed device array instead of engine memory: tiles (world_words * 64
+ * words each), then each tile's per-step scratch (tile_scr_words), then one
+ * selection byte per world.  Each GPU the library runs on holds its own
+ * copy of the array from module load until the process ends. */
+constexpr size_t kNoAllocWords = (size_t)64 << 20;            /* 256 MiB */
+static __device__ __align__(256) uint32_t b3_noalloc_scratch[kNoAllocWords];
+
+/* The array's device address on each device, looked up once per device
+ * with that device current.  The symbol's name in host code is a host-side
+ * stand-in, never a device address: kernels get this pointer. */
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+uint32_t* g_noalloc_ptr[kMaxDevices];
+
+hipError_t noalloc_scratch(uint32_t** out) {
+    int dev = -1;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void* p = nullptr;
+        err = hipGetSymbolAddress(&p, HIP_SYMBOL(b3_noalloc_scratch));
+        if (err != hipSuccess) return err;
+        if (!p) return hipErrorInvalidSymbol;
+        if ((err = b3i_lds_limit((const void*)b3k_step)) != hipSuccess) return err;
+        g_noalloc_ptr[dev] = (uint32_t*)p;
+    }
+    *out = g_noalloc_ptr[dev];
+    return hipSuccess;
+}
+
+/* Words of the array one call over `count` worlds of geometry g uses. */
+size_t noalloc_words(const Geometry& g, int count) {
+    size_t tiles = ((size_t)count + 63) / 64;
+    return tiles * ((size_t)g.world_words * 64 + (size_t)g.tile_scr_words) + ((size_t)count + 3) / 4;
 }
 
 }  // namespace
@@ -416,7 +489,8 @@ hipError_t b3_engine_download(B3Engine* e, B3Batch worlds) {
     if (err != hipSuccess) return err;
     if (e->count == 0) return hipSuccess;
     dim3 grid((unsigned)((e->g.world_words + 63) / 64), (unsigned)e->tiles);
-    b3k_download<<<grid, kXposeThreads>>>(e->live, (uint32_t*)e->staging, e->count, e->g.world_words);
+    b3k_download<<<grid, kXposeThreads>>>(e->live, (uint32_t*)e->staging, e->count, e->g.world_words,
+        (size_t)e->g.world_words, 0, nullptr);
     if ((err = hipGetLastError()) != hipSuccess) return err;
     unsigned char* host = (unsigned char*)malloc((size_t)e->count * e->world_bytes);
     if (!host) return hipErrorOutOfMemory;
@@ -438,7 +512,8 @@ hipError_t b3_batch_restore_gpu(B3Engine* e, const unsigned char* reset, hipStre
     if (!reset) {
         /* NULL restores every world: the whole structs, transposed into the tiles. */
         dim3 grid((unsigned)((e->g.world_words + 63) / 64), (unsigned)e->tiles);
-        b3k_upload<<<grid, kXposeThreads, 0, stream>>>(e->snap, e->live, e->count, e->g.world_words);
+        b3k_upload<<<grid, kXposeThreads, 0, stream>>>(e->snap, e->live, e->count, e->g.world_words,
+            (size_t)e->g.world_words, 0);
         return hipGetLastError();
     }
     b3k_restore<<<e->tiles * kRestoreSlices, 64, 0, stream>>>(e->live, e->snap, e->g, e->count, reset);
@@ -505,6 +580,37 @@ hipError_t b3_engine_set_options(B3Engine* e, unsigned int options) {
     }
     e->options = options;
     return hipSuccess;
+}
+
+hipError_t b3_batch_step_worlds_gpu(B3Batch worlds, unsigned long long config_signature, float dt, int substeps,
+        const unsigned char* active, hipStream_t stream) {
+    Geometry g;
+    size_t world_bytes;
+    if (!geometry_of(config_signature, &g, &world_bytes)) return hipErrorInvalidValue;
+    if (!batch_valid(worlds, world_bytes) || !isfinite(dt) || dt < 0.0f || substeps < 1) return hipErrorInvalidValue;
+    if (((uintptr_t)worlds.data | worlds.stride | worlds.world_offset) & 3u) return hipErrorInvalidValue;
+    if (worlds.count == 0 || dt == 0.0f) return hipSuccess;
+    size_t lds = (size_t)lds_rows(g) * kLanes * sizeof(float);
+    if (lds > kCuLdsBytes) return hipErrorInvalidValue;
+    if (noalloc_words(g, worlds.count) > kNoAllocWords) return hipErrorOutOfMemory;
+    uint32_t* base = nullptr;
+    hipError_t err = noalloc_scratch(&base);
+    if (err != hipSuccess) return err;
+    int tiles = (worlds.count + 63) / 64;
+    uint32_t* tile_words = base;
+    uint32_t* step_scratch = base + (size_t)tiles * g.world_words * 64;
+    unsigned char* select = (unsigned char*)(step_scratch + (size_t)tiles * g.tile_scr_words);
+    uint32_t* aos = (uint32_t*)worlds.data;
+    size_t stride = worlds.stride / 4, offset = worlds.world_offset / 4;
+    dim3 grid((unsigned)((g.world_words + 63) / 64), (unsigned)tiles);
+    b3k_upload<<<grid, kXposeThreads, 0, stream>>>(aos, tile_words, worlds.count, g.world_words, stride, offset);
+    b3k_step_select<<<tiles, 64, 0, stream>>>(tile_words, g, worlds.count, active, select);
+    b3k_step<<<tiles, 64, lds, stream>>>(tile_words, nullptr, step_scratch, g, worlds.count, dt, substeps, select,
+        nullptr, 0u);
+    /* only the stepped worlds are written back: the others are not touched */
+    b3k_download<<<grid, kXposeThreads, 0, stream>>>(tile_words, aos, worlds.count, g.world_words, stride, offset,
+        select);
+    return hipGetLastError();
 }
 
 }  // extern "C"
