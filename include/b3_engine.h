@@ -191,6 +191,19 @@ hipError_t b3_batch_art_step_gpu(B3Engine* engine, float dt, int substeps, const
 hipError_t b3_batch_step_worlds_gpu(B3Batch worlds, unsigned long long config_signature, float dt, int substeps,
     const unsigned char* active, hipStream_t stream);
 
+/* ---- the CPU step ----
+ * The reference's host b3_step (09_step.inl:262-264) and b3_batch_step
+ * (b3_batch.cuh:39-48), capacity-agnostic: the caller passes its
+ * B3_CONFIG_SIGNATURE.  b3_setup.h wraps them under the reference's names
+ * (b3_step, b3_batch_step).  They run the engine's own step built for the
+ * host, in place on host B3World structs (4-byte aligned), with results
+ * bit-identical to the reference's CPU path, prepared contact fields
+ * included.  No HIP call; safe to call from several threads on disjoint
+ * worlds. */
+void b3_host_step(void* world, unsigned long long config_signature, float dt, int substeps);
+int b3_host_batch_step(B3Batch batch, unsigned long long config_signature, float dt, int substeps,
+    const unsigned char* active);
+
 /* ---- per-substep force laws ----
  * The reference's optional force hook B3_USER_FORCES (01_config.inl:189-198,
  * 09_step.inl:20-53) is a macro compiled into the step: once per substep,

@@ -451,6 +451,30 @@ B3S_FN void b3_apply_linear_impulse(B3World* w, int body, B3Vec3 impulse) {
     if (b->type == B3_DYNAMIC) b->lin_vel = b3_madd(b->lin_vel, b->inv_mass, impulse);
 }
 
+/* ---- the CPU step (09_step.inl:262-264, b3_batch.cuh:39-48) ----
+ * b3_step and b3_batch_step with the reference's names and meaning, for
+ * host code such as a CPU environment step (puffysics_hover.h:38-56): the
+ * engine's step built for the host, run in place on the caller's structs
+ * (libb3engine.so, b3_host_step / b3_host_batch_step, given the caller's
+ * B3_CONFIG_SIGNATURE).  b3_step returns without stepping for dt <= 0 (as
+ * the reference) or a world whose counts or indices are out of range.
+ * b3_batch_step returns 1, or 0 without touching any world when the batch,
+ * dt (finite, >= 0), substeps (>= 1) or a selected world is invalid; dt == 0
+ * is a successful no-op; active NULL steps every world. */
+#ifdef __cplusplus
+extern "C" {
+#endif
+void b3_host_step(void* world, unsigned long long config_signature, float dt, int substeps);
+int b3_host_batch_step(B3Batch batch, unsigned long long config_signature, float dt, int substeps,
+    const unsigned char* active);
+#ifdef __cplusplus
+}
+#endif
+B3S_FN void b3_step(B3World* w, float dt, int substeps) { b3_host_step(w, B3_CONFIG_SIGNATURE, dt, substeps); }
+B3S_FN int b3_batch_step(B3Batch batch, float dt, int substeps, const unsigned char* active) {
+    return b3_host_batch_step(batch, B3_CONFIG_SIGNATURE, dt, substeps, active);
+}
+
 /* ---- batch views (b3_batch.cuh:21-60) ---- */
 
 B3S_FN int b3_batch_valid(B3Batch batch) {

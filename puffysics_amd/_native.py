@@ -36,6 +36,8 @@ ENGINE_SYMBOLS = [
     ("b3_fluid_state_words", _i, [_vp]),
     ("b3_batch_step_fluid_gpu", _i, [_vp, _f, _i, _vp, _vp, _vp, _vp, _vp]),
     ("b3_batch_step_worlds_gpu", _i, [None, _ull, _f, _i, _vp, _vp]),
+    ("b3_host_step", None, [_vp, _ull, _f, _i]),
+    ("b3_host_batch_step", _i, [None, _ull, _f, _i, _vp]),
     ("b3w_masks_gpu", _i, [_i, _ull, _i, _i, _vp, _vp, _vp]),
     ("b3w_inputs_gpu", _i, [_vp, _i, _ull, _i, _vp, _vp]),
 ]

@@ -220,11 +220,11 @@ B3D_FN V3 support(const Obb* o, V3 dir) {
     float sz = dot(o->ax[2], dir) < 0.0f ? -o->h.z : o->h.z;
     return add(o->c, add(scale(o->ax[0], sx), add(scale(o->ax[1], sy), scale(o->ax[2], sz))));
 }
-/* Clip polygons live in a per-lane buffer with a stride of 64 floats
- * between consecutive words (LDS on the GPU): vertex i of a polygon at
- * words 3i..3i+2.  Two polygons of kClipVerts vertices are used. */
+/* Clip polygons live in a per-lane buffer with a stride of B3D_LANES
+ * floats between consecutive words (LDS on the GPU): vertex i of a polygon
+ * at words 3i..3i+2.  Two polygons of kClipVerts vertices are used. */
 constexpr int kClipVerts = 8;
-constexpr int kClipStride = 64;
+constexpr int kClipStride = B3D_LANES;
 constexpr int kClipWords = 2 * 3 * kClipVerts;
 B3D_FN V3 clip_get(const float* poly, int i) {
     const float* v = poly + 3 * i * kClipStride;

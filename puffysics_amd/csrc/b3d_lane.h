@@ -44,7 +44,7 @@
 
 namespace b3d {
 
-constexpr int kLanes = 64;
+constexpr int kLanes = B3D_LANES;
 constexpr int kVelWords = 7;
 
 /* ---- word offsets of the B3 structs ---- */

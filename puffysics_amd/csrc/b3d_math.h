@@ -29,6 +29,14 @@
 #endif
 /* B3D_FN for free functions, B3D_MFN for member functions. */
 
+/* Worlds per tile, and the stride between consecutive words of one world
+ * in the tiles, scratch and LDS rows: 64 (one wave) on the GPU.  A host
+ * build with B3D_LANES 1 steps plain B3World structs in place (the
+ * library's CPU b3_step). */
+#ifndef B3D_LANES
+#define B3D_LANES 64
+#endif
+
 namespace b3d {
 
 struct V3 { float x, y, z; };
