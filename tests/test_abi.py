@@ -15,10 +15,9 @@ HIP_ERROR_INVALID_VALUE = 1
 
 
 def declared(header):
+    """Names of the functions a header declares at file scope."""
     text = open(os.path.join(ROOT, "include", header)).read()
-    return set(re.findall(r"^hipError_t (\w+)\(|^int (\w+)\(", text, re.M)[i][j]
-               for i in range(len(re.findall(r"^hipError_t (\w+)\(|^int (\w+)\(", text, re.M)))
-               for j in range(2)) - {""}
+    return set(re.findall(r"^(?:hipError_t|int|void) (\w+)\(", text, re.M))
 
 
 def test_every_declared_symbol_is_exported():
