@@ -56,6 +56,55 @@ def ref_lib(scene):
     return _refs[scene]
 
 
+# The -O3 builds of the reference's CPU path (oracle/Makefile FAST_CFLAGS),
+# by the x86-64 level they need: the flags each level adds over the last.
+FAST_LEVELS = (
+    ("v4", "-O3 -march=x86-64-v4 -ffp-contract=off -fno-fast-math",
+     {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"}),
+    ("v3", "-O3 -march=x86-64-v3 -ffp-contract=off -fno-fast-math",
+     {"avx", "avx2", "bmi1", "bmi2", "f16c", "fma", "abm", "movbe", "xsave"}),
+)
+
+
+def host_cpu_flags():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    return set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    return set()
+
+
+def fast_levels_supported():
+    """The -O3 build levels this host can run, best first."""
+    flags = host_cpu_flags()
+    out = []
+    need = set()
+    for name, cflags, req in reversed(FAST_LEVELS):
+        need |= req
+        if need <= flags:
+            out.append((name, cflags))
+    return out[::-1]
+
+
+def ref_fast_lib(scene, level):
+    """The reference's CPU path built -O3 for x86-64 `level`, or None."""
+    path = os.path.join(REF_DIR, "libb3ref_%s_%d.so" % (level, scene))
+    if not os.path.exists(path):
+        return None
+    key = (level, scene)
+    if key not in _refs:
+        lib = C.CDLL(path)
+        lib.ref_world_size.restype = C.c_size_t
+        lib.ref_build_batch.argtypes = [_i, _vp, _i, _ull, _i]
+        lib.ref_run.restype = C.c_longlong
+        lib.ref_run.argtypes = [_i, _vp, _vp, _i, _ull, _i, _i, _f, _i, _i, _vp]
+        _refs[key] = lib
+    return _refs[key]
+
+
 def emu():
     global _emu
     if _emu is None:

@@ -110,3 +110,31 @@ def test_reference_capsule_box_nan_is_reproduced():
         assert (int(ct["shape_a"]), int(ct["shape_b"])) == (15, 31)
         assert np.isnan(ct["normal"]["x"]) and np.isnan(ct["normal"]["y"])
     assert len(diff_words(a, b, sc.sig)) == 0
+
+
+@pytest.mark.parametrize("scene", SCENE_IDS)
+def test_fast_reference_builds_match_the_reference(scene):
+    """The -O3 x86-64-v3 / v4 builds of the reference's CPU path that time
+    the CPU baseline step to the -O2 build's bits (every level this host
+    can run), over 40 steps of the scene's workload."""
+    from b3test import fast_levels_supported, ref_fast_lib
+    base = ref_lib(scene)
+    if base is None:
+        pytest.skip("reference build absent")
+    sc = scenes.SCENES[scene]
+    count = 48
+    ws = base.ref_world_size()
+    want = np.zeros(count * ws, np.uint8)
+    base.ref_build_batch(scene, want.ctypes.data, count, scenes.SEED, 0)
+    initial = want.copy()
+    base.ref_run(scene, want.ctypes.data, initial.ctypes.data, count, scenes.SEED, 0, 40, sc.dt, sc.substeps, 1, None)
+    levels = fast_levels_supported()
+    assert levels, "this host runs neither x86-64-v3 nor v4"
+    for level, _ in levels:
+        lib = ref_fast_lib(scene, level)
+        assert lib is not None, level
+        got = initial.copy()
+        lib.ref_run(scene, got.ctypes.data, initial.ctypes.data, count, scenes.SEED, 0, 40, sc.dt, sc.substeps, 2,
+                    None)
+        dt = world_dtype(sc.sig)
+        assert len(diff_words(got.view(dt), want.view(dt), sc.sig)) == 0, level
