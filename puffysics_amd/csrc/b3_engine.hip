@@ -155,7 +155,8 @@ __global__ __launch_bounds__(64 * kTileWaves) void b3k_step_shared(uint32_t* liv
     S.waves = kTileWaves;
     S.lds_bounds = 1;
     Lane L = lane_view(live, scratch, lds, g, tile, lane, opts);
-    L.stage = &S;
+    L.st = S;
+    L.staged = true;
     L.active = stepping;
     if (wave == 0) {
         step_world<Masks>(L, dt, substeps);

@@ -347,9 +347,12 @@ struct Lane {
     int sslot;          /* rank among the tile's stepping lanes: the slot of
                            the body, delta-pose and shape records */
     unsigned int opts;  /* kKeepSolverFields */
-    const PairStage* stage;  /* non-null: the tile's waves share the narrowphase */
+    PairStage st;       /* with `staged`: the tile's waves share the narrowphase
+                           (held by value, so that no pointer to a local
+                           escapes and its pointers keep their memory spaces) */
+    bool staged;
     bool active;        /* the lane steps its world.  Only a shared tile
-                           (stage non-null) runs idle lanes: they go through
+                           (staged) runs idle lanes: they go through
                            every workgroup barrier with their work skipped */
     Geometry g;
 };
@@ -369,7 +372,8 @@ B3D_FN Lane lane_view(uint32_t* live, uint32_t* scratch, float* vel_rows, const 
         unsigned int opts = 0) {
     Lane L;
     L.opts = opts;
-    L.stage = nullptr;
+    L.st = PairStage{};
+    L.staged = false;
     L.sslot = lane;
     L.w = live + (size_t)tile * g.world_words * kLanes + lane;
     L.scr = scratch ? scratch + (size_t)tile * g.tile_scr_words + lane : nullptr;
@@ -769,7 +773,7 @@ B3D_FN uint32_t shape_key(int i, int j) { return ((uint32_t)i << 16) | (uint32_t
 /* With a shared narrowphase the workgroup's LDS also holds the old contacts'
  * keys, after wave 0's clip rows and shape bounds, for the candidate search
  * to merge against. */
-B3D_FN bool lds_old_keys(const Lane& L) { return L.stage && L.stage->lds_bounds; }
+B3D_FN bool lds_old_keys(const Lane& L) { return L.staged && L.st.lds_bounds; }
 /* A shared tile's LDS, per lane: wave 0's rows (clip rows, then shape
  * bounds, later velocities) and the helpers' clip rows, then, past both
  * and past the shape bounds, the old contact keys, the bound-overlap masks
@@ -1231,8 +1235,8 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
     const Geometry& g = L.g;
     uint32_t* cand = L.scr + g.scr_cand * kLanes;
     int ncand = 0;
-    bool masks = Masks && L.stage;
-    if (L.stage) {
+    bool masks = Masks && L.staged;
+    if (L.staged) {
         float* hit = hit_rows(L);
         for (int k = 0; k <= hit_words(g); k++) hit[k * kLanes] = 0.0f;
         hit[(hit_words(g) + 1) * kLanes] = __builtin_bit_cast(float, sorted);
@@ -1241,7 +1245,7 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
         /* the tile's waves test the bound pairs, then list the candidates
          * in the same order as below */
         B3D_BARRIER();
-        overlap_rows(L, bounds, ns, *L.stage);
+        overlap_rows(L, bounds, ns, L.st);
         B3D_BARRIER();
         ncand = mask_candidates(L, ns);
     } else {
@@ -1271,15 +1275,15 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
                 }
             }
         }
-        if (L.stage) {
-            sti(L.stage->p, 0, ncand);
+        if (L.staged) {
+            sti(L.st.p, 0, ncand);
             B3D_BARRIER();
         }
     }
-    if (L.stage) {
+    if (L.staged) {
         /* the tile's waves split the narrowphase, then write the new
          * contacts at the places the candidate order gives them */
-        const PairStage& S = *L.stage;
+        const PairStage& S = L.st;
         const float* hit = hit_rows(L);
         pair_share(L, S, masks, ncand, nj, old_n, sorted);
         B3D_BARRIER();
@@ -1315,7 +1319,7 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
         pshape_load(L, (int)(key >> 16), &A);
         pshape_load(L, (int)(key & 0xffffu), &B);
         if (match >= 0) old_load(L, match, &orec);
-        if (L.stage) mani_load(*L.stage, 0, &ms);
+        if (L.staged) mani_load(L.st, 0, &ms);
     }
     if (ncand > 1) {
         key1 = ldu(cand, 2);
@@ -1333,12 +1337,12 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
             else An = A;
             pshape_load(L, (int)(key1 & 0xffffu), &Bn);
             if (match1 >= 0) old_load(L, match1, &orecn);
-            if (L.stage) mani_load(*L.stage, t + 1, &msn);
+            if (L.staged) mani_load(L.st, t + 1, &msn);
         }
         int i = (int)(key >> 16), j = (int)(key & 0xffffu);
         Mani m;
         m.count = 0;
-        if (L.stage) m = ms;
+        if (L.staged) m = ms;
         else if (!pair_skipped(L, A, B, jkey, nj)) collide_pair(&m, A.P, B.P, L.vel);
         if (m.count > 0 && cc >= g.max_c) {
             overflow = 1;
@@ -1380,7 +1384,7 @@ B3D_FN void find_contacts(const Lane& L) {
             key = pair_key(ldi(L.w, jw(L, j, J_BODY_A)), ldi(L.w, jw(L, j, J_BODY_B)));
         sti(joint_rec(L, j), JS_KEY, (int)key);
     }
-    if (bounds_in_lds(g) || (L.stage && L.stage->lds_bounds)) {
+    if (bounds_in_lds(g) || (L.staged && L.st.lds_bounds)) {
         float* bounds = L.vel + kClipWords * kLanes;
         shape_pass(L, ns, bounds);
         find_pairs<Masks>(L, bounds, ns, nj, old_n, sorted);
@@ -1433,8 +1437,8 @@ B3D_FN int sch_level(const Lane& L, int c) { return 1 + L.g.max_b + c; }
 B3D_FN int sch_p(const Lane& L, int lev) { return 1 + L.g.max_b + L.g.max_c + lev; }
 /* stage words of the schedule */
 B3D_FN int stage_sched_words(const Geometry& g) { return 3 * g.max_c; }
-B3D_FN uint32_t* sch_slots(const Lane& L, int c) { return L.stage->p + (size_t)(1 + c) * kLanes; }
-B3D_FN uint32_t* sch_entry(const Lane& L, int i) { return L.stage->p + (size_t)(1 + L.g.max_c + 2 * i) * kLanes; }
+B3D_FN uint32_t* sch_slots(const Lane& L, int c) { return L.st.p + (size_t)(1 + c) * kLanes; }
+B3D_FN uint32_t* sch_entry(const Lane& L, int i) { return L.st.p + (size_t)(1 + L.g.max_c + 2 * i) * kLanes; }
 
 /* The largest level count among the tile's stepping lanes (every wave of
  * the tile gets the same value). */
@@ -1455,8 +1459,8 @@ B3D_FN int prepare_contacts(const Lane& L, Soft cs, Soft ss) {
     const int keep = (L.opts & kKeepSolverFields) != 0;
     /* a shared tile prepares its contacts in parallel (every waves-th chunk
      * per wave) and warm-starts them afterwards, level by level */
-    const int fuse = !L.stage && !keep && !(ldi(L.scr + L.g.scr_flags * kLanes, 0) & kLaneRestitution);
-    const int first = L.stage ? L.stage->wave : 0, stride = L.stage ? L.stage->waves : 1;
+    const int fuse = !L.staged && !keep && !(ldi(L.scr + L.g.scr_flags * kLanes, 0) & kLaneRestitution);
+    const int first = L.staged ? L.st.wave : 0, stride = L.staged ? L.st.waves : 1;
     for (int c0 = first * kPrepChunk; c0 < cc; c0 += stride * kPrepChunk) {
         int a[kPrepChunk], b[kPrepChunk], pc[kPrepChunk], fl[kPrepChunk], slot[kPrepChunk];
         int pslot[kPrepChunk][kMaxManifold];
@@ -1621,7 +1625,7 @@ B3D_FN int prepare_contacts(const Lane& L, Soft cs, Soft ss) {
             /* the packed record */
             qsu(r, R_AB, (uint32_t)(a[k] | (b[k] << 16)));
             qsu(r, R_INFO, (uint32_t)(pc[k] | ((fl[k] | fixed[k]) << 8)));
-            if (L.stage) {
+            if (L.staged) {
                 int packed = slot[k];
 #pragma unroll
                 for (int p = 0; p < kMaxManifold; p++)
@@ -2272,7 +2276,7 @@ B3D_FN void solve_contacts(const Lane& L, float inv_h, float contact_speed, int 
  * Every wave runs 1 + nlev barriers (nlev from tile_levels). */
 B3D_FN void solve_contacts_leveled(const Lane& L, float inv_h, float contact_speed, int use_bias, Soft cs, Soft ss,
         int nlev) {
-    const PairStage& S = *L.stage;
+    const PairStage& S = L.st;
     int relax = !use_bias;
     int mine = sch_get(L, 0);
     B3D_BARRIER();
@@ -2313,7 +2317,7 @@ B3D_FN void solve_contacts_leveled(const Lane& L, float inv_h, float contact_spe
  * as warm_start_contacts applies them, level by level like the sweeps
  * (1 + nlev barriers). */
 B3D_FN void warm_contacts_leveled(const Lane& L, int nlev) {
-    const PairStage& S = *L.stage;
+    const PairStage& S = L.st;
     int mine = sch_get(L, 0);
     B3D_BARRIER();
     int first = 0;
@@ -3047,7 +3051,7 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
         body_prepass(L, h);
     }
     int nlev = 0;
-    if (L.stage) {
+    if (L.staged) {
         /* the tile's waves prepare the contacts together; wave 0 levels
          * them; all warm-start them level by level (the helper waves meet
          * wave 0 at each barrier, sweep_helper) */
@@ -3079,14 +3083,14 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
             else
                 integrate_velocities(L);
         }
-        if (L.stage) solve_contacts_leveled(L, inv_h, contact_speed, 1, cs, ss, nlev);
+        if (L.staged) solve_contacts_leveled(L, inv_h, contact_speed, 1, cs, ss, nlev);
         else solve_contacts(L, inv_h, contact_speed, 1, cs, ss);
         if (act) {
             solve_joints(L, h, inv_h, 1);
             integrate_positions(L, h, inv_dt);
             delta_geometry(L);
         }
-        if (L.stage) solve_contacts_leveled(L, inv_h, contact_speed, 0, cs, ss, nlev);
+        if (L.staged) solve_contacts_leveled(L, inv_h, contact_speed, 0, cs, ss, nlev);
         else solve_contacts(L, inv_h, contact_speed, 0, cs, ss);
         if (act) {
             solve_joints(L, h, inv_h, 0);

@@ -126,7 +126,8 @@ void emu_step_shared(uint32_t* tiles, int count, unsigned long long sig, float d
         S.wave = 0;
         S.waves = 1;
         S.lds_bounds = 1;
-        L.stage = &S;
+        L.st = S;
+        L.staged = true;
         if (masks < 0 ? shared_masks(g) : (masks > 0 && g.max_s <= 64)) step_world<true>(L, dt, substeps);
         else step_world<false>(L, dt, substeps);
     }
@@ -169,7 +170,8 @@ int emu_step_shared_idle(uint32_t* tiles, int count, unsigned long long sig, flo
         S.wave = 0;
         S.waves = 1;
         S.lds_bounds = 1;
-        L.stage = &S;
+        L.st = S;
+        L.staged = true;
         L.active = active;
         host_barriers = 0;
         if (use_masks) step_world<true>(L, dt, substeps);
@@ -180,6 +182,7 @@ int emu_step_shared_idle(uint32_t* tiles, int count, unsigned long long sig, flo
             host_barriers = 0;
             S.wave = 1;
             S.waves = 2;
+            L.st = S;
             if (use_masks) pair_helper<true>(L, S);
             else pair_helper<false>(L, S);
             sweep_helper(L, dt, substeps);
