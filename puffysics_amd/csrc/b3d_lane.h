@@ -266,10 +266,15 @@ constexpr int PR_RA = 0, PR_NMASS = 3, PR_RB = 4, PR_LEVER = 7, kPRows = 2;
  * prepare_joints (bodies a | b << 16 and JF_* flags), then everything that
  * depends only on the bodies' delta poses (recomputed after every position
  * update): twist angle, the hinge perpendicular rows and the relative
- * rotation's x, y, the point anchors and separation, and the weld's angular
- * error. */
+ * rotation's x, y, the point anchors and separation, the weld's angular
+ * error; the inverse of the point rows' 3x3 mass matrix (JS_PKI) and the
+ * perpendicular rows' 2x2 mass matrix with its reciprocal determinant
+ * (JS_KXX, JS_KXY, JS_KYY, JS_KINV; NaN when singular).  Last, fixed for
+ * the step: the hinge axis through each body's inverse inertia (JS_IAX,
+ * JS_IBX). */
 constexpr int JS_KEY = 0, JS_AB = 1, JS_INFO = 2, JS_TW = 3, JS_RELX = 4, JS_RELY = 5, JS_PX = 6, JS_PY = 9,
-              JS_RA = 12, JS_RB = 15, JS_PSEP = 18, JS_CV = 21, kJointScr = 24;
+              JS_RA = 12, JS_RB = 15, JS_PSEP = 18, JS_CV = 21, JS_PKI = 24, JS_KXX = 33, JS_KXY = 34, JS_KYY = 35,
+              JS_KINV = 36, JS_IAX = 37, JS_IBX = 40, kJointScr = 43;
 constexpr int JF_WELD = 1, JF_FIXED = 2, JF_SPRING = 4, JF_MOTOR = 8, JF_LIMIT = 16, JF_DYN_A = 32, JF_DYN_B = 64;
 
 constexpr int kStatic = 0, kKinematic = 1, kDynamic = 2;
@@ -1820,6 +1825,10 @@ B3D_FN void prepare_joints(const Lane& L, float h) {
                 float kk = dot(axis, mv(isum, axis));
                 stf(w, jw(L, i, J_AXIAL_MASS), kk > 0.0f ? 1.0f / kk : 0.0f);
                 st3(w, jw(L, i, J_ROTATION_AXIS), axis);
+                /* the spring, motor and limit rows' angular impulse directions
+                 * (06:470-560 multiply by the inverse inertias every solve) */
+                st3(joint_rec(L, i), JS_IAX, mv(ia, axis));
+                st3(joint_rec(L, i), JS_IBX, mv(ib, axis));
                 Q rel = qinv_mul(fqa, fqb);
                 V3 px, py;
                 hinge_perps(fqa, rel, &px, &py);
@@ -1974,6 +1983,8 @@ B3D_FN void joint_geometry(const Lane& L) {
         }
         Q dqa[kPrepChunk], dqb[kPrepChunk], fqa[kPrepChunk], fqb[kPrepChunk];
         V3 dpa[kPrepChunk], dpb[kPrepChunk], fpa[kPrepChunk], fpb[kPrepChunk], dcen[kPrepChunk];
+        float ma[kPrepChunk], mb[kPrepChunk];
+        M3 ia[kPrepChunk], ib[kPrepChunk];
 #pragma unroll
         for (int k = 0; k < kPrepChunk; k++) {
             int j = j0 + k;
@@ -1989,6 +2000,19 @@ B3D_FN void joint_geometry(const Lane& L) {
             fpa[k] = ld3(w, jw(L, j, J_FRAME_P_A));
             fpb[k] = ld3(w, jw(L, j, J_FRAME_P_B));
             dcen[k] = ld3(w, jw(L, j, J_DELTA_CENTER));
+            /* the masses as jrow_load gives them to the solves */
+            ma[k] = 0.0f;
+            mb[k] = 0.0f;
+            ia[k] = m3zero();
+            ib[k] = m3zero();
+            if (info[k] & JF_DYN_A) {
+                ma[k] = ldf(w, jw(L, j, J_INV_MASS_A));
+                ia[k] = ldm3(w, jw(L, j, J_INV_I_A));
+            }
+            if (info[k] & JF_DYN_B) {
+                mb[k] = ldf(w, jw(L, j, J_INV_MASS_B));
+                ib[k] = ldm3(w, jw(L, j, J_INV_I_B));
+            }
         }
 #pragma unroll
         for (int k = 0; k < kPrepChunk; k++) {
@@ -2004,6 +2028,9 @@ B3D_FN void joint_geometry(const Lane& L) {
             st3(r, JS_RA, ra);
             st3(r, JS_RB, rb);
             st3(r, JS_PSEP, add(add(sub(dpb[k], dpa[k]), sub(rb, ra)), dcen[k]));
+            /* the point rows' matrix as b3_solve3 inverts it in every solve
+             * (06:241-255, 03_math.inl:343-345) */
+            stm3(r, JS_PKI, inv3(point_k(ma[k], mb[k], ia[k], ib[k], ra, rb)));
             int fixed = info[k] & JF_FIXED;
             if (info[k] & JF_WELD) {
                 if (fixed) continue;
@@ -2022,6 +2049,17 @@ B3D_FN void joint_geometry(const Lane& L) {
                 hinge_perps(qa, rel, &px, &py);
                 st3(r, JS_PX, px);
                 st3(r, JS_PY, py);
+                /* the perpendicular rows' 2x2 matrix and b3_solve2's
+                 * reciprocal determinant (06:600-626, 03_math.inl:347-359) */
+                M3 isum = madd3(ia[k], ib[k]);
+                float kxx = dot(px, mv(isum, px));
+                float kyy = dot(py, mv(isum, py));
+                float kxy = dot(px, mv(isum, py));
+                float det = kxx * kyy - kxy * kxy;
+                stf(r, JS_KXX, kxx);
+                stf(r, JS_KXY, kxy);
+                stf(r, JS_KYY, kyy);
+                stf(r, JS_KINV, det <= 1.0e-12f ? __builtin_nanf("") : 1.0f / det);
                 /* the solve's latest hinge rows are part of the joint state */
                 st3(w, jw(L, j, J_PERP_X), px);
                 st3(w, jw(L, j, J_PERP_Y), py);
@@ -2469,8 +2507,11 @@ struct JRow {
     M3 ia, ib;
     Soft soft;
     V3 ra, rb, psep, lin_imp;
+    M3 pki;                 /* inverse of the point rows' mass matrix */
     /* revolute */
     V3 axis, px, py;
+    V3 ia_ax, ib_ax;        /* inverse inertias times the axis */
+    float kxx, kxy, kyy, kinv;   /* perpendicular rows' matrix, 1 / det or NaN */
     float axial_mass, max_torque, speed, target, lower, upper;
     Soft spring_soft;
     float tw, relx, rely;
@@ -2520,6 +2561,7 @@ B3D_FN void jrow_load(const Lane& L, int j, JHead h, JRow* r) {
     r->rb = ld3(g, JS_RB);
     r->psep = ld3(g, JS_PSEP);
     r->lin_imp = ld3(w, jw(L, j, J_LINEAR_IMPULSE));
+    r->pki = ldm3(g, JS_PKI);
     int fixed = f & JF_FIXED;
     if (f & JF_WELD) {
         r->lin_hz = ldf(w, jw(L, j, J_LINEAR_HERTZ));
@@ -2534,9 +2576,12 @@ B3D_FN void jrow_load(const Lane& L, int j, JHead h, JRow* r) {
         return;
     }
     if (fixed) return;
-    r->axis = ld3(w, jw(L, j, J_ROTATION_AXIS));
     r->px = ld3(g, JS_PX);
     r->py = ld3(g, JS_PY);
+    r->kxx = ldf(g, JS_KXX);
+    r->kxy = ldf(g, JS_KXY);
+    r->kyy = ldf(g, JS_KYY);
+    r->kinv = ldf(g, JS_KINV);
     r->relx = ldf(g, JS_RELX);
     r->rely = ldf(g, JS_RELY);
     r->perp_imp.x = ldf(w, jw(L, j, J_PERP_IMPULSE));
@@ -2544,6 +2589,9 @@ B3D_FN void jrow_load(const Lane& L, int j, JHead h, JRow* r) {
     if (f & (JF_SPRING | JF_MOTOR | JF_LIMIT)) {
         r->tw = ldf(g, JS_TW);
         r->axial_mass = ldf(w, jw(L, j, J_AXIAL_MASS));
+        r->axis = ld3(w, jw(L, j, J_ROTATION_AXIS));
+        r->ia_ax = ld3(g, JS_IAX);
+        r->ib_ax = ld3(g, JS_IBX);
     }
     if (f & (JF_SPRING | JF_MOTOR)) r->max_torque = ldf(w, jw(L, j, J_MAX_MOTOR_TORQUE));
     if (f & JF_SPRING) {
@@ -2577,8 +2625,9 @@ B3D_FN void solve_point(const Lane& L, int j, const JRow& r, V3* va, V3* wa, V3*
         mscale = soft.mass_scale;
         iscale = soft.impulse_scale;
     }
-    /* b3_solve3 of the point mass (06:241-255, 03_math.inl:343-345) */
-    V3 bsol = solve3(point_k(r.ma, r.mb, r.ia, r.ib, r.ra, r.rb), add(cdot, bias));
+    /* b3_solve3 of the point mass (06:241-255, 03_math.inl:343-345), its
+     * inverse taken once per delta state (joint_geometry) */
+    V3 bsol = mv(r.pki, add(cdot, bias));
     V3 impulse = msub(scale(bsol, -mscale), iscale, r.lin_imp);
     st3(L.w, jw(L, j, J_LINEAR_IMPULSE), add(r.lin_imp, impulse));
     *va = msub(*va, r.ma, impulse);
@@ -2640,11 +2689,8 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
     int en_spring = r.info & JF_SPRING, en_motor = r.info & JF_MOTOR, en_limit = r.info & JF_LIMIT;
     float axial_mass = r.axial_mass;
     float tw = r.tw;
-    V3 ia_ax = zero3(), ib_ax = zero3();
-    if (!fixed) {
-        ia_ax = mv(r.ia, axis);
-        ib_ax = mv(r.ib, axis);
-    }
+    /* mv(ia, axis), mv(ib, axis) of the step (prepare_joints) */
+    const V3 ia_ax = r.ia_ax, ib_ax = r.ib_ax;
     if (en_spring && !fixed) {
         Soft ss = r.spring_soft;
         float c = tw - r.target;
@@ -2712,13 +2758,15 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
         V2 rhs;
         rhs.x = dot(wrel, r.px) + bias.x;
         rhs.y = dot(wrel, r.py) + bias.y;
-        M3 isum = madd3(r.ia, r.ib);
-        M2 kang;
-        kang.cx.x = dot(r.px, mv(isum, r.px));
-        kang.cy.y = dot(r.py, mv(isum, r.py));
-        kang.cx.y = dot(r.px, mv(isum, r.py));
-        kang.cy.x = kang.cx.y;
-        V2 sol = solve2(kang, rhs);
+        /* b3_solve2 (03_math.inl:347-359) with the matrix and the reciprocal
+         * determinant of the delta state (joint_geometry) */
+        V2 sol;
+        sol.x = 0.0f;
+        sol.y = 0.0f;
+        if (r.kinv == r.kinv) {
+            sol.x = r.kinv * (r.kyy * rhs.x - r.kxy * rhs.y);
+            sol.y = r.kinv * (-r.kxy * rhs.x + r.kxx * rhs.y);
+        }
         V2 dimp;
         dimp.x = -mscale * sol.x - iscale * r.perp_imp.x;
         dimp.y = -mscale * sol.y - iscale * r.perp_imp.y;
@@ -2740,29 +2788,24 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
 }
 
 /* b3_solve_joints_global (07_packed.inl:48-81): sweeps in joint order; all
- * of a joint's row is requested before its rows are solved. */
+ * of a joint's row is requested before its rows are solved.  The row is
+ * loaded right before its solve, with its head (the bodies and flags that
+ * select which fields to load) fetched one solve ahead: a second row in
+ * flight during a solve costs more in registers than the one round trip it
+ * would hide. */
 B3D_FN void solve_joints(const Lane& L, float h, float inv_h, int use_bias) {
     int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
     if (nj <= 0) return;
-    /* solve t of the sweeps is joint t % nj; the row of solve t+1 is in
-     * flight during solve t (a different joint's row unless nj == 1, when it
-     * is loaded after the solve that writes it), the head of t+2 before */
     int total = (use_bias ? kJointIters : kRelaxIters) * nj;
-    JHead h1 = jhead_load(L, nj > 1 ? 1 : 0);
-    JRow cur, nxt;
-    jrow_load(L, 0, jhead_load(L, 0), &cur);
+    JHead head = jhead_load(L, 0);
     int j = 0;
     for (int t = 0; t < total; t++) {
+        JRow cur;
+        jrow_load(L, j, head, &cur);
         int jn = j + 1 == nj ? 0 : j + 1;
-        int jnn = jn + 1 == nj ? 0 : jn + 1;
-        JHead h2 = h1;
-        if (t + 2 < total) h2 = jhead_load(L, jnn);
-        if (t + 1 < total && nj > 1) jrow_load(L, jn, h1, &nxt);
+        if (t + 1 < total) head = jhead_load(L, jn);
         if (cur.info & JF_WELD) solve_weld(L, j, cur, use_bias);
         else solve_revolute(L, j, cur, h, inv_h, use_bias);
-        if (t + 1 < total && nj == 1) jrow_load(L, jn, h1, &nxt);
-        cur = nxt;
-        h1 = h2;
         j = jn;
     }
 }
