@@ -209,8 +209,8 @@ int b3_host_batch_step(B3Batch batch, unsigned long long config_signature, float
  * 09_step.inl:20-53) is a macro compiled into the step: once per substep,
  * before the velocity update, it may add to each body's applied force and
  * torque; that substep integrates the sums, and the applied values are
- * restored for the next substep.  This library compiles its laws into the
- * step kernel the same way, one entry point per law; each is
+ * restored for the next substep.  This library compiles its law into the
+ * step kernel the same way, behind its own entry point:
  * b3_batch_step_gpu (same masks, fused restore, validation and errors) with
  * the law in the hook. */
 
@@ -232,43 +232,6 @@ typedef struct B3GravityLaw {
 } B3GravityLaw;
 hipError_t b3_batch_step_gravity_gpu(B3Engine* engine, float dt, int substeps, const unsigned char* step_mask,
     const unsigned char* reset_mask, B3GravityLaw law, const float* masses, hipStream_t stream);
-
-/* Ambient-fluid forces (ambient.h:76-370, after Padilla, Segall and
- * Sorkine-Hornung): buoyancy, dynamic pressure, Blasius skin friction and
- * a lagged added-mass reaction on every dynamic body, from surface samples
- * of its shapes.  This is b3_fluid_step(law, world, state, h) run in the
- * hook: it reads each body's start-of-step position, rotation and center
- * and its current velocities, as the reference's hook would.  B3FluidLaw is
- * B3Fluid (ambient.h:24-35); b3_fluid_law_default gives b3_fluid_default
- * (ambient.h:46-60).  Limits: sphere_samples <= 1024,
- * box_face_samples <= B3_FLUID_MAX_FACE_SAMPLES, capsule_rings <=
- * B3_FLUID_MAX_RINGS, else hipErrorInvalidValue.
- *
- * `state` is a device array of count * b3_fluid_state_words(engine) 32-bit
- * words holding each world's B3FluidState (ambient.h:38-42): per body
- * b < max_bodies its previous linear then angular velocity (6 floats), then
- * have_prev (an int).  Zero it to initialise (b3_fluid_state_init); worlds
- * selected by reset_mask get have_prev = 0 (b3_fluid_state_reset) as they
- * are restored.  The step writes it like b3_fluid_step. */
-#define B3_FLUID_MAX_FACE_SAMPLES 64
-#define B3_FLUID_MAX_RINGS 1024
-typedef struct B3FluidLaw {
-    float density;
-    float separation_cos;
-    float mu;
-    float drag_scale;
-    float fric_scale;
-    float added_scale;
-    int sphere_samples;
-    int box_face_samples;
-    int capsule_rings;
-    int buoyancy;
-} B3FluidLaw;
-hipError_t b3_fluid_law_default(B3FluidLaw* out);
-/* Words of one world's fluid state (6 * max_bodies + 1), or -1 for NULL. */
-int b3_fluid_state_words(const B3Engine* engine);
-hipError_t b3_batch_step_fluid_gpu(B3Engine* engine, float dt, int substeps, const unsigned char* step_mask,
-    const unsigned char* reset_mask, const B3FluidLaw* law, float* state, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1356,20 +1356,12 @@ static void o_solve_joints(OWorld* w, b3r h, b3r inv_h, int use_bias) {         
 /* Integration and the step driver: src/puffysics/09_step.inl           */
 /* ------------------------------------------------------------------ */
 
-/* Ambient-fluid parameters (B3Fluid, ambient.h:24-35). */
-typedef struct {
-    float density, separation_cos, mu, drag_scale, fric_scale, added_scale;
-    int sphere_samples, box_face_samples, capsule_rings, buoyancy;
-} OFluid;
-
 /* A force law in the B3_USER_FORCES hook (01_config.inl:189-198): it adds
  * to the bodies' applied forces and torques of the world it is given. */
 typedef struct OForceLaw {
     void (*apply)(const struct OForceLaw* law, OWorld* w, b3r h);
     b3r gravity, softening;   /* o_gravity_law */
     const float* masses;      /* o_gravity_law: this world's masses, or NULL */
-    const OFluid* fluid;      /* o_fluid_law */
-    float* fluid_state;       /* o_fluid_law: this world's state (OFluidState words) */
 } OForceLaw;
 
 /* Plummer-softened gravity between the world's bodies (nbody_rigid.cuh:
@@ -1401,240 +1393,6 @@ static void o_gravity_law(const OForceLaw* f, OWorld* w, b3r h) {
             if (b->type == B3_DYNAMIC) b->force = o_sub(b->force, force);
         }
     }
-}
-
-/* ---- ambient-fluid forces (ambient.h:76-370) ----
- * The state of one world is 6 * max_bodies + 1 words: each body's previous
- * linear and angular velocity (B3FluidState.prev_lin / prev_ang,
- * ambient.h:38-42), then have_prev as an int. */
-#define O_FLUID_ALPHA_N 32                                                               /* ambient.h:22-24 */
-#define O_FLUID_GOLDEN 2.39996322972865332f                                              /* :25 */
-
-static b3r o_fcomp(OV3 v, int i) { return i == 0 ? v.x : (i == 1 ? v.y : v.z); }        /* :76-78 */
-static OV3 o_fset(OV3 v, int i, b3r x) {                                                 /* :80-90 */
-    if (i == 0) v.x = x;
-    else if (i == 1) v.y = x;
-    else v.z = x;
-    return v;
-}
-
-/* Simpson rule for the ellipsoid added-mass integral (:94-126). */
-static b3r o_fluid_alpha(b3r s2, b3r a, b3r b, b3r c) {
-    b3r l2 = a * a;
-    if (b * b > l2) l2 = b * b;
-    if (c * c > l2) l2 = c * c;
-    if (l2 <= 1.0e-12f) return 0.0f;
-    b3r abc = a * b * c;
-    int n = O_FLUID_ALPHA_N;
-    if (n & 1) n++;
-    b3r one = 1.0f;
-    b3r hstep = one / (b3r)(float)n;
-    b3r sum = 0.0f;
-    for (int i = 0; i <= n; i++) {
-        b3r t = (b3r)(float)i * hstep;
-        b3r inv = 1.0f - t * t;
-        b3r g = 0.0f;
-        if (inv > 1.0e-12f) {
-            b3r u = l2 * t * t / inv;
-            b3r du = 2.0f * l2 * t / (inv * inv);
-            b3r d = o_sqrt((a * a + u) * (b * b + u) * (c * c + u));
-            g = abc * du / ((s2 + u) * d);
-        }
-        b3r wgt = (i == 0 || i == n) ? 1.0f : ((i & 1) ? 4.0f : 2.0f);
-        sum += wgt * g;
-    }
-    return sum * hstep / 3.0f;
-}
-
-static OV3 o_fluid_added_diag(const OFluid* f, b3r a, b3r b, b3r c, b3r vol) {          /* :128-139 */
-    b3r ax = o_fluid_alpha(a * a, a, b, c);
-    b3r ay = o_fluid_alpha(b * b, a, b, c);
-    b3r az = o_fluid_alpha(c * c, a, b, c);
-    return o_v(f->density * vol * ax / (2.0f - ax), f->density * vol * ay / (2.0f - ay),
-        f->density * vol * az / (2.0f - az));
-}
-
-static void o_fluid_volume(const OShape* s, b3r* vol, OV3* centroid) {                  /* :141-157 */
-    if (s->type == B3_SPHERE) {
-        *vol = (4.0f / 3.0f) * B3_PI * s->radius * s->radius * s->radius;
-    } else if (s->type == B3_BOX) {
-        *vol = 8.0f * s->half.x * s->half.y * s->half.z;
-    } else {
-        b3r r = s->radius;
-        *vol = B3_PI * r * r * (2.0f * s->half.y) + (4.0f / 3.0f) * B3_PI * r * r * r;
-    }
-    *centroid = s->local_pos;
-}
-
-static void o_fluid_axes(const OShape* s, b3r* a, b3r* b, b3r* c) {                      /* :159-175 */
-    if (s->type == B3_SPHERE) {
-        *a = *b = *c = s->radius;
-    } else if (s->type == B3_BOX) {
-        *a = s->half.x;
-        *b = s->half.y;
-        *c = s->half.z;
-    } else {
-        *a = s->radius;
-        *c = s->radius;
-        *b = 1.5f * s->half.y + s->radius;
-    }
-}
-
-/* Surface sample k of a shape in its own frame: position, outward normal
- * and area; 0 past the last sample (:177-256). */
-static int o_fluid_sample(const OFluid* f, const OShape* s, int k, OV3* pos, OV3* nrm, b3r* area) {
-    b3r one = 1.0f;
-    if (s->type == B3_SPHERE) {
-        int n = f->sphere_samples > 0 ? f->sphere_samples : 16;
-        if (k >= n) return 0;
-        b3r y = 1.0f - 2.0f * ((b3r)(float)k + 0.5f) / (b3r)(float)n;
-        b3r r = o_sqrt(o_max(0.0f, 1.0f - y * y));
-        b3r th = O_FLUID_GOLDEN * (b3r)(float)k;
-        *pos = o_v(s->radius * r * cosf(th), s->radius * y, s->radius * r * sinf(th));
-        *nrm = o_norm(*pos);
-        *area = 4.0f * B3_PI * s->radius * s->radius / (b3r)(float)n;
-        return 1;
-    }
-    if (s->type == B3_BOX) {
-        int kx = f->box_face_samples > 0 ? f->box_face_samples : 1;
-        int per_face = kx * kx;
-        int face = k / per_face;
-        int cell = k - face * per_face;
-        if (face >= 6) return 0;
-        int axis = face >> 1;
-        b3r sign = (face & 1) ? -1.0f : 1.0f;
-        int ua = (axis + 1) % 3, va = (axis + 2) % 3;
-        int iu = cell / kx, iv = cell - iu * kx;
-        b3r hu = o_fcomp(s->half, ua), hv = o_fcomp(s->half, va);
-        b3r u = -hu + 2.0f * hu * ((b3r)(float)iu + 0.5f) / (b3r)(float)kx;
-        b3r v = -hv + 2.0f * hv * ((b3r)(float)iv + 0.5f) / (b3r)(float)kx;
-        OV3 p = o_v(0.0f, 0.0f, 0.0f);
-        p = o_fset(p, axis, sign * o_fcomp(s->half, axis));
-        p = o_fset(p, ua, u);
-        p = o_fset(p, va, v);
-        *pos = p;
-        *nrm = o_fset(o_v(0.0f, 0.0f, 0.0f), axis, sign);
-        *area = (2.0f * hu) * (2.0f * hv) / (b3r)(float)per_face;
-        return 1;
-    }
-    if (s->type == B3_CAPSULE) {
-        int m = f->capsule_rings > 0 ? f->capsule_rings : 2;
-        int ka = 8;
-        int cyl = m * ka;
-        if (k < cyl) {
-            int ring = k / ka, around = k - ring * ka;
-            b3r y = -s->half.y + 2.0f * s->half.y * ((b3r)(float)ring + 0.5f) / (b3r)(float)m;
-            b3r th = O_FLUID_GOLDEN * (b3r)(float)around;
-            *pos = o_v(s->radius * cosf(th), y, s->radius * sinf(th));
-            *nrm = o_v(cosf(th), 0.0f, sinf(th));
-            *area = (2.0f * B3_PI * s->radius) * (2.0f * s->half.y) / (b3r)(float)(m * ka);
-            return 1;
-        }
-        int cn = f->sphere_samples > 0 ? f->sphere_samples : 16;
-        int kc = k - cyl;
-        int per_cap = cn >> 1;
-        if (kc >= 2 * per_cap) return 0;
-        int sgn = kc >= per_cap ? -1 : 1;
-        int j = kc - (sgn < 0 ? per_cap : 0);
-        b3r y = 1.0f - 2.0f * ((b3r)(float)j + 0.5f) / (b3r)(float)cn;
-        b3r r = o_sqrt(o_max(0.0f, 1.0f - y * y));
-        b3r th = O_FLUID_GOLDEN * (b3r)(float)j;
-        *pos = o_v(s->radius * r * cosf(th), (b3r)(float)sgn * s->half.y + s->radius * y, s->radius * r * sinf(th));
-        *nrm = o_norm(*pos);
-        *area = 2.0f * B3_PI * s->radius * s->radius / (b3r)(float)per_cap;
-        (void)one;
-        return 1;
-    }
-    return 0;
-}
-
-/* b3_fluid_body (:258-359) on body bi. */
-static void o_fluid_body(const OFluid* f, OWorld* w, float* st, int bi, b3r h) {
-    OBody* b = &w->bodies[bi];
-    if (b->type != B3_DYNAMIC) return;
-    OV3* prev_lin = (OV3*)(st + 6 * bi);
-    OV3* prev_ang = (OV3*)(st + 6 * bi + 3);
-    int have_prev;
-    memcpy(&have_prev, st + 6 * w->max_b, sizeof(int));
-    OV3 f_acc = o_v(0.0f, 0.0f, 0.0f), t_acc = o_v(0.0f, 0.0f, 0.0f), a_est = o_v(0.0f, 0.0f, 0.0f);
-    int use_added = have_prev && f->added_scale > 0.0f && h > 0.0f;
-    b3r one = 1.0f;
-    if (use_added) a_est = o_scale(o_sub(b->lin_vel, *prev_lin), one / h);
-    for (int si = 0; si < w->h->shape_count; si++) {
-        const OShape* s = &w->shapes[si];
-        if (s->body != bi) continue;
-        OV3 sp = o_xf(b->position, b->rotation, s->local_pos);
-        OQ sq = o_qmul(b->rotation, s->local_rot);
-        b3r vol;
-        OV3 c_local;
-        o_fluid_volume(s, &vol, &c_local);
-        if (f->buoyancy) {
-            OV3 cw = o_xf(sp, sq, c_local);
-            OV3 fb = o_scale(w->h->gravity, -f->density * vol);
-            f_acc = o_add(f_acc, fb);
-            t_acc = o_add(t_acc, o_cross(o_sub(cw, b->center), fb));
-        }
-        if (use_added) {
-            b3r ax, ay, az;
-            o_fluid_axes(s, &ax, &ay, &az);
-            OV3 ma = o_scale(o_fluid_added_diag(f, ax, ay, az, vol), f->added_scale);
-            for (int i = 0; i < 3; i++) {
-                OV3 axis = o_rot(sq, o_fset(o_v(0.0f, 0.0f, 0.0f), i, 1.0f));
-                b3r proj = o_dot(axis, a_est);
-                f_acc = o_msub(f_acc, o_fcomp(ma, i) * proj, axis);
-            }
-        }
-        b3r L = 0.0f;
-        if (f->mu > 0.0f && f->fric_scale > 0.0f) {
-            if (s->type == B3_SPHERE) {
-                L = 2.0f * s->radius * o_sqrt(B3_PI);
-            } else if (s->type == B3_BOX) {
-                L = o_sqrt(8.0f * (s->half.x * s->half.y + s->half.y * s->half.z + s->half.x * s->half.z));
-            } else {
-                b3r rr = s->radius;
-                L = o_sqrt(2.0f * B3_PI * rr * (2.0f * s->half.y) + 4.0f * B3_PI * rr * rr);
-            }
-        }
-        OV3 lp, ln;
-        b3r area;
-        for (int k = 0; o_fluid_sample(f, s, k, &lp, &ln, &area); k++) {
-            OV3 p = o_xf(sp, sq, lp);
-            OV3 n = o_rot(sq, ln);
-            OV3 r = o_sub(p, b->center);
-            OV3 rdot = o_add(b->lin_vel, o_cross(b->ang_vel, r));
-            b3r spd = o_sqrt(o_len2(rdot));
-            if (spd <= 1.0e-9f) continue;
-            b3r nd = o_dot(n, rdot);
-            if (nd / spd < f->separation_cos) continue;
-            b3r u2 = o_len2(rdot) - nd * nd;
-            b3r pdyn = -0.5f * f->density * u2 * f->drag_scale;
-            OV3 df = o_scale(n, pdyn * area);
-            f_acc = o_add(f_acc, df);
-            t_acc = o_add(t_acc, o_cross(r, df));
-            if (f->mu > 0.0f && f->fric_scale > 0.0f) {
-                OV3 ut = o_msub(rdot, nd, n);
-                b3r us = o_sqrt(o_len2(ut));
-                if (us > 1.0e-9f) {
-                    b3r re = f->density * us * L / f->mu;
-                    b3r cf = 0.0576f * powf(re, -0.2f);
-                    OV3 ff = o_scale(ut, (-0.5f * cf * f->density * us * area) * f->fric_scale);
-                    f_acc = o_add(f_acc, ff);
-                    t_acc = o_add(t_acc, o_cross(r, ff));
-                }
-            }
-        }
-    }
-    b->force = o_add(b->force, f_acc);
-    b->torque = o_add(b->torque, t_acc);
-    *prev_lin = b->lin_vel;
-    *prev_ang = b->ang_vel;
-}
-
-/* b3_fluid_step (:361-370) as the hook's law. */
-static void o_fluid_law(const OForceLaw* law, OWorld* w, b3r h) {
-    for (int bi = 0; bi < w->h->body_count; bi++) o_fluid_body(law->fluid, w, law->fluid_state, bi, h);
-    int one = 1;
-    memcpy(law->fluid_state + 6 * w->max_b, &one, sizeof(int));
 }
 
 static void o_integrate_velocities(OWorld* w, b3r h, const OForceLaw* law) {             /* :5-18, 20-53 */
@@ -1808,14 +1566,7 @@ void ocpu_step_gravity(void* world, unsigned long long sig, float dt, int subste
         float softening, const float* masses) {
     OWorld w;
     if (!o_view(&w, world, sig)) return;
-    OForceLaw law = {o_gravity_law, gravity, softening, masses, NULL, NULL};
-    o_step(&w, dt, substeps, &law, 0);
-}
-
-void ocpu_step_fluid(void* world, unsigned long long sig, float dt, int substeps, const void* fluid, float* state) {
-    OWorld w;
-    if (!o_view(&w, world, sig)) return;
-    OForceLaw law = {o_fluid_law, 0.0f, 0.0f, NULL, (const OFluid*)fluid, state};
+    OForceLaw law = {o_gravity_law, gravity, softening, masses};
     o_step(&w, dt, substeps, &law, 0);
 }
 

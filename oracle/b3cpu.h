@@ -30,12 +30,6 @@ void ocpu_step(void* world, unsigned long long sig, float dt, int substeps);
  * `masses` is NULL (1 / inv_mass of dynamic bodies) or body_count floats. */
 void ocpu_step_gravity(void* world, unsigned long long sig, float dt, int substeps, float gravity,
     float softening, const float* masses);
-/* b3_step with b3_fluid_step (ambient.h:258-370) in the B3_USER_FORCES
- * hook.  `fluid` points at a B3Fluid (ambient.h:24-35: six floats, then
- * sphere_samples, box_face_samples, capsule_rings, buoyancy as ints);
- * `state` is the world's 6 * max_bodies + 1 words: each body's previous
- * linear and angular velocity, then have_prev (int). */
-void ocpu_step_fluid(void* world, unsigned long long sig, float dt, int substeps, const void* fluid, float* state);
 /* b3_step built with B3_ART_CONTACTS=1 (01_config.inl:176-187): in a world
  * with revolute joints the warm start and the contact sweeps use
  * articulated responses (b3_art.cuh; 08_contacts.inl:194-232, 422-437). */

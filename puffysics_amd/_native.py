@@ -32,9 +32,6 @@ ENGINE_SYMBOLS = [
     ("b3_engine_device_view", _i, [_vp, C.POINTER(C.c_void_p), C.POINTER(C.c_size_t)]),
     ("b3_engine_set_options", _i, [_vp, C.c_uint]),
     ("b3_batch_step_gravity_gpu", _i, [_vp, _f, _i, _vp, _vp, "B3GravityLaw", _vp, _vp]),
-    ("b3_fluid_law_default", _i, [_vp]),
-    ("b3_fluid_state_words", _i, [_vp]),
-    ("b3_batch_step_fluid_gpu", _i, [_vp, _f, _i, _vp, _vp, _vp, _vp, _vp]),
     ("b3_batch_step_worlds_gpu", _i, [None, _ull, _f, _i, _vp, _vp]),
     ("b3_host_step", None, [_vp, _ull, _f, _i]),
     ("b3_host_batch_step", _i, [None, _ull, _f, _i, _vp]),

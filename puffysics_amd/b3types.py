@@ -113,13 +113,6 @@ class B3GravityLaw(C.Structure):
     _fields_ = [("gravity", C.c_float), ("softening", C.c_float)]
 
 
-class B3FluidLaw(C.Structure):
-    """Ambient-fluid law of b3_batch_step_fluid_gpu (B3Fluid, ambient.h:24-35)."""
-    _fields_ = [(n, C.c_float) for n in ("density", "separation_cos", "mu", "drag_scale", "fric_scale",
-                                         "added_scale")] + \
-               [(n, C.c_int) for n in ("sphere_samples", "box_face_samples", "capsule_rings", "buoyancy")]
-
-
 def signature(bodies, shapes, contacts, joints):
     """B3_CONFIG_SIGNATURE for a capacity set."""
     return bodies | (shapes << 16) | (contacts << 32) | (joints << 48)

@@ -14,7 +14,7 @@ import ctypes as C
 import numpy as np
 
 from . import _native
-from .b3types import B3FluidLaw, B3GravityLaw, B3StepStats, batch_of, world_dtype
+from .b3types import B3GravityLaw, B3StepStats, batch_of, world_dtype
 
 HIP_SUCCESS = 0
 HIP_ERROR_INVALID_VALUE = 1
@@ -85,21 +85,6 @@ def b3_batch_step_gravity_gpu(engine, dt, substeps, gravity, softening, masses=N
     return _native.engine_lib().b3_batch_step_gravity_gpu(engine, dt, substeps, _ptr(step_mask), _ptr(reset_mask),
                                                           B3GravityLaw(gravity, softening), _ptr(masses),
                                                           _stream(stream))
-
-
-def fluid_law_default():
-    """b3_fluid_default (ambient.h:46-60) as a B3FluidLaw."""
-    law = B3FluidLaw()
-    _native.engine_lib().b3_fluid_law_default(C.byref(law))
-    return law
-
-
-def b3_batch_step_fluid_gpu(engine, dt, substeps, law, state, step_mask=None, reset_mask=None, stream=None):
-    """b3_batch_step_gpu with b3_fluid_step (ambient.h:258-370) in the
-    per-substep force hook.  `state` is a device tensor of
-    count * b3_fluid_state_words 32-bit words (zeros to start)."""
-    return _native.engine_lib().b3_batch_step_fluid_gpu(engine, dt, substeps, _ptr(step_mask), _ptr(reset_mask),
-                                                        C.byref(law), _ptr(state), _stream(stream))
 
 
 B3_ENGINE_KEEP_SOLVER_FIELDS = 1
@@ -174,16 +159,6 @@ class B3Engine:
                      stream=None):
         self._check("b3_batch_step_gravity_gpu", b3_batch_step_gravity_gpu(
             self._h, dt, substeps, gravity, softening, masses, step_mask, reset_mask, stream))
-
-    def fluid_state(self):
-        """A zeroed fluid-state tensor for step_fluid (B3FluidState per world)."""
-        import torch
-        words = self._lib.b3_fluid_state_words(self._h)
-        return torch.zeros(self.count * words, dtype=torch.float32, device="cuda")
-
-    def step_fluid(self, dt, substeps, law, state, step_mask=None, reset_mask=None, stream=None):
-        self._check("b3_batch_step_fluid_gpu", b3_batch_step_fluid_gpu(
-            self._h, dt, substeps, law, state, step_mask, reset_mask, stream))
 
     def restore(self, reset=None, stream=None):
         self._check("b3_batch_restore_gpu", b3_batch_restore_gpu(self._h, reset, stream))

@@ -553,18 +553,6 @@ def oracle_step_gravity(worlds, sig, dt, substeps, gravity, softening, masses=No
                               None if m is None else m[k].ctypes.data)
 
 
-def oracle_step_fluid(worlds, sig, dt, substeps, law, state, active=None):
-    """b3_step with b3_fluid_step in the force hook, world by world on the
-    oracle; `law` a B3FluidLaw, `state` [count, 6 * max_bodies + 1] float32
-    (updated in place)."""
-    lib = oracle()
-    lib.ocpu_step_fluid.argtypes = [_vp, _ull, _f, _i, _vp, _vp]
-    for k in range(len(worlds)):
-        if active is not None and not active[k]:
-            continue
-        lib.ocpu_step_fluid(worlds[k:k + 1].ctypes.data, sig, dt, substeps, C.byref(law), state[k].ctypes.data)
-
-
 def ref_gravity_lib(caps):
     """The reference's b3_step with its B3_USER_FORCES hook running the
     reference's pairwise gravity, for capacity set `caps` (0, 2, 4 or 5), or
@@ -577,8 +565,6 @@ def ref_gravity_lib(caps):
         lib = C.CDLL(path)
         lib.refg_sig.restype = C.c_ulonglong
         lib.refg_step.argtypes = [_vp, _f, _i, _f, _f, _vp]
-        lib.refg_step_fluid.argtypes = [_vp, _f, _i, _vp, _vp]
-        lib.refg_fluid_size.restype = C.c_size_t
         _refs[key] = lib
     return _refs[key]
 
@@ -630,13 +616,6 @@ class EmuSig:
         act = None if active is None else np.ascontiguousarray(active, np.uint8)
         lib.emu_art_step(self.tiles.ctypes.data, self.count, self.sig, dt, substeps,
                          None if act is None else act.ctypes.data)
-
-    def step_fluid(self, dt, substeps, law, state, active=None):
-        lib = emu()
-        lib.emu_step_fluid.argtypes = [_vp, _i, _ull, _f, _i, _vp, _vp, _vp]
-        act = None if active is None else np.ascontiguousarray(active, np.uint8)
-        lib.emu_step_fluid(self.tiles.ctypes.data, self.count, self.sig, dt, substeps,
-                           None if act is None else act.ctypes.data, C.byref(law), state.ctypes.data)
 
     def worlds(self):
         out = np.zeros(self.count, dtype=self.dtype)

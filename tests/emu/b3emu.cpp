@@ -212,32 +212,6 @@ void emu_step_gravity(uint32_t* tiles, int count, unsigned long long sig, float 
     }
 }
 
-/* emu_step with b3_fluid_step in the force hook; `fluid` is a B3Fluid,
- * `state` count * (6 * max_bodies + 1) words. */
-void emu_step_fluid(uint32_t* tiles, int count, unsigned long long sig, float dt, int substeps,
-        const unsigned char* step_mask, const void* fluid, float* state) {
-    Geometry g;
-    size_t wb;
-    if (!geometry_of(sig, &g, &wb)) return;
-    static std::vector<float> trig;
-    if (trig.empty()) {
-        trig.resize(2 * kFluidTrig);
-        fluid_trig_table(trig.data());
-    }
-    int ntiles = (count + kLanes - 1) / kLanes;
-    std::vector<uint32_t> scratch((size_t)ntiles * g.tile_scr_words);
-    std::vector<float> vel((size_t)lds_rows(g) * kLanes);
-    size_t words = (size_t)6 * g.max_b + 1;
-    for (int w = 0; w < count; w++) {
-        if (step_mask && !step_mask[w]) continue;
-        FluidLaw law;
-        memcpy(&law.f, fluid, sizeof(FluidParams));
-        law.state = state + w * words;
-        law.trig = trig.data();
-        step_world(lane_of(tiles, scratch.data(), vel.data(), g, w), dt, substeps, law);
-    }
-}
-
 /* emu_step with articulated contacts (B3_ENGINE_ART_CONTACTS). */
 void emu_step_art(uint32_t* tiles, int count, unsigned long long sig, float dt, int substeps,
         const unsigned char* step_mask) {

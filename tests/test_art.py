@@ -347,17 +347,13 @@ def test_device_art_one_step_on_the_arm_scene():
 
 @pytest.mark.gpu
 def test_device_art_rejects_force_laws_and_resets():
-    """Force-law entry points are not available with the option on; the
+    """The force-law entry point is not available with the option on; the
     fused reset works as in the ordinary step."""
-    from puffysics_amd.engine import (B3_ENGINE_ART_CONTACTS, B3Engine, b3_batch_step_gravity_gpu,
-                                      fluid_law_default)
+    from puffysics_amd.engine import B3_ENGINE_ART_CONTACTS, B3Engine, b3_batch_step_gravity_gpu
     worlds = T.passive_hinge_worlds(64)
     eng = B3Engine(worlds, CUSTOM_SIG)
     eng.set_options(B3_ENGINE_ART_CONTACTS)
     assert b3_batch_step_gravity_gpu(eng.handle, DT, 4, 1.0, 0.1) == 801   # hipErrorNotSupported
-    from puffysics_amd.engine import b3_batch_step_fluid_gpu
-    st = torch.zeros(64 * (6 * 16 + 1), dtype=torch.float32, device="cuda")
-    assert b3_batch_step_fluid_gpu(eng.handle, DT, 4, fluid_law_default(), st) == 801
     for _ in range(5):
         eng.step(DT, 4)
     reset = np.zeros(64, np.uint8)

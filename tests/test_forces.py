@@ -1,6 +1,6 @@
 """The per-substep force hook (B3_USER_FORCES, 01_config.inl:189-198 and
-09_step.inl:20-53) with the built-in laws: pairwise gravity
-(nbody_rigid.cuh:15-66) and ambient fluid (ambient.h:76-370).
+09_step.inl:20-53) with the built-in law: pairwise gravity
+(nbody_rigid.cuh:15-66).
 
 The oracle's hook and law are pinned three ways on the CPU: against the
 reference's own b3_step compiled with its hook running the reference's own
@@ -199,126 +199,6 @@ def test_invalid_law_is_rejected_without_a_device():
         assert lib.b3_batch_step_gravity_gpu(None, DT, 4, None, None, B3GravityLaw(G, soft), None, None) == 1
 
 
-# ---- ambient fluid ----
-
-from puffysics_amd.b3types import B3FluidLaw  # noqa: E402
-
-AIR = B3FluidLaw(1.2, 0.0, 1.8e-5, 1.0, 1.0, 1.0, 48, 4, 8, 1)          # play_fluid.cu:117-119
-STILL = B3FluidLaw(50.0, 0.2, 0.0, 2.0, 1.0, 0.5, 20, 2, 3, 0)         # no skin friction, no buoyancy
-FLUID_CASES = [("features-air", 0, 30, AIR), ("features-still", 0, 30, STILL), ("bin-air", 4, 10, AIR),
-               ("arm-still", 5, 10, STILL)]
-
-
-def _state(count, sig):
-    return np.zeros((count, 6 * (sig & 0xFFFF) + 1), np.float32)
-
-
-@pytest.mark.parametrize("name,caps,steps,law", FLUID_CASES, ids=[c[0] for c in FLUID_CASES])
-def test_fluid_oracle_matches_reference_hook(name, caps, steps, law):
-    """The oracle's fluid law against the reference's own b3_fluid_step in
-    its hook, bit for bit on every live word and on the fluid state."""
-    lib = T.ref_gravity_lib(caps)
-    if lib is None:
-        pytest.skip("reference not built (oracle/_ref)")
-    import ctypes as C
-    assert lib.refg_fluid_size() == C.sizeof(B3FluidLaw)
-    worlds, sig = _case_worlds(caps, 6)
-    a, b = clone(worlds), clone(worlds)
-    sa, sb = _state(6, sig), _state(6, sig)
-    for t in range(steps):
-        if caps == 5:
-            _arm_inputs(a, t)
-            _arm_inputs(b, t)
-        T.oracle_step_fluid(a, sig, DT, 4, law, sa)
-        for k in range(6):
-            lib.refg_step_fluid(b[k:k + 1].ctypes.data, DT, 4, C.byref(law), sb[k].ctypes.data)
-    assert len(diff_words(a, b, sig)) == 0
-    assert (sa.view(np.uint32) == sb.view(np.uint32)).all()
-    assert np.isfinite(_v3(a["bodies"]["lin_vel"])).all()
-
-
-def _sphere_world(density=1000.0, vel=(0.0, 0.0, 0.0), gravity=(0.0, -10.0, 0.0), radius=0.2):
-    """One dynamic sphere in empty space."""
-    w = cr.new_worlds(1, gravity=gravity)
-    b = cr.body(w, 0, B3_DYNAMIC, (0.0, 2.0, 0.0), lin_vel=vel)
-    cr.sphere(w, 0, b, radius, density=density)
-    cr.finalize_mass(w, 0, b)
-    return w
-
-
-def test_fluid_buoyancy_closed_form():
-    """A sphere at rest: no drag (every sample's speed is zero), buoyancy
-    -rho V g, so dv = g h (1 - rho_fluid / rho_body) exactly to rounding."""
-    law = B3FluidLaw(500.0, 0.0, 0.0, 1.0, 1.0, 0.0, 48, 3, 8, 1)
-    w = _sphere_world(density=1000.0)
-    T.oracle_step_fluid(w, CUSTOM_SIG, 0.01, 1, law, _state(1, CUSTOM_SIG))
-    np.testing.assert_allclose(_v3(w["bodies"]["lin_vel"][0, 0]), [0.0, -10.0 * 0.01 * 0.5, 0.0], rtol=1e-5, atol=1e-7)
-
-
-def test_fluid_drag_against_the_hemisphere_integral():
-    """A sphere translating at speed U through still fluid (buoyancy off):
-    the sampled pressure -rho/2 (U^2 - (n.U)^2) over the upstream half,
-    integrated exactly, is a force pi/4 rho U^2 R^2 against the motion.  48
-    samples reproduce it within 10%; the force opposes the motion."""
-    rho, U, R, h = 1.2, 3.0, 0.2, 0.01
-    law = B3FluidLaw(rho, 0.0, 0.0, 1.0, 1.0, 0.0, 48, 3, 8, 0)
-    w = _sphere_world(vel=(U, 0.0, 0.0), gravity=(0.0, 0.0, 0.0), radius=R)
-    m = 1.0 / float(w["bodies"]["inv_mass"][0, 0])
-    T.oracle_step_fluid(w, CUSTOM_SIG, h, 1, law, _state(1, CUSTOM_SIG))
-    dv = _v3(w["bodies"]["lin_vel"][0, 0]) - [U, 0.0, 0.0]
-    expect = -np.pi / 4.0 * rho * U * U * R * R / m * h
-    assert dv[0] < 0.0
-    assert abs(dv[0] / expect - 1.0) < 0.1, (dv[0], expect)
-
-
-def test_fluid_sphere_added_mass():
-    """Lagged added mass: with the previous velocity v - a h stored, the
-    estimated acceleration is a and the reaction is -M_a a with the sphere's
-    classical added mass M_a = rho V / 2 (ellipsoid coefficient alpha = 2/3)."""
-    rho, h = 300.0, 0.01
-    a = np.array([2.0, -1.0, 0.5])
-    law = B3FluidLaw(rho, 0.0, 0.0, 1.0, 1.0, 1.0, 48, 3, 8, 0)
-    w = _sphere_world(gravity=(0.0, 0.0, 0.0))
-    st = _state(1, CUSTOM_SIG)
-    st[0, 0:3] = -a * h
-    st[0, 96] = np.array([1], np.int32).view(np.float32)[0]
-    T.oracle_step_fluid(w, CUSTOM_SIG, h, 1, law, st)
-    dv = _v3(w["bodies"]["lin_vel"][0, 0])
-    # m dv / h = -rho V / 2 a, with m = 1000 V
-    np.testing.assert_allclose(dv, -(rho / 1000.0) / 2.0 * a * h, rtol=5e-3)
-    assert st[0, 96].view(np.int32) == 1 and not st[0, 0:6].any()   # prev = the velocity the hook saw
-
-
-@pytest.mark.parametrize("caps", [0, 5])
-def test_fluid_lane_code_matches_oracle(caps):
-    worlds, sig = _case_worlds(caps, 70)
-    ref = clone(worlds)
-    emu = T.EmuSig(sig, worlds)
-    sr, se = _state(70, sig), _state(70, sig)
-    active = (np.arange(70) % 3 != 0).astype(np.uint8)
-    for t in range(12):
-        act = active if t % 2 else None
-        T.oracle_step_fluid(ref, sig, DT, 4, AIR, sr, act)
-        emu.step_fluid(DT, 4, AIR, se, act)
-    assert len(diff_words(emu.worlds(), ref, sig)) == 0
-    assert (sr.view(np.uint32) == se.view(np.uint32)).all()
-
-
-def test_fluid_invalid_arguments_without_a_device():
-    import ctypes as C
-    from puffysics_amd import _native
-    lib = _native.engine_lib()
-    law = B3FluidLaw(AIR.density, 0.0, 0.0, 1.0, 1.0, 1.0, 2000, 3, 8, 1)
-    assert lib.b3_batch_step_fluid_gpu(None, DT, 4, None, None, C.byref(AIR), None, None) == 1
-    out = B3FluidLaw()
-    assert lib.b3_fluid_law_default(C.byref(out)) == 0
-    assert (out.density, out.mu, out.sphere_samples, out.box_face_samples, out.capsule_rings, out.buoyancy) == \
-        (np.float32(1.2), np.float32(1.8e-5), 48, 3, 8, 1)
-    assert lib.b3_fluid_law_default(None) == 1
-    assert lib.b3_fluid_state_words(None) == -1
-    del law
-
-
 # ---- device ----
 
 torch = pytest.importorskip("torch")
@@ -396,68 +276,4 @@ def test_device_gravity_bad_arguments():
     assert b3_batch_step_gravity_gpu(eng.handle, 0.0, 4, 1.0, 0.1) == 0
     torch.cuda.synchronize()
     assert len(diff_words(eng.download(), before, scenes.SCENES[2].sig)) == 0
-    eng.close()
-
-
-@pytest.mark.gpu
-@pytest.mark.parametrize("caps", [0, 4])
-def test_device_fluid_bit_exact_without_skin_friction(caps):
-    """b3_batch_step_fluid_gpu against the oracle with mu = 0 (no powf):
-    bit-identical worlds and fluid state on hinge-free worlds, with step
-    masks."""
-    from puffysics_amd.engine import B3_ENGINE_KEEP_SOLVER_FIELDS, B3Engine
-    law = B3FluidLaw(1.2, 0.0, 0.0, 1.0, 1.0, 1.0, 48, 4, 8, 1)
-    if caps == 0:
-        worlds, sig = T.feature_worlds(100, hinges=False), CUSTOM_SIG
-    else:
-        worlds, sig = scenes.build(caps, 100), scenes.SCENES[caps].sig
-    ref = clone(worlds)
-    sr = _state(100, sig)
-    eng = B3Engine(worlds, sig)
-    eng.set_options(B3_ENGINE_KEEP_SOLVER_FIELDS)
-    st = eng.fluid_state()
-    active = (np.arange(100) % 5 != 2).astype(np.uint8)
-    d_active = _dev(active)
-    for t in range(20):
-        act = t % 3 == 0
-        T.oracle_step_fluid(ref, sig, DT, 4, law, sr, active if act else None)
-        eng.step_fluid(DT, 4, law, st, d_active if act else None)
-    torch.cuda.synchronize()
-    got = eng.download()
-    bad = diff_words(got, ref, sig)
-    assert len(bad) == 0, "%d differing words, first %s" % (len(bad), bad[:4].tolist())
-    assert (st.cpu().numpy().view(np.uint32) == sr.reshape(-1).view(np.uint32)).all()
-    eng.close()
-
-
-@pytest.mark.gpu
-def test_device_fluid_one_step_with_skin_friction_and_resets():
-    """Air with skin friction (the device's powf) on the arm scene: one step
-    within the single-step tolerance; a fused reset restores the world and
-    clears its have_prev."""
-    from puffysics_amd.engine import B3Engine
-    from test_gpu_parity import assert_close_state
-    sig = scenes.SCENES[5].sig
-    worlds = scenes.build(5, 128)
-    sr = _state(128, sig)
-    for t in range(3):
-        scenes.apply_inputs(5, worlds, t)
-        T.oracle_step_fluid(worlds, sig, DT, 4, AIR, sr)
-    ref = clone(worlds)
-    eng = B3Engine(worlds, sig)
-    st = torch.from_numpy(sr.reshape(-1).copy()).cuda()
-    T.oracle_step_fluid(ref, sig, DT, 4, AIR, sr)
-    eng.step_fluid(DT, 4, AIR, st)
-    torch.cuda.synchronize()
-    assert_close_state(eng.download(), ref)
-    eng.set_snapshots(worlds)
-    reset = np.zeros(128, np.uint8)
-    reset[::3] = 1
-    eng.step_fluid(DT, 4, AIR, st, _dev(1 - reset), _dev(reset))
-    torch.cuda.synchronize()
-    got = eng.download()
-    assert len(diff_words(got[::3], worlds[::3], sig)) == 0
-    words = 6 * 17 + 1
-    have = st.cpu().numpy().view(np.int32).reshape(128, words)[:, -1]
-    assert (have[::3] == 0).all() and (np.delete(have, np.s_[::3]) == 1).all()
     eng.close()
