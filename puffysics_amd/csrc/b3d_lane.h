@@ -1960,21 +1960,22 @@ B3D_FN M3 point_k(float ma, float mb, M3 ia, M3 ib, V3 ra, V3 rb) {
  * reference recomputes these in every row solve (08_contacts.inl:331-333,
  * 06_joints.inl:257-282, 285-332, 436-642); computing them once per delta
  * state gives the same bits. */
-B3D_FN void joint_geometry(const Lane& L);
+B3D_FN void joint_geometry(const Lane& L, int first = 0, int stride = 1);
 
 /* Geometry of the joints at new delta poses.  The contacts' separations
  * are computed by each solve from the bodies' delta poses. */
 B3D_FN void delta_geometry(const Lane& L) { joint_geometry(L); }
 
-/* The joint rows' delta-pose geometry. */
-B3D_FN void joint_geometry(const Lane& L) {
+/* The joint rows' delta-pose geometry, joints first, first + stride, ...
+ * (a shared tile's waves split them). */
+B3D_FN void joint_geometry(const Lane& L, int first, int stride) {
     uint32_t* w = L.w;
     int nj = clampi(ldi(w, H_JOINT_COUNT), 0, L.g.max_j);
-    for (int j0 = 0; j0 < nj; j0 += kPrepChunk) {
+    for (int j0 = first; j0 < nj; j0 += kPrepChunk * stride) {
         int a[kPrepChunk], b[kPrepChunk], info[kPrepChunk];
 #pragma unroll
         for (int k = 0; k < kPrepChunk; k++) {
-            int j = j0 + k;
+            int j = j0 + k * stride;
             if (j >= nj) continue;
             uint32_t ab = ldu(joint_rec(L, j), JS_AB);
             a[k] = (int)(ab & 0xffffu);
@@ -1987,7 +1988,7 @@ B3D_FN void joint_geometry(const Lane& L) {
         M3 ia[kPrepChunk], ib[kPrepChunk];
 #pragma unroll
         for (int k = 0; k < kPrepChunk; k++) {
-            int j = j0 + k;
+            int j = j0 + k * stride;
             if (j >= nj) continue;
             const uint32_t* da = delta_rec(L, a[k]);
             const uint32_t* db = delta_rec(L, b[k]);
@@ -2016,7 +2017,7 @@ B3D_FN void joint_geometry(const Lane& L) {
         }
 #pragma unroll
         for (int k = 0; k < kPrepChunk; k++) {
-            int j = j0 + k;
+            int j = j0 + k * stride;
             if (j >= nj) continue;
             uint32_t* r = joint_rec(L, j);
             Q qa = qmul(dqa[k], fqa[k]);
@@ -2871,15 +2872,16 @@ B3D_FN void body_prepass(const Lane& L, float h) {
 }
 
 /* Gravity, applied force and damping for dynamic bodies (09_step.inl:5-18, 41-53). */
-B3D_FN void integrate_velocities(const Lane& L) {
+/* Bodies first, first + stride, ... (a shared tile's waves split them). */
+B3D_FN void integrate_velocities(const Lane& L, int first = 0, int stride = 1) {
     int nb = body_count(L);
-    for (int b0 = 0; b0 < nb; b0 += kChunk) {
+    for (int b0 = first; b0 < nb; b0 += kChunk * stride) {
         int kind[kChunk];
         V3 dv[kChunk], dw[kChunk];
         float ld[kChunk], ad[kChunk];
 #pragma unroll
         for (int k = 0; k < kChunk; k++) {
-            int b = b0 + k;
+            int b = b0 + k * stride;
             if (b >= nb) continue;
             const uint32_t* r = body_rec(L, b);
             kind[k] = (int)ru(delta_rec(L, b), BD_KIND);
@@ -2890,7 +2892,7 @@ B3D_FN void integrate_velocities(const Lane& L) {
         }
 #pragma unroll
         for (int k = 0; k < kChunk; k++) {
-            int b = b0 + k;
+            int b = b0 + k * stride;
             if (b >= nb || !(kind[k] & kKindDynamic)) continue;
             set_vlin(L, b, madd(dv[k], ld[k], vlin(L, b)));
             set_vang(L, b, madd(dw[k], ad[k], vang(L, b)));
@@ -2899,20 +2901,20 @@ B3D_FN void integrate_velocities(const Lane& L) {
 }
 
 /* Axis locks, speed clamps and the substep pose update (09_step.inl:55-107). */
-B3D_FN void integrate_positions(const Lane& L, float h, float inv_dt) {
+B3D_FN void integrate_positions(const Lane& L, float h, float inv_dt, int first = 0, int stride = 1) {
     uint32_t* w = L.w;
     float max_lin = ldf(w, H_MAX_LINEAR_SPEED);
     float max_ang = kMaxRotation * inv_dt;
     float max_lin2 = max_lin * max_lin;
     float max_ang2 = max_ang * max_ang;
     int nb = body_count(L);
-    for (int b0 = 0; b0 < nb; b0 += kChunk) {
+    for (int b0 = first; b0 < nb; b0 += kChunk * stride) {
         int kind[kChunk];
         V3 dp[kChunk];
         Q dq[kChunk];
 #pragma unroll
         for (int k = 0; k < kChunk; k++) {
-            int b = b0 + k;
+            int b = b0 + k * stride;
             if (b >= nb) continue;
             const uint32_t* d = delta_rec(L, b);
             kind[k] = (int)ru(d, BD_KIND);
@@ -2921,7 +2923,7 @@ B3D_FN void integrate_positions(const Lane& L, float h, float inv_dt) {
         }
 #pragma unroll
         for (int k = 0; k < kChunk; k++) {
-            int b = b0 + k;
+            int b = b0 + k * stride;
             if (b >= nb || (kind[k] & kKindStatic)) continue;
             uint32_t flags = (uint32_t)kind[k];
             V3 v = vlin(L, b), av = vang(L, b);
@@ -3119,20 +3121,27 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
         warm_start_joints(L);
         joint_geometry(L);   /* the contacts' initial separations come from prepare_contacts */
     }
+    /* In a shared tile the waves split the velocity and position updates
+     * (bodies) and the joint geometry (joints) of every substep, between
+     * barriers: each body and joint is updated by one wave, and the next
+     * phase's readers see it after the barrier (sweep_helper runs the same
+     * barriers).  Wave 0 alone solves the joints and applies restitution. */
+    const int share = L.staged ? L.st.wave : 0, stride = L.staged ? L.st.waves : 1;
     for (int s = 0; s < subs; s++) {
+        if (L.staged) B3D_BARRIER();   /* the last joint and restitution impulses */
         if (act) {
-            if constexpr (Law::kActive)
+            if constexpr (Law::kActive)   /* one-wave kernels only: no tile sharing */
                 integrate_velocities_law(L, h, law);
             else
-                integrate_velocities(L);
+                integrate_velocities(L, share, stride);
         }
         if (L.staged) solve_contacts_leveled(L, inv_h, contact_speed, 1, cs, ss, nlev);
         else solve_contacts(L, inv_h, contact_speed, 1, cs, ss);
-        if (act) {
-            solve_joints(L, h, inv_h, 1);
-            integrate_positions(L, h, inv_dt);
-            delta_geometry(L);
-        }
+        if (act) solve_joints(L, h, inv_h, 1);
+        if (L.staged) B3D_BARRIER();   /* the joints' velocities */
+        if (act) integrate_positions(L, h, inv_dt, share, stride);
+        if (L.staged) B3D_BARRIER();   /* the delta poses */
+        if (act) joint_geometry(L, share, stride);
         if (L.staged) solve_contacts_leveled(L, inv_h, contact_speed, 0, cs, ss, nlev);
         else solve_contacts(L, inv_h, contact_speed, 0, cs, ss);
         if (act) {
@@ -3152,8 +3161,9 @@ template <bool Masks = false>
 B3D_FN void step_world(const Lane& L, float dt, int substeps) { step_world<Masks>(L, dt, substeps, NoForces()); }
 
 /* A helper wave of a shared-narrowphase tile after its narrowphase share:
- * its share of the contact preparation, of the level-by-level warm start
- * and of every contact sweep, in step with wave 0 (the same barriers, in
+ * its share of the contact preparation, of the level-by-level warm start,
+ * of every contact sweep and of each substep's velocity and position
+ * updates and joint geometry, in step with wave 0 (the same barriers, in
  * the same order, as step_world's shared path).  Runs in all lanes; its
  * stepping lanes rank as wave 0's, so its body and delta record slots are
  * wave 0's, and its idle lanes have no contact levels (wave 0 set them). */
@@ -3176,7 +3186,13 @@ B3D_FN void sweep_helper(const Lane& L0, float dt, int substeps) {
     int nlev = tile_levels(L);
     warm_contacts_leveled(L, nlev);
     for (int s = 0; s < subs; s++) {
+        B3D_BARRIER();
+        if (L.active) integrate_velocities(L, L.st.wave, L.st.waves);
         solve_contacts_leveled(L, inv_h, contact_speed, 1, cs, ss, nlev);
+        B3D_BARRIER();
+        if (L.active) integrate_positions(L, h, inv_dt, L.st.wave, L.st.waves);
+        B3D_BARRIER();
+        if (L.active) joint_geometry(L, L.st.wave, L.st.waves);
         solve_contacts_leveled(L, inv_h, contact_speed, 0, cs, ss, nlev);
     }
 }
