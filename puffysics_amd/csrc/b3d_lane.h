@@ -491,6 +491,22 @@ B3D_FN void qs3(uint32_t* r, int k, V3 v) { qsf(r, k, v.x); qsf(r, k + 1, v.y); 
 B3D_FN Q qq(const uint32_t* r, int k) { return q4(qf(r, k), qf(r, k + 1), qf(r, k + 2), qf(r, k + 3)); }
 B3D_FN void qsq(uint32_t* r, int k, Q q) { qs3(r, k, q.v); qsf(r, k + 3, q.s); }
 B3D_FN uint64_t qu64(const uint32_t* r, int k) { return (uint64_t)qu(r, k) | ((uint64_t)qu(r, k + 1) << 32); }
+/* Loads of quad records that a sweep reads once, streaming (non-temporal)
+ * when S: in a large batch their next use is a whole sweep later, past what
+ * the L2 keeps, so they leave the L2 to the data reused within a sweep (in
+ * a small batch the records stay in the caches, and ordinary loads keep
+ * them there). */
+template <bool S>
+B3D_FN uint32_t qus(const uint32_t* r, int k) {
+#ifdef __HIP_DEVICE_COMPILE__
+    if constexpr (S) return __builtin_nontemporal_load(r + (k >> 2) * kRowWords + (k & 3));
+#endif
+    return qu(r, k);
+}
+template <bool S>
+B3D_FN float qfs(const uint32_t* r, int k) { return __builtin_bit_cast(float, qus<S>(r, k)); }
+template <bool S>
+B3D_FN V3 q3s(const uint32_t* r, int k) { return v3(qfs<S>(r, k), qfs<S>(r, k + 1), qfs<S>(r, k + 2)); }
 
 /* ---- packed word rows (word k of a record at quad row k / 4, word row
  * k % 4 of it; slot s at column s) ---- */
@@ -632,12 +648,13 @@ B3D_FN CHead rhead_load(const Lane& L, int c) {
     return h;
 }
 /* The head of contact c's packed record in a known slot. */
+template <bool S = false>
 B3D_FN CHead rhead_at(const Lane& L, int c, int slot) {
     const uint32_t* r = crec(L, c, slot);
-    CHead h = head_of(qu(r, R_AB), qu(r, R_INFO));
+    CHead h = head_of(qus<S>(r, R_AB), qus<S>(r, R_INFO));
     h.slot = slot;
-    h.friction = qf(r, R_FRICTION);
-    h.twist_mass = qf(r, R_TWIST_MASS);
+    h.friction = qfs<S>(r, R_FRICTION);
+    h.twist_mass = qfs<S>(r, R_TWIST_MASS);
     return h;
 }
 /* Inverse masses and world inertias of a record's bodies: exact zeros for a
@@ -2112,13 +2129,31 @@ struct CRow {
 
 /* Masses of a row, loaded when its solve starts; the softness is the
  * world's static or dynamic contact softness. */
+template <bool S>
 B3D_FN void crow_masses(const Lane& L, int c, CRow* r, Soft cs, Soft ss) {
-    rec_masses(crec(L, c, r->slot), r->flags, &r->ma, &r->ia, &r->mb, &r->ib);
+    const uint32_t* rc = crec(L, c, r->slot);
+    r->ma = 0.0f;
+    r->mb = 0.0f;
+    r->ia = m3zero();
+    r->ib = m3zero();
+    if (r->flags & CF_DYN_A) {
+        r->ma = qfs<S>(rc, R_MA);
+        r->ia.cx = q3s<S>(rc, R_IA);
+        r->ia.cy = q3s<S>(rc, R_IA + 3);
+        r->ia.cz = q3s<S>(rc, R_IA + 6);
+    }
+    if (r->flags & CF_DYN_B) {
+        r->mb = qfs<S>(rc, R_MB);
+        r->ib.cx = q3s<S>(rc, R_IB);
+        r->ib.cy = q3s<S>(rc, R_IB + 3);
+        r->ib.cz = v3(qfs<S>(rc, R_IB + 6), qfs<S>(rc, R_IB_ZYZ), qfs<S>(rc, R_IB_ZYZ + 1));
+    }
     r->soft = (r->flags & CF_STATIC) ? ss : cs;
 }
 
 /* Normal, points and friction data of a row: loaded one contact ahead.
  * Call where exactly the lanes with a contact c run. */
+template <bool S>
 B3D_FN void crow_load(const Lane& L, int c, CHead h, int relax, CRow* r, const int* ps = nullptr) {
     const uint32_t* rc = crec(L, c, h.slot);
     r->a = h.a;
@@ -2128,8 +2163,8 @@ B3D_FN void crow_load(const Lane& L, int c, CHead h, int relax, CRow* r, const i
     r->slot = h.slot;
     r->friction = h.friction;
     r->twist_mass = h.twist_mass;
-    r->n = q3(rc, R_N);
-    r->rolling = qf(rc, R_ROLLING);
+    r->n = q3s<S>(rc, R_N);
+    r->rolling = qfs<S>(rc, R_ROLLING);
     if (h.flags & CF_FIXED_A) {
         r->dpa = zero3();
         r->dqa = qid();
@@ -2153,28 +2188,28 @@ B3D_FN void crow_load(const Lane& L, int c, CHead h, int relax, CRow* r, const i
         q.tn = 0.0f;
         if (p >= h.pc) continue;
         const uint32_t* pr = prec(L, c, p, ps ? ps[p] : wave_slot(L));
-        q.ra = q3(pr, PR_RA);
-        q.nmass = qf(pr, PR_NMASS);
-        q.rb = q3(pr, PR_RB);
-        q.lever = relax ? qf(pr, PR_LEVER) : 0.0f;
-        q.base_sep = qf(rc, R_BASE_SEP + p);
-        q.ni = qf(rc, R_NI + 2 * p);
-        q.tn = qf(rc, R_TN + 2 * p);
+        q.ra = q3s<S>(pr, PR_RA);
+        q.nmass = qfs<S>(pr, PR_NMASS);
+        q.rb = q3s<S>(pr, PR_RB);
+        q.lever = relax ? qfs<S>(pr, PR_LEVER) : 0.0f;
+        q.base_sep = qfs<S>(rc, R_BASE_SEP + p);
+        q.ni = qfs<S>(rc, R_NI + 2 * p);
+        q.tn = qfs<S>(rc, R_TN + 2 * p);
     }
     if (relax) {
-        r->fi.x = qf(rc, R_FI);
-        r->fi.y = qf(rc, R_FI + 1);
-        r->twist_imp = qf(rc, R_TWIST);
-        r->t1 = q3(rc, R_T1);
+        r->fi.x = qfs<S>(rc, R_FI);
+        r->fi.y = qfs<S>(rc, R_FI + 1);
+        r->twist_imp = qfs<S>(rc, R_TWIST);
+        r->t1 = q3s<S>(rc, R_T1);
         /* tangent2 = tangent1 x normal as written by b3_contact_from_mani */
         r->t2 = cross(r->t1, r->n);
-        r->ca = q3(rc, R_CA);
-        r->cb = q3(rc, R_CB);
+        r->ca = q3s<S>(rc, R_CA);
+        r->cb = q3s<S>(rc, R_CB);
         /* the inverse of a symmetric 2x2 is stored symmetric bit for bit */
-        r->tm.cx.x = qf(rc, R_TM_XX);
-        r->tm.cx.y = qf(rc, R_TM_XY);
+        r->tm.cx.x = qfs<S>(rc, R_TM_XX);
+        r->tm.cx.y = qfs<S>(rc, R_TM_XY);
         r->tm.cy.x = r->tm.cx.y;
-        r->tm.cy.y = qf(rc, R_TM_YY);
+        r->tm.cy.y = qfs<S>(rc, R_TM_YY);
     }
 }
 
@@ -2285,22 +2320,23 @@ B3D_FN void crow_solve(const Lane& L, int c, CRow& r, float inv_h, float contact
 
 /* b3_solve_contacts (08:415-437): one Gauss-Seidel sweep in contact order.
  * Row c+1 (masses included) is in flight while row c is solved, and the
- * head of row c+2 while row c+1 loads. */
+ * head of row c+2 while row c+1 loads.  The one-wave step runs large
+ * batches, so the rows are streamed (qus). */
 B3D_FN void solve_contacts(const Lane& L, float inv_h, float contact_speed, int use_bias, Soft cs, Soft ss) {
     int cc = ldi(L.w, H_CONTACT_COUNT);
     if (cc <= 0) return;
     int relax = !use_bias;
     CHead h1 = rhead_load(L, 0);
     CRow cur, nxt;
-    crow_load(L, 0, h1, relax, &cur);
-    crow_masses(L, 0, &cur, cs, ss);
+    crow_load<true>(L, 0, h1, relax, &cur);
+    crow_masses<true>(L, 0, &cur, cs, ss);
     if (cc > 1) h1 = rhead_load(L, 1);
     for (int c = 0; c < cc; c++) {
         CHead h2 = h1;
         if (c + 2 < cc) h2 = rhead_load(L, c + 2);
         if (c + 1 < cc) {
-            crow_load(L, c + 1, h1, relax, &nxt);
-            crow_masses(L, c + 1, &nxt, cs, ss);
+            crow_load<true>(L, c + 1, h1, relax, &nxt);
+            crow_masses<true>(L, c + 1, &nxt, cs, ss);
         }
         crow_solve(L, c, cur, inv_h, contact_speed, use_bias);
         cur = nxt;
@@ -2342,8 +2378,8 @@ B3D_FN void solve_contacts_leveled(const Lane& L, float inv_h, float contact_spe
                 for (int p = 0; p < kMaxManifold; p++) ps[p] = (e >> (6 + 6 * p)) & 63;
                 CHead h = rhead_at(L, c, e & 63);
                 CRow r;
-                crow_load(L, c, h, relax, &r, ps);
-                crow_masses(L, c, &r, cs, ss);
+                crow_load<false>(L, c, h, relax, &r, ps);
+                crow_masses<false>(L, c, &r, cs, ss);
                 crow_solve(L, c, r, inv_h, contact_speed, use_bias);
             }
             first = end;
