@@ -199,7 +199,21 @@ B3D_FN Obb make_obb(V3 c, Q q, V3 h) {
     axes(q, &o.ax[0], &o.ax[1], &o.ax[2]);
     return o;
 }
-B3D_FN float half_i(V3 h, int i) { return i == 0 ? h.x : (i == 1 ? h.y : h.z); }
+/* Component or axis i of a box, chosen among values: the empty asm fixes
+ * the loaded components as values first, since a choice among the fields'
+ * addresses (what the optimiser makes of a choice among loads) keeps the
+ * box in private memory. */
+B3D_FN void opaque3(V3& v) {
+#ifdef __HIP_DEVICE_COMPILE__
+    asm("" : "+v"(v.x), "+v"(v.y), "+v"(v.z));
+#else
+    (void)v;
+#endif
+}
+B3D_FN float half_i(V3 h, int i) {
+    opaque3(h);
+    return i == 0 ? h.x : (i == 1 ? h.y : h.z);
+}
 /* Field-wise choice between two boxes (a pointer select would force both
  * into memory). */
 B3D_FN V3 vsel(bool c, V3 x, V3 y) { return v3(c ? x.x : y.x, c ? x.y : y.y, c ? x.z : y.z); }
@@ -213,7 +227,13 @@ B3D_FN Obb obb_sel(bool c, const Obb* x, const Obb* y) {
     return o;
 }
 /* Axis i of a box, selected without indexing so the box stays in registers. */
-B3D_FN V3 axis_i(const Obb* o, int i) { return i == 0 ? o->ax[0] : (i == 1 ? o->ax[1] : o->ax[2]); }
+B3D_FN V3 axis_i(const Obb* o, int i) {
+    V3 a0 = o->ax[0], a1 = o->ax[1], a2 = o->ax[2];
+    opaque3(a0);
+    opaque3(a1);
+    opaque3(a2);
+    return i == 0 ? a0 : (i == 1 ? a1 : a2);
+}
 B3D_FN V3 support(const Obb* o, V3 dir) {
     float sx = dot(o->ax[0], dir) < 0.0f ? -o->h.x : o->h.x;
     float sy = dot(o->ax[1], dir) < 0.0f ? -o->h.y : o->h.y;
