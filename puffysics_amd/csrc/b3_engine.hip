@@ -19,11 +19,12 @@
  *   b3k_step                   optional fused restore, then one b3_step per
  *                              selected lane; LDS holds the lane's clip
  *                              polygons, then its body velocities
- *   b3k_step_shared<Masks>     the same for batches of at most one tile per
+ *   b3k_step_shared<Masks, JL> the same for batches of at most one tile per
  *                              CU, with the narrowphase, the contact writes,
  *                              preparation and contact sweeps split over
  *                              four waves per tile (Masks: the candidate
- *                              search too, for 12 shapes or more)
+ *                              search too, for 12 shapes or more; JL: the
+ *                              joint rows in LDS, when they fit)
  *   b3k_apply                  dense force / torque / impulse inputs
  *   b3k_stats                  per-world B3StepStats
  */
@@ -133,8 +134,9 @@ __global__ __launch_bounds__(64) void b3k_step(uint32_t* live, const uint32_t* s
  * the step mask) run the same control flow with L.active false, their
  * work skipped and their candidate and level counts zero; the barrier
  * count (find_pairs' fixed barriers, then 1 + nlev per levelled pass, with
- * nlev the tile's largest level count) is the same in every lane. */
-template <bool Masks>
+ * nlev the tile's largest level count) is the same in every lane.
+ * JL: the joint rows live in LDS past the level rows (joint_rows_fit). */
+template <bool Masks, bool JL>
 __global__ __launch_bounds__(64 * kTileWaves) void b3k_step_shared(uint32_t* live, const uint32_t* snap,
         uint32_t* scratch, uint32_t* stage, size_t stage_tile_words, Geometry g, int count, float dt, int substeps,
         const unsigned char* step_mask, const unsigned char* reset_mask, unsigned int opts) {
@@ -158,8 +160,9 @@ __global__ __launch_bounds__(64 * kTileWaves) void b3k_step_shared(uint32_t* liv
     L.st = S;
     L.staged = true;
     L.active = stepping;
+    if (JL) L.jl = lds + (size_t)joint_lds_word(g) * kLanes + lane;
     if (wave == 0) {
-        step_world<Masks>(L, dt, substeps);
+        step_world<Masks, JL>(L, dt, substeps);
     } else {
         pair_helper<Masks>(L, S);
         sweep_helper(L, dt, substeps);
@@ -375,8 +378,10 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
     e->tile_words = (size_t)g.world_words * 64;
     e->lds_bytes = lds;
     err = b3i_lds_limit((const void*)b3k_step);
-    if (err == hipSuccess) err = b3i_lds_limit((const void*)b3k_step_shared<true>);
-    if (err == hipSuccess) err = b3i_lds_limit((const void*)b3k_step_shared<false>);
+    if (err == hipSuccess) err = b3i_lds_limit((const void*)b3k_step_shared<true, false>);
+    if (err == hipSuccess) err = b3i_lds_limit((const void*)b3k_step_shared<false, false>);
+    if (err == hipSuccess) err = b3i_lds_limit((const void*)b3k_step_shared<true, true>);
+    if (err == hipSuccess) err = b3i_lds_limit((const void*)b3k_step_shared<false, true>);
     if (err != hipSuccess) {
         free(e);
         return err;
@@ -405,9 +410,13 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
          * built (the helpers' clip rows are only used after them) */
         size_t bounds_lds = (size_t)(kClipWords + 6 * g.max_s) * kLanes * sizeof(float);
         if (bounds_lds > shared_lds) shared_lds = bounds_lds;
-        /* and, past wave 0's rows, the contact levels of the shared sweeps */
+        /* and, past wave 0's rows, the contact levels of the shared sweeps,
+         * then the joint rows when they fit */
         size_t sched_lds = (size_t)(lds_rows(g) + sched_words(g)) * kLanes * sizeof(float);
         if (sched_lds > shared_lds) shared_lds = sched_lds;
+        bool joint_lds = joint_rows_fit(g);
+        size_t joint_bytes = (size_t)(joint_lds_word(g) + g.max_j * kJLWords) * kLanes * sizeof(float);
+        if (joint_lds && joint_bytes > shared_lds) shared_lds = joint_bytes;
         if ((err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device)) != hipSuccess) {
             (void)b3_engine_destroy(e);
             return err;
@@ -419,6 +428,7 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
             e->stage_tile_words = (1 + stage_words) * kLanes;
             e->lds_shared_bytes = shared_lds;
             e->shared_masks = shared_masks(g);
+            e->joint_lds = joint_lds;
             err = hipMalloc((void**)&e->pair_stage, (size_t)e->tiles * e->stage_tile_words * sizeof(uint32_t));
             if (err != hipSuccess) {
                 (void)b3_engine_destroy(e);
@@ -530,14 +540,10 @@ hipError_t b3_batch_step_gpu(B3Engine* e, float dt, int substeps, const unsigned
     if (dt == 0.0f) return reset_mask ? b3_batch_restore_gpu(e, reset_mask, stream) : hipSuccess;
     if (e->options & B3_ENGINE_ART_CONTACTS) return b3i_step_art(e, dt, substeps, step_mask, reset_mask, stream);
     if (e->pair_stage && !(e->options & B3_ENGINE_ONE_WAVE_PER_TILE)) {
-        if (e->shared_masks)
-            b3k_step_shared<true><<<e->tiles, 64 * kTileWaves, e->lds_shared_bytes, stream>>>(e->live, e->snap,
-                e->scratch, e->pair_stage, e->stage_tile_words, e->g, e->count, dt, substeps, step_mask, reset_mask,
-                e->options);
-        else
-            b3k_step_shared<false><<<e->tiles, 64 * kTileWaves, e->lds_shared_bytes, stream>>>(e->live, e->snap,
-                e->scratch, e->pair_stage, e->stage_tile_words, e->g, e->count, dt, substeps, step_mask, reset_mask,
-                e->options);
+        auto kernel = e->shared_masks ? (e->joint_lds ? b3k_step_shared<true, true> : b3k_step_shared<true, false>)
+                                      : (e->joint_lds ? b3k_step_shared<false, true> : b3k_step_shared<false, false>);
+        kernel<<<e->tiles, 64 * kTileWaves, e->lds_shared_bytes, stream>>>(e->live, e->snap, e->scratch,
+            e->pair_stage, e->stage_tile_words, e->g, e->count, dt, substeps, step_mask, reset_mask, e->options);
         return hipGetLastError();
     }
     b3k_step<<<e->tiles, 64, e->lds_bytes, stream>>>(e->live, e->snap, e->scratch, e->g, e->count, dt, substeps,

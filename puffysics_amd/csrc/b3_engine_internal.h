@@ -27,6 +27,7 @@ struct B3Engine {
     size_t stage_tile_words;
     size_t lds_shared_bytes; /* LDS of a workgroup of kTileWaves waves */
     bool shared_masks;       /* ... which also split the candidate search (b3d::shared_masks) */
+    bool joint_lds;          /* ... and keep the joint rows in LDS (b3d::joint_rows_fit) */
 };
 
 /* Waves per tile when the narrowphase is shared. */

@@ -359,6 +359,8 @@ struct Lane {
     bool active;        /* the lane steps its world.  Only a shared tile
                            (staged) runs idle lanes: they go through
                            every workgroup barrier with their work skipped */
+    float* jl;          /* LDS joint rows + lane (shared tiles with room for
+                           them, joint_rows_fit), else null */
     Geometry g;
 };
 
@@ -383,6 +385,7 @@ B3D_FN Lane lane_view(uint32_t* live, uint32_t* scratch, float* vel_rows, const 
     L.w = live + (size_t)tile * g.world_words * kLanes + lane;
     L.scr = scratch ? scratch + (size_t)tile * g.tile_scr_words + lane : nullptr;
     L.sq = scratch ? scratch + (size_t)tile * g.tile_scr_words + (size_t)g.scr_words * kLanes : nullptr;
+    L.jl = nullptr;
     L.vel = vel_rows ? vel_rows + lane : nullptr;
     L.lane = lane;
     L.active = true;
@@ -2650,8 +2653,200 @@ B3D_FN void jrow_load(const Lane& L, int j, JHead h, JRow* r) {
     }
 }
 
+/* Joint rows in LDS (shared tiles, when they fit beside the velocity and
+ * level rows): per joint, the head, the fields jrow_load reads from the
+ * joint's words and the step's constants of the scratch record (fixed for
+ * the step, staged once by stage_joint_rows), and the accumulated impulses,
+ * which the solves update there and joint_writeback returns to the world
+ * at the end of the step.  The delta-state geometry stays in the scratch
+ * record (joint_geometry writes it), loaded one solve ahead.  A weld's
+ * fields share the hinge fields' words. */
+constexpr int JL_AB = 0, JL_INFO = 1, JL_MA = 2, JL_IA = 3, JL_MB = 12, JL_IB = 13, JL_SOFT = 22, JL_LIN_IMP = 25,
+              JL_AXIAL = 28, JL_AXIS = 29, JL_IAX = 32, JL_IBX = 35, JL_MAXT = 38, JL_TARGET = 39, JL_SSOFT = 40,
+              JL_SPEED = 43, JL_LOWER = 44, JL_UPPER = 45, JL_PERP_IMP = 46, JL_SPRING_IMP = 48, JL_MOTOR_IMP = 49,
+              JL_LOWER_IMP = 50, JL_UPPER_IMP = 51,
+              JL_LIN_HZ = 28, JL_LIN_SPRING = 29, JL_ANG_HZ = 32, JL_ANG_SPRING = 33, JL_ANG_MASS = 36,
+              JL_ANG_IMP = 45, kJLWords = 52;
+/* LDS words per lane that a shared tile may use (160 KB over 64 lanes). */
+constexpr int kSharedLdsWordsMax = 640;
+B3D_FN int joint_lds_word(const Geometry& g) { return lds_rows(g) + sched_words(g); }
+B3D_FN bool joint_rows_fit(const Geometry& g) {
+    return g.max_j > 0 && joint_lds_word(g) + g.max_j * kJLWords <= kSharedLdsWordsMax;
+}
+B3D_FN float* jl_rec(const Lane& L, int j) { return L.jl + j * kJLWords * kLanes; }
+B3D_FN float jlf(const float* q, int k) { return q[k * kLanes]; }
+B3D_FN V3 jl3(const float* q, int k) { return v3(q[k * kLanes], q[(k + 1) * kLanes], q[(k + 2) * kLanes]); }
+B3D_FN M3 jlm3(const float* q, int k) { M3 m; m.cx = jl3(q, k); m.cy = jl3(q, k + 3); m.cz = jl3(q, k + 6); return m; }
+B3D_FN Soft jlsoft(const float* q, int k) {
+    Soft s;
+    s.bias_rate = q[k * kLanes];
+    s.mass_scale = q[(k + 1) * kLanes];
+    s.impulse_scale = q[(k + 2) * kLanes];
+    return s;
+}
+B3D_FN void jlsf(float* q, int k, float v) { q[k * kLanes] = v; }
+B3D_FN void jls3(float* q, int k, V3 v) { jlsf(q, k, v.x); jlsf(q, k + 1, v.y); jlsf(q, k + 2, v.z); }
+B3D_FN void jlsm3(float* q, int k, M3 m) { jls3(q, k, m.cx); jls3(q, k + 3, m.cy); jls3(q, k + 6, m.cz); }
+B3D_FN void jlssoft(float* q, int k, Soft s) { jlsf(q, k, s.bias_rate); jlsf(q, k + 1, s.mass_scale); jlsf(q, k + 2, s.impulse_scale); }
+/* An accumulated impulse of joint j: to the LDS row (JL) or the joint's words. */
+template <bool JL>
+B3D_FN void jimp_store(const Lane& L, int j, int world_word, int lds_word, float v) {
+    if constexpr (JL) jlsf(jl_rec(L, j), lds_word, v);
+    else stf(L.w, jw(L, j, world_word), v);
+}
+template <bool JL>
+B3D_FN void jimp_store3(const Lane& L, int j, int world_word, int lds_word, V3 v) {
+    if constexpr (JL) jls3(jl_rec(L, j), lds_word, v);
+    else st3(L.w, jw(L, j, world_word), v);
+}
+
+/* The step's joint rows to LDS (wave 0, after prepare_joints): each row as
+ * jrow_load reads it, less the delta-state geometry. */
+B3D_FN void stage_joint_rows(const Lane& L) {
+    int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
+    for (int j = 0; j < nj; j++) {
+        JRow r = {};
+        jrow_load(L, j, jhead_load(L, j), &r);
+        float* q = jl_rec(L, j);
+        jlsf(q, JL_AB, __builtin_bit_cast(float, (uint32_t)(r.a | (r.b << 16))));
+        jlsf(q, JL_INFO, __builtin_bit_cast(float, r.info));
+        jlsf(q, JL_MA, r.ma);
+        jlsm3(q, JL_IA, r.ia);
+        jlsf(q, JL_MB, r.mb);
+        jlsm3(q, JL_IB, r.ib);
+        jlssoft(q, JL_SOFT, r.soft);
+        jls3(q, JL_LIN_IMP, r.lin_imp);
+        if (r.info & JF_WELD) {
+            jlsf(q, JL_LIN_HZ, r.lin_hz);
+            jlssoft(q, JL_LIN_SPRING, r.lin_spring);
+            jlsf(q, JL_ANG_HZ, r.ang_hz);
+            jlssoft(q, JL_ANG_SPRING, r.ang_spring);
+            jlsm3(q, JL_ANG_MASS, r.ang_mass);
+            jls3(q, JL_ANG_IMP, r.ang_imp);
+        } else {
+            jlsf(q, JL_AXIAL, r.axial_mass);
+            jls3(q, JL_AXIS, r.axis);
+            jls3(q, JL_IAX, r.ia_ax);
+            jls3(q, JL_IBX, r.ib_ax);
+            jlsf(q, JL_MAXT, r.max_torque);
+            jlsf(q, JL_TARGET, r.target);
+            jlssoft(q, JL_SSOFT, r.spring_soft);
+            jlsf(q, JL_SPEED, r.speed);
+            jlsf(q, JL_LOWER, r.lower);
+            jlsf(q, JL_UPPER, r.upper);
+            jlsf(q, JL_PERP_IMP, r.perp_imp.x);
+            jlsf(q, JL_PERP_IMP + 1, r.perp_imp.y);
+            jlsf(q, JL_SPRING_IMP, r.spring_imp);
+            jlsf(q, JL_MOTOR_IMP, r.motor_imp);
+            jlsf(q, JL_LOWER_IMP, r.lower_imp);
+            jlsf(q, JL_UPPER_IMP, r.upper_imp);
+        }
+    }
+}
+
+/* The LDS rows' impulses back to the joints' words (the words the solves
+ * update; a disabled row's impulse is the world's own value, unchanged). */
+B3D_FN void joint_writeback(const Lane& L) {
+    int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
+    uint32_t* w = L.w;
+    for (int j = 0; j < nj; j++) {
+        const float* q = jl_rec(L, j);
+        int info = __builtin_bit_cast(int, jlf(q, JL_INFO));
+        st3(w, jw(L, j, J_LINEAR_IMPULSE), jl3(q, JL_LIN_IMP));
+        if (info & JF_FIXED) continue;
+        if (info & JF_WELD) {
+            st3(w, jw(L, j, J_ANGULAR_IMPULSE), jl3(q, JL_ANG_IMP));
+            continue;
+        }
+        stf(w, jw(L, j, J_PERP_IMPULSE), jlf(q, JL_PERP_IMP));
+        stf(w, jw(L, j, J_PERP_IMPULSE + 1), jlf(q, JL_PERP_IMP + 1));
+        if (info & JF_SPRING) stf(w, jw(L, j, J_SPRING_IMPULSE), jlf(q, JL_SPRING_IMP));
+        if (info & JF_MOTOR) stf(w, jw(L, j, J_MOTOR_IMPULSE), jlf(q, JL_MOTOR_IMP));
+        if (info & JF_LIMIT) {
+            stf(w, jw(L, j, J_LOWER_IMPULSE), jlf(q, JL_LOWER_IMP));
+            stf(w, jw(L, j, J_UPPER_IMPULSE), jlf(q, JL_UPPER_IMP));
+        }
+    }
+}
+
+/* A row's delta-state geometry from the scratch record (every field, in
+ * one batch of loads), and the rest of the row from its LDS row. */
+struct JGeo { V3 ra, rb, psep, px, py, cv; M3 pki; float kxx, kxy, kyy, kinv, relx, rely, tw; };
+B3D_FN JGeo jgeo_load(const Lane& L, int j) {
+    const uint32_t* g = joint_rec(L, j);
+    JGeo o;
+    o.tw = ldf(g, JS_TW);
+    o.relx = ldf(g, JS_RELX);
+    o.rely = ldf(g, JS_RELY);
+    o.px = ld3(g, JS_PX);
+    o.py = ld3(g, JS_PY);
+    o.ra = ld3(g, JS_RA);
+    o.rb = ld3(g, JS_RB);
+    o.psep = ld3(g, JS_PSEP);
+    o.cv = ld3(g, JS_CV);
+    o.pki = ldm3(g, JS_PKI);
+    o.kxx = ldf(g, JS_KXX);
+    o.kxy = ldf(g, JS_KXY);
+    o.kyy = ldf(g, JS_KYY);
+    o.kinv = ldf(g, JS_KINV);
+    return o;
+}
+B3D_FN void jrow_lds(const Lane& L, int j, const JGeo& g, JRow* r) {
+    const float* q = jl_rec(L, j);
+    uint32_t ab = __builtin_bit_cast(uint32_t, jlf(q, JL_AB));
+    r->a = (int)(ab & 0xffffu);
+    r->b = (int)(ab >> 16);
+    r->info = __builtin_bit_cast(int, jlf(q, JL_INFO));
+    r->ma = jlf(q, JL_MA);
+    r->ia = jlm3(q, JL_IA);
+    r->mb = jlf(q, JL_MB);
+    r->ib = jlm3(q, JL_IB);
+    r->soft = jlsoft(q, JL_SOFT);
+    r->lin_imp = jl3(q, JL_LIN_IMP);
+    r->ra = g.ra;
+    r->rb = g.rb;
+    r->psep = g.psep;
+    r->pki = g.pki;
+    if (r->info & JF_WELD) {
+        r->lin_hz = jlf(q, JL_LIN_HZ);
+        r->lin_spring = jlsoft(q, JL_LIN_SPRING);
+        r->ang_hz = jlf(q, JL_ANG_HZ);
+        r->ang_spring = jlsoft(q, JL_ANG_SPRING);
+        r->ang_mass = jlm3(q, JL_ANG_MASS);
+        r->ang_imp = jl3(q, JL_ANG_IMP);
+        r->cv = g.cv;
+        return;
+    }
+    r->axial_mass = jlf(q, JL_AXIAL);
+    r->axis = jl3(q, JL_AXIS);
+    r->ia_ax = jl3(q, JL_IAX);
+    r->ib_ax = jl3(q, JL_IBX);
+    r->max_torque = jlf(q, JL_MAXT);
+    r->target = jlf(q, JL_TARGET);
+    r->spring_soft = jlsoft(q, JL_SSOFT);
+    r->speed = jlf(q, JL_SPEED);
+    r->lower = jlf(q, JL_LOWER);
+    r->upper = jlf(q, JL_UPPER);
+    r->perp_imp.x = jlf(q, JL_PERP_IMP);
+    r->perp_imp.y = jlf(q, JL_PERP_IMP + 1);
+    r->spring_imp = jlf(q, JL_SPRING_IMP);
+    r->motor_imp = jlf(q, JL_MOTOR_IMP);
+    r->lower_imp = jlf(q, JL_LOWER_IMP);
+    r->upper_imp = jlf(q, JL_UPPER_IMP);
+    r->px = g.px;
+    r->py = g.py;
+    r->kxx = g.kxx;
+    r->kxy = g.kxy;
+    r->kyy = g.kyy;
+    r->kinv = g.kinv;
+    r->relx = g.relx;
+    r->rely = g.rely;
+    r->tw = g.tw;
+}
+
 /* Point rows shared by weld and revolute (06:257-282), with the anchors,
  * separation and inverted mass of the current delta state. */
+template <bool JL>
 B3D_FN void solve_point(const Lane& L, int j, const JRow& r, V3* va, V3* wa, V3* vb, V3* wb, Soft soft,
         int use_bias) {
     V3 cdot = sub(add(*vb, cross(*wb, r.rb)), add(*va, cross(*wa, r.ra)));
@@ -2666,7 +2861,7 @@ B3D_FN void solve_point(const Lane& L, int j, const JRow& r, V3* va, V3* wa, V3*
      * inverse taken once per delta state (joint_geometry) */
     V3 bsol = mv(r.pki, add(cdot, bias));
     V3 impulse = msub(scale(bsol, -mscale), iscale, r.lin_imp);
-    st3(L.w, jw(L, j, J_LINEAR_IMPULSE), add(r.lin_imp, impulse));
+    jimp_store3<JL>(L, j, J_LINEAR_IMPULSE, JL_LIN_IMP, add(r.lin_imp, impulse));
     *va = msub(*va, r.ma, impulse);
     *wa = sub(*wa, mv(r.ia, cross(r.ra, impulse)));
     *vb = madd(*vb, r.mb, impulse);
@@ -2674,6 +2869,7 @@ B3D_FN void solve_point(const Lane& L, int j, const JRow& r, V3* va, V3* wa, V3*
 }
 
 /* b3_solve_weld (06:285-332). */
+template <bool JL>
 B3D_FN void solve_weld(const Lane& L, int j, const JRow& r, int use_bias) {
     V3 va = vlin(L, r.a), wa = vang(L, r.a), vb = vlin(L, r.b), wb = vang(L, r.b);
     if (!(r.info & JF_FIXED)) {
@@ -2686,12 +2882,12 @@ B3D_FN void solve_weld(const Lane& L, int j, const JRow& r, int use_bias) {
         }
         V3 cdot = sub(wb, wa);
         V3 impulse = msub(scale(mv(r.ang_mass, add(cdot, bias)), -mscale), iscale, r.ang_imp);
-        st3(L.w, jw(L, j, J_ANGULAR_IMPULSE), add(r.ang_imp, impulse));
+        jimp_store3<JL>(L, j, J_ANGULAR_IMPULSE, JL_ANG_IMP, add(r.ang_imp, impulse));
         wa = sub(wa, mv(r.ia, impulse));
         wb = add(wb, mv(r.ib, impulse));
     }
     int lin_bias = use_bias || r.lin_hz > 0.0f;
-    solve_point(L, j, r, &va, &wa, &vb, &wb, r.lin_spring, lin_bias);
+    solve_point<JL>(L, j, r, &va, &wa, &vb, &wb, r.lin_spring, lin_bias);
     if (is_dyn_flag(L, r.a)) {
         set_vlin(L, r.a, va);
         set_vang(L, r.a, wa);
@@ -2718,8 +2914,8 @@ B3D_FN float limit_impulse(float c, float cdot, float inv_h, int use_bias, Soft 
 
 /* b3_solve_revolute (06:436-642): spring, motor, lower and upper limit,
  * two perpendicular angular rows, then the point rows. */
+template <bool JL>
 B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float inv_h, int use_bias) {
-    uint32_t* w = L.w;
     V3 va = vlin(L, r.a), wa = vang(L, r.a), vb = vlin(L, r.b), wb = vang(L, r.b);
     V3 axis = r.axis;
     int fixed = r.info & JF_FIXED;
@@ -2741,7 +2937,7 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
             nimp = clampf(nimp, -maxp, maxp);
         }
         dimp = nimp - old;
-        stf(w, jw(L, j, J_SPRING_IMPULSE), nimp);
+        jimp_store<JL>(L, j, J_SPRING_IMPULSE, JL_SPRING_IMP, nimp);
         wa = msub(wa, dimp, ia_ax);
         wb = madd(wb, dimp, ib_ax);
     }
@@ -2752,7 +2948,7 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
             if (tw <= r.lower + 0.01f && r.speed < 0.0f) blocked = 1;
         }
         if (blocked) {
-            stf(w, jw(L, j, J_MOTOR_IMPULSE), 0.0f);
+            jimp_store<JL>(L, j, J_MOTOR_IMPULSE, JL_MOTOR_IMP, 0.0f);
         } else {
             float old = r.motor_imp;
             float cdot = dot(sub(wb, wa), axis) - r.speed;
@@ -2761,7 +2957,7 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
             float maxp = r.max_torque * h;
             nimp = clampf(nimp, -maxp, maxp);
             dimp = nimp - old;
-            stf(w, jw(L, j, J_MOTOR_IMPULSE), nimp);
+            jimp_store<JL>(L, j, J_MOTOR_IMPULSE, JL_MOTOR_IMP, nimp);
             wa = msub(wa, dimp, ia_ax);
             wb = madd(wb, dimp, ib_ax);
         }
@@ -2769,13 +2965,13 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
     if (en_limit && !fixed) {
         float old = r.lower_imp;
         float lo = limit_impulse(tw - r.lower, dot(sub(wb, wa), axis), inv_h, use_bias, r.soft, axial_mass, old);
-        stf(w, jw(L, j, J_LOWER_IMPULSE), lo);
+        jimp_store<JL>(L, j, J_LOWER_IMPULSE, JL_LOWER_IMP, lo);
         float dimp = lo - old;
         wa = msub(wa, dimp, ia_ax);
         wb = madd(wb, dimp, ib_ax);
         old = r.upper_imp;
         float up = limit_impulse(r.upper - tw, dot(sub(wa, wb), axis), inv_h, use_bias, r.soft, axial_mass, old);
-        stf(w, jw(L, j, J_UPPER_IMPULSE), up);
+        jimp_store<JL>(L, j, J_UPPER_IMPULSE, JL_UPPER_IMP, up);
         dimp = up - old;
         wa = madd(wa, dimp, ia_ax);
         wb = msub(wb, dimp, ib_ax);
@@ -2807,13 +3003,13 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
         V2 dimp;
         dimp.x = -mscale * sol.x - iscale * r.perp_imp.x;
         dimp.y = -mscale * sol.y - iscale * r.perp_imp.y;
-        stf(w, jw(L, j, J_PERP_IMPULSE), r.perp_imp.x + dimp.x);
-        stf(w, jw(L, j, J_PERP_IMPULSE + 1), r.perp_imp.y + dimp.y);
+        jimp_store<JL>(L, j, J_PERP_IMPULSE, JL_PERP_IMP, r.perp_imp.x + dimp.x);
+        jimp_store<JL>(L, j, J_PERP_IMPULSE + 1, JL_PERP_IMP + 1, r.perp_imp.y + dimp.y);
         V3 ang = add(scale(r.px, dimp.x), scale(r.py, dimp.y));
         wa = sub(wa, mv(r.ia, ang));
         wb = add(wb, mv(r.ib, ang));
     }
-    solve_point(L, j, r, &va, &wa, &vb, &wb, r.soft, use_bias);
+    solve_point<JL>(L, j, r, &va, &wa, &vb, &wb, r.soft, use_bias);
     if (is_dyn_flag(L, r.a)) {
         set_vlin(L, r.a, va);
         set_vang(L, r.a, wa);
@@ -2830,10 +3026,27 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
  * select which fields to load) fetched one solve ahead: a second row in
  * flight during a solve costs more in registers than the one round trip it
  * would hide. */
+template <bool JL = false>
 B3D_FN void solve_joints(const Lane& L, float h, float inv_h, int use_bias) {
     int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
     if (nj <= 0) return;
     int total = (use_bias ? kJointIters : kRelaxIters) * nj;
+    if constexpr (JL) {
+        /* rows from LDS; each row's geometry loaded during the solve before
+         * it (the geometry does not change during a pass) */
+        JGeo g = jgeo_load(L, 0);
+        int j = 0;
+        for (int t = 0; t < total; t++) {
+            JRow cur;
+            jrow_lds(L, j, g, &cur);
+            int jn = j + 1 == nj ? 0 : j + 1;
+            if (t + 1 < total) g = jgeo_load(L, jn);
+            if (cur.info & JF_WELD) solve_weld<true>(L, j, cur, use_bias);
+            else solve_revolute<true>(L, j, cur, h, inv_h, use_bias);
+            j = jn;
+        }
+        return;
+    }
     JHead head = jhead_load(L, 0);
     int j = 0;
     for (int t = 0; t < total; t++) {
@@ -2841,8 +3054,8 @@ B3D_FN void solve_joints(const Lane& L, float h, float inv_h, int use_bias) {
         jrow_load(L, j, head, &cur);
         int jn = j + 1 == nj ? 0 : j + 1;
         if (t + 1 < total) head = jhead_load(L, jn);
-        if (cur.info & JF_WELD) solve_weld(L, j, cur, use_bias);
-        else solve_revolute(L, j, cur, h, inv_h, use_bias);
+        if (cur.info & JF_WELD) solve_weld<false>(L, j, cur, use_bias);
+        else solve_revolute<false>(L, j, cur, h, inv_h, use_bias);
         j = jn;
     }
 }
@@ -3102,7 +3315,7 @@ B3D_FN void integrate_velocities_law(const Lane& L, float h, const Law& law) {
  * the force law `law` in the B3_USER_FORCES hook.  Body velocities are
  * staged in the velocity rows after contact generation (which uses the
  * same rows for clip polygons) and written back at the end. */
-template <bool Masks = false, class Law>
+template <bool Masks = false, class Law, bool JL = false>
 B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
     if (!(dt > 0.0f)) return;
     Lane L = L0;
@@ -3142,6 +3355,7 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
         if (act) {
             sched_build(L);
             prepare_joints(L, h);
+            if constexpr (JL) stage_joint_rows(L);
         } else {
             sch_set(L, 0, 0);      /* no contact levels */
         }
@@ -3173,7 +3387,7 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
         }
         if (L.staged) solve_contacts_leveled(L, inv_h, contact_speed, 1, cs, ss, nlev);
         else solve_contacts(L, inv_h, contact_speed, 1, cs, ss);
-        if (act) solve_joints(L, h, inv_h, 1);
+        if (act) solve_joints<JL>(L, h, inv_h, 1);
         if (L.staged) B3D_BARRIER();   /* the joints' velocities */
         if (act) integrate_positions(L, h, inv_dt, share, stride);
         if (L.staged) B3D_BARRIER();   /* the delta poses */
@@ -3181,20 +3395,23 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
         if (L.staged) solve_contacts_leveled(L, inv_h, contact_speed, 0, cs, ss, nlev);
         else solve_contacts(L, inv_h, contact_speed, 0, cs, ss);
         if (act) {
-            solve_joints(L, h, inv_h, 0);
+            solve_joints<JL>(L, h, inv_h, 0);
             if (rest_wave) apply_restitution(L, rest_threshold);
         }
     }
     if (act) {
         contact_writeback(L);
+        if constexpr (JL) joint_writeback(L);
         finalize(L);
         vel_store(L);
     }
 }
 
-/* b3_step without a hook. */
-template <bool Masks = false>
-B3D_FN void step_world(const Lane& L, float dt, int substeps) { step_world<Masks>(L, dt, substeps, NoForces()); }
+/* b3_step without a hook; JL: the joint rows in LDS (L.jl, shared tiles). */
+template <bool Masks = false, bool JL = false>
+B3D_FN void step_world(const Lane& L, float dt, int substeps) {
+    step_world<Masks, NoForces, JL>(L, dt, substeps, NoForces());
+}
 
 /* A helper wave of a shared-narrowphase tile after its narrowphase share:
  * its share of the contact preparation, of the level-by-level warm start,

@@ -100,7 +100,13 @@ void emu_step(uint32_t* tiles, int count, unsigned long long sig, float dt, int 
  * wave per tile: the staged narrowphase, the parallel preparation's
  * staging, the contact levels, and the level-by-level warm start and
  * sweeps (with one wave, a level's contacts in level order rather than
- * contact order, which must not change any result). */
+ * contact order, which must not change any result), with the joint rows in
+ * LDS when they fit, as the device launch chooses. */
+/* Joint rows in LDS for emu_step_shared: -1 as the device chooses
+ * (joint_rows_fit), 0 never, 1 always (host memory has no LDS limit). */
+static int g_joint_lds = -1;
+void emu_set_joint_lds(int mode) { g_joint_lds = mode; }
+
 void emu_step_shared(uint32_t* tiles, int count, unsigned long long sig, float dt, int substeps,
         const unsigned char* step_mask, int masks) {
     Geometry g;
@@ -111,12 +117,15 @@ void emu_step_shared(uint32_t* tiles, int count, unsigned long long sig, float d
     int rows = shared_lds_words(g);
     if (kClipWords + 6 * g.max_s > rows) rows = kClipWords + 6 * g.max_s;
     if (lds_rows(g) + sched_words(g) > rows) rows = lds_rows(g) + sched_words(g);
+    bool jl = g_joint_lds < 0 ? joint_rows_fit(g) : (g_joint_lds > 0 && g.max_j > 0);
+    if (jl && joint_lds_word(g) + g.max_j * kJLWords > rows) rows = joint_lds_word(g) + g.max_j * kJLWords;
     std::vector<float> lds((size_t)rows * kLanes);
     size_t max_cand = (size_t)g.max_s * (size_t)(g.max_s - 1) / 2;
     size_t words = max_cand * kManiWords;
     if ((size_t)stage_sched_words(g) > words) words = (size_t)stage_sched_words(g);
     size_t stage_tile = (1 + words) * kLanes;
     std::vector<uint32_t> stage((size_t)ntiles * stage_tile);
+    bool use_masks = masks < 0 ? shared_masks(g) : (masks > 0 && g.max_s <= 64);
     for (int w = 0; w < count; w++) {
         if (step_mask && !step_mask[w]) continue;
         Lane L = lane_of(tiles, scratch.data(), lds.data(), g, w);
@@ -128,8 +137,15 @@ void emu_step_shared(uint32_t* tiles, int count, unsigned long long sig, float d
         S.lds_bounds = 1;
         L.st = S;
         L.staged = true;
-        if (masks < 0 ? shared_masks(g) : (masks > 0 && g.max_s <= 64)) step_world<true>(L, dt, substeps);
-        else step_world<false>(L, dt, substeps);
+        if (jl) {
+            L.jl = lds.data() + (size_t)joint_lds_word(g) * kLanes + w % kLanes;
+            if (use_masks) step_world<true, true>(L, dt, substeps);
+            else step_world<false, true>(L, dt, substeps);
+        } else if (use_masks) {
+            step_world<true>(L, dt, substeps);
+        } else {
+            step_world<false>(L, dt, substeps);
+        }
     }
 }
 

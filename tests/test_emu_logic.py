@@ -127,7 +127,7 @@ def test_lane_code_default_options_feature_worlds():
     assert has.any() and not has.all()
 
 
-@pytest.mark.parametrize("scene,count,steps", [(1, 70, 80), (2, 70, 65), (4, 66, 12), (5, 130, 40)])
+@pytest.mark.parametrize("scene,count,steps", [(1, 70, 80), (2, 70, 65), (3, 70, 40), (4, 66, 12), (5, 130, 40)])
 def test_shared_tile_path_on_the_host(scene, count, steps):
     """The shared-tile path of small batches (staged narrowphase, staged
     preparation, contact levels, level-by-level warm start and sweeps), run
@@ -178,17 +178,26 @@ def test_shared_candidate_search_variants_on_the_host(scene, count, steps, masks
     assert len(bad) == 0, "%d differing words, first %s" % (len(bad), bad[:4].tolist())
 
 
-@pytest.mark.parametrize("masks", [-1, 0])
-def test_shared_tile_path_on_the_host_feature_worlds(masks):
+@pytest.mark.parametrize("masks,joint_lds", [(-1, -1), (0, -1), (-1, 1), (0, 1)])
+def test_shared_tile_path_on_the_host_feature_worlds(masks, joint_lds):
     """The same on the coverage worlds (restitution, rolling, kinematic and
-    locked bodies, welds and hinges)."""
-    from b3test import EmuSig, feature_worlds, oracle_step_batch
+    locked bodies, welds and hinges), also with the joint rows in LDS
+    (joint_lds=1: staged once per step, impulses updated there and written
+    back at the end; these capacities leave the device no room for them)."""
+    import ctypes as C
+    from b3test import EmuSig, emu, feature_worlds, oracle_step_batch
     from puffysics_amd.creation import CUSTOM_SIG
     worlds = feature_worlds(40, hinges=True)
     ref = clone(worlds)
     emu_ = EmuSig(CUSTOM_SIG, worlds)
-    for _ in range(15):
-        oracle_step_batch(ref, CUSTOM_SIG, 1.0 / 60.0, 4)
-        emu_.step_shared(1.0 / 60.0, 4, masks=masks)
+    lib = emu()
+    lib.emu_set_joint_lds.argtypes = [C.c_int]
+    lib.emu_set_joint_lds(joint_lds)
+    try:
+        for _ in range(15):
+            oracle_step_batch(ref, CUSTOM_SIG, 1.0 / 60.0, 4)
+            emu_.step_shared(1.0 / 60.0, 4, masks=masks)
+    finally:
+        lib.emu_set_joint_lds(-1)
     bad = diff_words(emu_.worlds(), ref, CUSTOM_SIG)
     assert len(bad) == 0, "%d differing words, first %s" % (len(bad), bad[:4].tolist())
