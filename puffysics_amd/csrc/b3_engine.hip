@@ -165,7 +165,7 @@ __global__ __launch_bounds__(64 * kTileWaves) void b3k_step_shared(uint32_t* liv
         step_world<Masks, JL>(L, dt, substeps);
     } else {
         pair_helper<Masks>(L, S);
-        sweep_helper(L, dt, substeps);
+        sweep_helper<JL>(L, dt, substeps);
     }
 }
 
@@ -415,7 +415,7 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
         size_t sched_lds = (size_t)(lds_rows(g) + sched_words(g)) * kLanes * sizeof(float);
         if (sched_lds > shared_lds) shared_lds = sched_lds;
         bool joint_lds = joint_rows_fit(g);
-        size_t joint_bytes = (size_t)(joint_lds_word(g) + g.max_j * kJLWords) * kLanes * sizeof(float);
+        size_t joint_bytes = (size_t)(joint_lds_word(g) + joint_lds_words(g)) * kLanes * sizeof(float);
         if (joint_lds && joint_bytes > shared_lds) shared_lds = joint_bytes;
         if ((err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, e->device)) != hipSuccess) {
             (void)b3_engine_destroy(e);

@@ -2670,8 +2670,14 @@ constexpr int JL_AB = 0, JL_INFO = 1, JL_MA = 2, JL_IA = 3, JL_MB = 12, JL_IB = 
 /* LDS words per lane that a shared tile may use (160 KB over 64 lanes). */
 constexpr int kSharedLdsWordsMax = 640;
 B3D_FN int joint_lds_word(const Geometry& g) { return lds_rows(g) + sched_words(g); }
+/* Past the rows, the joint levels (joint_sched_build): the lane's level
+ * count, per level one past its last entry, the entries (joint numbers) in
+ * level order, and each body's last level. */
+static_assert(kJointIters == kRelaxIters, "one joint schedule serves both passes");
+B3D_FN int jsched_words(const Geometry& g) { return 1 + 2 * kJointIters * g.max_j + g.max_b; }
+B3D_FN int joint_lds_words(const Geometry& g) { return g.max_j * kJLWords + jsched_words(g); }
 B3D_FN bool joint_rows_fit(const Geometry& g) {
-    return g.max_j > 0 && joint_lds_word(g) + g.max_j * kJLWords <= kSharedLdsWordsMax;
+    return g.max_j > 0 && joint_lds_word(g) + joint_lds_words(g) <= kSharedLdsWordsMax;
 }
 B3D_FN float* jl_rec(const Lane& L, int j) { return L.jl + j * kJLWords * kLanes; }
 B3D_FN float jlf(const float* q, int k) { return q[k * kLanes]; }
@@ -2767,6 +2773,85 @@ B3D_FN void joint_writeback(const Lane& L) {
             stf(w, jw(L, j, J_UPPER_IMPULSE), jlf(q, JL_UPPER_IMP));
         }
     }
+}
+
+/* Joint levels of a shared tile with LDS joint rows: a pass's solves
+ * (joint t % nj for t < kJointIters * nj) each read and write the
+ * velocities of their dynamic bodies and their own row, so level 1 + the
+ * highest level among earlier solves on the same dynamic bodies keeps each
+ * body's and each row's sequence of updates in pass order, and the solves
+ * of one level are split among the tile's waves.  Both passes of a substep
+ * share the schedule, built once per step by wave 0 (after
+ * stage_joint_rows). */
+B3D_FN float* jsched(const Lane& L) { return L.jl + L.g.max_j * kJLWords * kLanes; }
+B3D_FN int jsch_get(const Lane& L, int k) { return __builtin_bit_cast(int, jsched(L)[k * kLanes]); }
+B3D_FN void jsch_set(const Lane& L, int k, int v) { jsched(L)[k * kLanes] = __builtin_bit_cast(float, v); }
+B3D_FN int jsch_p(const Lane& L, int lev) { return lev; }                     /* lev >= 1 */
+B3D_FN int jsch_entry(const Lane& L, int i) { return 1 + kJointIters * L.g.max_j + i; }
+B3D_FN int jsch_last(const Lane& L, int b) { return 1 + 2 * kJointIters * L.g.max_j + b; }
+/* Level of each solve of the pass, in pass order: count (place = 0) or,
+ * from the level starts in P, place the entries. */
+B3D_FN int joint_levels_scan(const Lane& L, int nj, int nb, int place) {
+    int total = kJointIters * nj;
+    for (int b = 0; b < nb; b++) jsch_set(L, jsch_last(L, b), 0);
+    int nlev = 0;
+    int j = 0;
+    for (int t = 0; t < total; t++) {
+        uint32_t ab = __builtin_bit_cast(uint32_t, jlf(jl_rec(L, j), JL_AB));
+        int a = (int)(ab & 0xffffu), b = (int)(ab >> 16);
+        bool da = is_dyn_flag(L, a), db = is_dyn_flag(L, b);
+        int la = da ? jsch_get(L, jsch_last(L, a)) : 0;
+        int lb = db ? jsch_get(L, jsch_last(L, b)) : 0;
+        int lev = (la > lb ? la : lb) + 1;
+        if (da) jsch_set(L, jsch_last(L, a), lev);
+        if (db) jsch_set(L, jsch_last(L, b), lev);
+        int at = jsch_get(L, jsch_p(L, lev));
+        jsch_set(L, jsch_p(L, lev), at + 1);
+        if (place) jsch_set(L, jsch_entry(L, at), j);
+        if (lev > nlev) nlev = lev;
+        j = j + 1 == nj ? 0 : j + 1;
+    }
+    return nlev;
+}
+B3D_FN void joint_sched_build(const Lane& L) {
+    int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
+    int nb = body_count(L);
+    int total = kJointIters * nj;
+    for (int lev = 1; lev <= total; lev++) jsch_set(L, jsch_p(L, lev), 0);
+    int nlev = joint_levels_scan(L, nj, nb, 0);
+    jsch_set(L, 0, nlev);
+    int run = 0;
+    for (int lev = 1; lev <= nlev; lev++) {
+        int n = jsch_get(L, jsch_p(L, lev));
+        jsch_set(L, jsch_p(L, lev), run);
+        run += n;
+    }
+    joint_levels_scan(L, nj, nb, 1);
+}
+/* The tile's largest joint level count (every wave gets the same value). */
+B3D_FN int tile_joint_levels(const Lane& L) {
+    int v = jsch_get(L, 0), m = 0;
+    for (int bit = 7; bit >= 0; bit--) {
+        int cand = m | (1 << bit);
+        if (wave_any(L, v >= cand)) m = cand;
+    }
+    return m;
+}
+/* The wave's next entry after entry i of level *lev (i + waves while in
+ * that level, else its first entry of the next level that has one), or -1. */
+B3D_FN int jlevel_next(const Lane& L, int i, int* lev, int mine) {
+    const PairStage& S = L.st;
+    int end = jsch_get(L, jsch_p(L, *lev));
+    if (i + S.waves < end) return i + S.waves;
+    for (int l = *lev + 1; l <= mine; l++) {
+        int start = end;
+        end = jsch_get(L, jsch_p(L, l));
+        if (start + S.wave < end) {
+            *lev = l;
+            return start + S.wave;
+        }
+    }
+    return -1;
 }
 
 /* A row's delta-state geometry from the scratch record (every field, in
@@ -3026,27 +3111,10 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
  * select which fields to load) fetched one solve ahead: a second row in
  * flight during a solve costs more in registers than the one round trip it
  * would hide. */
-template <bool JL = false>
 B3D_FN void solve_joints(const Lane& L, float h, float inv_h, int use_bias) {
     int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
     if (nj <= 0) return;
     int total = (use_bias ? kJointIters : kRelaxIters) * nj;
-    if constexpr (JL) {
-        /* rows from LDS; each row's geometry loaded during the solve before
-         * it (the geometry does not change during a pass) */
-        JGeo g = jgeo_load(L, 0);
-        int j = 0;
-        for (int t = 0; t < total; t++) {
-            JRow cur;
-            jrow_lds(L, j, g, &cur);
-            int jn = j + 1 == nj ? 0 : j + 1;
-            if (t + 1 < total) g = jgeo_load(L, jn);
-            if (cur.info & JF_WELD) solve_weld<true>(L, j, cur, use_bias);
-            else solve_revolute<true>(L, j, cur, h, inv_h, use_bias);
-            j = jn;
-        }
-        return;
-    }
     JHead head = jhead_load(L, 0);
     int j = 0;
     for (int t = 0; t < total; t++) {
@@ -3057,6 +3125,34 @@ B3D_FN void solve_joints(const Lane& L, float h, float inv_h, int use_bias) {
         if (cur.info & JF_WELD) solve_weld<false>(L, j, cur, use_bias);
         else solve_revolute<false>(L, j, cur, h, inv_h, use_bias);
         j = jn;
+    }
+}
+
+/* A joint pass of a shared tile with LDS joint rows, split by joint levels
+ * among its waves (every wave calls it, with the tile's level count): each
+ * wave solves its share of each level, a barrier after every level, with
+ * the geometry of its next solve in flight. */
+B3D_FN void solve_joints_leveled(const Lane& L, float h, float inv_h, int use_bias, int nlev) {
+    const PairStage& S = L.st;
+    int mine = jsch_get(L, 0);
+    int lev = 1, i = -1;
+    if (mine >= 1) i = S.wave < jsch_get(L, jsch_p(L, 1)) ? S.wave : jlevel_next(L, S.wave - S.waves, &lev, mine);
+    JGeo g;
+    if (i >= 0) g = jgeo_load(L, jsch_get(L, jsch_entry(L, i)));
+    for (int l = 1; l <= nlev; l++) {
+        while (i >= 0 && lev == l) {
+            int j = jsch_get(L, jsch_entry(L, i));
+            JRow cur;
+            jrow_lds(L, j, g, &cur);
+            int lev1 = lev;
+            int i1 = jlevel_next(L, i, &lev1, mine);
+            if (i1 >= 0) g = jgeo_load(L, jsch_get(L, jsch_entry(L, i1)));
+            if (cur.info & JF_WELD) solve_weld<true>(L, j, cur, use_bias);
+            else solve_revolute<true>(L, j, cur, h, inv_h, use_bias);
+            i = i1;
+            lev = lev1;
+        }
+        B3D_BARRIER();
     }
 }
 
@@ -3344,7 +3440,7 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
         vel_load(L);
         body_prepass(L, h);
     }
-    int nlev = 0;
+    int nlev = 0, njlev = 0;
     if (L.staged) {
         /* the tile's waves prepare the contacts together; wave 0 levels
          * them; all warm-start them level by level (the helper waves meet
@@ -3355,12 +3451,17 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
         if (act) {
             sched_build(L);
             prepare_joints(L, h);
-            if constexpr (JL) stage_joint_rows(L);
+            if constexpr (JL) {
+                stage_joint_rows(L);
+                joint_sched_build(L);
+            }
         } else {
             sch_set(L, 0, 0);      /* no contact levels */
+            if constexpr (JL) jsch_set(L, 0, 0);
         }
         B3D_BARRIER();
         nlev = tile_levels(L);
+        if constexpr (JL) njlev = tile_joint_levels(L);
         warm_contacts_leveled(L, nlev);
     } else {
         int warm_done = prepare_contacts(L, cs, ss);
@@ -3387,15 +3488,17 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
         }
         if (L.staged) solve_contacts_leveled(L, inv_h, contact_speed, 1, cs, ss, nlev);
         else solve_contacts(L, inv_h, contact_speed, 1, cs, ss);
-        if (act) solve_joints<JL>(L, h, inv_h, 1);
+        if constexpr (JL) solve_joints_leveled(L, h, inv_h, 1, njlev);
+        else if (act) solve_joints(L, h, inv_h, 1);
         if (L.staged) B3D_BARRIER();   /* the joints' velocities */
         if (act) integrate_positions(L, h, inv_dt, share, stride);
         if (L.staged) B3D_BARRIER();   /* the delta poses */
         if (act) joint_geometry(L, share, stride);
         if (L.staged) solve_contacts_leveled(L, inv_h, contact_speed, 0, cs, ss, nlev);
         else solve_contacts(L, inv_h, contact_speed, 0, cs, ss);
+        if constexpr (JL) solve_joints_leveled(L, h, inv_h, 0, njlev);
         if (act) {
-            solve_joints<JL>(L, h, inv_h, 0);
+            if constexpr (!JL) solve_joints(L, h, inv_h, 0);
             if (rest_wave) apply_restitution(L, rest_threshold);
         }
     }
@@ -3420,6 +3523,7 @@ B3D_FN void step_world(const Lane& L, float dt, int substeps) {
  * the same order, as step_world's shared path).  Runs in all lanes; its
  * stepping lanes rank as wave 0's, so its body and delta record slots are
  * wave 0's, and its idle lanes have no contact levels (wave 0 set them). */
+template <bool JL = false>
 B3D_FN void sweep_helper(const Lane& L0, float dt, int substeps) {
     Lane L = L0;
     L.sslot = wave_rank(L);
@@ -3435,18 +3539,22 @@ B3D_FN void sweep_helper(const Lane& L0, float dt, int substeps) {
     B3D_BARRIER();                 /* wave 0 has staged velocities and body records */
     if (L.active) prepare_contacts(L, cs, ss);
     B3D_BARRIER();                 /* all contacts prepared */
-    B3D_BARRIER();                 /* wave 0 has levelled them */
+    B3D_BARRIER();                 /* wave 0 has levelled them (and the joints, JL) */
     int nlev = tile_levels(L);
+    int njlev = 0;
+    if constexpr (JL) njlev = tile_joint_levels(L);
     warm_contacts_leveled(L, nlev);
     for (int s = 0; s < subs; s++) {
         B3D_BARRIER();
         if (L.active) integrate_velocities(L, L.st.wave, L.st.waves);
         solve_contacts_leveled(L, inv_h, contact_speed, 1, cs, ss, nlev);
+        if constexpr (JL) solve_joints_leveled(L, h, inv_h, 1, njlev);
         B3D_BARRIER();
         if (L.active) integrate_positions(L, h, inv_dt, L.st.wave, L.st.waves);
         B3D_BARRIER();
         if (L.active) joint_geometry(L, L.st.wave, L.st.waves);
         solve_contacts_leveled(L, inv_h, contact_speed, 0, cs, ss, nlev);
+        if constexpr (JL) solve_joints_leveled(L, h, inv_h, 0, njlev);
     }
 }
 

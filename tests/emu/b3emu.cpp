@@ -118,7 +118,7 @@ void emu_step_shared(uint32_t* tiles, int count, unsigned long long sig, float d
     if (kClipWords + 6 * g.max_s > rows) rows = kClipWords + 6 * g.max_s;
     if (lds_rows(g) + sched_words(g) > rows) rows = lds_rows(g) + sched_words(g);
     bool jl = g_joint_lds < 0 ? joint_rows_fit(g) : (g_joint_lds > 0 && g.max_j > 0);
-    if (jl && joint_lds_word(g) + g.max_j * kJLWords > rows) rows = joint_lds_word(g) + g.max_j * kJLWords;
+    if (jl && joint_lds_word(g) + joint_lds_words(g) > rows) rows = joint_lds_word(g) + joint_lds_words(g);
     std::vector<float> lds((size_t)rows * kLanes);
     size_t max_cand = (size_t)g.max_s * (size_t)(g.max_s - 1) / 2;
     size_t words = max_cand * kManiWords;
