@@ -155,10 +155,13 @@ void emu_step_shared(uint32_t* tiles, int count, unsigned long long sig, float d
  * lane passed the barriers a lane with its level count passes (find_pairs'
  * 3 or 4, step_world's 3, then 1 + levels per levelled pass: the warm start
  * and two sweeps per substep, and 3 per substep around the split velocity
- * and position updates and joint geometry), and an idle lane's own count equals a
- * helper's; otherwise -1 - the first world that did not.  Idle lanes have
- * no levels, so on the device, where every lane passes 1 + the tile's
- * largest level count per pass, all lanes meet the same barriers. */
+ * and position updates and joint geometry, and with the joint rows in LDS
+ * one per joint level in each of the two joint passes per substep), and an
+ * idle lane's own count equals a helper's; otherwise -1 - the first world
+ * that did not.  Idle lanes have no levels, so on the device, where every
+ * lane passes 1 + the tile's largest level count per pass (and the tile's
+ * largest joint level count per joint pass), all lanes meet the same
+ * barriers. */
 int emu_step_shared_idle(uint32_t* tiles, int count, unsigned long long sig, float dt, int substeps,
         const unsigned char* step_mask, int masks) {
     Geometry g;
@@ -169,6 +172,8 @@ int emu_step_shared_idle(uint32_t* tiles, int count, unsigned long long sig, flo
     int rows = shared_lds_words(g);
     if (kClipWords + 6 * g.max_s > rows) rows = kClipWords + 6 * g.max_s;
     if (lds_rows(g) + sched_words(g) > rows) rows = lds_rows(g) + sched_words(g);
+    bool jl = joint_rows_fit(g);
+    if (jl && joint_lds_word(g) + joint_lds_words(g) > rows) rows = joint_lds_word(g) + joint_lds_words(g);
     std::vector<float> lds((size_t)rows * kLanes);
     size_t max_cand = (size_t)g.max_s * (size_t)(g.max_s - 1) / 2;
     size_t words = max_cand * kManiWords;
@@ -190,11 +195,18 @@ int emu_step_shared_idle(uint32_t* tiles, int count, unsigned long long sig, flo
         L.st = S;
         L.staged = true;
         L.active = active;
+        if (jl) L.jl = lds.data() + (size_t)joint_lds_word(g) * kLanes + w % kLanes;
         host_barriers = 0;
-        if (use_masks) step_world<true>(L, dt, substeps);
-        else step_world<false>(L, dt, substeps);
+        if (jl) {
+            if (use_masks) step_world<true, true>(L, dt, substeps);
+            else step_world<false, true>(L, dt, substeps);
+        } else {
+            if (use_masks) step_world<true>(L, dt, substeps);
+            else step_world<false>(L, dt, substeps);
+        }
         int levels = active ? sch_get(L, 0) : 0;
-        if (host_barriers != fixed + passes * (1 + levels)) return -1 - w;
+        int jlevels = jl && active ? jsch_get(L, 0) : 0;
+        if (host_barriers != fixed + passes * (1 + levels) + 2 * subs * jlevels) return -1 - w;
         if (!active) {
             host_barriers = 0;
             S.wave = 1;
@@ -202,7 +214,8 @@ int emu_step_shared_idle(uint32_t* tiles, int count, unsigned long long sig, flo
             L.st = S;
             if (use_masks) pair_helper<true>(L, S);
             else pair_helper<false>(L, S);
-            sweep_helper(L, dt, substeps);
+            if (jl) sweep_helper<true>(L, dt, substeps);
+            else sweep_helper<false>(L, dt, substeps);
             if (host_barriers != fixed + passes) return -1 - w;
         }
     }
