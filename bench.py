@@ -124,8 +124,18 @@ def counted_flops(scene, first, count):
     return sum(window) / len(window), [lo, hi]
 
 
+def joint_rows_fit(max_b, max_s, max_c, max_j):
+    """Whether a shared tile keeps its joint rows in LDS (joint_rows_fit in
+    puffysics_amd/csrc/b3d_lane.h): the velocity or contact-generation
+    rows, the contact levels, 52 words per joint and the joint levels within
+    640 words per lane."""
+    lds_rows = max(7 * max_b, 48 + 6 * max_s if 48 + 6 * max_s <= 160 else 48)
+    words = lds_rows + 2 + max_b + 2 * max_c + 52 * max_j + 1 + 4 * max_j + max_b
+    return max_j > 0 and words <= 640
+
+
 def kernel_name(scene, count):
-    """The step kernel a batch launches: b3k_step_shared<Masks> when its
+    """The step kernel a batch launches: b3k_step_shared<Masks, JL> when its
     tiles fit one per CU (b3_engine_create), else b3k_step."""
     import torch
     from puffysics_amd import scenes
@@ -133,8 +143,9 @@ def kernel_name(scene, count):
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     if tiles > cus:
         return "b3k_step"
-    max_s = scenes.SCENES[scene].caps[1]
-    return "b3k_step_shared<true>" if 12 <= max_s <= 64 else "b3k_step_shared<false>"
+    caps = scenes.SCENES[scene].caps
+    masks = 12 <= caps[1] <= 64
+    return "b3k_step_shared<%s, %s>" % ("true" if masks else "false", "true" if joint_rows_fit(*caps) else "false")
 
 
 def load_counters(kernel, scene, count, digest):
