@@ -714,11 +714,18 @@ constexpr int kJointKeyRegs = 8;
  * whole chunk at once. */
 B3D_FN void shape_pass(const Lane& L, int ns, float* bounds) {
     V3 pad = v3(kSpeculative, kSpeculative, kSpeculative);
+    /* the next chunk's body indices are in flight while a chunk is posed */
+    int bn[kShapeChunk];
+#pragma unroll
+    for (int k = 0; k < kShapeChunk; k++)
+        if (k < ns) bn[k] = ldi(L.w, sw(L, k, S_BODY));
     for (int s0 = 0; s0 < ns; s0 += kShapeChunk) {
         int b[kShapeChunk];
 #pragma unroll
-        for (int k = 0; k < kShapeChunk; k++)
-            if (s0 + k < ns) b[k] = ldi(L.w, sw(L, s0 + k, S_BODY));
+        for (int k = 0; k < kShapeChunk; k++) {
+            b[k] = bn[k];
+            if (s0 + kShapeChunk + k < ns) bn[k] = ldi(L.w, sw(L, s0 + kShapeChunk + k, S_BODY));
+        }
         V3 bpos[kShapeChunk], center[kShapeChunk];
         Q brot[kShapeChunk];
         int btype[kShapeChunk];
@@ -1274,8 +1281,15 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
         B3D_BARRIER();
         ncand = mask_candidates(L, ns);
     } else {
-        int op = 0;
-        uint32_t okey = sorted && old_n > 0 ? old_key(L, 0) : 0xffffffffu;
+        /* the old keys in chunks of four, the next chunk in flight */
+        int op = 0, kbase = 0;
+        uint32_t kc[4], kn[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            kc[q] = sorted && q < old_n ? old_key(L, q) : 0xffffffffu;
+            kn[q] = sorted && 4 + q < old_n ? old_key(L, 4 + q) : 0xffffffffu;
+        }
+        uint32_t okey = kc[0];
         for (int i = 0; i < ns; i++) {
             const float* bi = bounds + i * 6 * kLanes;
             for (int j0 = i + 1; j0 < ns; j0 += 4) {
@@ -1290,7 +1304,16 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
                     if (sorted) {
                         while (op < old_n && okey < key) {
                             op++;
-                            okey = op < old_n ? old_key(L, op) : 0xffffffffu;
+                            if (op - kbase == 4) {
+                                kbase += 4;
+#pragma unroll
+                                for (int q = 0; q < 4; q++) {
+                                    kc[q] = kn[q];
+                                    kn[q] = kbase + 4 + q < old_n ? old_key(L, kbase + 4 + q) : 0xffffffffu;
+                                }
+                            }
+                            int d = op - kbase;
+                            okey = d == 0 ? kc[0] : (d == 1 ? kc[1] : (d == 2 ? kc[2] : kc[3]));
                         }
                         if (op < old_n && okey == key) match = op;
                     }
