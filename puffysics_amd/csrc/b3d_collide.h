@@ -263,8 +263,16 @@ B3D_FN int clip_plane(const float* in, int n, float* out, V3 pn, float po) {
     V3 prev = clip_get(in, n - 1);
     float pd = dot(prev, pn) - po;
     int pin = pd <= 0.0f;
-    for (int i = 0; i < n; i++) {
-        V3 cur = clip_get(in, i);
+    /* every input vertex is read before the first is used (unrolled over
+     * the polygon's at most kClipVerts vertices) */
+    V3 vin[kClipVerts];
+#pragma unroll
+    for (int i = 0; i < kClipVerts; i++)
+        if (i < n) vin[i] = clip_get(in, i);
+#pragma unroll
+    for (int i = 0; i < kClipVerts; i++) {
+        if (i >= n) break;
+        V3 cur = vin[i];
         float cd = dot(cur, pn) - po;
         int cin = cd <= 0.0f;
         if (cin != pin && c < kClipVerts) {
