@@ -563,9 +563,10 @@ B3D_FN void vel_load(const Lane& L) {
         }
     }
 }
-B3D_FN void vel_store(const Lane& L) {
+/* Bodies first, first + stride, ... (a shared tile's waves split them). */
+B3D_FN void vel_store(const Lane& L, int first = 0, int stride = 1) {
     int nb = body_count(L);
-    for (int b = 0; b < nb; b++) {
+    for (int b = first; b < nb; b += stride) {
         const float* v = L.vel + b * kVelWords * kLanes;
         for (int c = 0; c < 6; c++) stf(L.w, bw(L, b, B_LIN_VEL + c), v[c * kLanes]);
     }
@@ -2513,10 +2514,10 @@ B3D_FN void apply_restitution(const Lane& L, float threshold) {
 
 /* The impulses the sweeps and restitution accumulated, back into the
  * world's contact rows (the warm-start cache of the next step). */
-B3D_FN void contact_writeback(const Lane& L) {
+B3D_FN void contact_writeback(const Lane& L, int first = 0, int stride = 1) {
     uint32_t* w = L.w;
     int cc = ldi(w, H_CONTACT_COUNT);
-    for (int c0 = 0; c0 < cc; c0 += kChunk) {
+    for (int c0 = first * kChunk; c0 < cc; c0 += stride * kChunk) {
         CHead hd[kChunk];
 #pragma unroll
         for (int k = 0; k < kChunk; k++) {
@@ -2731,54 +2732,66 @@ B3D_FN void jimp_store3(const Lane& L, int j, int world_word, int lds_word, V3 v
 
 /* The step's joint rows to LDS (wave 0, after prepare_joints): each row as
  * jrow_load reads it, less the delta-state geometry. */
+B3D_FN void jl_stage_row(const Lane& L, int j, const JRow& r) {
+    float* q = jl_rec(L, j);
+    jlsf(q, JL_AB, __builtin_bit_cast(float, (uint32_t)(r.a | (r.b << 16))));
+    jlsf(q, JL_INFO, __builtin_bit_cast(float, r.info));
+    jlsf(q, JL_MA, r.ma);
+    jlsm3(q, JL_IA, r.ia);
+    jlsf(q, JL_MB, r.mb);
+    jlsm3(q, JL_IB, r.ib);
+    jlssoft(q, JL_SOFT, r.soft);
+    jls3(q, JL_LIN_IMP, r.lin_imp);
+    if (r.info & JF_WELD) {
+        jlsf(q, JL_LIN_HZ, r.lin_hz);
+        jlssoft(q, JL_LIN_SPRING, r.lin_spring);
+        jlsf(q, JL_ANG_HZ, r.ang_hz);
+        jlssoft(q, JL_ANG_SPRING, r.ang_spring);
+        jlsm3(q, JL_ANG_MASS, r.ang_mass);
+        jls3(q, JL_ANG_IMP, r.ang_imp);
+    } else {
+        jlsf(q, JL_AXIAL, r.axial_mass);
+        jls3(q, JL_AXIS, r.axis);
+        jls3(q, JL_IAX, r.ia_ax);
+        jls3(q, JL_IBX, r.ib_ax);
+        jlsf(q, JL_MAXT, r.max_torque);
+        jlsf(q, JL_TARGET, r.target);
+        jlssoft(q, JL_SSOFT, r.spring_soft);
+        jlsf(q, JL_SPEED, r.speed);
+        jlsf(q, JL_LOWER, r.lower);
+        jlsf(q, JL_UPPER, r.upper);
+        jlsf(q, JL_PERP_IMP, r.perp_imp.x);
+        jlsf(q, JL_PERP_IMP + 1, r.perp_imp.y);
+        jlsf(q, JL_SPRING_IMP, r.spring_imp);
+        jlsf(q, JL_MOTOR_IMP, r.motor_imp);
+        jlsf(q, JL_LOWER_IMP, r.lower_imp);
+        jlsf(q, JL_UPPER_IMP, r.upper_imp);
+    }
+}
+/* Two joints at a time: both rows' loads in flight before either is staged. */
 B3D_FN void stage_joint_rows(const Lane& L) {
     int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
-    for (int j = 0; j < nj; j++) {
-        JRow r = {};
-        jrow_load(L, j, jhead_load(L, j), &r);
-        float* q = jl_rec(L, j);
-        jlsf(q, JL_AB, __builtin_bit_cast(float, (uint32_t)(r.a | (r.b << 16))));
-        jlsf(q, JL_INFO, __builtin_bit_cast(float, r.info));
-        jlsf(q, JL_MA, r.ma);
-        jlsm3(q, JL_IA, r.ia);
-        jlsf(q, JL_MB, r.mb);
-        jlsm3(q, JL_IB, r.ib);
-        jlssoft(q, JL_SOFT, r.soft);
-        jls3(q, JL_LIN_IMP, r.lin_imp);
-        if (r.info & JF_WELD) {
-            jlsf(q, JL_LIN_HZ, r.lin_hz);
-            jlssoft(q, JL_LIN_SPRING, r.lin_spring);
-            jlsf(q, JL_ANG_HZ, r.ang_hz);
-            jlssoft(q, JL_ANG_SPRING, r.ang_spring);
-            jlsm3(q, JL_ANG_MASS, r.ang_mass);
-            jls3(q, JL_ANG_IMP, r.ang_imp);
-        } else {
-            jlsf(q, JL_AXIAL, r.axial_mass);
-            jls3(q, JL_AXIS, r.axis);
-            jls3(q, JL_IAX, r.ia_ax);
-            jls3(q, JL_IBX, r.ib_ax);
-            jlsf(q, JL_MAXT, r.max_torque);
-            jlsf(q, JL_TARGET, r.target);
-            jlssoft(q, JL_SSOFT, r.spring_soft);
-            jlsf(q, JL_SPEED, r.speed);
-            jlsf(q, JL_LOWER, r.lower);
-            jlsf(q, JL_UPPER, r.upper);
-            jlsf(q, JL_PERP_IMP, r.perp_imp.x);
-            jlsf(q, JL_PERP_IMP + 1, r.perp_imp.y);
-            jlsf(q, JL_SPRING_IMP, r.spring_imp);
-            jlsf(q, JL_MOTOR_IMP, r.motor_imp);
-            jlsf(q, JL_LOWER_IMP, r.lower_imp);
-            jlsf(q, JL_UPPER_IMP, r.upper_imp);
-        }
+    for (int j0 = 0; j0 < nj; j0 += 2) {
+        JHead hd[2];
+#pragma unroll
+        for (int k = 0; k < 2; k++)
+            if (j0 + k < nj) hd[k] = jhead_load(L, j0 + k);
+        JRow r[2] = {};
+#pragma unroll
+        for (int k = 0; k < 2; k++)
+            if (j0 + k < nj) jrow_load(L, j0 + k, hd[k], &r[k]);
+#pragma unroll
+        for (int k = 0; k < 2; k++)
+            if (j0 + k < nj) jl_stage_row(L, j0 + k, r[k]);
     }
 }
 
 /* The LDS rows' impulses back to the joints' words (the words the solves
  * update; a disabled row's impulse is the world's own value, unchanged). */
-B3D_FN void joint_writeback(const Lane& L) {
+B3D_FN void joint_writeback(const Lane& L, int first = 0, int stride = 1) {
     int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
     uint32_t* w = L.w;
-    for (int j = 0; j < nj; j++) {
+    for (int j = first; j < nj; j += stride) {
         const float* q = jl_rec(L, j);
         int info = __builtin_bit_cast(int, jlf(q, JL_INFO));
         st3(w, jw(L, j, J_LINEAR_IMPULSE), jl3(q, JL_LIN_IMP));
@@ -3318,10 +3331,10 @@ B3D_FN void integrate_positions(const Lane& L, float h, float inv_dt, int first 
 /* Commit the accumulated deltas and clear forces (09_step.inl:109-130);
  * delta pose, force and torque words already zero (identity) are left
  * alone. */
-B3D_FN void finalize(const Lane& L) {
+B3D_FN void finalize(const Lane& L, int first = 0, int stride = 1) {
     uint32_t* w = L.w;
     int nb = body_count(L);
-    for (int b0 = 0; b0 < nb; b0 += kChunk) {
+    for (int b0 = first * kChunk; b0 < nb; b0 += stride * kChunk) {
         int type[kChunk], kind[kChunk];
         V3 center[kChunk], dp[kChunk], lc[kChunk], inv_i[kChunk];
         Q dq[kChunk], rq[kChunk];
@@ -3491,10 +3504,11 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
         prepare_joints(L, h);
         if (wave_any(L, !warm_done)) warm_start_contacts(L, warm_done);
     }
-    if (act) {
-        warm_start_joints(L);
-        joint_geometry(L);   /* the contacts' initial separations come from prepare_contacts */
-    }
+    if (act) warm_start_joints(L);
+    /* a shared tile's waves split the first joint geometry, after the warm
+     * start has read the previous step's hinge rows, which it overwrites */
+    if (L.staged) B3D_BARRIER();
+    if (act) joint_geometry(L, L.staged ? L.st.wave : 0, L.staged ? L.st.waves : 1);
     /* In a shared tile the waves split the velocity and position updates
      * (bodies) and the joint geometry (joints) of every substep, between
      * barriers: each body and joint is updated by one wave, and the next
@@ -3525,11 +3539,14 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
             if (rest_wave) apply_restitution(L, rest_threshold);
         }
     }
+    /* a shared tile's waves split the write-back, after the last
+     * restitution and joint impulses (sweep_helper runs the same barrier) */
+    if (L.staged) B3D_BARRIER();
     if (act) {
-        contact_writeback(L);
-        if constexpr (JL) joint_writeback(L);
-        finalize(L);
-        vel_store(L);
+        contact_writeback(L, share, stride);
+        if constexpr (JL) joint_writeback(L, share, stride);
+        finalize(L, share, stride);
+        vel_store(L, share, stride);
     }
 }
 
@@ -3541,9 +3558,10 @@ B3D_FN void step_world(const Lane& L, float dt, int substeps) {
 
 /* A helper wave of a shared-narrowphase tile after its narrowphase share:
  * its share of the contact preparation, of the level-by-level warm start,
- * of every contact sweep and of each substep's velocity and position
- * updates and joint geometry, in step with wave 0 (the same barriers, in
- * the same order, as step_world's shared path).  Runs in all lanes; its
+ * of the first joint geometry, of every contact sweep, of each substep's
+ * velocity and position updates and joint geometry (and joint levels, JL),
+ * and of the write-back, in step with wave 0 (the same barriers, in the
+ * same order, as step_world's shared path).  Runs in all lanes; its
  * stepping lanes rank as wave 0's, so its body and delta record slots are
  * wave 0's, and its idle lanes have no contact levels (wave 0 set them). */
 template <bool JL = false>
@@ -3567,6 +3585,8 @@ B3D_FN void sweep_helper(const Lane& L0, float dt, int substeps) {
     int njlev = 0;
     if constexpr (JL) njlev = tile_joint_levels(L);
     warm_contacts_leveled(L, nlev);
+    B3D_BARRIER();                 /* wave 0 has warm-started the joints */
+    if (L.active) joint_geometry(L, L.st.wave, L.st.waves);
     for (int s = 0; s < subs; s++) {
         B3D_BARRIER();
         if (L.active) integrate_velocities(L, L.st.wave, L.st.waves);
@@ -3578,6 +3598,13 @@ B3D_FN void sweep_helper(const Lane& L0, float dt, int substeps) {
         if (L.active) joint_geometry(L, L.st.wave, L.st.waves);
         solve_contacts_leveled(L, inv_h, contact_speed, 0, cs, ss, nlev);
         if constexpr (JL) solve_joints_leveled(L, h, inv_h, 0, njlev);
+    }
+    B3D_BARRIER();                 /* wave 0's restitution */
+    if (L.active) {
+        contact_writeback(L, L.st.wave, L.st.waves);
+        if constexpr (JL) joint_writeback(L, L.st.wave, L.st.waves);
+        finalize(L, L.st.wave, L.st.waves);
+        vel_store(L, L.st.wave, L.st.waves);
     }
 }
 

@@ -153,7 +153,8 @@ void emu_step_shared(uint32_t* tiles, int count, unsigned long long sig, float d
  * too, as the device runs them: as wave 0 (step_world) and as a helper wave
  * (pair_helper, sweep_helper) with L.active false.  Returns 0 when every
  * lane passed the barriers a lane with its level count passes (find_pairs'
- * 3 or 4, step_world's 3, then 1 + levels per levelled pass: the warm start
+ * 3 or 4, step_world's 3, 2 around the first joint geometry and the
+ * write-back, then 1 + levels per levelled pass: the warm start
  * and two sweeps per substep, and 3 per substep around the split velocity
  * and position updates and joint geometry, and with the joint rows in LDS
  * one per joint level in each of the two joint passes per substep), and an
@@ -182,7 +183,7 @@ int emu_step_shared_idle(uint32_t* tiles, int count, unsigned long long sig, flo
     std::vector<uint32_t> stage((size_t)ntiles * stage_tile);
     bool use_masks = masks < 0 ? shared_masks(g) : (masks > 0 && g.max_s <= 64);
     int subs = substeps < 1 ? 1 : substeps;
-    int fixed = (use_masks ? 4 : 3) + 3 + 3 * subs, passes = 1 + 2 * subs;
+    int fixed = (use_masks ? 4 : 3) + 3 + 2 + 3 * subs, passes = 1 + 2 * subs;
     for (int w = 0; w < count; w++) {
         bool active = !step_mask || step_mask[w];
         Lane L = lane_of(tiles, scratch.data(), lds.data(), g, w);
