@@ -543,9 +543,11 @@ B3D_FN int is_dyn_flag(const Lane& L, int b) {
 B3D_FN int body_count(const Lane& L) { return clampi(ldi(L.w, H_BODY_COUNT), 0, L.g.max_b); }
 
 /* Stage velocities and flags of every body into the velocity rows. */
-B3D_FN void vel_load(const Lane& L) {
+/* Chunks of four bodies first, first + stride, ... (a shared tile's waves
+ * split them). */
+B3D_FN void vel_load(const Lane& L, int first = 0, int stride = 1) {
     int nb = body_count(L);
-    for (int b0 = 0; b0 < nb; b0 += 4) {
+    for (int b0 = 4 * first; b0 < nb; b0 += 4 * stride) {
         float v[4][kVelWords];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -3196,11 +3198,11 @@ B3D_FN void solve_joints_leveled(const Lane& L, float h, float inv_h, int use_bi
  * applied force / torque and the damping factors of 09_step.inl:5-18, whose
  * inputs do not change during a step (BS_*), and the body kind and the
  * step's starting delta pose (BD_*). */
-B3D_FN void body_prepass(const Lane& L, float h) {
+B3D_FN void body_prepass(const Lane& L, float h, int first = 0, int stride = 1) {
     uint32_t* w = L.w;
     V3 g = ld3(w, H_GRAVITY);
     int nb = body_count(L);
-    for (int b0 = 0; b0 < nb; b0 += kChunk) {
+    for (int b0 = first * kChunk; b0 < nb; b0 += stride * kChunk) {
         int type[kChunk];
         uint32_t flags[kChunk];
         float inv_mass[kChunk], lin_d[kChunk], ang_d[kChunk], gscale[kChunk];
@@ -3472,9 +3474,12 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
     find_contacts<Masks>(L);
     /* restitution runs in every lane of a wave where some world has it */
     const bool rest_wave = wave_any(L, act && (ldi(L.scr + L.g.scr_flags * kLanes, 0) & kLaneRestitution) != 0);
+    /* a shared tile's waves split the body work (sweep_helper does its
+     * share before the barrier that follows) */
+    const int share = L.staged ? L.st.wave : 0, stride = L.staged ? L.st.waves : 1;
     if (act) {
-        vel_load(L);
-        body_prepass(L, h);
+        vel_load(L, share, stride);
+        body_prepass(L, h, share, stride);
     }
     int nlev = 0, njlev = 0;
     if (L.staged) {
@@ -3508,13 +3513,12 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
     /* a shared tile's waves split the first joint geometry, after the warm
      * start has read the previous step's hinge rows, which it overwrites */
     if (L.staged) B3D_BARRIER();
-    if (act) joint_geometry(L, L.staged ? L.st.wave : 0, L.staged ? L.st.waves : 1);
+    if (act) joint_geometry(L, share, stride);
     /* In a shared tile the waves split the velocity and position updates
      * (bodies) and the joint geometry (joints) of every substep, between
      * barriers: each body and joint is updated by one wave, and the next
      * phase's readers see it after the barrier (sweep_helper runs the same
      * barriers).  Wave 0 alone solves the joints and applies restitution. */
-    const int share = L.staged ? L.st.wave : 0, stride = L.staged ? L.st.waves : 1;
     for (int s = 0; s < subs; s++) {
         if (L.staged) B3D_BARRIER();   /* the last joint and restitution impulses */
         if (act) {
@@ -3577,7 +3581,11 @@ B3D_FN void sweep_helper(const Lane& L0, float dt, int substeps) {
     Soft cs = make_soft(hertz, damping, h);
     Soft ss = make_soft(2.0f * hertz, 0.5f * damping, h);
     float contact_speed = ldf(L.w, H_CONTACT_SPEED);
-    B3D_BARRIER();                 /* wave 0 has staged velocities and body records */
+    if (L.active) {
+        vel_load(L, L.st.wave, L.st.waves);
+        body_prepass(L, h, L.st.wave, L.st.waves);
+    }
+    B3D_BARRIER();                 /* the velocities and body records are staged */
     if (L.active) prepare_contacts(L, cs, ss);
     B3D_BARRIER();                 /* all contacts prepared */
     B3D_BARRIER();                 /* wave 0 has levelled them (and the joints, JL) */
