@@ -1779,10 +1779,12 @@ B3D_FN void sched_build(const Lane& L) {
 
 /* b3_prepare_joints (06_joints.inl:161-202), plus the hinge axis through
  * each inverse inertia, which is fixed for the step. */
-B3D_FN void prepare_joints(const Lane& L, float h) {
+B3D_FN void prepare_joints(const Lane& L, float h, int first = 0, int stride = 1) {
     int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
     uint32_t* w = L.w;
-    for (int j0 = 0; j0 < nj; j0 += kPrepChunk) {
+    /* chunks of kPrepChunk joints first, first + stride, ... (a shared
+     * tile's waves split them) */
+    for (int j0 = first * kPrepChunk; j0 < nj; j0 += stride * kPrepChunk) {
         /* the joints' own fields, then (through their body indices) the bodies' */
         int a[kPrepChunk], b[kPrepChunk], jtype[kPrepChunk], en[kPrepChunk];
         float chz[kPrepChunk], cdr[kPrepChunk], lh[kPrepChunk], ld[kPrepChunk], ah[kPrepChunk], ad[kPrepChunk];
@@ -2770,10 +2772,11 @@ B3D_FN void jl_stage_row(const Lane& L, int j, const JRow& r) {
         jlsf(q, JL_UPPER_IMP, r.upper_imp);
     }
 }
-/* Two joints at a time: both rows' loads in flight before either is staged. */
-B3D_FN void stage_joint_rows(const Lane& L) {
+/* Two joints at a time: both rows' loads in flight before either is staged;
+ * pairs first, first + stride, ... (a shared tile's waves split them). */
+B3D_FN void stage_joint_rows(const Lane& L, int first = 0, int stride = 1) {
     int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
-    for (int j0 = 0; j0 < nj; j0 += 2) {
+    for (int j0 = 2 * first; j0 < nj; j0 += 2 * stride) {
         JHead hd[2];
 #pragma unroll
         for (int k = 0; k < 2; k++)
@@ -2819,8 +2822,8 @@ B3D_FN void joint_writeback(const Lane& L, int first = 0, int stride = 1) {
  * highest level among earlier solves on the same dynamic bodies keeps each
  * body's and each row's sequence of updates in pass order, and the solves
  * of one level are split among the tile's waves.  Both passes of a substep
- * share the schedule, built once per step by wave 0 (after
- * stage_joint_rows). */
+ * share the schedule, built once per step by wave 0 from the joints' heads
+ * (after prepare_joints). */
 B3D_FN float* jsched(const Lane& L) { return L.jl + L.g.max_j * kJLWords * kLanes; }
 B3D_FN int jsch_get(const Lane& L, int k) { return __builtin_bit_cast(int, jsched(L)[k * kLanes]); }
 B3D_FN void jsch_set(const Lane& L, int k, int v) { jsched(L)[k * kLanes] = __builtin_bit_cast(float, v); }
@@ -2835,7 +2838,7 @@ B3D_FN int joint_levels_scan(const Lane& L, int nj, int nb, int place) {
     int nlev = 0;
     int j = 0;
     for (int t = 0; t < total; t++) {
-        uint32_t ab = __builtin_bit_cast(uint32_t, jlf(jl_rec(L, j), JL_AB));
+        uint32_t ab = ldu(joint_rec(L, j), JS_AB);
         int a = (int)(ab & 0xffffu), b = (int)(ab >> 16);
         bool da = is_dyn_flag(L, a), db = is_dyn_flag(L, b);
         int la = da ? jsch_get(L, jsch_last(L, a)) : 0;
@@ -3483,19 +3486,20 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
     }
     int nlev = 0, njlev = 0;
     if (L.staged) {
-        /* the tile's waves prepare the contacts together; wave 0 levels
-         * them; all warm-start them level by level (the helper waves meet
-         * wave 0 at each barrier, sweep_helper) */
-        B3D_BARRIER();
-        if (act) prepare_contacts(L, cs, ss);
+        /* the tile's waves prepare the contacts and joints together (and
+         * stage the joint rows, JL); wave 0 levels the contacts (and
+         * joints); all warm-start the contacts level by level (the helper
+         * waves meet wave 0 at each barrier, sweep_helper) */
         B3D_BARRIER();
         if (act) {
+            prepare_contacts(L, cs, ss);
+            prepare_joints(L, h, share, stride);
+        }
+        B3D_BARRIER();
+        if (act) {
+            if constexpr (JL) stage_joint_rows(L, share, stride);
             sched_build(L);
-            prepare_joints(L, h);
-            if constexpr (JL) {
-                stage_joint_rows(L);
-                joint_sched_build(L);
-            }
+            if constexpr (JL) joint_sched_build(L);
         } else {
             sch_set(L, 0, 0);      /* no contact levels */
             if constexpr (JL) jsch_set(L, 0, 0);
@@ -3586,8 +3590,13 @@ B3D_FN void sweep_helper(const Lane& L0, float dt, int substeps) {
         body_prepass(L, h, L.st.wave, L.st.waves);
     }
     B3D_BARRIER();                 /* the velocities and body records are staged */
-    if (L.active) prepare_contacts(L, cs, ss);
-    B3D_BARRIER();                 /* all contacts prepared */
+    if (L.active) {
+        prepare_contacts(L, cs, ss);
+        prepare_joints(L, h, L.st.wave, L.st.waves);
+    }
+    B3D_BARRIER();                 /* all contacts and joints prepared */
+    if constexpr (JL)
+        if (L.active) stage_joint_rows(L, L.st.wave, L.st.waves);
     B3D_BARRIER();                 /* wave 0 has levelled them (and the joints, JL) */
     int nlev = tile_levels(L);
     int njlev = 0;
