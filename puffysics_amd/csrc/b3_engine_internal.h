@@ -85,15 +85,23 @@ __device__ inline void restore_tile(uint32_t* live, const uint32_t* snap, const 
                 if (chunk % nslices != slice) continue;
                 /* kRestoreBatch 256-byte snapshot reads in flight before
                  * their writes (the reads do not depend on the writes: the
-                 * snapshots and the live tiles are separate allocations) */
+                 * snapshots and the live tiles are separate allocations).
+                 * A word already equal to the snapshot's is not written:
+                 * each write is 4 bytes of a 256-byte row, which the memory
+                 * merges by reading and writing the whole sector, and most
+                 * of a world (shapes, body and joint constants) does not
+                 * change in a step. */
                 int k0 = c0 + lane;
-                uint32_t v[kRestoreBatch];
+                uint32_t v[kRestoreBatch], cur[kRestoreBatch];
 #pragma unroll
                 for (int i = 0; i < kRestoreBatch; i++)
-                    if (k0 + 64 * i < hi[r]) v[i] = src[k0 + 64 * i];
+                    if (k0 + 64 * i < hi[r]) {
+                        v[i] = src[k0 + 64 * i];
+                        cur[i] = lt[(size_t)(k0 + 64 * i) * 64 + l];
+                    }
 #pragma unroll
                 for (int i = 0; i < kRestoreBatch; i++)
-                    if (k0 + 64 * i < hi[r]) lt[(size_t)(k0 + 64 * i) * 64 + l] = v[i];
+                    if (k0 + 64 * i < hi[r] && cur[i] != v[i]) lt[(size_t)(k0 + 64 * i) * 64 + l] = v[i];
             }
         }
     }
