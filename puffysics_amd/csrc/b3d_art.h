@@ -1096,8 +1096,7 @@ B3D_FN ArtParams art_params(const Lane& L, float dt, int substeps) {
  * world rows, velocities staged, per-step body records. */
 B3D_FN void art_open(const Lane& L, const ArtParams& P) {
     find_contacts(L);
-    vel_load(L);
-    body_prepass(L, P.h);
+    body_prepass(L, P.h);   /* with the velocity rows */
     wrow_prepare(L, P.cs, P.ss);
 }
 

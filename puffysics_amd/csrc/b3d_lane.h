@@ -18,8 +18,9 @@
  *   scr  per-step scratch    (HBM)    shape bounds and the old warm cache
  *   vel  body velocity rows  (LDS)    body b component c at vel[(b*7+c)*64],
  *                                     c = 0..5 lin/ang velocity, 6 = flags
- * Body velocities stay in `vel` for the whole step (b3d_vel_load /
- * b3d_vel_store move them), everything else is read and written in place.
+ * Body velocities stay in `vel` for the whole step (body_prepass fills the
+ * rows, vel_store writes them back), everything else is read and written
+ * in place.
  *
  * The arithmetic is the reference's default b3_step path, operation for
  * operation (src/puffysics/08_contacts.inl, 06_joints.inl, 07_packed.inl,
@@ -542,30 +543,9 @@ B3D_FN int is_dyn_flag(const Lane& L, int b) {
 
 B3D_FN int body_count(const Lane& L) { return clampi(ldi(L.w, H_BODY_COUNT), 0, L.g.max_b); }
 
-/* Stage velocities and flags of every body into the velocity rows. */
-/* Chunks of four bodies first, first + stride, ... (a shared tile's waves
+/* The velocity rows back to the bodies (the rows are filled by
+ * body_prepass); bodies first, first + stride, ... (a shared tile's waves
  * split them). */
-B3D_FN void vel_load(const Lane& L, int first = 0, int stride = 1) {
-    int nb = body_count(L);
-    for (int b0 = 4 * first; b0 < nb; b0 += 4 * stride) {
-        float v[4][kVelWords];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            if (b0 + k >= nb) continue;
-#pragma unroll
-            for (int c = 0; c < 6; c++) v[k][c] = ldf(L.w, bw(L, b0 + k, B_LIN_VEL + c));
-            v[k][6] = ldf(L.w, bw(L, b0 + k, B_FLAGS));
-        }
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            if (b0 + k >= nb) continue;
-            float* row = L.vel + (b0 + k) * kVelWords * kLanes;
-#pragma unroll
-            for (int c = 0; c < kVelWords; c++) row[c * kLanes] = v[k][c];
-        }
-    }
-}
-/* Bodies first, first + stride, ... (a shared tile's waves split them). */
 B3D_FN void vel_store(const Lane& L, int first = 0, int stride = 1) {
     int nb = body_count(L);
     for (int b = first; b < nb; b += stride) {
@@ -3206,6 +3186,9 @@ B3D_FN void body_prepass(const Lane& L, float h, int first = 0, int stride = 1) 
     V3 g = ld3(w, H_GRAVITY);
     int nb = body_count(L);
     for (int b0 = first * kChunk; b0 < nb; b0 += stride * kChunk) {
+        /* the chunk's velocities go to the LDS rows in the same pass (one
+         * round trip per chunk for both) */
+        float vel[kChunk][6];
         int type[kChunk];
         uint32_t flags[kChunk];
         float inv_mass[kChunk], lin_d[kChunk], ang_d[kChunk], gscale[kChunk];
@@ -3216,6 +3199,8 @@ B3D_FN void body_prepass(const Lane& L, float h, int first = 0, int stride = 1) 
         for (int k = 0; k < kChunk; k++) {
             int b = b0 + k;
             if (b >= nb) continue;
+#pragma unroll
+            for (int c = 0; c < 6; c++) vel[k][c] = ldf(w, bw(L, b, B_LIN_VEL + c));
             dp[k] = ld3(w, bw(L, b, B_DELTA_POS));
             dq[k] = ldq(w, bw(L, b, B_DELTA_ROT));
             type[k] = ldi(w, bw(L, b, B_TYPE));
@@ -3232,6 +3217,10 @@ B3D_FN void body_prepass(const Lane& L, float h, int first = 0, int stride = 1) 
         for (int k = 0; k < kChunk; k++) {
             int b = b0 + k;
             if (b >= nb) continue;
+            float* row = L.vel + b * kVelWords * kLanes;
+#pragma unroll
+            for (int c = 0; c < 6; c++) row[c * kLanes] = vel[k][c];
+            row[6 * kLanes] = __builtin_bit_cast(float, flags[k]);
             uint32_t* r = body_rec(L, b);
             uint32_t* d = delta_rec(L, b);
             int kind = (int)(flags[k] & 0xffu) | (type[k] == kDynamic ? kKindDynamic : 0)
@@ -3480,10 +3469,7 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
     /* a shared tile's waves split the body work (sweep_helper does its
      * share before the barrier that follows) */
     const int share = L.staged ? L.st.wave : 0, stride = L.staged ? L.st.waves : 1;
-    if (act) {
-        vel_load(L, share, stride);
-        body_prepass(L, h, share, stride);
-    }
+    if (act) body_prepass(L, h, share, stride);   /* with the velocity rows */
     int nlev = 0, njlev = 0;
     if (L.staged) {
         /* the tile's waves prepare the contacts and joints together (and
@@ -3585,10 +3571,7 @@ B3D_FN void sweep_helper(const Lane& L0, float dt, int substeps) {
     Soft cs = make_soft(hertz, damping, h);
     Soft ss = make_soft(2.0f * hertz, 0.5f * damping, h);
     float contact_speed = ldf(L.w, H_CONTACT_SPEED);
-    if (L.active) {
-        vel_load(L, L.st.wave, L.st.waves);
-        body_prepass(L, h, L.st.wave, L.st.waves);
-    }
+    if (L.active) body_prepass(L, h, L.st.wave, L.st.waves);   /* with the velocity rows */
     B3D_BARRIER();                 /* the velocities and body records are staged */
     if (L.active) {
         prepare_contacts(L, cs, ss);
