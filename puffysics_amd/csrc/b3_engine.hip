@@ -20,11 +20,12 @@
  *                              selected lane; LDS holds the lane's clip
  *                              polygons, then its body velocities
  *   b3k_step_shared<Masks, JL> the same for batches of at most one tile per
- *                              CU, with the narrowphase, the contact writes,
- *                              preparation and contact sweeps split over
- *                              four waves per tile (Masks: the candidate
- *                              search too, for 12 shapes or more; JL: the
- *                              joint rows in LDS, when they fit)
+ *                              CU, with the contact writes, preparation,
+ *                              contact sweeps and body and joint work split
+ *                              over eight waves per tile and the
+ *                              narrowphase over the first four (Masks: the
+ *                              candidate search too, for 12 shapes or more;
+ *                              JL: the joint rows in LDS, when they fit)
  *   b3k_apply                  dense force / torque / impulse inputs
  *   b3k_stats                  per-world B3StepStats
  */
@@ -124,9 +125,10 @@ __global__ __launch_bounds__(64) void b3k_step(uint32_t* live, const uint32_t* s
  * leave most CUs idle): wave 0 steps its lanes' worlds as b3k_step does;
  * the other waves wait for its shape bounds (Masks: test their rows of the
  * bound pairs, then list their share of the candidates) or its candidate
- * lists, collide their share of the pairs into the stage, write their share
- * of the new contacts, prepare their share of them, then solve their share
- * of each level of every contact sweep.
+ * lists, collide their share of the pairs into the stage (the first
+ * kClipWaves waves, which have clip rows), write their share of the new
+ * contacts, prepare their share of them, then solve their share of each
+ * level of every contact sweep and split the body and joint work.
  * Barriers: every thread of the workgroup reaches every __syncthreads.  A
  * tile with no stepping world returns as a whole (lane l of every wave
  * holds world 64 tile + l, so the ballot is the same in every wave).
@@ -152,9 +154,11 @@ __global__ __launch_bounds__(64 * kTileWaves) void b3k_step_shared(uint32_t* liv
     if (!(dt > 0.0f) || __ballot(stepping) == 0) return;
     PairStage S;
     S.p = stage + (size_t)tile * stage_tile_words + lane;
-    S.clip = (wave == 0 ? lds : lds + (size_t)lds_rows(g) * kLanes + (size_t)(wave - 1) * kClipWords * kLanes) + lane;
+    S.clip = wave >= kClipWaves ? nullptr
+        : (wave == 0 ? lds : lds + (size_t)lds_rows(g) * kLanes + (size_t)(wave - 1) * kClipWords * kLanes) + lane;
     S.wave = wave;
     S.waves = kTileWaves;
+    S.cwaves = kClipWaves;
     S.lds_bounds = 1;
     Lane L = lane_view(live, scratch, lds, g, tile, lane, opts);
     L.st = S;
@@ -400,8 +404,8 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
             (void)b3_engine_destroy(e);
             return err;
         }
-        /* A batch of at most one tile per CU shares each tile's narrowphase
-         * among kTileWaves waves (b3k_step_shared). */
+        /* A batch of at most one tile per CU shares each tile's step among
+         * kTileWaves waves (b3k_step_shared). */
         int cus = 0;
         /* wave 0's rows and the helpers' clip rows, then the old contact
          * keys, the overlap masks and the hit bits of the candidates */

@@ -30,8 +30,11 @@ struct B3Engine {
     bool joint_lds;          /* ... and keep the joint rows in LDS (b3d::joint_rows_fit) */
 };
 
-/* Waves per tile when the narrowphase is shared. */
-constexpr int kTileWaves = 4;
+/* Waves per tile when the narrowphase is shared (two per SIMD: the shared
+ * kernel's ~240 VGPRs allow it); the first kClipWaves of them have LDS clip
+ * rows and collide, all of them share the rest of the step. */
+constexpr int kTileWaves = 8;
+static_assert(b3d::kClipWaves <= kTileWaves, "the colliding waves are among the tile's");
 
 /* A CU's LDS.  The dynamic-LDS limit of a kernel is one setting shared by
  * every engine in the process, so the library raises it to this maximum

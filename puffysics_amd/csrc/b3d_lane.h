@@ -337,8 +337,10 @@ B3D_FN bool geometry_of(unsigned long long sig, Geometry* g, size_t* world_bytes
 constexpr int kManiWords = 4 + 8 * kMaxManifold;
 struct PairStage {
     uint32_t* p;     /* lane base */
-    float* clip;     /* this wave's clip rows (lane base) */
+    float* clip;     /* this wave's clip rows (lane base; waves < cwaves) */
     int wave, waves;
+    int cwaves;      /* waves 0 .. cwaves-1 have clip rows and share the
+                        narrowphase; every wave shares the rest */
     int lds_bounds;  /* the workgroup's LDS also holds wave 0's shape bounds */
 };
 
@@ -794,8 +796,11 @@ B3D_FN bool lds_old_keys(const Lane& L) { return L.staged && L.st.lds_bounds; }
  * and past the shape bounds, the old contact keys, the bound-overlap masks
  * of the shape pairs and the candidates' hit bits, which the waves use
  * while colliding in their clip rows. */
+/* The waves of a shared tile that collide: wave 0 in its own rows, the
+ * others in clip rows of their own past them. */
+constexpr int kClipWaves = 4;
 B3D_FN int shared_keys_word(const Geometry& g) {
-    int a = lds_rows(g) + 3 * kClipWords, b = kClipWords + 6 * g.max_s;
+    int a = lds_rows(g) + (kClipWaves - 1) * kClipWords, b = kClipWords + 6 * g.max_s;
     return a > b ? a : b;
 }
 B3D_FN int shared_masks_word(const Geometry& g) { return shared_keys_word(g) + g.max_c; }
@@ -1079,9 +1084,11 @@ B3D_FN void share_candidate(const Lane& L, bool masks, int t, int* row, int* acc
 }
 
 /* This wave's share of the tile's narrowphase: candidates t = wave, wave +
- * waves, ..., each collided (empty when filtered) into the stage; the next
- * share's shapes are in flight during a collision. */
+ * cwaves, ..., each collided (empty when filtered) into the stage; the next
+ * share's shapes are in flight during a collision.  Waves past cwaves have
+ * no clip rows and no share. */
 B3D_FN void pair_share(const Lane& L, const PairStage& S, bool masks, int ncand, int nj, int old_n, int sorted) {
+    if (S.wave >= S.cwaves) return;
     uint32_t jkey[kJointKeyRegs];
 #pragma unroll
     for (int k = 0; k < kJointKeyRegs; k++) jkey[k] = k < nj ? ldu(joint_rec(L, k), JS_KEY) : 0xffffffffu;
@@ -1095,8 +1102,8 @@ B3D_FN void pair_share(const Lane& L, const PairStage& S, bool masks, int ncand,
         An = A;
         Bn = B;
     }
-    for (; t < ncand; t += S.waves) {
-        int tn = t + S.waves;
+    for (; t < ncand; t += S.cwaves) {
+        int tn = t + S.cwaves;
         if (tn < ncand) {
             share_candidate(L, masks, tn, &row, &acc, &in, &jn, old_n, sorted);
             pshape_load(L, in, &An);

@@ -134,6 +134,7 @@ void emu_step_shared(uint32_t* tiles, int count, unsigned long long sig, float d
         S.clip = lds.data() + w % kLanes;
         S.wave = 0;
         S.waves = 1;
+        S.cwaves = 1;
         S.lds_bounds = 1;
         L.st = S;
         L.staged = true;
@@ -192,6 +193,7 @@ int emu_step_shared_idle(uint32_t* tiles, int count, unsigned long long sig, flo
         S.clip = lds.data() + w % kLanes;
         S.wave = 0;
         S.waves = 1;
+        S.cwaves = 1;
         S.lds_bounds = 1;
         L.st = S;
         L.staged = true;
@@ -208,10 +210,13 @@ int emu_step_shared_idle(uint32_t* tiles, int count, unsigned long long sig, flo
         int levels = active ? sch_get(L, 0) : 0;
         int jlevels = jl && active ? jsch_get(L, 0) : 0;
         if (host_barriers != fixed + passes * (1 + levels) + 2 * subs * jlevels) return -1 - w;
-        if (!active) {
+        /* as a colliding helper (wave 1 of 2) and as one past the
+         * colliding waves (wave 5 of 8, 4 colliding) */
+        for (int h = 0; h < 2 && !active; h++) {
             host_barriers = 0;
-            S.wave = 1;
-            S.waves = 2;
+            S.wave = h ? 5 : 1;
+            S.waves = h ? 8 : 2;
+            S.cwaves = h ? 4 : 2;
             L.st = S;
             if (use_masks) pair_helper<true>(L, S);
             else pair_helper<false>(L, S);

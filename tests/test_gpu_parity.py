@@ -331,10 +331,10 @@ def test_default_options_differ_only_in_solver_fields():
 
 @pytest.mark.parametrize("scene,count,steps", [(2, 256, 40), (4, 192, 10), (5, 256, 30)])
 def test_shared_narrowphase_matches_one_wave_per_tile(scene, count, steps):
-    """Batches of at most one tile per CU split the narrowphase over four
-    waves per tile; the worlds equal those of the one-wave launch word for
-    word, through masks, resets (restored by four waves) and the fused
-    reset."""
+    """Batches of at most one tile per CU split the step over eight waves
+    per tile (the narrowphase over four of them); the worlds equal those of
+    the one-wave launch word for word, through masks, resets (restored by
+    eight waves) and the fused reset."""
     from puffysics_amd.engine import B3_ENGINE_KEEP_SOLVER_FIELDS, B3_ENGINE_ONE_WAVE_PER_TILE
     worlds = scenes.build(scene, count)
     shared = _engine(worlds, scene)
