@@ -126,7 +126,7 @@ __global__ __launch_bounds__(64) void b3k_step(uint32_t* live, const uint32_t* s
  * the other waves wait for its shape bounds (Masks: test their rows of the
  * bound pairs, then list their share of the candidates) or its candidate
  * lists, collide their share of the pairs into the stage (the first
- * kClipWaves waves, which have clip rows), write their share of the new
+ * clip_waves, which have clip rows), write their share of the new
  * contacts, prepare their share of them, then solve their share of each
  * level of every contact sweep and split the body and joint work.
  * Barriers: every thread of the workgroup reaches every __syncthreads.  A
@@ -154,11 +154,10 @@ __global__ __launch_bounds__(64 * kTileWaves) void b3k_step_shared(uint32_t* liv
     if (!(dt > 0.0f) || __ballot(stepping) == 0) return;
     PairStage S;
     S.p = stage + (size_t)tile * stage_tile_words + lane;
-    S.clip = wave >= kClipWaves ? nullptr
-        : (wave == 0 ? lds : lds + (size_t)lds_rows(g) * kLanes + (size_t)(wave - 1) * kClipWords * kLanes) + lane;
+    S.cwaves = clip_waves(g, kTileWaves);
+    S.clip = wave < S.cwaves ? lds + (size_t)clip_row_word(g, wave) * kLanes + lane : nullptr;
     S.wave = wave;
     S.waves = kTileWaves;
-    S.cwaves = kClipWaves;
     S.lds_bounds = 1;
     Lane L = lane_view(live, scratch, lds, g, tile, lane, opts);
     L.st = S;

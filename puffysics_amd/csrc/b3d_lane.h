@@ -796,9 +796,23 @@ B3D_FN bool lds_old_keys(const Lane& L) { return L.staged && L.st.lds_bounds; }
  * and past the shape bounds, the old contact keys, the bound-overlap masks
  * of the shape pairs and the candidates' hit bits, which the waves use
  * while colliding in their clip rows. */
-/* The waves of a shared tile that collide: wave 0 in its own rows, the
- * others in clip rows of their own past them. */
+/* The waves of a shared tile that collide: wave 0 in its own rows, waves
+ * 1 .. kClipWaves-1 in clip rows of their own past them, and further waves
+ * in wave 0's rows past its clip rows, as many as fit: those rows hold the
+ * shape bounds until the candidates are listed (a barrier before the
+ * narrowphase) and nothing else until the velocities are staged after
+ * contact generation. */
 constexpr int kClipWaves = 4;
+B3D_FN int clip_waves(const Geometry& g, int waves) {
+    int n = kClipWaves + (lds_rows(g) - kClipWords) / kClipWords;
+    return n < waves ? n : waves;
+}
+/* First word (per lane) of colliding wave `wave`'s clip rows. */
+B3D_FN int clip_row_word(const Geometry& g, int wave) {
+    if (wave == 0) return 0;
+    if (wave < kClipWaves) return lds_rows(g) + (wave - 1) * kClipWords;
+    return (1 + wave - kClipWaves) * kClipWords;
+}
 B3D_FN int shared_keys_word(const Geometry& g) {
     int a = lds_rows(g) + (kClipWaves - 1) * kClipWords, b = kClipWords + 6 * g.max_s;
     return a > b ? a : b;
