@@ -2351,28 +2351,35 @@ B3D_FN void crow_solve(const Lane& L, int c, CRow& r, float inv_h, float contact
 }
 
 /* b3_solve_contacts (08:415-437): one Gauss-Seidel sweep in contact order.
- * Row c+1 (masses included) is in flight while row c is solved, and the
- * head of row c+2 while row c+1 loads.  The one-wave step runs large
- * batches, so the rows are streamed (qus). */
+ * Rows c+1 and c+2 (masses included) are in flight while row c is solved,
+ * and the head of row c+3 while row c+2 loads.  The one-wave step runs
+ * large batches, so the rows are streamed (qus). */
 B3D_FN void solve_contacts(const Lane& L, float inv_h, float contact_speed, int use_bias, Soft cs, Soft ss) {
     int cc = ldi(L.w, H_CONTACT_COUNT);
     if (cc <= 0) return;
     int relax = !use_bias;
-    CHead h1 = rhead_load(L, 0);
-    CRow cur, nxt;
-    crow_load<true>(L, 0, h1, relax, &cur);
+    CHead h = rhead_load(L, 0);
+    CRow cur, nxt, nx2;
+    crow_load<true>(L, 0, h, relax, &cur);
     crow_masses<true>(L, 0, &cur, cs, ss);
-    if (cc > 1) h1 = rhead_load(L, 1);
+    if (cc > 1) {
+        h = rhead_load(L, 1);
+        crow_load<true>(L, 1, h, relax, &nxt);
+        crow_masses<true>(L, 1, &nxt, cs, ss);
+    }
+    CHead h2 = h;
+    if (cc > 2) h2 = rhead_load(L, 2);
     for (int c = 0; c < cc; c++) {
-        CHead h2 = h1;
-        if (c + 2 < cc) h2 = rhead_load(L, c + 2);
-        if (c + 1 < cc) {
-            crow_load<true>(L, c + 1, h1, relax, &nxt);
-            crow_masses<true>(L, c + 1, &nxt, cs, ss);
+        CHead h3 = h2;
+        if (c + 3 < cc) h3 = rhead_load(L, c + 3);
+        if (c + 2 < cc) {
+            crow_load<true>(L, c + 2, h2, relax, &nx2);
+            crow_masses<true>(L, c + 2, &nx2, cs, ss);
         }
         crow_solve(L, c, cur, inv_h, contact_speed, use_bias);
         cur = nxt;
-        h1 = h2;
+        nxt = nx2;
+        h2 = h3;
     }
 }
 
