@@ -1744,22 +1744,35 @@ B3D_FN int prepare_contacts(const Lane& L, Soft cs, Soft ss) {
 /* A shared tile's contact levels (wave 0, after the parallel preparation):
  * each contact's level from its dynamic bodies' last levels, in contact
  * order, then a counting sort of the contacts by level into the entries. */
+constexpr int kSchedChunk = 8;
 B3D_FN void sched_build(const Lane& L) {
     int cc = clampi(ldi(L.w, H_CONTACT_COUNT), 0, L.g.max_c);
     int nb = body_count(L);
     for (int b = 0; b < nb; b++) sch_set(L, sch_last(L, b), 0);
     for (int lev = 0; lev <= cc; lev++) sch_set(L, sch_p(L, lev), 0);
     int nlev = 0;
-    for (int c = 0; c < cc; c++) {
-        CHead hd = chead_load(L, c);
-        int la = (hd.flags & CF_DYN_A) ? sch_get(L, sch_last(L, hd.a)) : 0;
-        int lb = (hd.flags & CF_DYN_B) ? sch_get(L, sch_last(L, hd.b)) : 0;
-        int lev = (la > lb ? la : lb) + 1;
-        if (hd.flags & CF_DYN_A) sch_set(L, sch_last(L, hd.a), lev);
-        if (hd.flags & CF_DYN_B) sch_set(L, sch_last(L, hd.b), lev);
-        sch_set(L, sch_level(L, c), lev);
-        sch_set(L, sch_p(L, lev), sch_get(L, sch_p(L, lev)) + 1);
-        if (lev > nlev) nlev = lev;
+    /* the heads, then the slots, are loaded kSchedChunk contacts at a time
+     * ahead of the LDS and stage writes, which the compiler would not move
+     * loads across */
+    for (int c0 = 0; c0 < cc; c0 += kSchedChunk) {
+        CHead hds[kSchedChunk];
+#pragma unroll
+        for (int k = 0; k < kSchedChunk; k++)
+            if (c0 + k < cc) hds[k] = chead_load(L, c0 + k);
+#pragma unroll
+        for (int k = 0; k < kSchedChunk; k++) {
+            int c = c0 + k;
+            if (c >= cc) continue;
+            const CHead& hd = hds[k];
+            int la = (hd.flags & CF_DYN_A) ? sch_get(L, sch_last(L, hd.a)) : 0;
+            int lb = (hd.flags & CF_DYN_B) ? sch_get(L, sch_last(L, hd.b)) : 0;
+            int lev = (la > lb ? la : lb) + 1;
+            if (hd.flags & CF_DYN_A) sch_set(L, sch_last(L, hd.a), lev);
+            if (hd.flags & CF_DYN_B) sch_set(L, sch_last(L, hd.b), lev);
+            sch_set(L, sch_level(L, c), lev);
+            sch_set(L, sch_p(L, lev), sch_get(L, sch_p(L, lev)) + 1);
+            if (lev > nlev) nlev = lev;
+        }
     }
     sch_set(L, 0, nlev);
     int run = 0;
@@ -1768,13 +1781,22 @@ B3D_FN void sched_build(const Lane& L) {
         sch_set(L, sch_p(L, lev), run);
         run += n;
     }
-    for (int c = 0; c < cc; c++) {
-        int lev = sch_get(L, sch_level(L, c));
-        int at = sch_get(L, sch_p(L, lev));
-        sch_set(L, sch_p(L, lev), at + 1);
-        uint32_t* e = sch_entry(L, at);
-        sti(e, 0, c);
-        sti(e, 1, ldi(sch_slots(L, c), 0));
+    for (int c0 = 0; c0 < cc; c0 += kSchedChunk) {
+        uint32_t slots[kSchedChunk];
+#pragma unroll
+        for (int k = 0; k < kSchedChunk; k++)
+            if (c0 + k < cc) slots[k] = ldu(sch_slots(L, c0 + k), 0);
+#pragma unroll
+        for (int k = 0; k < kSchedChunk; k++) {
+            int c = c0 + k;
+            if (c >= cc) continue;
+            int lev = sch_get(L, sch_level(L, c));
+            int at = sch_get(L, sch_p(L, lev));
+            sch_set(L, sch_p(L, lev), at + 1);
+            uint32_t* e = sch_entry(L, at);
+            sti(e, 0, c);
+            sti(e, 1, (int)slots[k]);
+        }
     }
 }
 
@@ -2845,8 +2867,21 @@ B3D_FN int joint_levels_scan(const Lane& L, int nj, int nb, int place) {
     for (int b = 0; b < nb; b++) jsch_set(L, jsch_last(L, b), 0);
     int nlev = 0;
     int j = 0;
+    /* the first kJointKeyRegs joints' heads in registers, loaded together
+     * ahead of the LDS writes (which the compiler would not move loads
+     * across) */
+    uint32_t abr[kJointKeyRegs];
+#pragma unroll
+    for (int k = 0; k < kJointKeyRegs; k++) abr[k] = k < nj ? ldu(joint_rec(L, k), JS_AB) : 0u;
     for (int t = 0; t < total; t++) {
-        uint32_t ab = ldu(joint_rec(L, j), JS_AB);
+        uint32_t ab = abr[0];
+        if (j < kJointKeyRegs) {
+#pragma unroll
+            for (int k = 1; k < kJointKeyRegs; k++)
+                if (j == k) ab = abr[k];
+        } else {
+            ab = ldu(joint_rec(L, j), JS_AB);
+        }
         int a = (int)(ab & 0xffffu), b = (int)(ab >> 16);
         bool da = is_dyn_flag(L, a), db = is_dyn_flag(L, b);
         int la = da ? jsch_get(L, jsch_last(L, a)) : 0;
