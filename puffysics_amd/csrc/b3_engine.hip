@@ -426,7 +426,7 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
         }
         if (e->tiles <= cus && shared_lds <= kCuLdsBytes) {
             size_t max_cand = (size_t)g.max_s * (size_t)(g.max_s - 1) / 2;
-            size_t stage_words = max_cand * kManiWords;
+            size_t stage_words = max_cand * kStageWords;
             if ((size_t)stage_sched_words(g) > stage_words) stage_words = (size_t)stage_sched_words(g);
             e->stage_tile_words = (1 + stage_words) * kLanes;
             e->lds_shared_bytes = shared_lds;

@@ -331,10 +331,17 @@ B3D_FN bool geometry_of(unsigned long long sig, Geometry* g, size_t* world_bytes
 
 /* Manifolds of a tile's candidate pairs, computed by the tile's waves
  * together (small batches, where one wave per tile leaves CUs idle): the
- * lane's candidate count at word 0, then kManiWords words per candidate
- * (count, normal, then per point p_a, p_b, separation, feature), word k of a
- * lane at p[k * kLanes]. */
+ * lane's candidate count at word 0 (p[0], a row of the tile's 64 lanes),
+ * then, past that row, one record of kStageWords words per candidate and
+ * lane, lane-major (candidate t of lane l at record t * kLanes + l): the
+ * manifold's kManiWords words (count, normal, then per point p_a, p_b,
+ * separation, feature), the pair's shape key and its old contact (or -1),
+ * and padding to 16 bytes.  A lane's record is contiguous, so the contact
+ * writes, which take each lane's manifolds in its own contact order, read
+ * whole records; only candidates with a manifold have one written. */
 constexpr int kManiWords = 4 + 8 * kMaxManifold;
+constexpr int kStageWords = kManiWords + 4;
+static_assert(kStageWords % 4 == 0, "stage records are whole quads");
 struct PairStage {
     uint32_t* p;     /* lane base */
     float* clip;     /* this wave's clip rows (lane base; waves < cwaves) */
@@ -967,33 +974,63 @@ B3D_FN void warm_apply(const OldWarm& o, NewContact* nc) {
  * writes is; the two sorted lists are merged).  Then the list is walked
  * with the next pair's shape records and old contact in flight while the
  * current pair is tested and collided. */
-B3D_FN void mani_store(const PairStage& S, int t, const Mani& m) {
-    uint32_t* r = S.p + (size_t)(1 + t * kManiWords) * kLanes;
-    sti(r, 0, m.count);
-    if (m.count <= 0) return;
-    st3(r, 1, m.normal);
-#pragma unroll
-    for (int p = 0; p < kMaxManifold; p++) {
-        if (p >= m.count) continue;
-        st3(r, 4 + 8 * p, m.p_a[p]);
-        st3(r, 7 + 8 * p, m.p_b[p]);
-        stf(r, 10 + 8 * p, m.sep[p]);
-        sti(r, 11 + 8 * p, (int)m.feature[p]);
-    }
+/* Lane `lane`'s record of candidate t, in 16-byte quads (aligned: the
+ * stage's tiles are whole rows of 64 words, its records 40 words). */
+struct alignas(16) Quad { uint32_t x, y, z, w; };
+B3D_FN Quad* mani_rec(const PairStage& S, int lane, int t) {
+    return reinterpret_cast<Quad*>(S.p - lane + kLanes + ((size_t)t * kLanes + lane) * kStageWords);
 }
-/* All words of a staged manifold, requested at once (those past its point
- * count are stale and go unused), so that the load can run ahead. */
-B3D_FN void mani_load(const PairStage& S, int t, Mani* m) {
-    const uint32_t* r = S.p + (size_t)(1 + t * kManiWords) * kLanes;
-    m->count = ldi(r, 0);
-    m->normal = ld3(r, 1);
+/* The record of a candidate with a manifold, as whole quads (the points past
+ * its count hold whatever the collision left there and go unused). */
+B3D_FN void mani_store(const PairStage& S, int lane, int t, const Mani& m, uint32_t key, int match) {
+    uint32_t w[kStageWords];
+    w[0] = (uint32_t)m.count;
+    w[1] = __builtin_bit_cast(uint32_t, m.normal.x);
+    w[2] = __builtin_bit_cast(uint32_t, m.normal.y);
+    w[3] = __builtin_bit_cast(uint32_t, m.normal.z);
 #pragma unroll
     for (int p = 0; p < kMaxManifold; p++) {
-        m->p_a[p] = ld3(r, 4 + 8 * p);
-        m->p_b[p] = ld3(r, 7 + 8 * p);
-        m->sep[p] = ldf(r, 10 + 8 * p);
-        m->feature[p] = ldu(r, 11 + 8 * p);
+        w[4 + 8 * p] = __builtin_bit_cast(uint32_t, m.p_a[p].x);
+        w[5 + 8 * p] = __builtin_bit_cast(uint32_t, m.p_a[p].y);
+        w[6 + 8 * p] = __builtin_bit_cast(uint32_t, m.p_a[p].z);
+        w[7 + 8 * p] = __builtin_bit_cast(uint32_t, m.p_b[p].x);
+        w[8 + 8 * p] = __builtin_bit_cast(uint32_t, m.p_b[p].y);
+        w[9 + 8 * p] = __builtin_bit_cast(uint32_t, m.p_b[p].z);
+        w[10 + 8 * p] = __builtin_bit_cast(uint32_t, m.sep[p]);
+        w[11 + 8 * p] = m.feature[p];
     }
+    w[kManiWords] = key;
+    w[kManiWords + 1] = (uint32_t)match;
+    w[kManiWords + 2] = 0u;
+    w[kManiWords + 3] = 0u;
+    Quad* r = mani_rec(S, lane, t);
+#pragma unroll
+    for (int q = 0; q < kStageWords / 4; q++) r[q] = Quad{w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]};
+}
+B3D_FN void mani_load(const PairStage& S, int lane, int t, Mani* m, uint32_t* key, int* match) {
+    const Quad* r = mani_rec(S, lane, t);
+    uint32_t w[kStageWords];
+#pragma unroll
+    for (int q = 0; q < kStageWords / 4; q++) {
+        Quad v = r[q];
+        w[4 * q] = v.x;
+        w[4 * q + 1] = v.y;
+        w[4 * q + 2] = v.z;
+        w[4 * q + 3] = v.w;
+    }
+    m->count = (int)w[0];
+    m->normal = v3(__builtin_bit_cast(float, w[1]), __builtin_bit_cast(float, w[2]), __builtin_bit_cast(float, w[3]));
+#pragma unroll
+    for (int p = 0; p < kMaxManifold; p++) {
+        m->p_a[p] = v3(__builtin_bit_cast(float, w[4 + 8 * p]), __builtin_bit_cast(float, w[5 + 8 * p]),
+            __builtin_bit_cast(float, w[6 + 8 * p]));
+        m->p_b[p] = v3(__builtin_bit_cast(float, w[7 + 8 * p]), __builtin_bit_cast(float, w[8 + 8 * p]),
+            __builtin_bit_cast(float, w[9 + 8 * p]));
+        m->sep[p] = __builtin_bit_cast(float, w[10 + 8 * p]);
+        m->feature[p] = w[11 + 8 * p];
+    }
+    *key = w[kManiWords];
+    *match = (int)w[kManiWords + 1];
 }
 
 /* Whether candidate pair (A, B) is filtered out before the narrowphase
@@ -1080,18 +1117,17 @@ B3D_FN int mask_candidates(const Lane& L, int ns) {
     for (int i = 0; i < ns; i++) n += __builtin_popcountll(overlap_mask(L, i));
     return n;
 }
-/* Candidate t's shapes: from the masks (listing it, with its old-contact
- * match, in the candidate rows), or from wave 0's list. */
-B3D_FN void share_candidate(const Lane& L, bool masks, int t, int* row, int* acc, int* i, int* j, int old_n,
-        int sorted) {
-    uint32_t* cand = L.scr + L.g.scr_cand * kLanes;
+/* Candidate t's shapes and old-contact match: from the masks (with a
+ * search of the old keys), or from wave 0's list. */
+B3D_FN void share_candidate(const Lane& L, bool masks, int t, int* row, int* acc, int* i, int* j, int* match,
+        int old_n, int sorted) {
+    const uint32_t* cand = L.scr + L.g.scr_cand * kLanes;
     if (masks) {
         mask_candidate(L, t, row, acc, i, j);
-        uint32_t key = shape_key(*i, *j);
-        sti(cand, 2 * t, (int)key);
-        sti(cand, 2 * t + 1, sorted ? old_match(L, old_n, key) : -1);
+        *match = sorted ? old_match(L, old_n, shape_key(*i, *j)) : -1;
     } else {
         uint32_t key = ldu(cand, 2 * t);
+        *match = ldi(cand, 2 * t + 1);
         *i = (int)(key >> 16);
         *j = (int)(key & 0xffffu);
     }
@@ -1106,11 +1142,11 @@ B3D_FN void pair_share(const Lane& L, const PairStage& S, bool masks, int ncand,
     uint32_t jkey[kJointKeyRegs];
 #pragma unroll
     for (int k = 0; k < kJointKeyRegs; k++) jkey[k] = k < nj ? ldu(joint_rec(L, k), JS_KEY) : 0xffffffffu;
-    int row = 0, acc = 0, i = 0, j = 0, in = 0, jn = 0;
+    int row = 0, acc = 0, i = 0, j = 0, in = 0, jn = 0, match = -1, matchn = -1;
     PairShape A, B, An, Bn;
     int t = S.wave;
     if (t < ncand) {
-        share_candidate(L, masks, t, &row, &acc, &i, &j, old_n, sorted);
+        share_candidate(L, masks, t, &row, &acc, &i, &j, &match, old_n, sorted);
         pshape_load(L, i, &A);
         pshape_load(L, j, &B);
         An = A;
@@ -1119,19 +1155,22 @@ B3D_FN void pair_share(const Lane& L, const PairStage& S, bool masks, int ncand,
     for (; t < ncand; t += S.cwaves) {
         int tn = t + S.cwaves;
         if (tn < ncand) {
-            share_candidate(L, masks, tn, &row, &acc, &in, &jn, old_n, sorted);
+            share_candidate(L, masks, tn, &row, &acc, &in, &jn, &matchn, old_n, sorted);
             pshape_load(L, in, &An);
             pshape_load(L, jn, &Bn);
         }
         Mani m;
         m.count = 0;
         if (!pair_skipped(L, A, B, jkey, nj)) collide_pair(&m, A.P, B.P, S.clip);
-        mani_store(S, t, m);
-        if (m.count > 0) lds_or(hit_rows(L) + (t >> 5) * kLanes, 1u << (t & 31));
+        if (m.count > 0) {
+            mani_store(S, L.lane, t, m, shape_key(i, j), match);
+            lds_or(hit_rows(L) + (t >> 5) * kLanes, 1u << (t & 31));
+        }
         A = An;
         B = Bn;
         i = in;
         j = jn;
+        match = matchn;
     }
 }
 
@@ -1209,31 +1248,40 @@ B3D_FN int write_new_contact(const Lane& L, int cc, int i, int j, const PairShap
     return info;
 }
 
-/* This wave's share of writing the new contacts: candidate t with a
- * manifold becomes contact number (candidates below t with one), as the
- * sequential append would number it; those past the capacity are dropped
- * (the header is wave 0's). */
+/* This wave's share of writing the new contacts: contacts k = wave, wave +
+ * waves, ..., below the lane's count of candidates with a manifold and the
+ * capacity.  Contact k is the candidate holding the lane's k-th manifold,
+ * as the sequential append numbers them; those past the capacity are
+ * dropped (the header is wave 0's).  All lanes write contact k at once, so
+ * each field's store covers one row of the tile's lanes. */
 B3D_FN void append_share(const Lane& L, const PairStage& S, int ncand, int old_n, int sorted) {
-    const uint32_t* cand = L.scr + L.g.scr_cand * kLanes;
     const float* hit = hit_rows(L);
+    int nwords = (ncand + 31) >> 5, total = 0;
+    for (int k = 0; k < nwords; k++) total += __builtin_popcount(__builtin_bit_cast(uint32_t, hit[k * kLanes]));
+    int cap = total < L.g.max_c ? total : L.g.max_c;
     int acc = 0, word = 0, rest = 0;
-    for (int t = S.wave; t < ncand; t += S.waves) {
-        while (word < (t >> 5)) acc += __builtin_popcount(__builtin_bit_cast(uint32_t, hit[word++ * kLanes]));
-        uint32_t bits = __builtin_bit_cast(uint32_t, hit[(t >> 5) * kLanes]);
-        if (!((bits >> (t & 31)) & 1u)) continue;
-        int idx = acc + __builtin_popcount(bits & ((1u << (t & 31)) - 1u));
-        if (idx >= L.g.max_c) continue;
-        uint32_t key = ldu(cand, 2 * t);
-        int match = ldi(cand, 2 * t + 1);
+    for (int k = S.wave; k < cap; k += S.waves) {
+        /* the word holding the k-th manifold (acc: manifolds in the words
+         * before it), then the bit */
+        uint32_t bits = __builtin_bit_cast(uint32_t, hit[word * kLanes]);
+        while (acc + __builtin_popcount(bits) <= k) {
+            acc += __builtin_popcount(bits);
+            word++;
+            bits = __builtin_bit_cast(uint32_t, hit[word * kLanes]);
+        }
+        for (int r = k - acc; r > 0; r--) bits &= bits - 1;
+        int t = word * 32 + __builtin_ctz(bits);
+        Mani m;
+        uint32_t key;
+        int match;
+        mani_load(S, L.lane, t, &m, &key, &match);
         int i = (int)(key >> 16), j = (int)(key & 0xffffu);
         PairShape A, B;
         pshape_load(L, i, &A);
         pshape_load(L, j, &B);
         OldWarm orec;
         if (sorted && match >= 0) old_load(L, match, &orec);
-        Mani m;
-        mani_load(S, t, &m);
-        rest |= write_new_contact(L, idx, i, j, A, B, m, sorted, match, orec, old_n) & CF_RESTITUTION;
+        rest |= write_new_contact(L, k, i, j, A, B, m, sorted, match, orec, old_n) & CF_RESTITUTION;
     }
     if (rest) lds_or(const_cast<float*>(hit) + hit_words(L.g) * kLanes, 1u);
 }
@@ -1362,7 +1410,6 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
     for (int k = 0; k < kJointKeyRegs; k++) jkey[k] = k < nj ? ldu(joint_rec(L, k), JS_KEY) : 0xffffffffu;
     PairShape A, B, An, Bn;
     OldWarm orec, orecn;
-    Mani ms, msn;   /* staged manifolds of candidates t and t + 1 */
     uint32_t key = 0, key1 = 0;
     int match = -1, match1 = -1;
     if (ncand > 0) {
@@ -1371,7 +1418,6 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
         pshape_load(L, (int)(key >> 16), &A);
         pshape_load(L, (int)(key & 0xffffu), &B);
         if (match >= 0) old_load(L, match, &orec);
-        if (L.staged) mani_load(L.st, 0, &ms);
     }
     if (ncand > 1) {
         key1 = ldu(cand, 2);
@@ -1389,13 +1435,11 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
             else An = A;
             pshape_load(L, (int)(key1 & 0xffffu), &Bn);
             if (match1 >= 0) old_load(L, match1, &orecn);
-            if (L.staged) mani_load(L.st, t + 1, &msn);
         }
         int i = (int)(key >> 16), j = (int)(key & 0xffffu);
         Mani m;
         m.count = 0;
-        if (L.staged) m = ms;
-        else if (!pair_skipped(L, A, B, jkey, nj)) collide_pair(&m, A.P, B.P, L.vel);
+        if (!pair_skipped(L, A, B, jkey, nj)) collide_pair(&m, A.P, B.P, L.vel);
         if (m.count > 0 && cc >= g.max_c) {
             overflow = 1;
             dropped++;
@@ -1406,7 +1450,6 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
         A = An;
         B = Bn;
         orec = orecn;
-        ms = msn;
         key = key1;
         key1 = key2;
         match = match1;

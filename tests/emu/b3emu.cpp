@@ -121,7 +121,7 @@ void emu_step_shared(uint32_t* tiles, int count, unsigned long long sig, float d
     if (jl && joint_lds_word(g) + joint_lds_words(g) > rows) rows = joint_lds_word(g) + joint_lds_words(g);
     std::vector<float> lds((size_t)rows * kLanes);
     size_t max_cand = (size_t)g.max_s * (size_t)(g.max_s - 1) / 2;
-    size_t words = max_cand * kManiWords;
+    size_t words = max_cand * kStageWords;
     if ((size_t)stage_sched_words(g) > words) words = (size_t)stage_sched_words(g);
     size_t stage_tile = (1 + words) * kLanes;
     std::vector<uint32_t> stage((size_t)ntiles * stage_tile);
@@ -178,7 +178,7 @@ int emu_step_shared_idle(uint32_t* tiles, int count, unsigned long long sig, flo
     if (jl && joint_lds_word(g) + joint_lds_words(g) > rows) rows = joint_lds_word(g) + joint_lds_words(g);
     std::vector<float> lds((size_t)rows * kLanes);
     size_t max_cand = (size_t)g.max_s * (size_t)(g.max_s - 1) / 2;
-    size_t words = max_cand * kManiWords;
+    size_t words = max_cand * kStageWords;
     if ((size_t)stage_sched_words(g) > words) words = (size_t)stage_sched_words(g);
     size_t stage_tile = (1 + words) * kLanes;
     std::vector<uint32_t> stage((size_t)ntiles * stage_tile);
