@@ -2492,47 +2492,114 @@ B3D_FN void solve_contacts_leveled(const Lane& L, float inv_h, float contact_spe
     }
 }
 
+/* A wave's walk over its entries of a levelled contact pass: entries
+ * first + wave, first + wave + waves, ... of each level [first, end) in
+ * turn, among the lane's own `mine` levels.  The current entry comes with
+ * its head, and the next entry is in flight: the entries (in the stage) and
+ * the heads do not change during a pass, so they are loaded an item ahead,
+ * across the level barriers. */
+struct CWalk {
+    int i, lev, c, e;      /* the current entry (i < 0: none left): its index,
+                              level, contact and record slots */
+    CHead h;
+    int i1, lev1, c1, e1;  /* the next entry */
+};
+/* The wave's next entry after entry i of level *lev, or -1. */
+B3D_FN int clevel_next(const Lane& L, int i, int* lev, int mine) {
+    const PairStage& S = L.st;
+    int end = sch_get(L, sch_p(L, *lev));
+    if (i + S.waves < end) return i + S.waves;
+    for (int l = *lev + 1; l <= mine; l++) {
+        int start = end;
+        end = sch_get(L, sch_p(L, l));
+        if (start + S.wave < end) {
+            *lev = l;
+            return start + S.wave;
+        }
+    }
+    return -1;
+}
+B3D_FN void centry_load(const Lane& L, int i, int* c, int* e) {
+    *c = 0;
+    *e = 0;
+    if (i < 0) return;
+    const uint32_t* ep = sch_entry(L, i);
+    *c = ldi(ep, 0);
+    *e = ldi(ep, 1);
+}
+/* The walk at entry i of level lev (contact c, slots e): its head, and the
+ * next entry. */
+B3D_FN CWalk cwalk_at(const Lane& L, int i, int lev, int c, int e, int mine) {
+    CWalk w;
+    w.i = i;
+    w.lev = lev;
+    w.c = c;
+    w.e = e;
+    w.h = head_of(0u, 0u);
+    if (i >= 0) w.h = rhead_at(L, c, e & 63);
+    w.lev1 = lev;
+    w.i1 = i >= 0 ? clevel_next(L, i, &w.lev1, mine) : -1;
+    centry_load(L, w.i1, &w.c1, &w.e1);
+    return w;
+}
+B3D_FN CWalk cwalk_start(const Lane& L, int mine) {
+    const PairStage& S = L.st;
+    int lev = 1, i = -1, c, e;
+    if (mine >= 1) i = S.wave < sch_get(L, sch_p(L, 1)) ? S.wave : clevel_next(L, S.wave - S.waves, &lev, mine);
+    centry_load(L, i, &c, &e);
+    return cwalk_at(L, i, lev, c, e, mine);
+}
+
 /* b3_warm_start (08:194-232) for a shared tile: each contact's impulses
  * as warm_start_contacts applies them, level by level like the sweeps
- * (1 + nlev barriers). */
+ * (1 + nlev barriers).  An item's row loads with the next item's head and
+ * the entry after it (the walk), before its impulses are applied. */
 B3D_FN void warm_contacts_leveled(const Lane& L, int nlev) {
-    const PairStage& S = L.st;
     int mine = sch_get(L, 0);
+    CWalk w = cwalk_start(L, mine);
     B3D_BARRIER();
-    int first = 0;
-    for (int lev = 1; lev <= nlev; lev++) {
-        if (lev <= mine) {
-            int end = sch_get(L, sch_p(L, lev));
-            for (int i = first + S.wave; i < end; i += S.waves) {
-                const uint32_t* en = sch_entry(L, i);
-                int c = ldi(en, 0), e = ldi(en, 1);
-                CHead h = rhead_at(L, c, e & 63);
-                const uint32_t* r = crec(L, c, h.slot);
-                float ma, mb;
-                M3 ia, ib;
-                rec_masses(r, h.flags, &ma, &ia, &mb, &ib);
-                V3 n = q3(r, R_N);
+    for (int l = 1; l <= nlev; l++) {
+        while (w.i >= 0 && w.lev == l) {
+            int c = w.c, e = w.e;
+            CHead h = w.h;
+            const uint32_t* r = crec(L, c, h.slot);
+            float ma, mb;
+            M3 ia, ib;
+            rec_masses(r, h.flags, &ma, &ia, &mb, &ib);
+            V3 n = q3(r, R_N);
+            V3 ra[kMaxManifold], rb[kMaxManifold];
+            float ni[kMaxManifold];
 #pragma unroll
-                for (int p = 0; p < kMaxManifold; p++) {
-                    if (p >= h.pc) continue;
-                    const uint32_t* pr = prec(L, c, p, (e >> (6 + 6 * p)) & 63);
-                    V3 P = scale(n, qf(r, R_NI + 2 * p));
-                    apply_impulse(L, h.a, ma, ia, q3(pr, PR_RA), P, -1.0f);
-                    apply_impulse(L, h.b, mb, ib, q3(pr, PR_RB), P, 1.0f);
-                }
-                V3 t1 = q3(r, R_T1);
-                V2 fi;
-                fi.x = qf(r, R_FI);
-                fi.y = qf(r, R_FI + 1);
-                V3 t2 = cross(t1, n);
-                V3 f = add(scale(t1, fi.x), scale(t2, fi.y));
-                apply_impulse(L, h.a, ma, ia, q3(r, R_CA), f, -1.0f);
-                apply_impulse(L, h.b, mb, ib, q3(r, R_CB), f, 1.0f);
-                V3 tr = add(scale(n, qf(r, R_TWIST)), q3(r, R_ROLL));
-                if (is_dyn_flag(L, h.a)) set_vang(L, h.a, sub(vang(L, h.a), mv(ia, tr)));
-                if (is_dyn_flag(L, h.b)) set_vang(L, h.b, add(vang(L, h.b), mv(ib, tr)));
+            for (int p = 0; p < kMaxManifold; p++) {
+                if (p >= h.pc) continue;
+                const uint32_t* pr = prec(L, c, p, (e >> (6 + 6 * p)) & 63);
+                ra[p] = q3(pr, PR_RA);
+                rb[p] = q3(pr, PR_RB);
+                ni[p] = qf(r, R_NI + 2 * p);
             }
-            first = end;
+            V3 t1 = q3(r, R_T1);
+            V2 fi;
+            fi.x = qf(r, R_FI);
+            fi.y = qf(r, R_FI + 1);
+            V3 ca = q3(r, R_CA), cb = q3(r, R_CB);
+            float twist = qf(r, R_TWIST);
+            V3 roll = q3(r, R_ROLL);
+            CWalk nx = cwalk_at(L, w.i1, w.lev1, w.c1, w.e1, mine);
+#pragma unroll
+            for (int p = 0; p < kMaxManifold; p++) {
+                if (p >= h.pc) continue;
+                V3 P = scale(n, ni[p]);
+                apply_impulse(L, h.a, ma, ia, ra[p], P, -1.0f);
+                apply_impulse(L, h.b, mb, ib, rb[p], P, 1.0f);
+            }
+            V3 t2 = cross(t1, n);
+            V3 f = add(scale(t1, fi.x), scale(t2, fi.y));
+            apply_impulse(L, h.a, ma, ia, ca, f, -1.0f);
+            apply_impulse(L, h.b, mb, ib, cb, f, 1.0f);
+            V3 tr = add(scale(n, twist), roll);
+            if (is_dyn_flag(L, h.a)) set_vang(L, h.a, sub(vang(L, h.a), mv(ia, tr)));
+            if (is_dyn_flag(L, h.b)) set_vang(L, h.b, add(vang(L, h.b), mv(ib, tr)));
+            w = nx;
         }
         B3D_BARRIER();
     }
