@@ -704,19 +704,22 @@ constexpr int kJointKeyRegs = 8;
  * bounds go to `bounds` (lane-strided lo.xyz, hi.xyz per shape), the rest to
  * the shape records.  Shapes are done in chunks, body poses requested for a
  * whole chunk at once. */
-B3D_FN void shape_pass(const Lane& L, int ns, float* bounds) {
+B3D_FN void shape_pass(const Lane& L, int ns, float* bounds, int first = 0, int stride = 1) {
     V3 pad = v3(kSpeculative, kSpeculative, kSpeculative);
-    /* the next chunk's body indices are in flight while a chunk is posed */
+    /* chunks of kShapeChunk shapes first, first + stride, ... (a shared
+     * tile's waves split them); the next chunk's body indices are in
+     * flight while a chunk is posed */
+    const int step = stride * kShapeChunk;
     int bn[kShapeChunk];
 #pragma unroll
     for (int k = 0; k < kShapeChunk; k++)
-        if (k < ns) bn[k] = ldi(L.w, sw(L, k, S_BODY));
-    for (int s0 = 0; s0 < ns; s0 += kShapeChunk) {
+        if (first * kShapeChunk + k < ns) bn[k] = ldi(L.w, sw(L, first * kShapeChunk + k, S_BODY));
+    for (int s0 = first * kShapeChunk; s0 < ns; s0 += step) {
         int b[kShapeChunk];
 #pragma unroll
         for (int k = 0; k < kShapeChunk; k++) {
             b[k] = bn[k];
-            if (s0 + kShapeChunk + k < ns) bn[k] = ldi(L.w, sw(L, s0 + kShapeChunk + k, S_BODY));
+            if (s0 + step + k < ns) bn[k] = ldi(L.w, sw(L, s0 + step + k, S_BODY));
         }
         V3 bpos[kShapeChunk], center[kShapeChunk];
         Q brot[kShapeChunk];
@@ -791,9 +794,10 @@ B3D_FN Posed posed_from(const uint32_t* r) {
 /* Shape pair (i, j) as one ordered 32-bit key (shape ids are below 2^16). */
 B3D_FN uint32_t shape_key(int i, int j) { return ((uint32_t)i << 16) | (uint32_t)j; }
 
-/* Copy the contacts' warm-start data into the old-cache scratch
- * (08_contacts.inl:65-91); returns whether their shape pairs are strictly
- * increasing, as every list the step itself writes is. */
+/* The contacts' warm-start data go to the old-cache scratch
+ * (08_contacts.inl:65-91) in two parts, old_keys (which also tells whether
+ * their shape pairs are strictly increasing, as every list the step itself
+ * writes is) and old_warm_copy. */
 /* With a shared narrowphase the workgroup's LDS also holds the old contacts'
  * keys, after wave 0's clip rows and shape bounds, for the candidate search
  * to merge against. */
@@ -832,11 +836,44 @@ B3D_FN uint32_t old_key(const Lane& L, int k) {
     return ldu(old_rec(L, k), O_KEY);
 }
 
-B3D_FN int save_old(const Lane& L, int old_n) {
+/* The old contacts' shape pairs and keys (to the old-cache records and,
+ * in a shared tile, to LDS); returns whether the pairs are strictly
+ * increasing.  The heads of kKeyChunk contacts load together. */
+constexpr int kKeyChunk = 8;
+B3D_FN int old_keys(const Lane& L, int old_n) {
     int sorted = 1;
     uint32_t prev = 0;
-    for (int k0 = 0; k0 < old_n; k0 += kChunk) {
-        int sa[kChunk], sb[kChunk], pc[kChunk];
+    for (int k0 = 0; k0 < old_n; k0 += kKeyChunk) {
+        int sa[kKeyChunk], sb[kKeyChunk];
+#pragma unroll
+        for (int q = 0; q < kKeyChunk; q++) {
+            int k = k0 + q;
+            if (k >= old_n) continue;
+            sa[q] = ldi(L.w, cw(L, k, C_SHAPE_A));
+            sb[q] = ldi(L.w, cw(L, k, C_SHAPE_B));
+        }
+#pragma unroll
+        for (int q = 0; q < kKeyChunk; q++) {
+            int k = k0 + q;
+            if (k >= old_n) continue;
+            uint32_t* o = old_rec(L, k);
+            uint32_t key = shape_key(sa[q], sb[q]);
+            if (k > 0 && !(prev < key && (uint32_t)sa[q] < 65536u && (uint32_t)sb[q] < 65536u)) sorted = 0;
+            prev = key;
+            sti(o, O_SHAPE_A, sa[q]);
+            sti(o, O_SHAPE_B, sb[q]);
+            sti(o, O_KEY, (int)key);
+            if (lds_old_keys(L)) old_key_rows(L)[k * kLanes] = __builtin_bit_cast(float, key);
+        }
+    }
+    return sorted;
+}
+/* The old contacts' warm-start data (point count, features, impulses) to
+ * their old-cache records: chunks first, first + stride, ... (a shared
+ * tile's waves split them). */
+B3D_FN void old_warm_copy(const Lane& L, int old_n, int first = 0, int stride = 1) {
+    for (int k0 = first * kChunk; k0 < old_n; k0 += stride * kChunk) {
+        int pc[kChunk];
         uint32_t feat[kChunk][kMaxManifold];
         float ni[kChunk][kMaxManifold], fx[kChunk], fy[kChunk], tw[kChunk];
         V3 roll[kChunk];
@@ -844,8 +881,6 @@ B3D_FN int save_old(const Lane& L, int old_n) {
         for (int q = 0; q < kChunk; q++) {
             int k = k0 + q;
             if (k >= old_n) continue;
-            sa[q] = ldi(L.w, cw(L, k, C_SHAPE_A));
-            sb[q] = ldi(L.w, cw(L, k, C_SHAPE_B));
             pc[q] = clampi(ldi(L.w, cw(L, k, C_POINT_COUNT)), 0, kMaxManifold);
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
@@ -862,14 +897,7 @@ B3D_FN int save_old(const Lane& L, int old_n) {
             int k = k0 + q;
             if (k >= old_n) continue;
             uint32_t* o = old_rec(L, k);
-            uint32_t key = shape_key(sa[q], sb[q]);
-            if (k > 0 && !(prev < key && (uint32_t)sa[q] < 65536u && (uint32_t)sb[q] < 65536u)) sorted = 0;
-            prev = key;
-            sti(o, O_SHAPE_A, sa[q]);
-            sti(o, O_SHAPE_B, sb[q]);
             sti(o, O_POINT_COUNT, pc[q]);
-            sti(o, O_KEY, (int)key);
-            if (lds_old_keys(L)) old_key_rows(L)[k * kLanes] = __builtin_bit_cast(float, key);
 #pragma unroll
             for (int p = 0; p < kMaxManifold; p++) {
                 if (p >= pc[q]) continue;
@@ -882,7 +910,6 @@ B3D_FN int save_old(const Lane& L, int old_n) {
             st3(o, O_ROLLING_IMPULSE, roll[q]);
         }
     }
-    return sorted;
 }
 
 /* A new contact assembled in registers before it is written out. */
@@ -1298,7 +1325,13 @@ B3D_FN void pair_helper(const Lane& L0, const PairStage& S) {
     int nj = L.active ? clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j) : 0;
     int old_n = L.active ? clampi(ldi(L.w, H_CONTACT_COUNT), 0, L.g.max_c) : 0;
     constexpr bool masks = Masks;
-    B3D_BARRIER();                 /* wave 0's shape bounds and old keys (or its candidates) */
+    if (masks && L.active) {
+        /* this wave's share of the old contacts' warm data and of the
+         * shape pass (find_contacts) */
+        old_warm_copy(L, old_n, S.wave, S.waves);
+        shape_pass(L, ns, L.vel + kClipWords * kLanes, S.wave, S.waves);
+    }
+    B3D_BARRIER();                 /* the shape bounds and old keys (or wave 0's candidates) */
     int ncand;
     if (masks) {
         overlap_rows(L, L.vel + kClipWords * kLanes, ns, S);
@@ -1469,7 +1502,13 @@ B3D_FN void find_contacts(const Lane& L) {
     /* an idle lane of a shared tile has no old contacts, shapes or joints:
      * it only meets the other waves at find_pairs' barriers */
     int old_n = L.active ? clampi(ldi(L.w, H_CONTACT_COUNT), 0, g.max_c) : 0;
-    int sorted = L.active ? save_old(L, old_n) : 0;
+    /* with the overlap masks a shared tile's waves split the old contacts'
+     * warm data and the shape pass before the first barrier (pair_helper);
+     * wave 0 lists the keys */
+    const bool split = Masks && L.staged;
+    const int first = split ? L.st.wave : 0, stride = split ? L.st.waves : 1;
+    int sorted = L.active ? old_keys(L, old_n) : 0;
+    if (L.active) old_warm_copy(L, old_n, first, stride);
     int ns = L.active ? clampi(ldi(L.w, H_SHAPE_COUNT), 0, g.max_s) : 0;
     int nj = L.active ? clampi(ldi(L.w, H_JOINT_COUNT), 0, g.max_j) : 0;
     /* joint-connected body pairs (08:95-108) as sorted-pair keys */
@@ -1481,7 +1520,7 @@ B3D_FN void find_contacts(const Lane& L) {
     }
     if (bounds_in_lds(g) || (L.staged && L.st.lds_bounds)) {
         float* bounds = L.vel + kClipWords * kLanes;
-        shape_pass(L, ns, bounds);
+        shape_pass(L, ns, bounds, first, stride);
         find_pairs<Masks>(L, bounds, ns, nj, old_n, sorted);
     } else {
         float* bounds = (float*)(L.scr + g.scr_bounds * kLanes);
