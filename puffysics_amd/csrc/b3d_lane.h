@@ -1557,11 +1557,13 @@ B3D_FN void apply_impulse(const Lane& L, int b, float m, M3 i, V3 r, V3 p, float
  * body's sequence of updates in contact order; contacts of one level are
  * solved by the tile's waves together.
  * Per lane in the workgroup's LDS, past wave 0's rows: the lane's level
- * count, each body's last level, each contact's level, and P: per level
- * its contact count, then (prefix) its first entry, then (after the fill)
- * one past its last.  In the stage (free once the manifolds are appended):
- * each contact's record slots (slot | point p's slot << 6 + 6p), then the
- * entries in level order, two words each (contact, slots). */
+ * count, each body's last level, each contact's level (| its point count
+ * << 16), and P: per level its contact count, then (prefix) its first
+ * entry, then (after the fill) one past its last.  In the stage (free once
+ * the manifolds are appended): the entries in level order, two words each
+ * (contact, record slots: slot | point p's slot << 6 + 6p).
+ * sched_build runs on wave 0 while the other waves prepare the contacts:
+ * it needs only the contacts' heads, and it ranks the record slots itself. */
 B3D_FN float* sched_rows(const Lane& L) { return L.vel + lds_rows(L.g) * kLanes; }
 B3D_FN int sched_words(const Geometry& g) { return 2 + g.max_b + 2 * g.max_c; }
 B3D_FN int sch_get(const Lane& L, int k) { return __builtin_bit_cast(int, sched_rows(L)[k * kLanes]); }
@@ -1570,9 +1572,8 @@ B3D_FN int sch_last(const Lane& L, int b) { return 1 + b; }
 B3D_FN int sch_level(const Lane& L, int c) { return 1 + L.g.max_b + c; }
 B3D_FN int sch_p(const Lane& L, int lev) { return 1 + L.g.max_b + L.g.max_c + lev; }
 /* stage words of the schedule */
-B3D_FN int stage_sched_words(const Geometry& g) { return 3 * g.max_c; }
-B3D_FN uint32_t* sch_slots(const Lane& L, int c) { return L.st.p + (size_t)(1 + c) * kLanes; }
-B3D_FN uint32_t* sch_entry(const Lane& L, int i) { return L.st.p + (size_t)(1 + L.g.max_c + 2 * i) * kLanes; }
+B3D_FN int stage_sched_words(const Geometry& g) { return 2 * g.max_c; }
+B3D_FN uint32_t* sch_entry(const Lane& L, int i) { return L.st.p + (size_t)(1 + 2 * i) * kLanes; }
 
 /* The largest level count among the tile's stepping lanes (every wave of
  * the tile gets the same value). */
@@ -1586,15 +1587,15 @@ B3D_FN int tile_levels(const Lane& L) {
 }
 
 constexpr int kPrepChunk = 2;
-B3D_FN int prepare_contacts(const Lane& L, Soft cs, Soft ss) {
+B3D_FN int prepare_contacts(const Lane& L, Soft cs, Soft ss, int first = 0, int stride = 1) {
     uint32_t* w = L.w;
     int cc = ldi(w, H_CONTACT_COUNT);
     const float inv_tau = 1.0f / kSpeculative;
     const int keep = (L.opts & kKeepSolverFields) != 0;
-    /* a shared tile prepares its contacts in parallel (every waves-th chunk
-     * per wave) and warm-starts them afterwards, level by level */
+    /* a shared tile prepares its contacts in parallel (chunks first,
+     * first + stride, ... per wave) and warm-starts them afterwards, level
+     * by level */
     const int fuse = !L.staged && !keep && !(ldi(L.scr + L.g.scr_flags * kLanes, 0) & kLaneRestitution);
-    const int first = L.staged ? L.st.wave : 0, stride = L.staged ? L.st.waves : 1;
     for (int c0 = first * kPrepChunk; c0 < cc; c0 += stride * kPrepChunk) {
         int a[kPrepChunk], b[kPrepChunk], pc[kPrepChunk], fl[kPrepChunk], slot[kPrepChunk];
         int pslot[kPrepChunk][kMaxManifold];
@@ -1759,13 +1760,6 @@ B3D_FN int prepare_contacts(const Lane& L, Soft cs, Soft ss) {
             /* the packed record */
             qsu(r, R_AB, (uint32_t)(a[k] | (b[k] << 16)));
             qsu(r, R_INFO, (uint32_t)(pc[k] | ((fl[k] | fixed[k]) << 8)));
-            if (L.staged) {
-                int packed = slot[k];
-#pragma unroll
-                for (int p = 0; p < kMaxManifold; p++)
-                    if (p < pc[k]) packed |= pslot[k][p] << (6 + 6 * p);
-                sti(sch_slots(L, c), 0, packed);
-            }
             qsf(r, R_FRICTION, fric[k]);
             qsf(r, R_TWIST_MASS, twist_mass);
             qs3(r, R_N, n[k]);
@@ -1851,7 +1845,7 @@ B3D_FN void sched_build(const Lane& L) {
             int lev = (la > lb ? la : lb) + 1;
             if (hd.flags & CF_DYN_A) sch_set(L, sch_last(L, hd.a), lev);
             if (hd.flags & CF_DYN_B) sch_set(L, sch_last(L, hd.b), lev);
-            sch_set(L, sch_level(L, c), lev);
+            sch_set(L, sch_level(L, c), lev | (hd.pc << 16));
             sch_set(L, sch_p(L, lev), sch_get(L, sch_p(L, lev)) + 1);
             if (lev > nlev) nlev = lev;
         }
@@ -1863,22 +1857,23 @@ B3D_FN void sched_build(const Lane& L) {
         sch_set(L, sch_p(L, lev), run);
         run += n;
     }
-    for (int c0 = 0; c0 < cc; c0 += kSchedChunk) {
-        uint32_t slots[kSchedChunk];
+    /* each entry with the contact's record slots, ranked as
+     * prepare_contacts ranks them: among the lanes with contact c, and
+     * among those with its point p */
+    for (int c = 0; c < cc; c++) {
+        int lw = sch_get(L, sch_level(L, c));
+        int lev = lw & 0xffff, pc = lw >> 16;
+        int packed = wave_slot(L);
 #pragma unroll
-        for (int k = 0; k < kSchedChunk; k++)
-            if (c0 + k < cc) slots[k] = ldu(sch_slots(L, c0 + k), 0);
-#pragma unroll
-        for (int k = 0; k < kSchedChunk; k++) {
-            int c = c0 + k;
-            if (c >= cc) continue;
-            int lev = sch_get(L, sch_level(L, c));
-            int at = sch_get(L, sch_p(L, lev));
-            sch_set(L, sch_p(L, lev), at + 1);
-            uint32_t* e = sch_entry(L, at);
-            sti(e, 0, c);
-            sti(e, 1, (int)slots[k]);
+        for (int p = 0; p < kMaxManifold; p++) {
+            if (p >= pc) continue;
+            packed |= wave_slot(L) << (6 + 6 * p);
         }
+        int at = sch_get(L, sch_p(L, lev));
+        sch_set(L, sch_p(L, lev), at + 1);
+        uint32_t* e = sch_entry(L, at);
+        sti(e, 0, c);
+        sti(e, 1, packed);
     }
 }
 
@@ -3690,16 +3685,19 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
          * waves meet wave 0 at each barrier, sweep_helper) */
         B3D_BARRIER();
         if (act) {
-            prepare_contacts(L, cs, ss);
+            /* wave 0 levels the contacts while the others prepare them
+             * (alone, it does both) */
+            sched_build(L);
+            if (stride == 1) prepare_contacts(L, cs, ss);
             prepare_joints(L, h, share, stride);
+        } else {
+            sch_set(L, 0, 0);      /* no contact levels */
         }
         B3D_BARRIER();
         if (act) {
             if constexpr (JL) stage_joint_rows(L, share, stride);
-            sched_build(L);
             if constexpr (JL) joint_sched_build(L);
         } else {
-            sch_set(L, 0, 0);      /* no contact levels */
             if constexpr (JL) jsch_set(L, 0, 0);
         }
         B3D_BARRIER();
@@ -3786,7 +3784,8 @@ B3D_FN void sweep_helper(const Lane& L0, float dt, int substeps) {
     if (L.active) body_prepass(L, h, L.st.wave, L.st.waves);   /* with the velocity rows */
     B3D_BARRIER();                 /* the velocities and body records are staged */
     if (L.active) {
-        prepare_contacts(L, cs, ss);
+        /* the contacts split over the waves but wave 0, which levels them */
+        prepare_contacts(L, cs, ss, L.st.wave - 1, L.st.waves - 1);
         prepare_joints(L, h, L.st.wave, L.st.waves);
     }
     B3D_BARRIER();                 /* all contacts and joints prepared */
