@@ -925,9 +925,16 @@ struct NewContact {
     V3 roll;
 };
 
-B3D_FN bool overlaps(const float* bi, const float* bj) {
-    return bi[0] <= bj[3 * kLanes] && bi[3 * kLanes] >= bj[0] && bi[kLanes] <= bj[4 * kLanes]
-        && bi[4 * kLanes] >= bj[kLanes] && bi[2 * kLanes] <= bj[5 * kLanes] && bi[5 * kLanes] >= bj[2 * kLanes];
+/* A shape's padded bounds from its LDS rows (lower x y z, upper x y z), and
+ * their overlap test: all six words load together and the comparisons
+ * combine without branches (a chain of && would wait on each load in
+ * turn). */
+struct Box6 { float lx, ly, lz, hx, hy, hz; };
+B3D_FN Box6 box_load(const float* b) {
+    return Box6{b[0], b[kLanes], b[2 * kLanes], b[3 * kLanes], b[4 * kLanes], b[5 * kLanes]};
+}
+B3D_FN bool box_overlap(const Box6& a, const Box6& b) {
+    return (a.lx <= b.hx) & (a.hx >= b.lx) & (a.ly <= b.hy) & (a.hy >= b.ly) & (a.lz <= b.hz) & (a.hz >= b.lz);
 }
 
 /* The pair loop's view of one shape (its per-step shape record). */
@@ -1096,10 +1103,18 @@ B3D_FN uint64_t overlap_mask(const Lane& L, int i) {
 }
 B3D_FN void overlap_rows(const Lane& L, const float* bounds, int ns, const PairStage& S) {
     for (int i = S.wave; i < ns; i += S.waves) {
-        const float* bi = bounds + i * 6 * kLanes;
+        Box6 bi = box_load(bounds + i * 6 * kLanes);
         uint64_t m = 0;
-        for (int j = i + 1; j < ns; j++)
-            if (overlaps(bi, bounds + j * 6 * kLanes)) m |= 1ull << j;
+        /* four shapes' bounds in flight at a time */
+        for (int j0 = i + 1; j0 < ns; j0 += 4) {
+            Box6 bj[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                if (j0 + k < ns) bj[k] = box_load(bounds + (j0 + k) * 6 * kLanes);
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                if (j0 + k < ns && box_overlap(bi, bj[k])) m |= 1ull << (j0 + k);
+        }
         float* r = L.vel + (shared_masks_word(L.g) + 2 * i) * kLanes;
         r[0] = __builtin_bit_cast(float, (uint32_t)m);
         r[kLanes] = __builtin_bit_cast(float, (uint32_t)(m >> 32));
@@ -1376,11 +1391,15 @@ B3D_FN void find_pairs(const Lane& L, const float* bounds, int ns, int nj, int o
         }
         uint32_t okey = kc[0];
         for (int i = 0; i < ns; i++) {
-            const float* bi = bounds + i * 6 * kLanes;
+            Box6 bi = box_load(bounds + i * 6 * kLanes);
             for (int j0 = i + 1; j0 < ns; j0 += 4) {
                 bool ov[4];
+                Box6 bj[4];
 #pragma unroll
-                for (int k = 0; k < 4; k++) ov[k] = j0 + k < ns && overlaps(bi, bounds + (j0 + k) * 6 * kLanes);
+                for (int k = 0; k < 4; k++)
+                    if (j0 + k < ns) bj[k] = box_load(bounds + (j0 + k) * 6 * kLanes);
+#pragma unroll
+                for (int k = 0; k < 4; k++) ov[k] = j0 + k < ns && box_overlap(bi, bj[k]);
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     if (!ov[k]) continue;
