@@ -6,7 +6,7 @@
  *
  * Every function keeps the reference's fp32 operation order, so when built
  * with -ffp-contract=off (no FMA contraction, no fast-math) its results are
- * bit-identical to the reference's CPU path; tests/test_oracle_ref.py checks
+ * bit-identical to the reference's CPU path; tests/test_oracle_golden.py checks
  * exactly that against the reference compiled from its own sources.  The
  * restatement covers the default feature set only (B3_ART_CONTACTS=0, no
  * packed/compact/cached solver experiments, libm twist, normalised-Euler
