@@ -6,7 +6,9 @@
   - a kernel's dynamic-LDS limit, one setting shared by every engine in the
     process, is not lowered by an engine created later;
   - idle lanes of a shared tile (worlds outside the step mask, or past the
-    end of the batch) stay untouched while the tile's other worlds step.
+    end of the batch) stay untouched while the tile's other worlds step;
+  - an empty batch validates its arguments and then succeeds without a
+    launch (b3_batch.cuh:81-101).
 """
 import numpy as np
 import pytest
@@ -106,3 +108,30 @@ def test_shared_tile_with_sparse_step_mask(scene, count):
     assert len(bad) == 0, "%d differing words, first %s" % (len(bad), bad[:4].tolist())
     idle = active == 0
     assert len(diff_words(got[idle], worlds[idle], sc.sig)) == 0
+
+
+def test_empty_batch():
+    """Zero worlds: every entry point succeeds with nothing to do, while the
+    step still refuses an invalid dt or substep count first (the reference's
+    b3_batch_step_gpu validates, then returns cudaSuccess for an empty
+    batch, b3_batch.cuh:83-86; b3_batch_restore_gpu likewise, :95-98)."""
+    from puffysics_amd.engine import (HIP_ERROR_INVALID_VALUE, b3_batch_apply_gpu, b3_batch_restore_gpu,
+                                      b3_batch_step_gpu)
+    for scene in (1, 5):
+        sc = scenes.SCENES[scene]
+        empty = scenes.build(scene, 64)[:0].copy()
+        eng = _engine(empty, scene)
+        assert eng.count == 0
+        assert b3_batch_step_gpu(eng.handle, sc.dt, sc.substeps) == 0
+        assert b3_batch_step_gpu(eng.handle, 0.0, sc.substeps) == 0
+        for dt, subs in ((float("nan"), 4), (-1.0, 4), (sc.dt, 0)):
+            assert b3_batch_step_gpu(eng.handle, dt, subs) == HIP_ERROR_INVALID_VALUE
+        assert b3_batch_restore_gpu(eng.handle) == 0
+        force = torch.zeros(3, device="cuda")
+        assert b3_batch_apply_gpu(eng.handle, force=force) == 0
+        eng.set_snapshots(empty)
+        eng.upload(empty)
+        assert len(eng.download()) == 0
+        assert len(eng.stats()) == 0
+        torch.cuda.synchronize()
+        eng.close()
