@@ -13,23 +13,35 @@ The headline (`value`, `config`, `roofline`, `cpu_baseline`) is the arm at
 
 One vector step = masked restore + scene inputs + masked step on one HIP
 stream, with the worlds resident in HBM; an env-step is one world stepped
-(substeps not counted).  Each workload runs W untimed vector steps, then K
-timed ones per repeat (default: 50, then 1000; 2000 for the bin; 3
-repeats, median).  The step kernel's own duration is timed with HIP events
-on its stream around every 8th launch.
+(substeps not counted).  Each workload is first settled untimed to W vector
+steps before its window start (vector step 500; 1000 for the bin: halfway
+through the benchmark run, once the stacks stand, the bin's bodies have
+landed and the arm's resets run at their steady rate), and its device state
+is saved.  Each repeat (3, median) restores that state, runs the W untimed
+warm-up steps and times the window of K vector steps from the window start
+(defaults: W = 50, K to the end of the benchmark run: 500; 1000 for the
+bin), so every repeat times the same work.  The step kernel's own duration
+is timed with HIP events on its stream around every 8th launch.
 
-Per workload:
-  roofline   algorithmic bytes per launch (the byte model below on the live
-             contact counts) / kernel time, against 8 TB/s; counted flops per
-             launch (tests/golden/flops.json: the oracle's fp32 operations
-             on the same workload) / kernel time, against the fp32 vector
+Per workload, all over the same window:
+  roofline   algorithmic bytes per launch (the byte model below on each
+             stepped world's live contact count after each step of the
+             window, from one more untimed pass of it) / kernel time,
+             against 8 TB/s; counted flops per launch
+             (tests/golden/flops.json: the oracle's fp32 operations on the
+             same workload and steps) / kernel time, against the fp32 vector
              peak (157.3 TFLOP/s with packed FMA, 78.6 without); measured HBM
              bytes (rocprofv3 FETCH_SIZE / WRITE_SIZE in profiles/) only
-             when that profile was taken of this source tree.
+             when that profile was taken of this source tree over launches
+             of a window with the same start.
   cpu        the reference's own CPU path (b3_batch_step / b3_batch_restore,
              oracle/_ref) built -O3 for this host's x86-64 level, one pinned
              thread per physical core available to the process, on the
-             workload's full world count over a bounded number of steps.
+             workload's full world count, started from the device's state at
+             the window start (bit-identical to the reference's) and run
+             over the window's first steps, repeated for a bounded time.
+`--profile-commands DIR` / `--profile-summary DIR` (with --scene) give the
+rocprofv3 runs of the same window and reduce them to profiles/.
 """
 import argparse
 import ctypes as C
@@ -57,6 +69,13 @@ BYTES_SHAPE = 80
 BYTES_CONTACT = 136        # 68-byte warm cache read and written
 BYTES_JOINT = 192          # 120 constants + 36 impulses read + 36 written
 BYTES_WORLD = 58           # 56 header + step and reset mask bytes
+
+# Each workload's timed window starts at this vector step, halfway through
+# its benchmark run (1,000 vector steps; 2,000 for the bin): the stacks stand,
+# the bin's bodies have landed and the arm's resets run at their steady
+# rate.  The default window runs to the end of the benchmark run.
+WINDOW_START = {1: 500, 2: 500, 3: 500, 4: 1000, 5: 500}
+RUN_LENGTH = {1: 1000, 2: 1000, 3: 1000, 4: 2000, 5: 1000}
 
 
 def log(msg):
@@ -148,9 +167,11 @@ def kernel_name(scene, count):
     return "b3k_step_shared<%s, %s>" % ("true" if masks else "false", "true" if joint_rows_fit(*caps) else "false")
 
 
-def load_counters(kernel, scene, count, digest):
+def load_counters(kernel, scene, count, digest, start, end):
     """Per-launch counter figures of a kernel on a workload from the committed
-    rocprofv3 summary, if it was taken of this source tree; else None."""
+    rocprofv3 summary, if it was taken of this source tree over launches of
+    the window [start, end) (same start: every window from a start is the
+    same stationary run); else None."""
     path = os.path.join(ROOT, "profiles", "counters_%s%d.json" % (NAMES[scene], count))
     if not os.path.exists(path):
         return None
@@ -158,12 +179,18 @@ def load_counters(kernel, scene, count, digest):
         c = json.load(f)
     if c.get("source_digest") != digest or c.get("kernel") != kernel:
         return None
+    w = c.get("window")
+    if not w or w[0] != start or w[1] > end:
+        return None
     return c
 
 
-def cpu_baseline(scene, count, warmup, seconds):
-    """The reference's CPU path on the workload's worlds: `warmup` untimed
-    vector steps, then as many as fit in about `seconds` (at least 3)."""
+def cpu_baseline(scene, count, state, initial, start, end, seconds):
+    """The reference's CPU path on the workload's worlds over the GPU's timed
+    window: from `state` (the worlds at vector step `start`, downloaded from
+    the device, bit-identical to what the reference computes), vector steps
+    [start, end) or the first of them, repeated from `state` until about
+    `seconds` of stepping have been timed."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from b3test import fast_levels_supported, oracle, ref_fast_lib, ref_lib
@@ -180,43 +207,51 @@ def cpu_baseline(scene, count, warmup, seconds):
             break
     if lib is None and ref_lib(scene) is not None:
         lib, flags = ref_lib(scene), "-O2 -ffp-contract=off -fno-fast-math"
+    src = np.ascontiguousarray(state).view(np.uint8).ravel()
+    init = np.ascontiguousarray(initial).view(np.uint8).ravel().copy()
+    worlds = np.empty_like(src)
     if lib is not None:
         kind = "reference"
-        ws = lib.ref_world_size()
-        worlds = np.zeros(count * ws, np.uint8)
-        lib.ref_build_batch(scene, worlds.ctypes.data, count, scenes.SEED, 0)
-        initial = worlds.copy()
-
-        def run(t0, n):
-            return lib.ref_run(scene, worlds.ctypes.data, initial.ctypes.data, count, scenes.SEED, t0, n, sc.dt,
-                               sc.substeps, nthreads, cpu_arr)
+        assert lib.ref_world_size() * count == src.size
+        fn = lib.ref_run
+        args = lambda t0, n: (scene, worlds.ctypes.data, init.ctypes.data, count, scenes.SEED, t0, n, sc.dt,
+                              sc.substeps, nthreads, cpu_arr)
     else:
         kind, flags = "port", "-O2 -ffp-contract=off -fno-fast-math"
-        worlds = scenes.build(scene, count)
-        initial = worlds.copy()
         fn = getattr(oracle(), "ocpu_run_%d" % scene)
-
-        def run(t0, n):
-            return fn(worlds.ctypes.data, initial.ctypes.data, count, scenes.SEED, t0, n, sc.dt, sc.substeps,
-                      nthreads, cpu_arr)
-    if warmup:
-        run(0, warmup)
+        args = lambda t0, n: (worlds.ctypes.data, init.ctypes.data, count, scenes.SEED, t0, n, sc.dt, sc.substeps,
+                              nthreads, cpu_arr)
+    worlds[:] = src
     t0 = time.perf_counter()
-    done = run(warmup, 1)
+    fn(*args(start, 1))
     first = time.perf_counter() - t0
-    nsteps = int(max(3, min(2000, seconds / max(first, 1e-6))))
-    t0 = time.perf_counter()
-    env_steps = run(warmup + 1, nsteps)
-    el = time.perf_counter() - t0
-    del done
+    per_pass = int(max(1, min(end - start, seconds / max(first, 1e-6))))
+    env_steps, el, passes = 0, 0.0, 0
+    while passes == 0 or el < seconds:
+        worlds[:] = src
+        t0 = time.perf_counter()
+        env_steps += fn(*args(start, per_pass))
+        el += time.perf_counter() - t0
+        passes += 1
     return {"value": round(env_steps / el, 1), "unit": "env-steps/s", "cores": nthreads, "kind": kind,
             "flags": flags, "affinity_physical_cores": affinity_cores, "cgroup_cpu_quota": quota,
-            "sample": "all %d worlds, vector steps %d..%d of the same workload (after %d untimed), %d pinned threads "
-                      "(one per physical core available), %.1f s" % (count, warmup + 1, warmup + nsteps, warmup + 1,
-                                                                     nthreads, el)}
+            "window": [start, start + per_pass],
+            "sample": "all %d worlds from the device's state at vector step %d, vector steps %d..%d of the same "
+                      "workload (inside the GPU's timed window %d..%d), %d pass%s, %d pinned threads (one per "
+                      "physical core available), %.1f s" % (count, start, start, start + per_pass, start, end, passes,
+                                                          "" if passes == 1 else "es", nthreads, el)}
 
 
-def run_workload(scene, count, steps, warmup, repeats, event_every, digest):
+def window_of(scene, steps, warmup):
+    """The vector steps a workload's run covers: untimed settling [0, settle),
+    then per repeat `warmup` untimed steps [settle, start) and the timed
+    window [start, start + steps), every repeat from the same saved state."""
+    start = WINDOW_START[scene]
+    w = min(warmup, start)
+    return start - w, start, start + steps
+
+
+def run_workload(scene, count, steps, warmup, repeats, event_every, digest, cpu_seconds=None):
     import numpy as np
     import torch
     from puffysics_amd import scenes
@@ -226,79 +261,106 @@ def run_workload(scene, count, steps, warmup, repeats, event_every, digest):
     log("%s: building %d worlds" % (NAMES[scene], count))
     worlds = scenes.build(scene, count)
     eng = B3Engine(worlds, sc.sig)
+    tiles = eng.tiles()
     stream = torch.cuda.current_stream()
-    total = warmup + steps * repeats
-    reset = torch.empty((total, count), dtype=torch.uint8, device="cuda")
-    stepm = torch.empty((total, count), dtype=torch.uint8, device="cuda")
-    for t in range(total):
+    settle, start, end = window_of(scene, steps, warmup)
+    reset = torch.empty((end, count), dtype=torch.uint8, device="cuda")
+    stepm = torch.empty((end, count), dtype=torch.uint8, device="cuda")
+    for t in range(end):
         eng.scene_masks(scene, scenes.SEED, t, reset[t], stepm[t])
     step_counts = stepm.sum(dim=1, dtype=torch.int64).cpu().numpy()
     reset_any = reset.amax(dim=1).cpu().numpy()
 
-    for t in range(warmup):
+    def vector_step(t):
         if reset_any[t]:
             eng.restore(reset[t])
         eng.scene_inputs(scene, scenes.SEED, t, stepm[t])
+
+    log("  settling: vector steps 0..%d untimed" % settle)
+    for t in range(settle):
+        vector_step(t)
         eng.step(sc.dt, sc.substeps, stepm[t])
+    saved = tiles.clone()                      # the state every repeat starts from
     torch.cuda.synchronize()
 
+    def warm_up():
+        tiles.copy_(saved)
+        for t in range(settle, start):
+            vector_step(t)
+            eng.step(sc.dt, sc.substeps, stepm[t])
+
     rates, ms, kernel_ms = [], [], []
-    t = warmup
     timed = range(0, steps, max(1, event_every))
     for r in range(repeats):
+        warm_up()
         k_start = {i: torch.cuda.Event(enable_timing=True) for i in timed}
         k_end = {i: torch.cuda.Event(enable_timing=True) for i in timed}
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t_begin, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
-        start.record(stream)
-        t_begin = t
+        t_begin.record(stream)
         for i in range(steps):
-            if reset_any[t]:
-                eng.restore(reset[t])
-            eng.scene_inputs(scene, scenes.SEED, t, stepm[t])
+            t = start + i
+            vector_step(t)
             if i in k_start:
                 k_start[i].record(stream)
             eng.step(sc.dt, sc.substeps, stepm[t])
             if i in k_end:
                 k_end[i].record(stream)
-            t += 1
-        end.record(stream)
+        t_end.record(stream)
         torch.cuda.synchronize()
-        el_ms = start.elapsed_time(end)
-        env = int(step_counts[t_begin:t].sum())
+        el_ms = t_begin.elapsed_time(t_end)
+        env = int(step_counts[start:end].sum())
         rates.append(env / (el_ms * 1e-3))
         ms.append(el_ms / steps)
         kernel_ms.append(sum(k_start[i].elapsed_time(k_end[i]) for i in timed) / len(timed))
-        log("  repeat %d: %.4f ms/step, %.4g env-steps/s, step kernel %.4f ms" % (r, ms[-1], rates[-1],
-                                                                                 kernel_ms[-1]))
+        log("  repeat %d: vector steps %d..%d, %.4f ms/step, %.4g env-steps/s, step kernel %.4f ms" % (
+            r, start, end, ms[-1], rates[-1], kernel_ms[-1]))
     med = sorted(range(repeats), key=lambda i: rates[i])[repeats // 2]
 
-    st = eng.stats()
+    # The byte model over the same window, untimed: the same steps again from
+    # the saved state, with each stepped world's live contact count after
+    # each step.  The state at the window's start seeds the CPU baseline.
+    warm_up()
+    torch.cuda.synchronize()
+    state_at_start = eng.download() if cpu_seconds else None
+    base = torch.from_numpy(world_bytes_model(worlds, np.zeros(count))).cuda()
+    cc_word = worlds.dtype.fields["contact_count"][1] // 4
+    bytes_sum = torch.zeros((), dtype=torch.float64, device="cuda")
+    contact_sum = torch.zeros((), dtype=torch.float64, device="cuda")
+    for t in range(start, end):
+        vector_step(t)
+        eng.step(sc.dt, sc.substeps, stepm[t])
+        cc = tiles[:, cc_word, :].reshape(-1)[:count].double()
+        on = stepm[t].double()
+        bytes_sum += (on * (base + BYTES_CONTACT * cc)).sum()
+        contact_sum += cc.mean()
+    torch.cuda.synchronize()
     eng.close()
-    per_world = world_bytes_model(worlds, st["contact_count"])
-    mean_stepped = float(step_counts[warmup:].mean())
+    stepped = float(step_counts[start:end].sum())
+    bytes_launch = float(bytes_sum) / steps
+    mean_stepped = stepped / steps
+    bytes_env = float(bytes_sum) / stepped
     k_ms = kernel_ms[med]
     kernel = kernel_name(scene, count)
-    bytes_env = float(per_world.mean())
-    hbm_gbs = bytes_env * mean_stepped / (k_ms * 1e-3) / 1e9
-    # the median repeat's window of vector steps
-    first = warmup + med * steps
-    flops_env, window = counted_flops(scene, first, steps)
+    hbm_gbs = bytes_launch / (k_ms * 1e-3) / 1e9
+    flops_env, counted = counted_flops(scene, start, steps)
     tflops = flops_env * mean_stepped / (k_ms * 1e-3) / 1e12
-    counters = load_counters(kernel, scene, count, digest)
+    counters = load_counters(kernel, scene, count, digest, start, end)
     traffic = None
     if counters:
         traffic = counters["fetch_bytes_per_launch"] + counters["write_bytes_per_launch"]
     roofline = {"bound": "hbm", "achieved": round(hbm_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(hbm_gbs / HBM_PEAK_GBS, 5), "traffic": traffic,
                 "kernel": kernel, "kernel_ms": round(k_ms, 5), "kernel_launches_timed": len(timed),
+                "window": [start, end],
+                "bytes_per_launch": round(bytes_launch, 1),
                 "bytes_per_env_step": round(bytes_env, 1),
-                "mean_contacts_per_world": round(float(st["contact_count"].mean()), 2),
+                "mean_contacts_per_world": round(float(contact_sum) / steps, 2),
                 "mean_stepped_worlds": round(mean_stepped, 1),
                 "valu": {"achieved": round(tflops, 3), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tflops / FP32_PEAK_TFLOPS, 5),
                          "frac_nonpacked": round(tflops / FP32_NONPACKED_TFLOPS, 5),
-                         "flops_per_env_step": round(flops_env, 1), "counted_steps": window,
+                         "flops_per_env_step": round(flops_env, 1), "counted_steps": counted,
                          "source": "tests/golden/flops.json (oracle fp32 operations counted on the workload)"}}
     # the lower of the two ceilings, and the fraction of it reached
     ceil_hbm = HBM_PEAK_GBS * 1e9 / bytes_env
@@ -311,23 +373,215 @@ def run_workload(scene, count, steps, warmup, repeats, event_every, digest):
         roofline["traffic_gbs"] = round(traffic / (k_ms * 1e-3) / 1e9, 1)
         roofline["traffic_frac"] = round(traffic / (k_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
         roofline["traffic_profile"] = "profiles/counters_%s%d.json" % (NAMES[scene], count)
+        roofline["traffic_window"] = counters["window"]
     else:
-        roofline["traffic_note"] = "no rocprofv3 counter profile of this source tree (%s) in profiles/" % digest
+        roofline["traffic_note"] = ("no rocprofv3 counter profile of this source tree (%s) over a window inside "
+                                    "[%d, %d) in profiles/" % (digest, start, end))
     masks = "2% reset / 90% step" if scene == 5 else ("impulse every 60 steps" if scene == 2 else "none")
     config = {"workload": "%s%d: %d worlds of the %s scene, dt %.6g, %d substeps, masks %s" % (
                   NAMES[scene], count, count, NAMES[scene], sc.dt, sc.substeps, masks),
-              "worlds": count, "scene": NAMES[scene], "dt": sc.dt, "substeps": sc.substeps, "repeats": repeats}
-    return {"value": round(rates[med], 1), "unit": "env-steps/s", "steps": steps, "warmup": warmup,
-            "ms_per_step": round(ms[med], 5), "config": config, "roofline": roofline,
-            "repeat_values": [round(v, 1) for v in rates]}
+              "worlds": count, "scene": NAMES[scene], "dt": sc.dt, "substeps": sc.substeps, "repeats": repeats,
+              "window": [start, end], "settled_untimed": settle}
+    out = {"value": round(rates[med], 1), "unit": "env-steps/s", "steps": steps, "warmup": start - settle,
+           "ms_per_step": round(ms[med], 5), "config": config, "roofline": roofline,
+           "repeat_values": [round(v, 1) for v in rates]}
+    if cpu_seconds:
+        log("%s%d: cpu baseline from vector step %d" % (NAMES[scene], count, start))
+        out["cpu_baseline"] = cpu_baseline(scene, count, state_at_start, worlds, start, end, cpu_seconds)
+        out["gpu_over_cpu"] = round(out["value"] / out["cpu_baseline"]["value"], 1)
+    return out
+
+
+# ---- rocprofv3 summaries of the step kernel over the timed window ----
+# Each profile run is `bench.py --scene N --no-cpu` with the same --steps,
+# --warmup and --repeats under rocprofv3 (one run per counter set, as the
+# tool collects no more than one hardware pass at a time).  The step kernel
+# is launched once per vector step in the bench's fixed order (settling,
+# then per repeat the warm-up and the timed window, then the byte model's
+# pass), so its timed launches are known by their position.
+
+PROFILE_RUNS = [("trace", "--kernel-trace --stats"),
+                ("fetch", "--pmc FETCH_SIZE"),
+                ("write", "--pmc WRITE_SIZE"),
+                ("sq1", "--pmc SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_INSTS_VALU SQ_ACTIVE_INST_VALU SQ_INSTS_LDS "
+                        "SQ_LDS_BANK_CONFLICT SQ_INSTS_VMEM_RD"),
+                ("sq2", "--pmc SQ_INSTS_VMEM_WR SQ_INSTS_SALU SQ_WAIT_INST_ANY SQ_ACTIVE_INST_ANY "
+                        "SQ_INST_CYCLES_VMEM_RD GRBM_GUI_ACTIVE")]
+COPY_MIB = 1024
+
+
+def timed_step_launches(scene, steps, warmup, repeats):
+    """Positions, among a bench run's step-kernel launches, of the timed ones."""
+    settle, start, end = window_of(scene, steps, warmup)
+    w = start - settle
+    out = []
+    for r in range(repeats):
+        first = settle + r * (w + steps) + w
+        out.extend(range(first, first + steps))
+    return out
+
+
+def profile_commands(scene, steps, warmup, repeats, outdir):
+    bench = "python3 bench.py --scene %d --no-cpu --steps %d --warmup %d --repeats %d" % (scene, steps, warmup,
+                                                                                          repeats)
+    cmds = []
+    for name, opts in PROFILE_RUNS:
+        flt = "" if name == "trace" else " --kernel-include-regex b3k_step"
+        cmds.append("timeout -s KILL 300 rocprofv3 %s%s -d %s/%s -o run -f csv -- %s" % (opts, flt, outdir, name,
+                                                                                          bench))
+    for name, counter in (("copy_fetch", "FETCH_SIZE"), ("copy_write", "WRITE_SIZE")):
+        cmds.append("timeout -s KILL 120 rocprofv3 --pmc %s -d %s/%s -o run -f csv -- python3 bench.py "
+                    "--copy-calibration %d" % (counter, outdir, name, COPY_MIB))
+    return cmds
+
+
+def _csv_rows(d, suffix):
+    import csv
+    import glob
+    paths = sorted(glob.glob(os.path.join(d, "**", "*" + suffix), recursive=True))
+    if not paths:
+        raise SystemExit("no %s under %s" % (suffix, d))
+    with open(paths[0], newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def _short(name):
+    name = name.replace("(anonymous namespace)::", "").replace("void ", "")
+    return name.split("(")[0] if name.startswith("b3k_") else name[:150]
+
+
+def _step_kernel(names):
+    """The workload's step kernel: the launched kernel named b3k_step or
+    b3k_step_shared<...>."""
+    cands = [n for n in names if _short(n) == "b3k_step" or _short(n).startswith("b3k_step_shared<")]
+    if len(set(cands)) != 1:
+        raise SystemExit("expected one step kernel, found %s" % sorted(set(cands)))
+    return cands[0]
+
+
+def _counter_means(rows, picks):
+    """Per-counter mean over the step kernel's launches at positions `picks`."""
+    step = _step_kernel({r["Kernel_Name"] for r in rows})
+    by_dispatch = {}
+    for r in rows:
+        if r["Kernel_Name"] == step:
+            by_dispatch.setdefault(int(r["Dispatch_Id"]), {})[r["Counter_Name"]] = float(r["Counter_Value"])
+    order = sorted(by_dispatch)
+    sel = [by_dispatch[order[i]] for i in picks]
+    names = sorted({k for d in sel for k in d})
+    return {k: sum(d[k] for d in sel) / len(sel) for k in names}, len(order)
+
+
+def profile_summary(root, scene, count, steps, warmup, repeats, digest):
+    """Writes profiles/<kernel>_<workload>.md and profiles/counters_<workload>.json
+    from the runs of profile_commands under `root`."""
+    settle, start, end = window_of(scene, steps, warmup)
+    picks = timed_step_launches(scene, steps, warmup, repeats)
+    trace = _csv_rows(os.path.join(root, "trace"), "kernel_trace.csv")
+    step = _step_kernel({r["Kernel_Name"] for r in trace})
+    launches = sorted((r for r in trace if r["Kernel_Name"] == step), key=lambda r: int(r["Dispatch_Id"]))
+    expect = settle + (repeats + 1) * (start - settle + steps)
+    if len(launches) != expect:
+        raise SystemExit("%d step launches traced, the bench's plan has %d" % (len(launches), expect))
+    dur = [(int(launches[i]["End_Timestamp"]) - int(launches[i]["Start_Timestamp"])) / 1e3 for i in picks]
+    avg_us = sum(dur) / len(dur)
+    # every kernel over the timed repeats' span of time
+    spans = []
+    for r in range(repeats):
+        a, b = picks[r * steps], picks[r * steps + steps - 1]
+        spans.append((int(launches[a]["Start_Timestamp"]), int(launches[b]["End_Timestamp"])))
+    table = {}
+    for row in trace:
+        t0, t1 = int(row["Start_Timestamp"]), int(row["End_Timestamp"])
+        if any(a <= t0 and t1 <= b for a, b in spans):
+            table.setdefault(_short(row["Kernel_Name"]), []).append((t1 - t0) / 1e3)
+    fetch, nf = _counter_means(_csv_rows(os.path.join(root, "fetch"), "counter_collection.csv"), picks)
+    write, _ = _counter_means(_csv_rows(os.path.join(root, "write"), "counter_collection.csv"), picks)
+    sq = {}
+    for name in ("sq1", "sq2"):
+        sq.update(_counter_means(_csv_rows(os.path.join(root, name), "counter_collection.csv"), picks)[0])
+    copy_bytes = COPY_MIB << 20
+    scale = {}
+    for name, counter in (("copy_fetch", "FETCH_SIZE"), ("copy_write", "WRITE_SIZE")):
+        rows = [r for r in _csv_rows(os.path.join(root, name), "counter_collection.csv")
+                if r["Counter_Name"] == counter and float(r["Counter_Value"]) > 0]
+        kib = sorted(float(r["Counter_Value"]) for r in rows)[len(rows) // 2]
+        scale[counter] = round(copy_bytes / (kib * 1024), 3)
+    fetch_b = fetch["FETCH_SIZE"] * 1024 * scale["FETCH_SIZE"]
+    write_b = write["WRITE_SIZE"] * 1024 * scale["WRITE_SIZE"]
+    l0 = launches[0]
+    regs = {"vgpr": int(l0["VGPR_Count"]), "agpr": int(l0["Accum_VGPR_Count"]), "sgpr": int(l0["SGPR_Count"]),
+            "lds_bytes": int(l0["LDS_Block_Size"]), "scratch": int(l0["Scratch_Size"]),
+            "wg": int(l0["Workgroup_Size_X"]), "grid": int(l0["Grid_Size_X"])}
+    kernel = _short(step)
+    workload = "%s%d" % (NAMES[scene], count)
+    counters = {"kernel": kernel if kernel == "b3k_step" else kernel.replace(",", ", ").replace(",  ", ", "),
+                "workload": workload, "source_digest": digest, "window": [start, start + steps],
+                "timed_launches": len(picks), "launches_profiled": nf,
+                "fetch_bytes_per_launch": round(fetch_b), "write_bytes_per_launch": round(write_b),
+                "trace_avg_us": round(avg_us, 2), "fetch_scale": scale["FETCH_SIZE"],
+                "write_scale": scale["WRITE_SIZE"], "sq": {k: round(v, 1) for k, v in sq.items()}, "registers": regs}
+    os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
+    with open(os.path.join(ROOT, "profiles", "counters_%s.json" % workload), "w") as f:
+        json.dump(counters, f, indent=1)
+        f.write("\n")
+    cmds = profile_commands(scene, steps, warmup, repeats, "gpurun_out/prof_%s" % workload)
+    tag = kernel.replace("<", "_").replace(">", "").replace(", ", "_").replace(",", "_")
+    lines = ["# %s on the %s workload (%d worlds), one MI355X" % (kernel, NAMES[scene], count), "",
+             "Source digest `%s` (`bench.engine_source_digest()`: the engine sources this profile was taken of)."
+             % digest, "",
+             "Commands (each its own run, from the repository root, with `export TMPDIR=/tmp` for the tool), then "
+             "this summary:", ""]
+    lines += ["    " + c for c in cmds]
+    lines += ["    python3 bench.py --profile-summary gpurun_out/prof_%s --scene %d --steps %d --warmup %d "
+              "--repeats %d" % (workload, scene, steps, warmup, repeats), "",
+              "Every run is the bench's own run of this workload: settled untimed to vector step %d, then per "
+              "repeat %d untimed warm-up steps and the timed window of vector steps %d..%d, all %d repeats from the "
+              "same saved state, then one more pass of the window for the byte model.  The figures below are the "
+              "step kernel's %d launches inside the timed windows (positions known from that order; %d launches "
+              "of it in all)." % (settle, start - settle, start, start + steps, repeats, len(picks), len(launches)),
+              "", "## Kernel trace, timed windows", "",
+              "| kernel | calls | avg us | min us | max us |", "|---|---|---|---|---|"]
+    for name, d in sorted(table.items(), key=lambda kv: -sum(kv[1])):
+        lines.append("| %s | %d | %.2f | %.2f | %.2f |" % (name, len(d), sum(d) / len(d), min(d), max(d)))
+    wc = sq.get("SQ_WAVE_CYCLES", 0) or 1
+    lines += ["", "Step kernel over its timed launches: **%.2f us** average." % avg_us, "",
+              "## Counters of `%s` (mean per timed launch)" % kernel, "",
+              "Registers (the dispatch records): %d VGPRs (arch), %d AGPRs, %d SGPRs, LDS %d bytes, scratch %d "
+              "bytes; workgroup %d threads, grid %d." % (regs["vgpr"], regs["agpr"], regs["sgpr"], regs["lds_bytes"],
+                                                         regs["scratch"], regs["wg"], regs["grid"]), "",
+              "| counter | value |", "|---|---|"]
+    for k in sorted(sq):
+        lines.append("| %s | %.4g |" % (k, sq[k]))
+    lines += ["| FETCH_SIZE (KiB) | %.4g |" % fetch["FETCH_SIZE"], "| WRITE_SIZE (KiB) | %.4g |" % write["WRITE_SIZE"],
+              "", "## Derived", "",
+              "- HBM bytes per launch: fetch %.3g + write %.3g = %.3g B, each counter scaled by what it reads for "
+              "a plain %d MiB device copy (x%.3f fetch, x%.3f write). Over the %.2f us average: %.0f GB/s, %.1f%% "
+              "of 8 TB/s." % (fetch_b, write_b, fetch_b + write_b, COPY_MIB, scale["FETCH_SIZE"],
+                              scale["WRITE_SIZE"], avg_us, (fetch_b + write_b) / (avg_us * 1e-6) / 1e9,
+                              (fetch_b + write_b) / (avg_us * 1e-6) / 1e9 / 80.0),
+              "- VALU active %.1f%% and any instruction active %.1f%% of wave cycles (SQ_ACTIVE_INST_VALU, "
+              "SQ_ACTIVE_INST_ANY over SQ_WAVE_CYCLES); waiting on any instruction %.1f%%." % (
+                  100 * sq.get("SQ_ACTIVE_INST_VALU", 0) / wc, 100 * sq.get("SQ_ACTIVE_INST_ANY", 0) / wc,
+                  100 * sq.get("SQ_WAIT_INST_ANY", 0) / wc),
+              "- Waves %d; VALU instructions per wave %.3g; LDS instructions %.3g with %.0f bank-conflict cycles."
+              % (sq.get("SQ_WAVES", 0), sq.get("SQ_INSTS_VALU", 0) / max(1.0, sq.get("SQ_WAVES", 1)),
+                 sq.get("SQ_INSTS_LDS", 0), sq.get("SQ_LDS_BANK_CONFLICT", 0)), ""]
+    path = os.path.join(ROOT, "profiles", "%s_%s.md" % (tag, workload))
+    with open(path, "w") as f:
+        f.write("\n".join(lines))
+    log("wrote %s and profiles/counters_%s.json" % (os.path.relpath(path, ROOT), workload))
 
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None,
-                    help="timed vector steps per repeat of every workload (default: 1000; 2000 for the bin)")
-    ap.add_argument("--warmup", type=int, default=50)
+                    help="timed vector steps per repeat of every workload (default: from the window start to the "
+                         "end of the benchmark run: 500; 1000 for the bin)")
+    ap.add_argument("--warmup", type=int, default=50,
+                    help="untimed vector steps before each repeat's window (after settling to the window start "
+                         "less these)")
     ap.add_argument("--repeats", type=int, default=3)
     ap.add_argument("--event-every", type=int, default=8, metavar="N",
                     help="time every N-th step launch with a pair of HIP events (each pair is a gap in the "
@@ -339,6 +593,10 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only copy MIB MiB device-to-device 10 times with a plain copy kernel (for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
+    ap.add_argument("--profile-commands", metavar="DIR",
+                    help="with --scene: print the rocprofv3 runs whose outputs --profile-summary reads, and exit")
+    ap.add_argument("--profile-summary", metavar="DIR",
+                    help="with --scene: summarise those runs under DIR into profiles/ and exit")
     args = ap.parse_args()
     if args.copy_calibration:
         import torch
@@ -355,6 +613,22 @@ def main():
               "with no exchange, but only --gpus 1 is measured here", file=sys.stderr)
         sys.exit(2)
 
+    def steps_of(scene):
+        return args.steps if args.steps is not None else RUN_LENGTH[scene] - WINDOW_START[scene]
+
+    if args.profile_commands or args.profile_summary:
+        if not args.scene:
+            raise SystemExit("--profile-commands / --profile-summary need --scene")
+        from puffysics_amd import scenes
+        count = args.worlds or scenes.SCENES[args.scene].worlds
+        if args.profile_commands:
+            print("\n".join(profile_commands(args.scene, steps_of(args.scene), args.warmup, args.repeats,
+                                             args.profile_commands)))
+        else:
+            profile_summary(args.profile_summary, args.scene, count, steps_of(args.scene), args.warmup,
+                            args.repeats, engine_source_digest())
+        return
+
     import torch
     from puffysics_amd import scenes
     torch.cuda.set_device(0)
@@ -363,14 +637,9 @@ def main():
     results = {}
     for scene in todo:
         count = (args.worlds if args.scene and args.worlds else scenes.SCENES[scene].worlds)
-        steps = args.steps if args.steps is not None else (2000 if scene == 4 else 1000)
-        res = run_workload(scene, count, steps, args.warmup, args.repeats, args.event_every, digest)
+        res = run_workload(scene, count, steps_of(scene), args.warmup, args.repeats, args.event_every, digest,
+                           None if args.no_cpu else args.cpu_seconds)
         results["%s%d" % (NAMES[scene], count)] = (scene, count, res)
-    if not args.no_cpu:
-        for key, (scene, count, res) in results.items():
-            log("%s: cpu baseline" % key)
-            res["cpu_baseline"] = cpu_baseline(scene, count, args.warmup, args.cpu_seconds)
-            res["gpu_over_cpu"] = round(res["value"] / res["cpu_baseline"]["value"], 1)
     head_key = next((k for k, v in results.items() if v[0] == HEADLINE), next(iter(results)))
     head = results[head_key][2]
     out = {"metric": METRIC, "value": head["value"], "unit": "env-steps/s", "n_gpus": 1, "steps": head["steps"],

@@ -129,10 +129,13 @@ hipError_t b3_engine_device_view(const B3Engine* engine, void** tiles, size_t* w
 #define B3_ENGINE_ART_CONTACTS 2u
 /* B3_ENGINE_ONE_WAVE_PER_TILE: no counterpart in the reference (a launch
  * choice).  A batch of at most one 64-world tile per CU normally runs with
- * four waves per tile: they share the narrowphase (its pairs are
- * independent) and the contact sweeps (contacts on disjoint dynamic bodies,
- * level by level, keeping every body's updates in contact order), while one
- * wave does the rest.  That allocates at creation a staging buffer of
+ * eight waves per tile: they share the narrowphase (its pairs are
+ * independent; four to seven waves collide, as many as have LDS rows for
+ * their clip polygons), the contact sweeps and warm start (contacts on
+ * disjoint dynamic bodies, level by level, keeping every body's updates in
+ * contact order), the velocity and position updates, the joint geometry
+ * and, when the joint rows fit in LDS, the joint passes (by joint levels),
+ * while wave 0 does the rest.  That allocates at creation a staging buffer of
  * 4 * tiles * 64 * (1 + max(36 * max_shapes * (max_shapes - 1) / 2,
  * 3 * max_contacts)) bytes.  This option launches one wave per tile as for
  * larger batches.  Results are identical either way. */
@@ -155,39 +158,49 @@ hipError_t b3_engine_set_options(B3Engine* engine, unsigned int options);
 hipError_t b3_batch_art_step_gpu(B3Engine* engine, float dt, int substeps, const unsigned char* step_mask,
     const unsigned char* reset_mask, hipStream_t stream);
 
-/* The step without allocation.  No counterpart in the reference as a
- * separate entry point: it is for callers that cannot allocate device
- * memory at all, such as code under HIP graph capture, tight serving loops
- * and harnesses that forbid hipMalloc, and that hold their worlds in their
- * own device memory.  The reference's b3_batch_step_gpu (b3_batch.cuh:
- * 81-89) steps such worlds without allocating because its kernel keeps all
- * scratch per thread; this engine's step needs per-step scratch, which
- * b3_batch_step_gpu takes from the engine (allocated by b3_engine_create)
- * and this entry point from a fixed device array of the library.
+/* The step without allocation.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory at all, such as code under
+ * HIP graph capture, tight serving loops and harnesses that forbid
+ * hipMalloc, and that hold their worlds in their own device memory.  The
+ * engine's step needs per-step scratch, which b3_batch_step_gpu takes from
+ * the engine (allocated by b3_engine_create) and this entry point from a
+ * fixed device array of the library.
  *
  * Steps the device-resident B3World structs viewed by `worlds` (a B3Batch
- * over device memory, as b3_batch_valid accepts, with data, stride and
- * world_offset multiples of 4) whose capacities are `config_signature`, in
- * place: the worlds selected by `active` (device bytes, nonzero selects,
- * NULL selects all) that are structurally valid (counts within the
- * capacities, every body and shape index in range; others are left as they
- * are).  The results equal b3_batch_step_gpu's on an engine with default
- * options.  dt must be finite and >= 0, substeps >= 1; an empty batch or
- * dt == 0 is a no-op.  Enqueues on `stream`; calls no allocating routine.
+ * over device memory of the current device, as b3_batch_valid accepts,
+ * with data, stride and world_offset multiples of 4) whose capacities are
+ * `config_signature`, in place: the worlds selected by `active` (device
+ * bytes, nonzero selects, NULL selects all) that are structurally valid
+ * (counts within the capacities, every body and shape index in range).  A
+ * world that is not selected or not valid is left exactly as it is, and
+ * the call still returns hipSuccess: a corrupt world is skipped, not
+ * reported.  The results equal b3_batch_step_gpu's on an engine with
+ * default options.  dt must be finite and >= 0, substeps >= 1; an empty
+ * batch or dt == 0 is a no-op.  Errors, all before any launch:
+ * hipErrorInvalidValue for invalid arguments or for `worlds` / `active`
+ * outside device memory, hipErrorInvalidDevice for another device's
+ * memory, hipErrorOutOfMemory when one 64-world tile of these worlds with
+ * its scratch exceeds the array.  Enqueues on `stream`; calls no
+ * allocating routine.
  *
- * Limit: the array holds 256 MiB, and a call needs
- *   ceil(count / 64) * 64 * (sizeof(B3World) + scratch per world) + count
- * bytes of it.  The per-step scratch per world is about the size of the
+ * Limit: the array holds 64 MiB, reserved on each device the library runs
+ * on until the process ends.  A tile of 64 worlds needs
+ *   64 * (sizeof(B3World) + scratch per world) + 64
+ * bytes of it; the per-step scratch per world is about the size of the
  * world (34.3 KB beside a 37.3 KB world of 17 bodies, 17 shapes, 64
- * contacts and 4 joints; 2.4 KB beside 3.5 KB for 2 bodies, 2 shapes, 4
- * contacts and 2 joints), so a call takes at most about 3,700 worlds of the
- * first kind and 45,000 of the second.  A larger batch returns
- * hipErrorOutOfMemory without launching;
- * split it over several calls.  All calls on one GPU share that GPU's
- * array: two calls that overlap in time on one GPU (different streams, or
- * host threads) race and corrupt each other's worlds; calls in one stream
- * are ordered and safe.  The array keeps the last call's contents; nothing
- * in it needs clearing between calls. */
+ * contacts and 4 joints).  A call runs its batch in chunks of as many
+ * tiles as the array holds (14 tiles, 896 worlds, of the first kind), one
+ * launch of each kernel per chunk, in order on the stream; a large batch
+ * therefore runs at a fraction of b3_batch_step_gpu's rate.
+ *
+ * Calls share the array of their GPU.  Each call's stream waits for the
+ * previous call's last kernel on that GPU (an event the library records
+ * after every call), so calls from different streams or host threads take
+ * turns.  A call made while its stream is being captured into a HIP graph
+ * neither waits nor records: the caller must order the graph's launches
+ * against other calls of this entry point on that GPU, or they race.  The
+ * array keeps the last call's contents; nothing in it needs clearing
+ * between calls. */
 hipError_t b3_batch_step_worlds_gpu(B3Batch worlds, unsigned long long config_signature, float dt, int substeps,
     const unsigned char* active, hipStream_t stream);
 

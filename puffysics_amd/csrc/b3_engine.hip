@@ -23,7 +23,8 @@
  *                              CU, with the contact writes, preparation,
  *                              contact sweeps and body and joint work split
  *                              over eight waves per tile and the
- *                              narrowphase over the first four (Masks: the
+ *                              narrowphase over the four to seven of them
+ *                              that have LDS rows for clip polygons (Masks: the
  *                              candidate search too, for 12 shapes or more;
  *                              JL: the joint rows in LDS, when they fit)
  *   b3k_apply                  dense force / torque / impulse inputs
@@ -310,43 +311,77 @@ hipError_t put_worlds(B3Engine* e, const unsigned char* host, uint32_t* dst) {
 
 /* ---- the step without allocation ----
  * b3_batch_step_worlds_gpu steps device-resident B3World structs in place
- * through the kernels of b3_batch_step_gpu, staging the batch as tiles in a
- * fixed device array instead of engine memory: tiles (world_words * 64
- * words each), then each tile's per-step scratch (tile_scr_words), then one
- * selection byte per world.  Each GPU the library runs on holds its own
- * copy of the array from module load until the process ends. */
-constexpr size_t kNoAllocWords = (size_t)64 << 20;            /* 256 MiB */
+ * through the kernels of b3_batch_step_gpu, staging them as tiles in a
+ * fixed device array instead of engine memory: a chunk's tiles
+ * (world_words * 64 words each), then each tile's per-step scratch
+ * (tile_scr_words), then one selection byte per world of the chunk.  A
+ * batch larger than one chunk runs chunk after chunk on the caller's
+ * stream.  Each GPU the library runs on holds its own copy of the array
+ * from module load until the process ends. */
+constexpr size_t kNoAllocWords = (size_t)16 << 20;            /* 64 MiB */
 static __device__ __align__(256) uint32_t b3_noalloc_scratch[kNoAllocWords];
 
-/* The array's device address on each device, looked up once per device
- * with that device current.  The symbol's name in host code is a host-side
- * stand-in, never a device address: kernels get this pointer. */
+/* Per device, set up once with that device current: the array's device
+ * address (the symbol's name in host code is a host-side stand-in, never a
+ * device address: kernels get this pointer), and an event recorded after
+ * each call's last kernel, which the next call's stream waits for, so that
+ * calls on different streams or host threads take turns with the array. */
 constexpr int kMaxDevices = 64;
+struct NoAllocDevice {
+    uint32_t* ptr;
+    hipEvent_t last;
+};
 std::mutex g_noalloc_mu;
-uint32_t* g_noalloc_ptr[kMaxDevices];
+NoAllocDevice g_noalloc[kMaxDevices];
 
-hipError_t noalloc_scratch(uint32_t** out) {
+/* The current device's set-up; call with g_noalloc_mu held.  The event is
+ * created by the first call that is not under graph capture (only those
+ * use it). */
+hipError_t noalloc_device(bool capturing, NoAllocDevice** out) {
     int dev = -1;
     hipError_t err = hipGetDevice(&dev);
     if (err != hipSuccess) return err;
     if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
-    std::lock_guard<std::mutex> lock(g_noalloc_mu);
-    if (!g_noalloc_ptr[dev]) {
+    NoAllocDevice& d = g_noalloc[dev];
+    if (!d.ptr) {
         void* p = nullptr;
-        err = hipGetSymbolAddress(&p, HIP_SYMBOL(b3_noalloc_scratch));
-        if (err != hipSuccess) return err;
+        if ((err = hipGetSymbolAddress(&p, HIP_SYMBOL(b3_noalloc_scratch))) != hipSuccess) return err;
         if (!p) return hipErrorInvalidSymbol;
         if ((err = b3i_lds_limit((const void*)b3k_step)) != hipSuccess) return err;
-        g_noalloc_ptr[dev] = (uint32_t*)p;
+        d.ptr = (uint32_t*)p;
     }
-    *out = g_noalloc_ptr[dev];
+    if (!capturing && !d.last && (err = hipEventCreateWithFlags(&d.last, hipEventDisableTiming)) != hipSuccess)
+        return err;
+    *out = &d;
     return hipSuccess;
 }
 
-/* Words of the array one call over `count` worlds of geometry g uses. */
-size_t noalloc_words(const Geometry& g, int count) {
-    size_t tiles = ((size_t)count + 63) / 64;
-    return tiles * ((size_t)g.world_words * 64 + (size_t)g.tile_scr_words) + ((size_t)count + 3) / 4;
+/* Words of the array per tile of geometry g: its worlds, their scratch and
+ * their 64 selection bytes. */
+size_t noalloc_tile_words(const Geometry& g) {
+    return (size_t)g.world_words * 64 + (size_t)g.tile_scr_words + 64 / 4;
+}
+
+/* hipSuccess when the bytes [p, p + bytes) start and end in device memory
+ * of the current device; hipErrorInvalidDevice when they are another
+ * device's, hipErrorInvalidValue when they are not device memory.  A failed
+ * lookup's error is cleared, so that it does not surface in a later call's
+ * hipGetLastError. */
+hipError_t device_range_here(const void* p, size_t bytes) {
+    int dev = -1;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    const void* ends[2] = {p, (const unsigned char*)p + (bytes ? bytes - 1 : 0)};
+    for (const void* q : ends) {
+        hipPointerAttribute_t a;
+        if (hipPointerGetAttributes(&a, q) != hipSuccess) {
+            (void)hipGetLastError();
+            return hipErrorInvalidValue;
+        }
+        if (a.type != hipMemoryTypeDevice && a.type != hipMemoryTypeManaged) return hipErrorInvalidValue;
+        if (a.device != dev) return hipErrorInvalidDevice;
+    }
+    return hipSuccess;
 }
 
 }  // namespace
@@ -602,25 +637,46 @@ hipError_t b3_batch_step_worlds_gpu(B3Batch worlds, unsigned long long config_si
     if (worlds.count == 0 || dt == 0.0f) return hipSuccess;
     size_t lds = (size_t)lds_rows(g) * kLanes * sizeof(float);
     if (lds > kCuLdsBytes) return hipErrorInvalidValue;
-    if (noalloc_words(g, worlds.count) > kNoAllocWords) return hipErrorOutOfMemory;
-    uint32_t* base = nullptr;
-    hipError_t err = noalloc_scratch(&base);
+    size_t chunk_tiles = kNoAllocWords / noalloc_tile_words(g);
+    if (chunk_tiles == 0) return hipErrorOutOfMemory;   /* one tile of these worlds exceeds the array */
+    size_t span = (size_t)(worlds.count - 1) * worlds.stride + worlds.world_offset + world_bytes;
+    hipError_t err = device_range_here(worlds.data, span);
+    if (err == hipSuccess && active) err = device_range_here(active, (size_t)worlds.count);
     if (err != hipSuccess) return err;
-    int tiles = (worlds.count + 63) / 64;
-    uint32_t* tile_words = base;
-    uint32_t* step_scratch = base + (size_t)tiles * g.world_words * 64;
-    unsigned char* select = (unsigned char*)(step_scratch + (size_t)tiles * g.tile_scr_words);
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    if ((err = hipStreamIsCapturing(stream, &capture)) != hipSuccess) return err;
+    bool capturing = capture != hipStreamCaptureStatusNone;
+
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    NoAllocDevice* nd = nullptr;
+    if ((err = noalloc_device(capturing, &nd)) != hipSuccess) return err;
+    /* Take turns with the previous call on this GPU, whatever its stream.  A
+     * call under capture cannot wait for work outside the graph: the caller
+     * orders the graph's launches against other calls. */
+    if (!capturing && (err = hipStreamWaitEvent(stream, nd->last, 0)) != hipSuccess) return err;
+    int chunk = (int)(chunk_tiles * 64 < (size_t)worlds.count ? chunk_tiles * 64 : (size_t)worlds.count);
     uint32_t* aos = (uint32_t*)worlds.data;
     size_t stride = worlds.stride / 4, offset = worlds.world_offset / 4;
-    dim3 grid((unsigned)((g.world_words + 63) / 64), (unsigned)tiles);
-    b3k_upload<<<grid, kXposeThreads, 0, stream>>>(aos, tile_words, worlds.count, g.world_words, stride, offset);
-    b3k_step_select<<<tiles, 64, 0, stream>>>(tile_words, g, worlds.count, active, select);
-    b3k_step<<<tiles, 64, lds, stream>>>(tile_words, nullptr, step_scratch, g, worlds.count, dt, substeps, select,
-        nullptr, 0u);
-    /* only the stepped worlds are written back: the others are not touched */
-    b3k_download<<<grid, kXposeThreads, 0, stream>>>(tile_words, aos, worlds.count, g.world_words, stride, offset,
-        select);
-    return hipGetLastError();
+    for (int first = 0; first < worlds.count; first += chunk) {
+        int n = worlds.count - first < chunk ? worlds.count - first : chunk;
+        int tiles = (n + 63) / 64;
+        uint32_t* tile_words = nd->ptr;
+        uint32_t* step_scratch = tile_words + (size_t)tiles * g.world_words * 64;
+        unsigned char* select = (unsigned char*)(step_scratch + (size_t)tiles * g.tile_scr_words);
+        uint32_t* chunk_aos = aos + (size_t)first * stride;
+        const unsigned char* chunk_active = active ? active + first : nullptr;
+        dim3 grid((unsigned)((g.world_words + 63) / 64), (unsigned)tiles);
+        b3k_upload<<<grid, kXposeThreads, 0, stream>>>(chunk_aos, tile_words, n, g.world_words, stride, offset);
+        b3k_step_select<<<tiles, 64, 0, stream>>>(tile_words, g, n, chunk_active, select);
+        b3k_step<<<tiles, 64, lds, stream>>>(tile_words, nullptr, step_scratch, g, n, dt, substeps, select, nullptr,
+            0u);
+        /* only the stepped worlds are written back: the others are not touched */
+        b3k_download<<<grid, kXposeThreads, 0, stream>>>(tile_words, chunk_aos, n, g.world_words, stride, offset,
+            select);
+        if ((err = hipGetLastError()) != hipSuccess) return err;
+    }
+    if (!capturing && (err = hipEventRecord(nd->last, stream)) != hipSuccess) return err;
+    return hipSuccess;
 }
 
 }  // extern "C"

@@ -87,6 +87,47 @@ def b3_batch_step_gravity_gpu(engine, dt, substeps, gravity, softening, masses=N
                                                           _stream(stream))
 
 
+class _DLDevice(C.Structure):
+    _fields_ = [("device_type", C.c_int32), ("device_id", C.c_int32)]
+
+
+class _DLDataType(C.Structure):
+    _fields_ = [("code", C.c_uint8), ("bits", C.c_uint8), ("lanes", C.c_uint16)]
+
+
+class _DLTensor(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("device", _DLDevice), ("ndim", C.c_int32), ("dtype", _DLDataType),
+                ("shape", C.POINTER(C.c_int64)), ("strides", C.POINTER(C.c_int64)), ("byte_offset", C.c_uint64)]
+
+
+class _DLManagedTensor(C.Structure):
+    _fields_ = [("dl_tensor", _DLTensor), ("manager_ctx", C.c_void_p), ("deleter", C.c_void_p)]
+
+
+_DL_ROCM, _DL_CPU, _DL_INT = 10, 1, 0
+_dl_keep = []
+
+
+def device_tensor(ptr, shape, device_type=_DL_ROCM, device_id=None):
+    """A torch int32 tensor of `shape` over memory the caller owns (the
+    engine's device tiles), through a DLPack capsule: no copy, no
+    allocation.  The memory must outlive the tensor."""
+    import torch
+    if device_id is None:
+        device_id = torch.cuda.current_device() if device_type == _DL_ROCM else 0
+    shp = (C.c_int64 * len(shape))(*shape)
+    m = _DLManagedTensor()
+    m.dl_tensor = _DLTensor(ptr, _DLDevice(device_type, device_id), len(shape), _DLDataType(_DL_INT, 32, 1), shp,
+                            None, 0)
+    m.manager_ctx = None
+    m.deleter = None
+    _dl_keep.append((m, shp))         # the capsule's struct and shape stay valid for the process
+    new = C.pythonapi.PyCapsule_New
+    new.restype = C.py_object
+    new.argtypes = [C.c_void_p, C.c_char_p, C.c_void_p]
+    return torch.utils.dlpack.from_dlpack(new(C.addressof(m), b"dltensor", None))
+
+
 B3_ENGINE_KEEP_SOLVER_FIELDS = 1
 B3_ENGINE_ART_CONTACTS = 2
 B3_ENGINE_ONE_WAVE_PER_TILE = 4
@@ -177,6 +218,15 @@ class B3Engine:
     def scene_masks(self, scene, seed, step, reset_out, step_out, stream=None):
         self._check("b3w_masks_gpu", self._lib.b3w_masks_gpu(scene, seed, step, self.count, _ptr(reset_out),
                                                              _ptr(step_out), _stream(stream)))
+
+    def tiles(self):
+        """The live world state as a torch int32 tensor [tiles, world_words,
+        64] sharing the engine's device memory (b3_engine_device_view): word
+        k of world w is tiles[w // 64, k, w % 64].  Valid until close()."""
+        ptr, words = C.c_void_p(), C.c_size_t()
+        self._check("b3_engine_device_view", self._lib.b3_engine_device_view(self._h, C.byref(ptr), C.byref(words)))
+        ntiles = (self.count + 63) // 64
+        return device_tensor(ptr.value, (ntiles, words.value, 64))
 
     def scene_inputs(self, scene, seed, step, step_mask=None, stream=None):
         self._check("b3w_inputs_gpu", self._lib.b3w_inputs_gpu(self._h, scene, seed, step, _ptr(step_mask),

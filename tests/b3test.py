@@ -193,22 +193,33 @@ def live_word_mask(worlds, sig):
     point slots.  Struct padding is left out."""
     W = world_ctype(sig)
     nwords = C.sizeof(W) // 4
-    mask = np.zeros((len(worlds), nwords), bool)
+    n = len(worlds)
+    mask = np.zeros((n, nwords), bool)
     bo, so, co, jo = (W.bodies.offset // 4, W.shapes.offset // 4, W.contacts.offset // 4, W.joints.offset // 4)
     bw, sw, cw, jw = 50, 22, C.sizeof(B3Contact) // 4, 115
     pts = B3Contact.points.offset // 4
     pw = C.sizeof(B3Point) // 4
     mask[:, :17] = True
-    for i, w in enumerate(worlds):
-        mask[i, bo:bo + bw * int(w["body_count"])] = True
-        mask[i, so:so + sw * int(w["shape_count"])] = True
-        mask[i, so + SHAPE_PAD_WORD:so + sw * int(w["shape_count"]):sw] = False
-        mask[i, jo:jo + jw * int(w["joint_count"])] = True
-        for c in range(int(w["contact_count"])):
-            base = co + c * cw
-            pc = int(w["contacts"][c]["point_count"])
-            mask[i, base:base + pts + pw * pc] = True
-            mask[i, base + pts + pw * 4:base + cw] = True
+    counts = {f: np.asarray(worlds[f]).astype(np.int64) for f in
+              ("body_count", "shape_count", "joint_count", "contact_count")}
+
+    def slots(base, width, cap, count):
+        for k in range(cap):
+            mask[:, base + k * width:base + (k + 1) * width] = (k < count)[:, None]
+
+    slots(bo, bw, worlds.dtype["bodies"].shape[0], counts["body_count"])
+    slots(so, sw, worlds.dtype["shapes"].shape[0], counts["shape_count"])
+    mask[:, so + SHAPE_PAD_WORD:so + sw * worlds.dtype["shapes"].shape[0]:sw] = False
+    slots(jo, jw, worlds.dtype["joints"].shape[0], counts["joint_count"])
+    max_c = worlds.dtype["contacts"].shape[0]
+    pc = np.asarray(worlds["contacts"]["point_count"]).astype(np.int64)
+    for c in range(max_c):
+        live = c < counts["contact_count"]
+        base = co + c * cw
+        mask[:, base:base + pts] = live[:, None]
+        for p in range(4):
+            mask[:, base + pts + pw * p:base + pts + pw * (p + 1)] = (live & (p < pc[:, c]))[:, None]
+        mask[:, base + pts + pw * 4:base + cw] = live[:, None]
     return mask
 
 
@@ -246,23 +257,25 @@ def solver_field_words(worlds):
     c_off = dt.fields["contacts"][1]
     p_dt = c_dt.fields["points"][0].base
     p_off = c_dt.fields["points"][1]
+    ncount = np.asarray(worlds["contact_count"]).astype(np.int64)
+    pc = np.asarray(worlds["contacts"]["point_count"]).astype(np.int64)
 
     def span(off, sub):
         return off // 4, (off + sub.itemsize) // 4
 
-    for i, w in enumerate(worlds):
-        for c in range(int(w["contact_count"])):
-            base = c_off + c * c_dt.itemsize
-            for f in SOLVER_FIELDS:
-                a, b = span(base + c_dt.fields[f][1], c_dt.fields[f][0])
-                mask[i, a:b] = True
-            for p in range(int(w["contacts"][c]["point_count"])):
-                pb = base + p_off + p * p_dt.itemsize
-                for f in POINT_SOLVER_FIELDS:
-                    a, b = span(pb + p_dt.fields[f][1], p_dt.fields[f][0])
-                    mask[i, a:b] = True
+    for c in range(dt.fields["contacts"][0].shape[0]):
+        live = c < ncount
+        base = c_off + c * c_dt.itemsize
+        for f in SOLVER_FIELDS:
+            a, b = span(base + c_dt.fields[f][1], c_dt.fields[f][0])
+            mask[:, a:b] |= live[:, None]
+        for p in range(c_dt.fields["points"][0].shape[0]):
+            on = live & (p < pc[:, c])
+            pb = base + p_off + p * p_dt.itemsize
+            for f in POINT_SOLVER_FIELDS:
+                a, b = span(pb + p_dt.fields[f][1], p_dt.fields[f][0])
+                mask[:, a:b] |= on[:, None]
     return mask
-
 
 
 # ---- coverage worlds: features the five benchmark scenes do not reach ----
@@ -693,3 +706,143 @@ def gpu_run(eng, scene, t0, nsteps, seed=scenes.SEED):
         eng.scene_inputs(scene, seed, t, stepm)
         eng.step(sc.dt, sc.substeps, stepm)
     torch.cuda.synchronize()
+
+
+# ---- per-world aggregates and body checksums from the body block ----
+# A batch's bodies as a [count, max_bodies, 50] block of 32-bit words (the
+# B3Body layout of include/b3_types.h), read from host worlds or from the
+# engine's device tiles, so that the same statistics can be taken every
+# vector step on both sides without downloading whole worlds.
+
+BODY_WORDS = 50
+BW_ROT, BW_CENTER, BW_LIN_VEL, BW_ANG_VEL, BW_INV_MASS, BW_INV_INERTIA, BW_TYPE = 3, 7, 13, 16, 32, 33, 48
+CANON_NAN = 0x7FC00000
+GRAVITY = 9.81
+
+
+def body_block(worlds):
+    """uint32 [count, max_bodies, 50] view of the host worlds' bodies."""
+    bo = worlds.dtype.fields["bodies"][1] // 4
+    nb = worlds.dtype["bodies"].shape[0]
+    return words(worlds)[:, bo:bo + nb * BODY_WORDS].reshape(len(worlds), nb, BODY_WORDS)
+
+
+def device_body_block(tiles, worlds_dtype, count):
+    """int32 [count, max_bodies, 50] copy of the bodies in the engine's
+    device tiles ([tiles, world_words, 64], word k of world w at
+    tiles[w // 64, k, w % 64])."""
+    bo = worlds_dtype.fields["bodies"][1] // 4
+    nb = worlds_dtype["bodies"].shape[0]
+    blk = tiles[:, bo:bo + nb * BODY_WORDS, :].permute(0, 2, 1)
+    return blk.reshape(-1, nb, BODY_WORDS)[:count]
+
+
+def _cross(ax, ay, az, bx, by, bz):
+    return ay * bz - az * by, az * bx - ax * bz, ax * by - ay * bx
+
+
+def stats_of_block(blk):
+    """Per-world mean height and mean energy of the dynamic bodies (numpy,
+    float64): linear and rotational kinetic energy (0.5 w.I w with
+    I = R diag(1/inv_i) R^T, evaluated in the body frame) plus gravitational
+    potential energy."""
+    need = [BW_ROT, BW_ROT + 1, BW_ROT + 2, BW_ROT + 3, BW_CENTER + 1, BW_LIN_VEL, BW_LIN_VEL + 1, BW_LIN_VEL + 2,
+            BW_ANG_VEL, BW_ANG_VEL + 1, BW_ANG_VEL + 2, BW_INV_MASS, BW_INV_INERTIA, BW_INV_INERTIA + 1,
+            BW_INV_INERTIA + 2, BW_TYPE]
+    sel = np.ascontiguousarray(blk[..., need])        # one gather of the words used
+    f = sel.view(np.float32).astype(np.float64)
+    at = {k: i for i, k in enumerate(need)}
+
+    def col(k):
+        return f[..., at[k]]
+
+    dyn = sel[..., at[BW_TYPE]].view(np.int32) == 2
+    inv_m = col(BW_INV_MASS)
+    m = np.where(inv_m > 0, 1.0 / np.where(inv_m > 0, inv_m, 1.0), 0.0)
+    vx, vy, vz = col(BW_LIN_VEL), col(BW_LIN_VEL + 1), col(BW_LIN_VEL + 2)
+    v2 = vx * vx + vy * vy + vz * vz
+    nx, ny, nz = -col(BW_ROT), -col(BW_ROT + 1), -col(BW_ROT + 2)
+    qs = col(BW_ROT + 3)
+    wx, wy, wz = col(BW_ANG_VEL), col(BW_ANG_VEL + 1), col(BW_ANG_VEL + 2)
+    tx, ty, tz = (2.0 * c for c in _cross(nx, ny, nz, wx, wy, wz))     # body-frame w: R^T w
+    cx, cy, cz = _cross(nx, ny, nz, tx, ty, tz)
+    lx, ly, lz = wx + qs * tx + cx, wy + qs * ty + cy, wz + qs * tz + cz
+    rot = 0.0
+    for k, wl in enumerate((lx, ly, lz)):
+        ii = col(BW_INV_INERTIA + k)
+        inertia = np.where(ii > 0, 1.0 / np.where(ii > 0, ii, 1.0), 0.0)
+        rot = rot + inertia * wl * wl
+    rot = 0.5 * rot
+    y = col(BW_CENTER + 1)
+    e = 0.5 * m * v2 + rot + m * GRAVITY * y
+    n = np.maximum(dyn.sum(axis=1), 1)
+    return np.where(dyn, y, 0).sum(axis=1) / n, np.where(dyn, e, 0).sum(axis=1) / n
+
+
+def stats_of_device_block(blk):
+    """stats_of_block for a torch int32 block on the device, same operations
+    in float64; returns a [2, count] tensor (mean height, mean energy)."""
+    import torch
+    f = blk.view(torch.float32).double()
+    dyn = blk[..., BW_TYPE] == 2
+    inv_m = f[..., BW_INV_MASS]
+    pos = inv_m > 0
+    m = torch.where(pos, 1.0 / torch.where(pos, inv_m, torch.ones_like(inv_m)), torch.zeros_like(inv_m))
+    v2 = (f[..., BW_LIN_VEL:BW_LIN_VEL + 3] ** 2).sum(-1)
+    qv = f[..., BW_ROT:BW_ROT + 3]
+    qs = f[..., BW_ROT + 3:BW_ROT + 4]
+    w = f[..., BW_ANG_VEL:BW_ANG_VEL + 3]
+    t = 2.0 * torch.linalg.cross(-qv, w)
+    wl = w + qs * t + torch.linalg.cross(-qv, t)
+    ii = f[..., BW_INV_INERTIA:BW_INV_INERTIA + 3]
+    ipos = ii > 0
+    inertia = torch.where(ipos, 1.0 / torch.where(ipos, ii, torch.ones_like(ii)), torch.zeros_like(ii))
+    rot = 0.5 * (inertia * wl * wl).sum(-1)
+    y = f[..., BW_CENTER + 1]
+    e = 0.5 * m * v2 + rot + m * GRAVITY * y
+    n = dyn.sum(dim=1).clamp(min=1).double()
+    zero = torch.zeros_like(y)
+    return torch.stack([torch.where(dyn, y, zero).sum(dim=1) / n, torch.where(dyn, e, zero).sum(dim=1) / n])
+
+
+def _hash_weights(nwords):
+    """Fixed weights in [1, 1024): a word times its weight stays below 2^42
+    and a sum of up to 2^11 such products below 2^53, so the float64 sums
+    below are exact whatever their order, and any single differing word
+    changes the sum."""
+    k = np.arange(nwords, dtype=np.int64)
+    return ((k * 2654435761 + 12345) % 1023 + 1).astype(np.float64)
+
+
+def body_hash(blk):
+    """Per-world exact checksum of a uint32 body block (NaN floats
+    canonicalised: their bits depend on operand order)."""
+    x = blk.reshape(len(blk), -1)
+    x = np.where(np.isnan(x.view(np.float32)), np.uint32(CANON_NAN), x)
+    return x.astype(np.float64) @ _hash_weights(x.shape[1])
+
+
+def device_body_hash(blk):
+    """body_hash of a torch int32 body block on the device."""
+    import torch
+    x = blk.reshape(blk.shape[0], -1)
+    x = torch.where(torch.isnan(x.view(torch.float32)), torch.full_like(x, CANON_NAN), x)
+    u = x.long() & 0xFFFFFFFF
+    wts = torch.from_numpy(_hash_weights(x.shape[1])).to(x.device)
+    return u.double() @ wts
+
+
+def oracle_stats(worlds, checksum=True):
+    """[3, count]: mean height, mean energy and body checksum (zero unless
+    `checksum`) per world, from the oracle library's C restatement of
+    stats_of_block and body_hash."""
+    lib = oracle()
+    fn = lib.ostat_bodies
+    fn.restype = None
+    fn.argtypes = [_vp, _i, C.c_size_t, _i, _i, _vp, _vp, _vp]
+    w = np.ascontiguousarray(worlds)
+    n = len(w)
+    out = np.zeros((3, n), np.float64)
+    fn(w.ctypes.data, n, w.dtype.itemsize, w.dtype.fields["bodies"][1] // 4, w.dtype["bodies"].shape[0],
+       out[0].ctypes.data, out[1].ctypes.data, out[2].ctypes.data if checksum else None)
+    return out

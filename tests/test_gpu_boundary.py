@@ -2,7 +2,7 @@
   - the step, restore and scene inputs captured into a HIP graph replay
     bit-identically to the same calls made eagerly ("enqueues on stream
     without allocation or synchronization; safe in capture",
-    b3_batch.cuh:77-80);
+    b3_batch.cuh:77-80), on both step kernels;
   - a kernel's dynamic-LDS limit, one setting shared by every engine in the
     process, is not lowered by an engine created later;
   - idle lanes of a shared tile (worlds outside the step mask, or past the
@@ -34,16 +34,22 @@ def _vector_step(eng, scene, t, reset, stepm):
     eng.step(sc.dt, sc.substeps, stepm, reset)
 
 
-@pytest.mark.parametrize("scene,count", [(5, 4096), (5, 300), (4, 130)])
-def test_graph_replay_equals_eager(scene, count):
+@pytest.mark.parametrize("scene,count,options", [(5, 4096, 1), (5, 300, 1), (4, 130, 1), (5, 300, 4), (5, 17000, 0)],
+                         ids=["arm4096-shared-keep", "arm300-shared-keep", "bin130-shared-keep",
+                              "arm300-one_wave", "arm17000-one_wave-default"])
+def test_graph_replay_equals_eager(scene, count, options):
     """Masks, inputs and the fused restore + step of one vector step are
     captured once; each replay is checked against the same calls made
     eagerly on a twin engine, with downloads (eager work and
-    synchronisation) between replays.  4,096 arm worlds take the one-wave
-    kernel, 300 and the bin the shared-tile kernel."""
+    synchronisation) between replays.  Batches of at most one tile per CU
+    (4,096 and 300 arm worlds, 130 bin worlds) take the shared-tile kernel;
+    the one-wave kernel b3k_step runs when forced (option
+    B3_ENGINE_ONE_WAVE_PER_TILE = 4) and for 17,000 arm worlds (266 tiles)
+    with the default options, the configuration of the 65,536-world
+    benchmark."""
     sc = scenes.SCENES[scene]
     worlds = scenes.build(scene, count)
-    graphed, eager = _engine(worlds, scene), _engine(worlds, scene)
+    graphed, eager = _engine(worlds, scene, options), _engine(worlds, scene, options)
     reset_g = torch.zeros(count, dtype=torch.uint8, device="cuda")
     stepm_g = torch.zeros(count, dtype=torch.uint8, device="cuda")
     reset_e = torch.zeros_like(reset_g)

@@ -1,12 +1,16 @@
 """b3_batch_step_worlds_gpu, the step without allocation, against
 b3_batch_step_gpu (the engine's step) on the same worlds.
 
-The new entry point steps caller-owned device B3World structs in place with
-its scratch in a fixed device array of the library.  Its results must equal
-the engine's word for word; it must leave unselected worlds, corrupt worlds
-and the bytes around each world (an Env struct's other fields) untouched,
-and refuse a batch beyond its array without launching.  Two calls in a row,
-the second on a smaller batch of another signature, share the array.
+The entry point steps caller-owned device B3World structs in place with its
+scratch in a fixed device array of the library, a batch larger than the
+array chunk after chunk.  Its results must equal the engine's word for word;
+it must leave unselected worlds, corrupt worlds and the bytes around each
+world (an Env struct's other fields) untouched, and refuse what it cannot
+step without launching.  Two calls in a row, the second on a smaller batch
+of another signature, share the array; so do two calls in flight on two
+streams at once, which take turns.  A first-ever call inside HIP graph
+capture sets the array up and replays like eager calls, and a warm call
+takes no device memory.
 """
 import numpy as np
 import pytest
@@ -18,6 +22,7 @@ from puffysics_amd.b3types import B3Batch
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
+HIP_ERROR_INVALID_VALUE = 1
 HIP_ERROR_OUT_OF_MEMORY = 2
 FILL = 0xA5
 
@@ -123,18 +128,50 @@ def test_no_alloc_step_skips_corrupt_worlds():
     assert len(diff_words(got[keep], want[keep], sc.sig)) == 0
 
 
-def test_no_alloc_step_refuses_a_batch_beyond_its_array():
-    """4,000 arm worlds need more than the 256 MiB array: refused with
-    hipErrorOutOfMemory, nothing launched, the worlds untouched.  Invalid
-    arguments are refused before any launch as well."""
+def test_no_alloc_step_runs_a_large_batch_in_chunks():
+    """2,000 arm worlds with a step mask are three chunks of the 64 MiB array
+    (896 + 896 + 208 worlds): equal to the engine's step on the same
+    worlds."""
+    lib = _lib()
+    scene, count = 5, 2000
+    sc = scenes.SCENES[scene]
+    worlds = _warm_worlds(scene, count, 5)
+    active = (np.arange(count) % 11 != 5).astype(np.uint8)
+    dev = _to_device(worlds, worlds.dtype.itemsize, 0)
+    act = torch.from_numpy(active).cuda()
+    rc = lib.b3_batch_step_worlds_gpu(B3Batch(dev.data_ptr(), worlds.dtype.itemsize, 0, count), sc.sig, sc.dt,
+                                      sc.substeps, act.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    got, _ = _from_device(dev, worlds.dtype, count, worlds.dtype.itemsize, 0)
+    want = _engine_steps(worlds, sc.sig, sc.dt, sc.substeps, active, 1)
+    bad = diff_words(got, want, sc.sig)
+    assert len(bad) == 0, "%d differing words, first %s" % (len(bad), bad[:4].tolist())
+
+
+def test_no_alloc_step_refuses_what_it_cannot_step():
+    """Refused without a launch, the worlds untouched: a tile of worlds with
+    its scratch larger than the array (4,000 contacts per world:
+    hipErrorOutOfMemory); worlds or a step mask in host memory
+    (hipErrorInvalidValue); invalid arguments."""
+    from puffysics_amd.b3types import signature, world_dtype
     lib = _lib()
     sc = scenes.SCENES[5]
     wb = 37272
-    dev = torch.full((4000 * wb,), 7, dtype=torch.uint8, device="cuda")
+    dev = torch.full((40 * wb,), 7, dtype=torch.uint8, device="cuda")
     stream = torch.cuda.current_stream().cuda_stream
-    rc = lib.b3_batch_step_worlds_gpu(B3Batch(dev.data_ptr(), wb, 0, 4000), sc.sig, sc.dt, sc.substeps, None,
-                                      stream)
-    assert rc == HIP_ERROR_OUT_OF_MEMORY
+    big = signature(2, 2, 4000, 1)
+    big_wb = world_dtype(big).itemsize
+    assert 64 * big_wb > 64 << 20
+    big_dev = torch.full((big_wb,), 7, dtype=torch.uint8, device="cuda")
+    assert lib.b3_batch_step_worlds_gpu(B3Batch(big_dev.data_ptr(), big_wb, 0, 1), big, sc.dt, sc.substeps, None,
+                                        stream) == HIP_ERROR_OUT_OF_MEMORY
+    host = np.full(10 * wb, 7, np.uint8)
+    assert lib.b3_batch_step_worlds_gpu(B3Batch(host.ctypes.data, wb, 0, 10), sc.sig, sc.dt, sc.substeps, None,
+                                        stream) == HIP_ERROR_INVALID_VALUE
+    host_mask = np.ones(10, np.uint8)
+    assert lib.b3_batch_step_worlds_gpu(B3Batch(dev.data_ptr(), wb, 0, 10), sc.sig, sc.dt, sc.substeps,
+                                        host_mask.ctypes.data, stream) == HIP_ERROR_INVALID_VALUE
     assert lib.b3_batch_step_worlds_gpu(B3Batch(dev.data_ptr(), wb - 4, 0, 10), sc.sig, sc.dt, sc.substeps,
                                         None, stream) != 0
     assert lib.b3_batch_step_worlds_gpu(B3Batch(dev.data_ptr() + 2, wb, 0, 10), sc.sig, sc.dt, sc.substeps,
@@ -143,4 +180,102 @@ def test_no_alloc_step_refuses_a_batch_beyond_its_array():
                                         None, stream) != 0
     assert lib.b3_batch_step_worlds_gpu(B3Batch(None, wb, 0, 0), sc.sig, sc.dt, sc.substeps, None, stream) == 0
     torch.cuda.synchronize()
-    assert int((dev != 7).sum()) == 0
+    assert int((dev != 7).sum()) == 0 and int((big_dev != 7).sum()) == 0
+    assert (host == 7).all()
+    # the refusals leave no error behind for the next call
+    small = _warm_worlds(2, 64, 3)
+    d2 = _to_device(small, small.dtype.itemsize, 0)
+    s2 = scenes.SCENES[2]
+    assert lib.b3_batch_step_worlds_gpu(B3Batch(d2.data_ptr(), small.dtype.itemsize, 0, 64), s2.sig, s2.dt,
+                                        s2.substeps, None, stream) == 0
+    torch.cuda.synchronize()
+
+
+def test_no_alloc_calls_on_two_streams_take_turns():
+    """300 arm worlds on one stream and 200 box stacks on another, issued
+    back to back with no synchronisation between them, both through the
+    one array: each batch equals the engine's step of it."""
+    lib = _lib()
+    cases = [(5, 300), (2, 200)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    devs, inputs = [], []
+    for scene, count in cases:
+        worlds = _warm_worlds(scene, count, 5)
+        inputs.append(worlds)
+        devs.append(_to_device(worlds, worlds.dtype.itemsize, 0))
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for (scene, count), dev, worlds, st in zip(cases, devs, inputs, streams):
+            sc = scenes.SCENES[scene]
+            rc = lib.b3_batch_step_worlds_gpu(B3Batch(dev.data_ptr(), worlds.dtype.itemsize, 0, count), sc.sig,
+                                              sc.dt, sc.substeps, None, st.cuda_stream)
+            assert rc == 0
+    torch.cuda.synchronize()
+    for (scene, count), dev, worlds in zip(cases, devs, inputs):
+        sc = scenes.SCENES[scene]
+        got, _ = _from_device(dev, worlds.dtype, count, worlds.dtype.itemsize, 0)
+        want = _engine_steps(worlds, sc.sig, sc.dt, sc.substeps, None, 3)
+        bad = diff_words(got, want, sc.sig)
+        assert len(bad) == 0, "scene %d: %d differing words, first %s" % (scene, len(bad), bad[:4].tolist())
+
+
+CAPTURE_SCRIPT = r"""
+import sys
+import numpy as np
+import torch
+sys.path[:0] = [%(root)r, %(tests)r]
+from b3test import clone, diff_words, oracle_run
+from puffysics_amd import _native, scenes
+from puffysics_amd.b3types import B3Batch
+
+lib = _native.engine_lib()
+scene, count = 2, 200
+sc = scenes.SCENES[scene]
+worlds = scenes.build(scene, count)
+oracle_run(scene, worlds, clone(worlds), 0, 5)
+wb = worlds.dtype.itemsize
+raw = worlds.view(np.uint8)
+graphed = torch.from_numpy(raw.copy()).cuda()
+eager = torch.from_numpy(raw.copy()).cuda()
+torch.cuda.synchronize()
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):
+    # the first call of this process: the array is set up under capture
+    rc = lib.b3_batch_step_worlds_gpu(B3Batch(graphed.data_ptr(), wb, 0, count), sc.sig, sc.dt, sc.substeps,
+                                      None, torch.cuda.current_stream().cuda_stream)
+assert rc == 0, rc
+torch.cuda.synchronize()
+assert bool((graphed.cpu().numpy() == raw).all()), "capture ran the step"
+stream = torch.cuda.current_stream().cuda_stream
+for r in range(3):
+    graph.replay()
+    assert lib.b3_batch_step_worlds_gpu(B3Batch(eager.data_ptr(), wb, 0, count), sc.sig, sc.dt, sc.substeps,
+                                        None, stream) == 0
+    torch.cuda.synchronize()
+    a = graphed.cpu().numpy().view(worlds.dtype)
+    b = eager.cpu().numpy().view(worlds.dtype)
+    bad = diff_words(a, b, sc.sig)
+    assert len(bad) == 0, "replay %%d: %%d differing words" %% (r, len(bad))
+free_before = torch.cuda.mem_get_info()[0]
+assert lib.b3_batch_step_worlds_gpu(B3Batch(eager.data_ptr(), wb, 0, count), sc.sig, sc.dt, sc.substeps, None,
+                                    stream) == 0
+torch.cuda.synchronize()
+free_after = torch.cuda.mem_get_info()[0]
+assert free_after == free_before, (free_before, free_after)
+print("capture ok", flush=True)
+"""
+
+
+def test_no_alloc_first_call_under_graph_capture():
+    """In a fresh process, the first call is made inside torch.cuda.graph
+    capture: it returns hipSuccess, the capture runs nothing, and each
+    replay equals an eager call on a twin copy of the worlds.  Afterwards a
+    warm call leaves the device's free memory unchanged."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    script = CAPTURE_SCRIPT % {"root": root, "tests": os.path.join(root, "tests")}
+    out = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stdout[-2000:] + out.stderr[-4000:]
+    assert "capture ok" in out.stdout
