@@ -1149,11 +1149,13 @@ B3D_FN void step_world_art(const Lane& L0, float* ws, float dt, int substeps) {
 
 /* ---- the reduced-coordinate integrator (b3_art_step) ---- */
 
-B3D_FN Q qaxis_angle(V3 axis, float radians) {                           /* 03_math.inl:321-326 */
+/* 03_math.inl:321-326, with the host C library's sinf and cosf bits
+ * (or_sinf, or_cosf in b3d_math.h). */
+B3D_FN Q qaxis_angle(V3 axis, float radians) {
     axis = norm(axis);
     float h = 0.5f * radians;
-    float s = sinf(h);
-    return q4(s * axis.x, s * axis.y, s * axis.z, cosf(h));
+    float s = or_sinf(h);
+    return q4(s * axis.x, s * axis.y, s * axis.z, or_cosf(h));
 }
 
 /* art_refresh with each joint's rate about its axis and its angle, the

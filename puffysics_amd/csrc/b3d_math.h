@@ -228,6 +228,117 @@ B3D_FN float fd_atan2f(float y, float x) {
     }
 }
 
+/* ---- sinf and cosf with the host C library's bits ----
+ *
+ * b3_q_axis_angle calls libm sinf and cosf (03_math.inl:321-326); on its CPU
+ * path glibc 2.35 evaluates them by the method of Arm's optimized-routines
+ * (Szabolcs Nagy, 2018, sincosf.h, which glibc carries as
+ * sysdeps/ieee754/flt-32):
+ *   - the argument goes to double; |x| < pi/4 is evaluated directly (and
+ *     |x| < 2^-12 returns x, or 1 for the cosine);
+ *   - |x| < 120 is reduced by n = round(x 2/pi) as x - n pi/2, with n taken
+ *     from the integer part of x (2/pi) 2^24 plus 2^23, shifted;
+ *   - larger |x| is reduced with 2/pi as a table of 32-bit windows of its
+ *     bits, three products of the 24-bit mantissa giving a 62-bit fixed
+ *     point fraction (Payne and Hanek);
+ *   - n mod 4 picks the sign and whether the sine or the cosine polynomial
+ *     runs on the reduced argument: x + x^3 (s1 + x^2 s2 + x^4 s3), or
+ *     c0 + c1 x^2 + c2 x^4 + c3 x^6 + c4 x^8, in double, rounded once to
+ *     float.
+ * The coefficients are that source's hex doubles.  glibc on an x86-64 host
+ * with FMA runs its FMA build, in which the compiler contracts every
+ * a + b c of the polynomials and the reduction's x - n pi/2 into one fused
+ * operation; the functions below make exactly those fma calls (and nothing
+ * else is contracted: -ffp-contract=off).  Checked on all 2^32 floats
+ * against this host's sinf and cosf (tests/test_sincos.py), and on the
+ * device against the host's (tests/test_gpu_sincos.py). */
+struct SinCosTab { double sign[4], hpi_inv, hpi, c0, c1, c2, c3, c4, s1, s2, s3; };
+B3D_FN const SinCosTab& sincos_tab(int k) {
+    /* k = 1: the quadrants where the cosine polynomial's sign is flipped */
+    static constexpr SinCosTab t[2] = {
+        {{1.0, -1.0, -1.0, 1.0}, 0x1.45f306dc9c883p+23, 0x1.921fb54442d18p+0, 0x1p+0, -0x1.ffffffd0c621cp-2,
+         0x1.55553e1068f19p-5, -0x1.6c087e89a359dp-10, 0x1.99343027bf8c3p-16, -0x1.555545995a603p-3,
+         0x1.1107605230bc4p-7, -0x1.994eb3774cf24p-13},
+        {{1.0, -1.0, -1.0, 1.0}, 0x1.45f306dc9c883p+23, 0x1.921fb54442d18p+0, -0x1p+0, 0x1.ffffffd0c621cp-2,
+         -0x1.55553e1068f19p-5, 0x1.6c087e89a359dp-10, -0x1.99343027bf8c3p-16, -0x1.555545995a603p-3,
+         0x1.1107605230bc4p-7, -0x1.994eb3774cf24p-13}};
+    return t[k];
+}
+/* 2/pi: window i (i >= 3) holds bits 8 (i - 3) .. 8 (i - 3) + 31 of its
+ * binary fraction, windows 0-2 its first 8, 16 and 24 bits. */
+B3D_FN uint32_t two_over_pi_window(int i) {
+    static constexpr uint32_t w[24] = {
+        0x000000a2, 0x0000a2f9, 0x00a2f983, 0xa2f9836e, 0xf9836e4e, 0x836e4e44, 0x6e4e4415, 0x4e441529,
+        0x441529fc, 0x1529fc27, 0x29fc2757, 0xfc2757d1, 0x2757d1f5, 0x57d1f534, 0xd1f534dd, 0xf534ddc0,
+        0x34ddc0db, 0xddc0db62, 0xc0db6295, 0xdb629599, 0x6295993c, 0x95993c43, 0x993c4390, 0x3c439041};
+    return w[i];
+}
+/* the exponent and top mantissa bits that the range tests compare */
+B3D_FN uint32_t top12_(float x) { return (fbits_(x) >> 20) & 0x7ffu; }
+/* The sine (odd n) or cosine (even n) polynomial of the reduced argument. */
+B3D_FN float sincos_poly(double x, double x2, const SinCosTab& p, int n) {
+    if ((n & 1) == 0) {
+        double x3 = x * x2;
+        double s1 = fma(x2, p.s3, p.s2);
+        double x7 = x3 * x2;
+        double s = fma(x3, p.s1, x);
+        return (float)fma(x7, s1, s);
+    }
+    double x4 = x2 * x2;
+    double c2 = fma(x2, p.c4, p.c3);
+    double c1 = fma(x2, p.c1, p.c0);
+    double x6 = x4 * x2;
+    double c = fma(x4, p.c2, c1);
+    return (float)fma(x6, c2, c);
+}
+/* x - n pi/2 for |x| < 120, n the nearest integer to x 2/pi. */
+B3D_FN double sincos_reduce_small(double x, const SinCosTab& p, int* np) {
+    double r = x * p.hpi_inv;
+    int n = ((int32_t)r + 0x800000) >> 24;
+    *np = n;
+    return fma(-(double)n, p.hpi, x);
+}
+/* The same for finite |x| >= 120, from the float's bits. */
+B3D_FN double sincos_reduce_large(uint32_t xi, int* np) {
+    int i = (int)((xi >> 26) & 15u);
+    int shift = (int)((xi >> 23) & 7u);
+    uint32_t m = ((xi & 0xffffffu) | 0x800000u) << shift;
+    uint64_t r0 = (uint64_t)(uint32_t)(m * two_over_pi_window(i));
+    uint64_t r1 = (uint64_t)m * two_over_pi_window(i + 4);
+    uint64_t r2 = (uint64_t)m * two_over_pi_window(i + 8);
+    r0 = (r2 >> 32) | (r0 << 32);
+    r0 += r1;
+    uint64_t n = (r0 + (1ull << 61)) >> 62;
+    r0 -= n << 62;
+    *np = (int)n;
+    return (double)(int64_t)r0 * 0x1.921fb54442d18p-62;
+}
+/* cos when want_cos, else sin, with glibc's bits for every non-NaN float. */
+B3D_FN float or_sincosf(float y, bool want_cos) {
+    double x = y;
+    int n;
+    if (top12_(y) < top12_(0x1.921fb6p-1f)) {                   /* |y| < pi/4 */
+        if (top12_(y) < top12_(0x1p-12f)) return want_cos ? 1.0f : y;
+        return sincos_poly(x, x * x, sincos_tab(0), want_cos ? 1 : 0);
+    }
+    int q;
+    if (top12_(y) < top12_(120.0f)) {
+        x = sincos_reduce_small(x, sincos_tab(0), &n);
+        q = n;
+    } else if (top12_(y) < top12_(__builtin_inff())) {
+        uint32_t xi = fbits_(y);
+        x = sincos_reduce_large(xi, &n);
+        q = n + (int)(xi >> 31);                                /* the original sign */
+    } else {
+        return (y - y) / (y - y);                               /* inf or NaN: NaN */
+    }
+    const SinCosTab& p = sincos_tab((q & 2) ? 1 : 0);
+    double s = p.sign[q & 3];
+    return sincos_poly(x * s, x * x, p, want_cos ? (n ^ 1) : n);
+}
+B3D_FN float or_sinf(float y) { return or_sincosf(y, false); }
+B3D_FN float or_cosf(float y) { return or_sincosf(y, true); }
+
 /* Angle of the twist about local Z (03_math.inl:293-309), with the host
  * library's atan2f bits (fd_atan2f above). */
 B3D_FN float twist(Q q) {

@@ -360,4 +360,46 @@ unsigned long long emu_atan_mismatches(int mode, unsigned long long lo, unsigned
     return total;
 }
 
+/* Counts the floats with bits in [lo, hi) (NaNs skipped: their payloads
+ * are not part of the contract) where the engine's or_sinf or or_cosf
+ * differ from libm's sinf or cosf, on `threads` threads; sin and cos
+ * counts go to out[0] and out[1]. */
+void emu_sincos_mismatches(unsigned long long lo, unsigned long long hi, int threads, unsigned long long* out) {
+    std::vector<unsigned long long> bs(threads, 0), bc(threads, 0);
+    std::vector<std::thread> pool;
+    for (int t = 0; t < threads; t++) {
+        pool.emplace_back([&, t]() {
+            unsigned long long a = lo + (hi - lo) * t / threads, b = lo + (hi - lo) * (t + 1) / threads;
+            for (unsigned long long i = a; i < b; i++) {
+                float x = emu_f((uint32_t)i);
+                if (x != x) continue;
+                bs[t] += !emu_same(sinf(x), or_sinf(x));
+                bc[t] += !emu_same(cosf(x), or_cosf(x));
+            }
+        });
+    }
+    out[0] = out[1] = 0;
+    for (int t = 0; t < threads; t++) {
+        pool[t].join();
+        out[0] += bs[t];
+        out[1] += bc[t];
+    }
+}
+
+/* The engine's or_sinf and or_cosf over arrays, built for the host. */
+void emu_or_sincosf(const float* x, float* s, float* c, long n) {
+    for (long i = 0; i < n; i++) {
+        s[i] = or_sinf(x[i]);
+        c[i] = or_cosf(x[i]);
+    }
+}
+
+/* libm's sinf and cosf over arrays. */
+void emu_libm_sincosf(const float* x, float* s, float* c, long n) {
+    for (long i = 0; i < n; i++) {
+        s[i] = sinf(x[i]);
+        c[i] = cosf(x[i]);
+    }
+}
+
 }  // extern "C"

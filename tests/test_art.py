@@ -325,9 +325,13 @@ def test_device_art_bit_exact_on_passive_hinges():
 
 
 @pytest.mark.gpu
-def test_device_art_one_step_on_the_arm_scene():
+def test_device_art_steps_on_the_arm_scene_bit_exact():
+    """The arm scene (motors, limits, contacts on the links) with
+    articulated contacts over 20 steps with its inputs: every live word
+    equals the oracle's (the hinge twist's atan2f has the host library's
+    bits on the device)."""
     from puffysics_amd.engine import B3_ENGINE_ART_CONTACTS, B3Engine
-    from test_gpu_parity import assert_close_state, contact_keys
+    from test_gpu_parity import contact_keys
     sig = scenes.SCENES[5].sig
     worlds = scenes.build(5, 128)
     for t in range(3):
@@ -336,13 +340,17 @@ def test_device_art_one_step_on_the_arm_scene():
     ref = clone(worlds)
     eng = B3Engine(worlds, sig)
     eng.set_options(B3_ENGINE_ART_CONTACTS)
-    T.oracle_step_art(ref, sig, DT, 4)
-    eng.step(DT, 4)
+    for t in range(3, 23):
+        _arm_inputs(ref, t)
+        T.oracle_step_art(ref, sig, DT, 4)
+        eng.scene_inputs(5, scenes.SEED, t)              # the same inputs on the device
+        eng.step(DT, 4)
     torch.cuda.synchronize()
     got = eng.download()
     eng.close()
     assert contact_keys(got) == contact_keys(ref)
-    assert_close_state(got, ref)
+    bad = diff_words(got, ref, sig)
+    assert len(bad) == 0, "%d differing words in worlds %s" % (len(bad), np.unique(bad[:, 0])[:10].tolist())
 
 
 @pytest.mark.gpu
@@ -367,16 +375,15 @@ def test_device_art_rejects_force_laws_and_resets():
 
 @pytest.mark.gpu
 def test_device_art_step_one_step_on_reduced_trees():
-    """One b3_art_step from the same state as the oracle: contact pairs,
-    point counts and features identical, body state within the single-step
-    tolerance (the joint angles go through the device's sinf, cosf and
-    atan2f)."""
+    """One b3_art_step from the same state as the oracle, bit for bit: the
+    joint angles go through sinf, cosf and atan2f, which the device
+    evaluates with the host library's bits (or_sinf, or_cosf and fd_atan2f
+    in b3d_math.h)."""
     from puffysics_amd.engine import B3_ENGINE_ART_CONTACTS, B3Engine
     from test_gpu_parity import contact_keys
     worlds = T.reduced_tree_worlds(130)
     for _ in range(15):
         T.oracle_art_step(worlds, CUSTOM_SIG, DT, 4)
-    pre = clone(worlds)
     ref = clone(worlds)
     eng = B3Engine(worlds, CUSTOM_SIG)
     eng.set_options(B3_ENGINE_ART_CONTACTS)
@@ -387,16 +394,31 @@ def test_device_art_step_one_step_on_reduced_trees():
     eng.close()
     assert ref["contact_count"].sum() > 100
     assert contact_keys(got) == contact_keys(ref)
-    # within the single-step tolerance, or, where a contact clamp amplifies
-    # the last-place differences (one world of 130 when measured), within
-    # twice the spread of the oracle under one-ulp libm perturbations
-    err = np.abs(T.body_state(got) - T.body_state(ref))
-    ok = err <= 1e-5 + 1e-4 * np.abs(T.body_state(ref))
-    if not ok.all():
-        spread = T.ulp_spread(pre, CUSTOM_SIG, DT, 4)
-        ok |= err <= 2.0 * spread
-        assert np.unique(np.argwhere(err > 1e-5 + 1e-4 * np.abs(T.body_state(ref)))[:, 0]).size <= 3
-    assert ok.all(), "max err %g at %s" % (err.max(), np.argwhere(~ok)[:5].tolist())
+    bad = diff_words(got, ref, CUSTOM_SIG)
+    assert len(bad) == 0, "%d differing words in worlds %s" % (len(bad), np.unique(bad[:, 0])[:10].tolist())
+
+
+@pytest.mark.gpu
+def test_device_art_step_bit_exact_on_reduced_trees_with_masks():
+    """b3_art_step over 30 steps with a step mask on every other step, from
+    the worlds' initial state: every live word equals the oracle's."""
+    from puffysics_amd.engine import B3_ENGINE_ART_CONTACTS, B3Engine
+    worlds = T.reduced_tree_worlds(256)
+    ref = clone(worlds)
+    eng = B3Engine(worlds, CUSTOM_SIG)
+    eng.set_options(B3_ENGINE_ART_CONTACTS)
+    active = (np.arange(256) % 7 != 5).astype(np.uint8)
+    d_active = _dev(active)
+    for t in range(30):
+        act = t % 2 == 1
+        T.oracle_art_step(ref, CUSTOM_SIG, DT, 4, active if act else None)
+        eng.art_step(DT, 4, d_active if act else None)
+    torch.cuda.synchronize()
+    got = eng.download()
+    eng.close()
+    bad = diff_words(got, ref, CUSTOM_SIG)
+    assert len(bad) == 0, "%d differing words in worlds %s" % (len(bad), np.unique(bad[:, 0])[:10].tolist())
+    assert ref["contact_count"].sum() > 0
 
 
 @pytest.mark.gpu
