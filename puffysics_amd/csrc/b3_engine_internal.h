@@ -28,6 +28,8 @@ struct B3Engine {
     size_t lds_shared_bytes; /* LDS of a workgroup of kTileWaves waves */
     bool shared_masks;       /* ... which also split the candidate search (b3d::shared_masks) */
     bool joint_lds;          /* ... and keep the joint rows in LDS (b3d::joint_rows_fit) */
+    int tile_parts;          /* workgroups per tile of the shared step (1 or 2), each with its own
+                                scratch and stage */
 };
 
 /* Waves per tile when the narrowphase is shared (two per SIMD: the shared
@@ -67,13 +69,14 @@ namespace b3d {
  * read 64 consecutive snapshot words and write them to their rows of the
  * tile.  A world's copy is cut into chunks of kRestoreChunk words; this
  * wave copies chunk k of every resetting world when k % nslices == slice,
- * so nslices waves share a tile's restores. */
+ * so nslices waves share a tile's restores.  Only the worlds of the lanes
+ * set in `lanes` are restored. */
 constexpr int kRestoreBatch = 8, kRestoreChunk = 64 * kRestoreBatch;
 __device__ inline void restore_tile(uint32_t* live, const uint32_t* snap, const Geometry& g, int count,
-        const unsigned char* reset, int tile, int slice, int nslices) {
+        const unsigned char* reset, int tile, int slice, int nslices, uint64_t lanes = ~0ull) {
     int lane = (int)(threadIdx.x & 63u);
     int w = tile * 64 + lane;
-    int want = w < count && reset[w] != 0;
+    int want = w < count && ((lanes >> lane) & 1u) && reset[w] != 0;
     uint64_t bits = __ballot(want);
     uint32_t* lt = live + (size_t)tile * g.world_words * 64;
     while (bits) {

@@ -384,17 +384,20 @@ struct Lane {
  * B3_ENGINE_KEEP_SOLVER_FIELDS. */
 constexpr unsigned int kKeepSolverFields = 1u;
 
-/* The lane view of world `lane` of tile `tile`. */
+/* The lane view of world `lane` of tile `tile`, with the per-step scratch
+ * of scratch tile `scr_tile` (the same by default; a tile whose lanes are
+ * stepped by several workgroups gives each its own). */
 B3D_FN Lane lane_view(uint32_t* live, uint32_t* scratch, float* vel_rows, const Geometry& g, int tile, int lane,
-        unsigned int opts = 0) {
+        unsigned int opts = 0, int scr_tile = -1) {
     Lane L;
     L.opts = opts;
     L.st = PairStage{};
     L.staged = false;
     L.sslot = lane;
+    if (scr_tile < 0) scr_tile = tile;
     L.w = live + (size_t)tile * g.world_words * kLanes + lane;
-    L.scr = scratch ? scratch + (size_t)tile * g.tile_scr_words + lane : nullptr;
-    L.sq = scratch ? scratch + (size_t)tile * g.tile_scr_words + (size_t)g.scr_words * kLanes : nullptr;
+    L.scr = scratch ? scratch + (size_t)scr_tile * g.tile_scr_words + lane : nullptr;
+    L.sq = scratch ? scratch + (size_t)scr_tile * g.tile_scr_words + (size_t)g.scr_words * kLanes : nullptr;
     L.jl = nullptr;
     L.vel = vel_rows ? vel_rows + lane : nullptr;
     L.lane = lane;
