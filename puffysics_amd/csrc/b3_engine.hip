@@ -16,9 +16,10 @@
  *                              B3World structs); four waves per tile, each
  *                              copying every fourth 512-word chunk of the
  *                              tile's resetting worlds with all 64 lanes
- *   b3k_step                   optional fused restore, then one b3_step per
+ *   b3k_step<JI>               optional fused restore, then one b3_step per
  *                              selected lane; LDS holds the lane's clip
- *                              polygons, then its body velocities
+ *                              polygons, then its body velocities (JI: and
+ *                              its joints' accumulated impulses)
  *   b3k_step_shared<Masks, JL> the same for batches of at most one tile per
  *                              CU, with the contact writes, preparation,
  *                              contact sweeps and body and joint work split
@@ -106,6 +107,10 @@ __global__ __launch_bounds__(64) void b3k_restore(uint32_t* live, const uint32_t
 
 /* ---- the step ---- */
 
+/* JI: the joints' accumulated impulses stay in LDS past the velocity rows
+ * for the whole step (ji_fit; the launch gives ji_lds_rows words per lane),
+ * instead of a read and a write of the joint's words in every solve. */
+template <bool JI>
 __global__ __launch_bounds__(64) void b3k_step(uint32_t* live, const uint32_t* snap, uint32_t* scratch,
         Geometry g, int count, float dt, int substeps, const unsigned char* step_mask,
         const unsigned char* reset_mask, unsigned int opts) {
@@ -118,7 +123,9 @@ __global__ __launch_bounds__(64) void b3k_step(uint32_t* live, const uint32_t* s
     int lane = threadIdx.x;
     int w = tile * 64 + lane;
     if (w >= count || (step_mask && !step_mask[w])) return;
-    step_world(lane_view(live, scratch, vel_rows, g, tile, lane, opts), dt, substeps);
+    Lane L = lane_view(live, scratch, vel_rows, g, tile, lane, opts);
+    if (JI) L.ji = vel_rows + (size_t)ji_word(g) * kLanes + lane;
+    step_world<false, false, JI>(L, dt, substeps);
 }
 
 /* The step with the narrowphase and the contact sweeps shared by
@@ -353,7 +360,7 @@ hipError_t noalloc_device(bool capturing, NoAllocDevice** out) {
         void* p = nullptr;
         if ((err = hipGetSymbolAddress(&p, HIP_SYMBOL(b3_noalloc_scratch))) != hipSuccess) return err;
         if (!p) return hipErrorInvalidSymbol;
-        if ((err = b3i_lds_limit((const void*)b3k_step)) != hipSuccess) return err;
+        if ((err = b3i_lds_limit((const void*)b3k_step<false>)) != hipSuccess) return err;
         d.ptr = (uint32_t*)p;
     }
     if (!capturing && !d.last && (err = hipEventCreateWithFlags(&d.last, hipEventDisableTiming)) != hipSuccess)
@@ -420,8 +427,11 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
     e->g = g;
     e->world_bytes = world_bytes;
     e->tile_words = (size_t)g.world_words * 64;
-    e->lds_bytes = lds;
-    err = b3i_lds_limit((const void*)b3k_step);
+    /* the one-wave step keeps the joints' impulses in LDS when they fit */
+    e->joint_impulses_lds = ji_fit(g);
+    e->lds_bytes = e->joint_impulses_lds ? (size_t)ji_lds_rows(g) * kLanes * sizeof(float) : lds;
+    err = b3i_lds_limit((const void*)b3k_step<false>);
+    if (err == hipSuccess) err = b3i_lds_limit((const void*)b3k_step<true>);
     if (err == hipSuccess) err = b3i_lds_limit((const void*)b3k_step_shared<true, false>);
     if (err == hipSuccess) err = b3i_lds_limit((const void*)b3k_step_shared<false, false>);
     if (err == hipSuccess) err = b3i_lds_limit((const void*)b3k_step_shared<true, true>);
@@ -604,7 +614,8 @@ hipError_t b3_batch_step_gpu(B3Engine* e, float dt, int substeps, const unsigned
             e->options, e->tile_parts);
         return hipGetLastError();
     }
-    b3k_step<<<e->tiles, 64, e->lds_bytes, stream>>>(e->live, e->snap, e->scratch, e->g, e->count, dt, substeps,
+    auto one_wave = e->joint_impulses_lds ? b3k_step<true> : b3k_step<false>;
+    one_wave<<<e->tiles, 64, e->lds_bytes, stream>>>(e->live, e->snap, e->scratch, e->g, e->count, dt, substeps,
         step_mask, reset_mask, e->options);
     return hipGetLastError();
 }
@@ -688,8 +699,8 @@ hipError_t b3_batch_step_worlds_gpu(B3Batch worlds, unsigned long long config_si
         dim3 grid((unsigned)((g.world_words + 63) / 64), (unsigned)tiles);
         b3k_upload<<<grid, kXposeThreads, 0, stream>>>(chunk_aos, tile_words, n, g.world_words, stride, offset);
         b3k_step_select<<<tiles, 64, 0, stream>>>(tile_words, g, n, chunk_active, select);
-        b3k_step<<<tiles, 64, lds, stream>>>(tile_words, nullptr, step_scratch, g, n, dt, substeps, select, nullptr,
-            0u);
+        b3k_step<false><<<tiles, 64, lds, stream>>>(tile_words, nullptr, step_scratch, g, n, dt, substeps, select,
+            nullptr, 0u);
         /* only the stepped worlds are written back: the others are not touched */
         b3k_download<<<grid, kXposeThreads, 0, stream>>>(tile_words, chunk_aos, n, g.world_words, stride, offset,
             select);

@@ -30,6 +30,7 @@ struct B3Engine {
     bool joint_lds;          /* ... and keep the joint rows in LDS (b3d::joint_rows_fit) */
     int tile_parts;          /* workgroups per tile of the shared step (1 or 2), each with its own
                                 scratch and stage */
+    bool joint_impulses_lds; /* the one-wave step keeps the joint impulses in LDS (b3d::ji_fit) */
 };
 
 /* Waves per tile when the narrowphase is shared (two per SIMD: the shared

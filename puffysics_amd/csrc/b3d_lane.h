@@ -371,6 +371,8 @@ struct Lane {
                            every workgroup barrier with their work skipped */
     float* jl;          /* LDS joint rows + lane (shared tiles with room for
                            them, joint_rows_fit), else null */
+    float* ji;          /* LDS joint impulses + lane (the one-wave step, when
+                           they fit past the velocity rows: ji_fit), else null */
     Geometry g;
 };
 
@@ -399,6 +401,7 @@ B3D_FN Lane lane_view(uint32_t* live, uint32_t* scratch, float* vel_rows, const 
     L.scr = scratch ? scratch + (size_t)scr_tile * g.tile_scr_words + lane : nullptr;
     L.sq = scratch ? scratch + (size_t)scr_tile * g.tile_scr_words + (size_t)g.scr_words * kLanes : nullptr;
     L.jl = nullptr;
+    L.ji = nullptr;
     L.vel = vel_rows ? vel_rows + lane : nullptr;
     L.lane = lane;
     L.active = true;
@@ -692,6 +695,67 @@ B3D_FN void rec_store_masses(uint32_t* r, int flags, float ma, M3 ia, float mb, 
     }
 }
 B3D_FN uint32_t* joint_rec(const Lane& L, int j) { return L.scr + (L.g.scr_joint + j * kJointScr) * kLanes; }
+/* Per-lane rows of LDS words (stride kLanes): a joint's LDS row (JL) or
+ * impulse row (JI), word k at q[k * kLanes]. */
+B3D_FN float jlf(const float* q, int k) { return q[k * kLanes]; }
+B3D_FN V3 jl3(const float* q, int k) { return v3(q[k * kLanes], q[(k + 1) * kLanes], q[(k + 2) * kLanes]); }
+B3D_FN M3 jlm3(const float* q, int k) { M3 m; m.cx = jl3(q, k); m.cy = jl3(q, k + 3); m.cz = jl3(q, k + 6); return m; }
+B3D_FN Soft jlsoft(const float* q, int k) {
+    Soft s;
+    s.bias_rate = q[k * kLanes];
+    s.mass_scale = q[(k + 1) * kLanes];
+    s.impulse_scale = q[(k + 2) * kLanes];
+    return s;
+}
+B3D_FN void jlsf(float* q, int k, float v) { q[k * kLanes] = v; }
+B3D_FN void jls3(float* q, int k, V3 v) { jlsf(q, k, v.x); jlsf(q, k + 1, v.y); jlsf(q, k + 2, v.z); }
+B3D_FN void jlsm3(float* q, int k, M3 m) { jls3(q, k, m.cx); jls3(q, k + 3, m.cy); jls3(q, k + 6, m.cz); }
+B3D_FN void jlssoft(float* q, int k, Soft s) { jlsf(q, k, s.bias_rate); jlsf(q, k + 1, s.mass_scale); jlsf(q, k + 2, s.impulse_scale); }
+
+/* Joint impulses in LDS (the one-wave step, JI): per joint kJIWords words
+ * past the velocity rows, the accumulated impulses that the solves read and
+ * write.  The joint warm start stages them from the joint's words, which
+ * joint_impulse_writeback updates once at the end of the step; the solves'
+ * other fields come from the world and the scratch record as without it.
+ * A weld's angular impulse shares the revolute's perpendicular and spring
+ * words. */
+constexpr int JI_LIN = 0, JI_PERP = 3, JI_SPRING = 5, JI_MOTOR = 6, JI_LOWER = 7, JI_UPPER = 8, JI_ANG = 3,
+              kJIWords = 9;
+B3D_FN int ji_word(const Geometry& g) { return g.max_b * kVelWords; }
+/* The impulses fit within the one-wave step's LDS rows (kMaxLdsRows words
+ * per lane: four waves per CU). */
+B3D_FN bool ji_fit(const Geometry& g) { return g.max_j > 0 && ji_word(g) + kJIWords * g.max_j <= kMaxLdsRows; }
+B3D_FN int ji_lds_rows(const Geometry& g) {
+    int r = ji_word(g) + kJIWords * g.max_j;
+    return r > lds_rows(g) ? r : lds_rows(g);
+}
+B3D_FN float* ji_rec(const Lane& L, int j) { return L.ji + j * kJIWords * kLanes; }
+/* The LDS word of a joint's impulse word. */
+B3D_FN int ji_of(int world_word) {
+    return world_word == J_LINEAR_IMPULSE ? JI_LIN
+         : world_word == J_ANGULAR_IMPULSE ? JI_ANG
+         : world_word == J_PERP_IMPULSE ? JI_PERP
+         : world_word == J_PERP_IMPULSE + 1 ? JI_PERP + 1
+         : world_word == J_SPRING_IMPULSE ? JI_SPRING
+         : world_word == J_MOTOR_IMPULSE ? JI_MOTOR
+         : world_word == J_LOWER_IMPULSE ? JI_LOWER : JI_UPPER;
+}
+/* An accumulated impulse of joint j as a solve reads it (JI: the LDS row). */
+template <bool JI>
+B3D_FN float jimp_ld(const Lane& L, int j, int world_word) {
+    if constexpr (JI) return ji_rec(L, j)[ji_of(world_word) * kLanes];
+    else return ldf(L.w, jw(L, j, world_word));
+}
+template <bool JI>
+B3D_FN V3 jimp_ld3(const Lane& L, int j, int world_word) {
+    if constexpr (JI) {
+        const float* q = ji_rec(L, j) + ji_of(world_word) * kLanes;
+        return v3(q[0], q[kLanes], q[2 * kLanes]);
+    } else {
+        return ld3(L.w, jw(L, j, world_word));
+    }
+}
+
 B3D_FN uint32_t* body_rec(const Lane& L, int b) {
     return L.sq + (size_t)(L.g.q_body + b * kBodyRows) * kRowWords + L.sslot;
 }
@@ -2081,7 +2145,9 @@ B3D_FN void warm_start_contacts(const Lane& L, int done) {
     }
 }
 
-/* b3_warm_start_joints (06:204-239). */
+/* b3_warm_start_joints (06:204-239).  JI: also stages each joint's
+ * accumulated impulses into its LDS impulse row, for the solves. */
+template <bool JI = false>
 B3D_FN void warm_start_joints(const Lane& L) {
     int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
     const uint32_t* w = L.w;
@@ -2091,11 +2157,25 @@ B3D_FN void warm_start_joints(const Lane& L) {
         V3 rb = rot(rq4(delta_rec(L, b), BD_DQ), ld3(w, jw(L, i, J_FRAME_P_B)));
         V3 lin = ld3(w, jw(L, i, J_LINEAR_IMPULSE));
         V3 ang = ld3(w, jw(L, i, J_ANGULAR_IMPULSE));
+        if constexpr (JI) {
+            jls3(ji_rec(L, i), JI_LIN, lin);
+            jls3(ji_rec(L, i), JI_ANG, ang);       /* a weld's; a hinge's words follow */
+        }
         if (ldi(w, jw(L, i, J_TYPE)) == kJointRevolute) {
-            float axial = ldf(w, jw(L, i, J_SPRING_IMPULSE)) + ldf(w, jw(L, i, J_MOTOR_IMPULSE))
-                + ldf(w, jw(L, i, J_LOWER_IMPULSE)) - ldf(w, jw(L, i, J_UPPER_IMPULSE));
-            ang = add(scale(ld3(w, jw(L, i, J_PERP_X)), ldf(w, jw(L, i, J_PERP_IMPULSE))),
-                scale(ld3(w, jw(L, i, J_PERP_Y)), ldf(w, jw(L, i, J_PERP_IMPULSE + 1))));
+            float spring = ldf(w, jw(L, i, J_SPRING_IMPULSE)), motor = ldf(w, jw(L, i, J_MOTOR_IMPULSE));
+            float lower = ldf(w, jw(L, i, J_LOWER_IMPULSE)), upper = ldf(w, jw(L, i, J_UPPER_IMPULSE));
+            float px = ldf(w, jw(L, i, J_PERP_IMPULSE)), py = ldf(w, jw(L, i, J_PERP_IMPULSE + 1));
+            if constexpr (JI) {
+                float* q = ji_rec(L, i);
+                jlsf(q, JI_PERP, px);
+                jlsf(q, JI_PERP + 1, py);
+                jlsf(q, JI_SPRING, spring);
+                jlsf(q, JI_MOTOR, motor);
+                jlsf(q, JI_LOWER, lower);
+                jlsf(q, JI_UPPER, upper);
+            }
+            float axial = spring + motor + lower - upper;
+            ang = add(scale(ld3(w, jw(L, i, J_PERP_X)), px), scale(ld3(w, jw(L, i, J_PERP_Y)), py));
             ang = madd(ang, axial, ld3(w, jw(L, i, J_ROTATION_AXIS)));
         }
         if (is_dyn_flag(L, a)) {
@@ -2800,7 +2880,8 @@ B3D_FN JHead jhead_load(const Lane& L, int j) {
 
 /* Everything one solve of joint j reads.  Fields of disabled rows and the
  * masses of bodies that are not dynamic (exact zeros in the row) are not
- * loaded. */
+ * loaded.  JI: the accumulated impulses from the LDS impulse row. */
+template <bool JI = false>
 B3D_FN void jrow_load(const Lane& L, int j, JHead h, JRow* r) {
     const uint32_t* w = L.w;
     const uint32_t* g = joint_rec(L, j);
@@ -2824,7 +2905,7 @@ B3D_FN void jrow_load(const Lane& L, int j, JHead h, JRow* r) {
     r->ra = ld3(g, JS_RA);
     r->rb = ld3(g, JS_RB);
     r->psep = ld3(g, JS_PSEP);
-    r->lin_imp = ld3(w, jw(L, j, J_LINEAR_IMPULSE));
+    r->lin_imp = jimp_ld3<JI>(L, j, J_LINEAR_IMPULSE);
     r->pki = ldm3(g, JS_PKI);
     int fixed = f & JF_FIXED;
     if (f & JF_WELD) {
@@ -2834,7 +2915,7 @@ B3D_FN void jrow_load(const Lane& L, int j, JHead h, JRow* r) {
             r->ang_hz = ldf(w, jw(L, j, J_ANGULAR_HERTZ));
             r->ang_spring = ldsoft(w, jw(L, j, J_ANGULAR_SPRING));
             r->cv = ld3(g, JS_CV);
-            r->ang_imp = ld3(w, jw(L, j, J_ANGULAR_IMPULSE));
+            r->ang_imp = jimp_ld3<JI>(L, j, J_ANGULAR_IMPULSE);
             r->ang_mass = ldm3(w, jw(L, j, J_ANGULAR_MASS));
         }
         return;
@@ -2848,8 +2929,8 @@ B3D_FN void jrow_load(const Lane& L, int j, JHead h, JRow* r) {
     r->kinv = ldf(g, JS_KINV);
     r->relx = ldf(g, JS_RELX);
     r->rely = ldf(g, JS_RELY);
-    r->perp_imp.x = ldf(w, jw(L, j, J_PERP_IMPULSE));
-    r->perp_imp.y = ldf(w, jw(L, j, J_PERP_IMPULSE + 1));
+    r->perp_imp.x = jimp_ld<JI>(L, j, J_PERP_IMPULSE);
+    r->perp_imp.y = jimp_ld<JI>(L, j, J_PERP_IMPULSE + 1);
     if (f & (JF_SPRING | JF_MOTOR | JF_LIMIT)) {
         r->tw = ldf(g, JS_TW);
         r->axial_mass = ldf(w, jw(L, j, J_AXIAL_MASS));
@@ -2861,19 +2942,19 @@ B3D_FN void jrow_load(const Lane& L, int j, JHead h, JRow* r) {
     if (f & JF_SPRING) {
         r->target = ldf(w, jw(L, j, J_TARGET_ANGLE));
         r->spring_soft = ldsoft(w, jw(L, j, J_SPRING_SOFTNESS));
-        r->spring_imp = ldf(w, jw(L, j, J_SPRING_IMPULSE));
+        r->spring_imp = jimp_ld<JI>(L, j, J_SPRING_IMPULSE);
     }
     if (f & JF_MOTOR) {
         r->speed = ldf(w, jw(L, j, J_MOTOR_SPEED));
-        r->motor_imp = ldf(w, jw(L, j, J_MOTOR_IMPULSE));
+        r->motor_imp = jimp_ld<JI>(L, j, J_MOTOR_IMPULSE);
     }
     if (f & (JF_MOTOR | JF_LIMIT)) {
         r->lower = ldf(w, jw(L, j, J_LOWER_ANGLE));
         r->upper = ldf(w, jw(L, j, J_UPPER_ANGLE));
     }
     if (f & JF_LIMIT) {
-        r->lower_imp = ldf(w, jw(L, j, J_LOWER_IMPULSE));
-        r->upper_imp = ldf(w, jw(L, j, J_UPPER_IMPULSE));
+        r->lower_imp = jimp_ld<JI>(L, j, J_LOWER_IMPULSE);
+        r->upper_imp = jimp_ld<JI>(L, j, J_UPPER_IMPULSE);
     }
 }
 
@@ -2904,30 +2985,43 @@ B3D_FN bool joint_rows_fit(const Geometry& g) {
     return g.max_j > 0 && joint_lds_word(g) + joint_lds_words(g) <= kSharedLdsWordsMax;
 }
 B3D_FN float* jl_rec(const Lane& L, int j) { return L.jl + j * kJLWords * kLanes; }
-B3D_FN float jlf(const float* q, int k) { return q[k * kLanes]; }
-B3D_FN V3 jl3(const float* q, int k) { return v3(q[k * kLanes], q[(k + 1) * kLanes], q[(k + 2) * kLanes]); }
-B3D_FN M3 jlm3(const float* q, int k) { M3 m; m.cx = jl3(q, k); m.cy = jl3(q, k + 3); m.cz = jl3(q, k + 6); return m; }
-B3D_FN Soft jlsoft(const float* q, int k) {
-    Soft s;
-    s.bias_rate = q[k * kLanes];
-    s.mass_scale = q[(k + 1) * kLanes];
-    s.impulse_scale = q[(k + 2) * kLanes];
-    return s;
-}
-B3D_FN void jlsf(float* q, int k, float v) { q[k * kLanes] = v; }
-B3D_FN void jls3(float* q, int k, V3 v) { jlsf(q, k, v.x); jlsf(q, k + 1, v.y); jlsf(q, k + 2, v.z); }
-B3D_FN void jlsm3(float* q, int k, M3 m) { jls3(q, k, m.cx); jls3(q, k + 3, m.cy); jls3(q, k + 6, m.cz); }
-B3D_FN void jlssoft(float* q, int k, Soft s) { jlsf(q, k, s.bias_rate); jlsf(q, k + 1, s.mass_scale); jlsf(q, k + 2, s.impulse_scale); }
-/* An accumulated impulse of joint j: to the LDS row (JL) or the joint's words. */
-template <bool JL>
+/* An accumulated impulse of joint j: to the LDS row (JL), the LDS impulse
+ * row (JI) or the joint's words. */
+template <bool JL, bool JI = false>
 B3D_FN void jimp_store(const Lane& L, int j, int world_word, int lds_word, float v) {
     if constexpr (JL) jlsf(jl_rec(L, j), lds_word, v);
+    else if constexpr (JI) jlsf(ji_rec(L, j), ji_of(world_word), v);
     else stf(L.w, jw(L, j, world_word), v);
 }
-template <bool JL>
+template <bool JL, bool JI = false>
 B3D_FN void jimp_store3(const Lane& L, int j, int world_word, int lds_word, V3 v) {
     if constexpr (JL) jls3(jl_rec(L, j), lds_word, v);
+    else if constexpr (JI) jls3(ji_rec(L, j), ji_of(world_word), v);
     else st3(L.w, jw(L, j, world_word), v);
+}
+/* The LDS impulses back to the joints' words: those the solves update (a
+ * disabled row's impulse keeps the world's own value). */
+B3D_FN void joint_impulse_writeback(const Lane& L) {
+    int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
+    uint32_t* w = L.w;
+    for (int j = 0; j < nj; j++) {
+        const float* q = ji_rec(L, j);
+        int info = ldi(joint_rec(L, j), JS_INFO);
+        st3(w, jw(L, j, J_LINEAR_IMPULSE), jl3(q, JI_LIN));
+        if (info & JF_FIXED) continue;
+        if (info & JF_WELD) {
+            st3(w, jw(L, j, J_ANGULAR_IMPULSE), jl3(q, JI_ANG));
+            continue;
+        }
+        stf(w, jw(L, j, J_PERP_IMPULSE), jlf(q, JI_PERP));
+        stf(w, jw(L, j, J_PERP_IMPULSE + 1), jlf(q, JI_PERP + 1));
+        if (info & JF_SPRING) stf(w, jw(L, j, J_SPRING_IMPULSE), jlf(q, JI_SPRING));
+        if (info & JF_MOTOR) stf(w, jw(L, j, J_MOTOR_IMPULSE), jlf(q, JI_MOTOR));
+        if (info & JF_LIMIT) {
+            stf(w, jw(L, j, J_LOWER_IMPULSE), jlf(q, JI_LOWER));
+            stf(w, jw(L, j, J_UPPER_IMPULSE), jlf(q, JI_UPPER));
+        }
+    }
 }
 
 /* The step's joint rows to LDS (wave 0, after prepare_joints): each row as
@@ -3181,7 +3275,7 @@ B3D_FN void jrow_lds(const Lane& L, int j, const JGeo& g, JRow* r) {
 
 /* Point rows shared by weld and revolute (06:257-282), with the anchors,
  * separation and inverted mass of the current delta state. */
-template <bool JL>
+template <bool JL, bool JI = false>
 B3D_FN void solve_point(const Lane& L, int j, const JRow& r, V3* va, V3* wa, V3* vb, V3* wb, Soft soft,
         int use_bias) {
     V3 cdot = sub(add(*vb, cross(*wb, r.rb)), add(*va, cross(*wa, r.ra)));
@@ -3196,7 +3290,7 @@ B3D_FN void solve_point(const Lane& L, int j, const JRow& r, V3* va, V3* wa, V3*
      * inverse taken once per delta state (joint_geometry) */
     V3 bsol = mv(r.pki, add(cdot, bias));
     V3 impulse = msub(scale(bsol, -mscale), iscale, r.lin_imp);
-    jimp_store3<JL>(L, j, J_LINEAR_IMPULSE, JL_LIN_IMP, add(r.lin_imp, impulse));
+    jimp_store3<JL, JI>(L, j, J_LINEAR_IMPULSE, JL_LIN_IMP, add(r.lin_imp, impulse));
     *va = msub(*va, r.ma, impulse);
     *wa = sub(*wa, mv(r.ia, cross(r.ra, impulse)));
     *vb = madd(*vb, r.mb, impulse);
@@ -3204,7 +3298,7 @@ B3D_FN void solve_point(const Lane& L, int j, const JRow& r, V3* va, V3* wa, V3*
 }
 
 /* b3_solve_weld (06:285-332). */
-template <bool JL>
+template <bool JL, bool JI = false>
 B3D_FN void solve_weld(const Lane& L, int j, const JRow& r, int use_bias) {
     V3 va = vlin(L, r.a), wa = vang(L, r.a), vb = vlin(L, r.b), wb = vang(L, r.b);
     if (!(r.info & JF_FIXED)) {
@@ -3217,12 +3311,12 @@ B3D_FN void solve_weld(const Lane& L, int j, const JRow& r, int use_bias) {
         }
         V3 cdot = sub(wb, wa);
         V3 impulse = msub(scale(mv(r.ang_mass, add(cdot, bias)), -mscale), iscale, r.ang_imp);
-        jimp_store3<JL>(L, j, J_ANGULAR_IMPULSE, JL_ANG_IMP, add(r.ang_imp, impulse));
+        jimp_store3<JL, JI>(L, j, J_ANGULAR_IMPULSE, JL_ANG_IMP, add(r.ang_imp, impulse));
         wa = sub(wa, mv(r.ia, impulse));
         wb = add(wb, mv(r.ib, impulse));
     }
     int lin_bias = use_bias || r.lin_hz > 0.0f;
-    solve_point<JL>(L, j, r, &va, &wa, &vb, &wb, r.lin_spring, lin_bias);
+    solve_point<JL, JI>(L, j, r, &va, &wa, &vb, &wb, r.lin_spring, lin_bias);
     if (is_dyn_flag(L, r.a)) {
         set_vlin(L, r.a, va);
         set_vang(L, r.a, wa);
@@ -3249,7 +3343,7 @@ B3D_FN float limit_impulse(float c, float cdot, float inv_h, int use_bias, Soft 
 
 /* b3_solve_revolute (06:436-642): spring, motor, lower and upper limit,
  * two perpendicular angular rows, then the point rows. */
-template <bool JL>
+template <bool JL, bool JI = false>
 B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float inv_h, int use_bias) {
     V3 va = vlin(L, r.a), wa = vang(L, r.a), vb = vlin(L, r.b), wb = vang(L, r.b);
     V3 axis = r.axis;
@@ -3272,7 +3366,7 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
             nimp = clampf(nimp, -maxp, maxp);
         }
         dimp = nimp - old;
-        jimp_store<JL>(L, j, J_SPRING_IMPULSE, JL_SPRING_IMP, nimp);
+        jimp_store<JL, JI>(L, j, J_SPRING_IMPULSE, JL_SPRING_IMP, nimp);
         wa = msub(wa, dimp, ia_ax);
         wb = madd(wb, dimp, ib_ax);
     }
@@ -3283,7 +3377,7 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
             if (tw <= r.lower + 0.01f && r.speed < 0.0f) blocked = 1;
         }
         if (blocked) {
-            jimp_store<JL>(L, j, J_MOTOR_IMPULSE, JL_MOTOR_IMP, 0.0f);
+            jimp_store<JL, JI>(L, j, J_MOTOR_IMPULSE, JL_MOTOR_IMP, 0.0f);
         } else {
             float old = r.motor_imp;
             float cdot = dot(sub(wb, wa), axis) - r.speed;
@@ -3292,7 +3386,7 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
             float maxp = r.max_torque * h;
             nimp = clampf(nimp, -maxp, maxp);
             dimp = nimp - old;
-            jimp_store<JL>(L, j, J_MOTOR_IMPULSE, JL_MOTOR_IMP, nimp);
+            jimp_store<JL, JI>(L, j, J_MOTOR_IMPULSE, JL_MOTOR_IMP, nimp);
             wa = msub(wa, dimp, ia_ax);
             wb = madd(wb, dimp, ib_ax);
         }
@@ -3300,13 +3394,13 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
     if (en_limit && !fixed) {
         float old = r.lower_imp;
         float lo = limit_impulse(tw - r.lower, dot(sub(wb, wa), axis), inv_h, use_bias, r.soft, axial_mass, old);
-        jimp_store<JL>(L, j, J_LOWER_IMPULSE, JL_LOWER_IMP, lo);
+        jimp_store<JL, JI>(L, j, J_LOWER_IMPULSE, JL_LOWER_IMP, lo);
         float dimp = lo - old;
         wa = msub(wa, dimp, ia_ax);
         wb = madd(wb, dimp, ib_ax);
         old = r.upper_imp;
         float up = limit_impulse(r.upper - tw, dot(sub(wa, wb), axis), inv_h, use_bias, r.soft, axial_mass, old);
-        jimp_store<JL>(L, j, J_UPPER_IMPULSE, JL_UPPER_IMP, up);
+        jimp_store<JL, JI>(L, j, J_UPPER_IMPULSE, JL_UPPER_IMP, up);
         dimp = up - old;
         wa = madd(wa, dimp, ia_ax);
         wb = msub(wb, dimp, ib_ax);
@@ -3338,13 +3432,13 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
         V2 dimp;
         dimp.x = -mscale * sol.x - iscale * r.perp_imp.x;
         dimp.y = -mscale * sol.y - iscale * r.perp_imp.y;
-        jimp_store<JL>(L, j, J_PERP_IMPULSE, JL_PERP_IMP, r.perp_imp.x + dimp.x);
-        jimp_store<JL>(L, j, J_PERP_IMPULSE + 1, JL_PERP_IMP + 1, r.perp_imp.y + dimp.y);
+        jimp_store<JL, JI>(L, j, J_PERP_IMPULSE, JL_PERP_IMP, r.perp_imp.x + dimp.x);
+        jimp_store<JL, JI>(L, j, J_PERP_IMPULSE + 1, JL_PERP_IMP + 1, r.perp_imp.y + dimp.y);
         V3 ang = add(scale(r.px, dimp.x), scale(r.py, dimp.y));
         wa = sub(wa, mv(r.ia, ang));
         wb = add(wb, mv(r.ib, ang));
     }
-    solve_point<JL>(L, j, r, &va, &wa, &vb, &wb, r.soft, use_bias);
+    solve_point<JL, JI>(L, j, r, &va, &wa, &vb, &wb, r.soft, use_bias);
     if (is_dyn_flag(L, r.a)) {
         set_vlin(L, r.a, va);
         set_vang(L, r.a, wa);
@@ -3361,6 +3455,7 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
  * select which fields to load) fetched one solve ahead: a second row in
  * flight during a solve costs more in registers than the one round trip it
  * would hide. */
+template <bool JI = false>
 B3D_FN void solve_joints(const Lane& L, float h, float inv_h, int use_bias) {
     int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
     if (nj <= 0) return;
@@ -3369,11 +3464,11 @@ B3D_FN void solve_joints(const Lane& L, float h, float inv_h, int use_bias) {
     int j = 0;
     for (int t = 0; t < total; t++) {
         JRow cur;
-        jrow_load(L, j, head, &cur);
+        jrow_load<JI>(L, j, head, &cur);
         int jn = j + 1 == nj ? 0 : j + 1;
         if (t + 1 < total) head = jhead_load(L, jn);
-        if (cur.info & JF_WELD) solve_weld<false>(L, j, cur, use_bias);
-        else solve_revolute<false>(L, j, cur, h, inv_h, use_bias);
+        if (cur.info & JF_WELD) solve_weld<false, JI>(L, j, cur, use_bias);
+        else solve_revolute<false, JI>(L, j, cur, h, inv_h, use_bias);
         j = jn;
     }
 }
@@ -3669,9 +3764,12 @@ B3D_FN void integrate_velocities_law(const Lane& L, float h, const Law& law) {
 /* One world's b3_step (09_step.inl:148-264, default configuration), with
  * the force law `law` in the B3_USER_FORCES hook.  Body velocities are
  * staged in the velocity rows after contact generation (which uses the
- * same rows for clip polygons) and written back at the end. */
-template <bool Masks = false, class Law, bool JL = false>
+ * same rows for clip polygons) and written back at the end.  JL: the joint
+ * rows in LDS (shared tiles); JI: the joint impulses in LDS (one wave per
+ * tile, L.ji), staged by the joint warm start and written back at the end. */
+template <bool Masks = false, class Law, bool JL = false, bool JI = false>
 B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
+    static_assert(!(JL && JI), "joint rows and joint impulses are two layouts of the same LDS words");
     if (!(dt > 0.0f)) return;
     Lane L = L0;
     L.sslot = wave_rank(L);
@@ -3731,7 +3829,7 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
         prepare_joints(L, h);
         if (wave_any(L, !warm_done)) warm_start_contacts(L, warm_done);
     }
-    if (act) warm_start_joints(L);
+    if (act) warm_start_joints<JI>(L);
     /* a shared tile's waves split the first joint geometry, after the warm
      * start has read the previous step's hinge rows, which it overwrites */
     if (L.staged) B3D_BARRIER();
@@ -3752,7 +3850,7 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
         if (L.staged) solve_contacts_leveled(L, inv_h, contact_speed, 1, cs, ss, nlev);
         else solve_contacts(L, inv_h, contact_speed, 1, cs, ss);
         if constexpr (JL) solve_joints_leveled(L, h, inv_h, 1, njlev);
-        else if (act) solve_joints(L, h, inv_h, 1);
+        else if (act) solve_joints<JI>(L, h, inv_h, 1);
         if (L.staged) B3D_BARRIER();   /* the joints' velocities */
         if (act) integrate_positions(L, h, inv_dt, share, stride);
         if (L.staged) B3D_BARRIER();   /* the delta poses */
@@ -3761,7 +3859,7 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
         else solve_contacts(L, inv_h, contact_speed, 0, cs, ss);
         if constexpr (JL) solve_joints_leveled(L, h, inv_h, 0, njlev);
         if (act) {
-            if constexpr (!JL) solve_joints(L, h, inv_h, 0);
+            if constexpr (!JL) solve_joints<JI>(L, h, inv_h, 0);
             if (rest_wave) apply_restitution(L, rest_threshold);
         }
     }
@@ -3771,15 +3869,17 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
     if (act) {
         contact_writeback(L, share, stride);
         if constexpr (JL) joint_writeback(L, share, stride);
+        if constexpr (JI) joint_impulse_writeback(L);
         finalize(L, share, stride);
         vel_store(L, share, stride);
     }
 }
 
-/* b3_step without a hook; JL: the joint rows in LDS (L.jl, shared tiles). */
-template <bool Masks = false, bool JL = false>
+/* b3_step without a hook; JL: the joint rows in LDS (L.jl, shared tiles);
+ * JI: the joint impulses in LDS (L.ji, one wave per tile). */
+template <bool Masks = false, bool JL = false, bool JI = false>
 B3D_FN void step_world(const Lane& L, float dt, int substeps) {
-    step_world<Masks, NoForces, JL>(L, dt, substeps, NoForces());
+    step_world<Masks, NoForces, JL, JI>(L, dt, substeps, NoForces());
 }
 
 /* A helper wave of a shared-narrowphase tile after its narrowphase share:

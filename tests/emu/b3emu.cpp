@@ -81,18 +81,30 @@ static Lane lane_of(uint32_t* tiles, uint32_t* scratch, float* vel, const Geomet
     return lane_view(tiles, scratch, vel, g, w / kLanes, w % kLanes, g_opts);
 }
 
+/* Joint impulses in LDS for emu_step, as b3k_step<true> keeps them: -1 as
+ * the device chooses (ji_fit), 0 never, 1 for every world with joints
+ * (host memory has no LDS limit). */
+static int g_joint_impulses = 0;
+void emu_set_joint_impulses_lds(int mode) { g_joint_impulses = mode; }
+
 void emu_step(uint32_t* tiles, int count, unsigned long long sig, float dt, int substeps,
         const unsigned char* step_mask) {
     Geometry g;
     size_t wb;
     if (!geometry_of(sig, &g, &wb)) return;
     int ntiles = (count + kLanes - 1) / kLanes;
+    bool ji = g_joint_impulses < 0 ? ji_fit(g) : (g_joint_impulses > 0 && g.max_j > 0);
     std::vector<uint32_t> scratch((size_t)ntiles * g.tile_scr_words);
-    std::vector<float> vel((size_t)lds_rows(g) * kLanes);
+    std::vector<float> vel((size_t)(ji ? ji_lds_rows(g) : lds_rows(g)) * kLanes);
     for (int w = 0; w < count; w++) {
         if (step_mask && !step_mask[w]) continue;
         Lane L = lane_of(tiles, scratch.data(), vel.data(), g, w);
-        step_world(L, dt, substeps);
+        if (ji) {
+            L.ji = vel.data() + (size_t)ji_word(g) * kLanes + w % kLanes;
+            step_world<false, false, true>(L, dt, substeps);
+        } else {
+            step_world(L, dt, substeps);
+        }
     }
 }
 

@@ -201,3 +201,56 @@ def test_shared_tile_path_on_the_host_feature_worlds(masks, joint_lds):
         lib.emu_set_joint_lds(-1)
     bad = diff_words(emu_.worlds(), ref, CUSTOM_SIG)
     assert len(bad) == 0, "%d differing words, first %s" % (len(bad), bad[:4].tolist())
+
+
+def _with_joint_impulses_lds(mode, fn):
+    """Run fn with emu_step keeping the joint impulses in LDS (mode -1: as
+    the one-wave kernel chooses, 1: always), then restore the default."""
+    import ctypes as C
+    from b3test import emu
+    lib = emu()
+    lib.emu_set_joint_impulses_lds.argtypes = [C.c_int]
+    lib.emu_set_joint_impulses_lds(mode)
+    try:
+        return fn()
+    finally:
+        lib.emu_set_joint_impulses_lds(0)
+
+
+@pytest.mark.parametrize("scene,count,steps", [(3, 70, 25), (5, 130, 40)])
+def test_lane_code_joint_impulses_in_lds(scene, count, steps):
+    """The one-wave step with the joints' accumulated impulses in LDS (staged
+    by the joint warm start, written back at the end of the step), as the
+    device runs the arm and chain scenes: bit-exact against the oracle."""
+    worlds = scenes.build(scene, count)
+    initial = clone(worlds)
+    e = EmuBatch(scene, worlds)
+    _with_joint_impulses_lds(-1, lambda: e.run(0, steps))
+    ref = clone(worlds)
+    oracle_run(scene, ref, initial, 0, steps)
+    bad = diff_words(e.worlds(), ref, scenes.SCENES[scene].sig)
+    assert len(bad) == 0, "first differences (world, word): %s" % bad[:10].tolist()
+    assert np.abs(ref["joints"]["motor_impulse"]).max() > 0
+
+
+def test_lane_code_joint_impulses_in_lds_every_feature():
+    """Welds (rigid and soft), spring-only and fixed hinges with the
+    impulses in LDS (forced: these worlds' joints do not fit the device's
+    LDS rows): bit-exact against the oracle over 60 steps with a mask."""
+    from b3test import EmuSig, feature_worlds, oracle_step_batch
+    from puffysics_amd.creation import CUSTOM_SIG
+    worlds = feature_worlds(40)
+    ref = clone(worlds)
+    emu = EmuSig(CUSTOM_SIG, worlds)
+    active = (np.arange(40) % 5 != 2).astype(np.uint8)
+
+    def run():
+        for t in range(60):
+            act = active if t % 3 == 0 else None
+            oracle_step_batch(ref, CUSTOM_SIG, 1.0 / 60.0, 4, act)
+            emu.step(1.0 / 60.0, 4, act)
+
+    _with_joint_impulses_lds(1, run)
+    bad = diff_words(emu.worlds(), ref, CUSTOM_SIG)
+    assert len(bad) == 0, bad[:10].tolist()
+    assert np.abs(ref["joints"]["angular_impulse"]["x"][:, 0]).max() > 0
