@@ -60,3 +60,35 @@ def test_what_the_mathematics_fixes():
     sn, cn = _engine_sincos(-y)
     assert (sn == -sp).all() and (cn == cp).all()               # odd and even
     assert np.abs(sp.astype(np.float64) ** 2 + cp.astype(np.float64) ** 2 - 1).max() < 3e-7
+
+
+def test_two_over_pi_table_is_two_over_pi():
+    """The Payne-Hanek reduction's table (two_over_pi_window in b3d_math.h)
+    against 2/pi computed here from Machin's formula: window i >= 3 holds
+    bits 8 (i - 3) .. 8 (i - 3) + 31 of 2/pi's binary fraction, windows 0-2
+    its first 8, 16 and 24 bits."""
+    import re
+    from b3test import ROOT
+
+    def arctan_inv(x, bits):                    # arctan(1/x) * 2^bits
+        one = 1 << (bits + 20)
+        total, term, k, sign = 0, one // x, 1, 1
+        while term:
+            total += sign * (term // k)
+            term //= x * x
+            k += 2
+            sign = -sign
+        return total >> 20
+
+    bits = 1200
+    pi = 4 * (4 * arctan_inv(5, bits) - arctan_inv(239, bits))
+    frac = bin((2 << (2 * bits)) // pi)[2:].zfill(bits)
+    want = [int(frac[:8], 2), int(frac[:16], 2), int(frac[:24], 2)] + [int(frac[8 * i:8 * i + 32], 2)
+                                                                      for i in range(21)]
+    src = open(os.path.join(ROOT, "puffysics_amd", "csrc", "b3d_math.h")).read()
+    body = src[src.index("two_over_pi_window"):]
+    body = body[body.index("{", body.index("w[24]")) + 1:body.index("};")]
+    got = [int(v, 16) for v in re.findall(r"0x[0-9a-fA-F]+", body)]
+    assert got == want
+    assert float.fromhex("0x1.45f306dc9c883p-1") == 2 / math.pi      # hpi_inv / 2^24
+    assert float.fromhex("0x1.921fb54442d18p+0") == math.pi / 2
