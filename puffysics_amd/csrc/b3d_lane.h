@@ -374,6 +374,14 @@ struct Lane {
     float* ji;          /* LDS joint impulses + lane (the one-wave step, when
                            they fit past the velocity rows: ji_fit), else null */
     Geometry g;
+    /* The world's header counts, read once per step (a read of the header
+     * word sits on the critical path of every phase that loops over them):
+     * with `counted`, nb and nj are the clamped body and joint counts; with
+     * `contacts_counted`, nc is the raw contact-count word as contact
+     * generation left it.  Without the flags the accessors read the world. */
+    bool counted = false;
+    bool contacts_counted = false;
+    int nb = 0, nj = 0, nc = 0;
 };
 
 /* Option: also write the prepared solver fields of every new contact
@@ -556,7 +564,23 @@ B3D_FN int is_dyn_flag(const Lane& L, int b) {
     return (__builtin_bit_cast(uint32_t, L.vel[(b * kVelWords + 6) * kLanes]) & kFlagDynamic) != 0;
 }
 
-B3D_FN int body_count(const Lane& L) { return clampi(ldi(L.w, H_BODY_COUNT), 0, L.g.max_b); }
+B3D_FN int body_count(const Lane& L) { return L.counted ? L.nb : clampi(ldi(L.w, H_BODY_COUNT), 0, L.g.max_b); }
+B3D_FN int joint_count(const Lane& L) { return L.counted ? L.nj : clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j); }
+/* the contact-count word, unclamped */
+B3D_FN int contact_count_word(const Lane& L) { return L.contacts_counted ? L.nc : ldi(L.w, H_CONTACT_COUNT); }
+/* Reads the header counts into the lane (an idle lane of a shared tile,
+ * which runs no phase that reads them, keeps zeros). */
+B3D_FN void count_bodies_and_joints(Lane& L) {
+    if (L.active) {
+        L.nb = body_count(L);
+        L.nj = joint_count(L);
+    }
+    L.counted = true;
+}
+B3D_FN void count_contacts(Lane& L) {
+    if (L.active) L.nc = ldi(L.w, H_CONTACT_COUNT);
+    L.contacts_counted = true;
+}
 
 /* The velocity rows back to the bodies (the rows are filled by
  * body_prepass); bodies first, first + stride, ... (a shared tile's waves
@@ -1675,7 +1699,7 @@ B3D_FN int tile_levels(const Lane& L) {
 constexpr int kPrepChunk = 2;
 B3D_FN int prepare_contacts(const Lane& L, Soft cs, Soft ss, int first = 0, int stride = 1) {
     uint32_t* w = L.w;
-    int cc = ldi(w, H_CONTACT_COUNT);
+    int cc = contact_count_word(L);
     const float inv_tau = 1.0f / kSpeculative;
     const int keep = (L.opts & kKeepSolverFields) != 0;
     /* a shared tile prepares its contacts in parallel (chunks first,
@@ -1908,7 +1932,7 @@ B3D_FN int prepare_contacts(const Lane& L, Soft cs, Soft ss, int first = 0, int 
  * order, then a counting sort of the contacts by level into the entries. */
 constexpr int kSchedChunk = 8;
 B3D_FN void sched_build(const Lane& L) {
-    int cc = clampi(ldi(L.w, H_CONTACT_COUNT), 0, L.g.max_c);
+    int cc = clampi(contact_count_word(L), 0, L.g.max_c);
     int nb = body_count(L);
     for (int b = 0; b < nb; b++) sch_set(L, sch_last(L, b), 0);
     for (int lev = 0; lev <= cc; lev++) sch_set(L, sch_p(L, lev), 0);
@@ -1966,7 +1990,7 @@ B3D_FN void sched_build(const Lane& L) {
 /* b3_prepare_joints (06_joints.inl:161-202), plus the hinge axis through
  * each inverse inertia, which is fixed for the step. */
 B3D_FN void prepare_joints(const Lane& L, float h, int first = 0, int stride = 1) {
-    int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
+    int nj = joint_count(L);
     uint32_t* w = L.w;
     /* chunks of kPrepChunk joints first, first + stride, ... (a shared
      * tile's waves split them) */
@@ -2079,7 +2103,7 @@ B3D_FN void prepare_joints(const Lane& L, float h, int first = 0, int stride = 1
  * whose warm start ran inside prepare_contacts (`done`) only take part in
  * the record slots' ranks. */
 B3D_FN void warm_start_contacts(const Lane& L, int done) {
-    int cc = ldi(L.w, H_CONTACT_COUNT);
+    int cc = contact_count_word(L);
     for (int c0 = 0; c0 < cc; c0 += kPrepChunk) {
         CHead hd[kPrepChunk];
 #pragma unroll
@@ -2149,7 +2173,7 @@ B3D_FN void warm_start_contacts(const Lane& L, int done) {
  * accumulated impulses into its LDS impulse row, for the solves. */
 template <bool JI = false>
 B3D_FN void warm_start_joints(const Lane& L) {
-    int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
+    int nj = joint_count(L);
     const uint32_t* w = L.w;
     for (int i = 0; i < nj; i++) {
         int a = ldi(w, jw(L, i, J_BODY_A)), b = ldi(w, jw(L, i, J_BODY_B));
@@ -2220,7 +2244,7 @@ B3D_FN void delta_geometry(const Lane& L) { joint_geometry(L); }
  * (a shared tile's waves split them). */
 B3D_FN void joint_geometry(const Lane& L, int first, int stride) {
     uint32_t* w = L.w;
-    int nj = clampi(ldi(w, H_JOINT_COUNT), 0, L.g.max_j);
+    int nj = joint_count(L);
     for (int j0 = first; j0 < nj; j0 += kPrepChunk * stride) {
         int a[kPrepChunk], b[kPrepChunk], info[kPrepChunk];
 #pragma unroll
@@ -2556,7 +2580,7 @@ B3D_FN void crow_solve(const Lane& L, int c, CRow& r, float inv_h, float contact
  * and the head of row c+3 while row c+2 loads.  The one-wave step runs
  * large batches, so the rows are streamed (qus). */
 B3D_FN void solve_contacts(const Lane& L, float inv_h, float contact_speed, int use_bias, Soft cs, Soft ss) {
-    int cc = ldi(L.w, H_CONTACT_COUNT);
+    int cc = contact_count_word(L);
     if (cc <= 0) return;
     int relax = !use_bias;
     CHead h = rhead_load(L, 0);
@@ -2743,7 +2767,7 @@ B3D_FN void warm_contacts_leveled(const Lane& L, int nlev) {
 
 /* b3_apply_restitution (08:439-480). */
 B3D_FN void apply_restitution(const Lane& L, float threshold) {
-    int cc = ldi(L.w, H_CONTACT_COUNT);
+    int cc = contact_count_word(L);
     for (int c = 0; c < cc; c++) {
         CHead hd = rhead_load(L, c);
         int ps[kMaxManifold];
@@ -2796,7 +2820,7 @@ B3D_FN void apply_restitution(const Lane& L, float threshold) {
  * world's contact rows (the warm-start cache of the next step). */
 B3D_FN void contact_writeback(const Lane& L, int first = 0, int stride = 1) {
     uint32_t* w = L.w;
-    int cc = ldi(w, H_CONTACT_COUNT);
+    int cc = contact_count_word(L);
     for (int c0 = first * kChunk; c0 < cc; c0 += stride * kChunk) {
         CHead hd[kChunk];
 #pragma unroll
@@ -3002,7 +3026,7 @@ B3D_FN void jimp_store3(const Lane& L, int j, int world_word, int lds_word, V3 v
 /* The LDS impulses back to the joints' words: those the solves update (a
  * disabled row's impulse keeps the world's own value). */
 B3D_FN void joint_impulse_writeback(const Lane& L) {
-    int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
+    int nj = joint_count(L);
     uint32_t* w = L.w;
     for (int j = 0; j < nj; j++) {
         const float* q = ji_rec(L, j);
@@ -3065,7 +3089,7 @@ B3D_FN void jl_stage_row(const Lane& L, int j, const JRow& r) {
 /* Two joints at a time: both rows' loads in flight before either is staged;
  * pairs first, first + stride, ... (a shared tile's waves split them). */
 B3D_FN void stage_joint_rows(const Lane& L, int first = 0, int stride = 1) {
-    int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
+    int nj = joint_count(L);
     for (int j0 = 2 * first; j0 < nj; j0 += 2 * stride) {
         JHead hd[2];
 #pragma unroll
@@ -3084,7 +3108,7 @@ B3D_FN void stage_joint_rows(const Lane& L, int first = 0, int stride = 1) {
 /* The LDS rows' impulses back to the joints' words (the words the solves
  * update; a disabled row's impulse is the world's own value, unchanged). */
 B3D_FN void joint_writeback(const Lane& L, int first = 0, int stride = 1) {
-    int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
+    int nj = joint_count(L);
     uint32_t* w = L.w;
     for (int j = first; j < nj; j += stride) {
         const float* q = jl_rec(L, j);
@@ -3158,7 +3182,7 @@ B3D_FN int joint_levels_scan(const Lane& L, int nj, int nb, int place) {
     return nlev;
 }
 B3D_FN void joint_sched_build(const Lane& L) {
-    int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
+    int nj = joint_count(L);
     int nb = body_count(L);
     int total = kJointIters * nj;
     for (int lev = 1; lev <= total; lev++) jsch_set(L, jsch_p(L, lev), 0);
@@ -3457,7 +3481,7 @@ B3D_FN void solve_revolute(const Lane& L, int j, const JRow& r, float h, float i
  * would hide. */
 template <bool JI = false>
 B3D_FN void solve_joints(const Lane& L, float h, float inv_h, int use_bias) {
-    int nj = clampi(ldi(L.w, H_JOINT_COUNT), 0, L.g.max_j);
+    int nj = joint_count(L);
     if (nj <= 0) return;
     int total = (use_bias ? kJointIters : kRelaxIters) * nj;
     JHead head = jhead_load(L, 0);
@@ -3791,6 +3815,8 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
     const bool act = L.active;
 
     find_contacts<Masks>(L);
+    count_bodies_and_joints(L);
+    count_contacts(L);
     /* restitution runs in every lane of a wave where some world has it */
     const bool rest_wave = wave_any(L, act && (ldi(L.scr + L.g.scr_flags * kLanes, 0) & kLaneRestitution) != 0);
     /* a shared tile's waves split the body work (sweep_helper does its
@@ -3903,8 +3929,10 @@ B3D_FN void sweep_helper(const Lane& L0, float dt, int substeps) {
     Soft cs = make_soft(hertz, damping, h);
     Soft ss = make_soft(2.0f * hertz, 0.5f * damping, h);
     float contact_speed = ldf(L.w, H_CONTACT_SPEED);
+    count_bodies_and_joints(L);
     if (L.active) body_prepass(L, h, L.st.wave, L.st.waves);   /* with the velocity rows */
     B3D_BARRIER();                 /* the velocities and body records are staged */
+    count_contacts(L);             /* wave 0 wrote the count before the barrier */
     if (L.active) {
         /* the contacts split over the waves but wave 0, which levels them */
         prepare_contacts(L, cs, ss, L.st.wave - 1, L.st.waves - 1);
