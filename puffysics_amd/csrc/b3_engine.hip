@@ -483,12 +483,19 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
             e->lds_shared_bytes = shared_lds;
             e->shared_masks = shared_masks(g);
             e->joint_lds = joint_lds;
-            /* Worlds of many shapes (those whose candidate search uses the
-             * overlap masks) step 32 to a workgroup when the CUs allow: the
-             * narrowphase and the sweeps then take the union of fewer
-             * worlds' code paths per step of their loops, on twice the CUs
-             * (the bin at 4,096 worlds: 0.84 -> 0.72 ms). */
-            if (e->shared_masks && 2 * e->tiles <= cus) e->tile_parts = 2;
+            /* Contact-bound worlds step fewer than 64 to a workgroup when the
+             * CUs allow: the narrowphase and the sweeps then take the union
+             * of fewer worlds' code paths per step of their loops, on more
+             * CUs.  Worlds of many shapes (whose candidate search uses the
+             * overlap masks) step 16 to a workgroup, or 32; worlds with more
+             * than four contacts per joint of capacity step 32.  Measured at
+             * 4,096 worlds: the bin 0.842 ms (64) -> 0.724 (32) -> 0.700
+             * (16); the stacks 0.228 -> 0.218 (32) -> 0.223 (16); the hover
+             * (4 contacts, 2 joints) 0.040 -> 0.041 and the chains (32, 8)
+             * 0.394 -> 0.397 -> 0.443, which stay at 64. */
+            if (e->shared_masks && 4 * e->tiles <= cus) e->tile_parts = 4;
+            else if (e->shared_masks && 2 * e->tiles <= cus) e->tile_parts = 2;
+            else if (g.max_c > 4 * g.max_j && 2 * e->tiles <= cus) e->tile_parts = 2;
             err = hipMalloc((void**)&e->pair_stage,
                 (size_t)e->tiles * e->tile_parts * e->stage_tile_words * sizeof(uint32_t));
             if (err != hipSuccess) {

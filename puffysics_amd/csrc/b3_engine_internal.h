@@ -28,7 +28,7 @@ struct B3Engine {
     size_t lds_shared_bytes; /* LDS of a workgroup of kTileWaves waves */
     bool shared_masks;       /* ... which also split the candidate search (b3d::shared_masks) */
     bool joint_lds;          /* ... and keep the joint rows in LDS (b3d::joint_rows_fit) */
-    int tile_parts;          /* workgroups per tile of the shared step (1 or 2), each with its own
+    int tile_parts;          /* workgroups per tile of the shared step (1, 2 or 4), each with its own
                                 scratch and stage */
     bool joint_impulses_lds; /* the one-wave step keeps the joint impulses in LDS (b3d::ji_fit) */
 };
