@@ -153,16 +153,23 @@ def joint_rows_fit(max_b, max_s, max_c, max_j):
     return max_j > 0 and words <= 640
 
 
+def joint_impulses_fit(max_b, max_s, max_c, max_j):
+    """Whether the one-wave step keeps the joint impulses in LDS (ji_fit in
+    puffysics_amd/csrc/b3d_lane.h): 7 velocity words per body and 9 impulse
+    words per joint within 160 words per lane."""
+    return max_j > 0 and 7 * max_b + 9 * max_j <= 160
+
+
 def kernel_name(scene, count):
     """The step kernel a batch launches: b3k_step_shared<Masks, JL> when its
-    tiles fit one per CU (b3_engine_create), else b3k_step."""
+    tiles fit one per CU (b3_engine_create), else b3k_step<JI>."""
     import torch
     from puffysics_amd import scenes
     tiles = (count + 63) // 64
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    if tiles > cus:
-        return "b3k_step"
     caps = scenes.SCENES[scene].caps
+    if tiles > cus:
+        return "b3k_step<%s>" % ("true" if joint_impulses_fit(*caps) else "false")
     masks = 12 <= caps[1] <= 64
     return "b3k_step_shared<%s, %s>" % ("true" if masks else "false", "true" if joint_rows_fit(*caps) else "false")
 
@@ -451,9 +458,9 @@ def _short(name):
 
 
 def _step_kernel(names):
-    """The workload's step kernel: the launched kernel named b3k_step or
+    """The workload's step kernel: the launched kernel named b3k_step<JI> or
     b3k_step_shared<...>."""
-    cands = [n for n in names if _short(n) == "b3k_step" or _short(n).startswith("b3k_step_shared<")]
+    cands = [n for n in names if _short(n).startswith("b3k_step<") or _short(n).startswith("b3k_step_shared<")]
     if len(set(cands)) != 1:
         raise SystemExit("expected one step kernel, found %s" % sorted(set(cands)))
     return cands[0]
@@ -470,6 +477,52 @@ def _counter_means(rows, picks):
     sel = [by_dispatch[order[i]] for i in picks]
     names = sorted({k for d in sel for k in d})
     return {k: sum(d[k] for d in sel) / len(sel) for k in names}, len(order)
+
+
+def code_object_resources(kernel):
+    """Registers and static memory of a kernel (its short name) from the
+    AMDGPU metadata notes of the gfx950 code object in the in-tree
+    puffysics_amd/libb3engine.so (llvm-readelf --notes of the object that
+    clang-offload-bundler takes out of the library's .hip_fatbin section);
+    None when the tools or the kernel are missing.  .vgpr_count counts the
+    AGPRs too."""
+    import subprocess
+    import tempfile
+    llvm = "/opt/rocm/llvm/bin"
+    lib = os.path.join(ROOT, "puffysics_amd", "libb3engine.so")
+    try:
+        with tempfile.TemporaryDirectory() as tmp:
+            fat, co = os.path.join(tmp, "fat.bin"), os.path.join(tmp, "co.elf")
+            subprocess.run(["objcopy", "-O", "binary", "--only-section=.hip_fatbin", lib, fat], check=True)
+            subprocess.run([os.path.join(llvm, "clang-offload-bundler"), "--unbundle", "--type=o",
+                            "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", "--input=" + fat, "--output=" + co],
+                           check=True)
+            notes = subprocess.run([os.path.join(llvm, "llvm-readelf"), "--notes", co], check=True,
+                                   capture_output=True, text=True).stdout
+    except (OSError, subprocess.CalledProcessError):
+        return None
+    blocks, cur = [], None
+    for line in notes.splitlines():
+        t = line.strip()
+        if t.startswith("- .agpr_count:"):
+            cur = {}
+            blocks.append(cur)
+            t = t[2:]
+        if cur is not None and t.startswith(".") and ":" in t:
+            k, v = t.split(":", 1)
+            cur[k[1:]] = v.strip()
+    names = [b.get("name", "") for b in blocks]
+    try:
+        dem = subprocess.run(["c++filt"], input="\n".join(names), check=True,
+                             capture_output=True, text=True).stdout.splitlines()
+    except (OSError, subprocess.CalledProcessError):
+        return None
+    for b, d in zip(blocks, dem):
+        if _short(d) == kernel:
+            return {"vgpr_total": int(b["vgpr_count"]), "agpr": int(b["agpr_count"]), "sgpr": int(b["sgpr_count"]),
+                    "lds_static_bytes": int(b["group_segment_fixed_size"]),
+                    "scratch_bytes": int(b["private_segment_fixed_size"])}
+    return None
 
 
 def profile_summary(root, scene, count, steps, warmup, repeats, digest):
@@ -510,12 +563,13 @@ def profile_summary(root, scene, count, steps, warmup, repeats, digest):
     fetch_b = fetch["FETCH_SIZE"] * 1024 * scale["FETCH_SIZE"]
     write_b = write["WRITE_SIZE"] * 1024 * scale["WRITE_SIZE"]
     l0 = launches[0]
-    regs = {"vgpr": int(l0["VGPR_Count"]), "agpr": int(l0["Accum_VGPR_Count"]), "sgpr": int(l0["SGPR_Count"]),
-            "lds_bytes": int(l0["LDS_Block_Size"]), "scratch": int(l0["Scratch_Size"]),
-            "wg": int(l0["Workgroup_Size_X"]), "grid": int(l0["Grid_Size_X"])}
     kernel = _short(step)
+    regs = code_object_resources(kernel)
+    if regs is None:
+        raise SystemExit("no code-object metadata for %s in puffysics_amd/libb3engine.so" % kernel)
+    regs.update(wg=int(l0["Workgroup_Size_X"]), grid=int(l0["Grid_Size_X"]))
     workload = "%s%d" % (NAMES[scene], count)
-    counters = {"kernel": kernel if kernel == "b3k_step" else kernel.replace(",", ", ").replace(",  ", ", "),
+    counters = {"kernel": kernel.replace(",", ", ").replace(",  ", ", "),
                 "workload": workload, "source_digest": digest, "window": [start, start + steps],
                 "timed_launches": len(picks), "launches_profiled": nf,
                 "fetch_bytes_per_launch": round(fetch_b), "write_bytes_per_launch": round(write_b),
@@ -547,9 +601,12 @@ def profile_summary(root, scene, count, steps, warmup, repeats, digest):
     wc = sq.get("SQ_WAVE_CYCLES", 0) or 1
     lines += ["", "Step kernel over its timed launches: **%.2f us** average." % avg_us, "",
               "## Counters of `%s` (mean per timed launch)" % kernel, "",
-              "Registers (the dispatch records): %d VGPRs (arch), %d AGPRs, %d SGPRs, LDS %d bytes, scratch %d "
-              "bytes; workgroup %d threads, grid %d." % (regs["vgpr"], regs["agpr"], regs["sgpr"], regs["lds_bytes"],
-                                                         regs["scratch"], regs["wg"], regs["grid"]), "",
+              "Registers (the AMDGPU metadata of the kernel in the gfx950 code object of "
+              "puffysics_amd/libb3engine.so, `llvm-readelf --notes`): %d VGPRs in all, %d of them AGPRs, %d SGPRs; "
+              "static LDS %d bytes (the step's LDS is dynamic, sized at launch), private segment %d bytes; "
+              "workgroup %d threads, grid %d (the dispatch records)." % (
+                  regs["vgpr_total"], regs["agpr"], regs["sgpr"], regs["lds_static_bytes"], regs["scratch_bytes"],
+                  regs["wg"], regs["grid"]), "",
               "| counter | value |", "|---|---|"]
     for k in sorted(sq):
         lines.append("| %s | %.4g |" % (k, sq[k]))
