@@ -161,13 +161,16 @@ def joint_impulses_fit(max_b, max_s, max_c, max_j):
 
 
 def kernel_name(scene, count):
-    """The step kernel a batch launches: b3k_step_shared<Masks, JL> when its
-    tiles fit one per CU (b3_engine_create), else b3k_step<JI>."""
+    """The step kernel a batch launches (b3_engine_create): b3k_step<JI, true>
+    for worlds of at most two shapes; else b3k_step_shared<Masks, JL> when
+    the tiles fit one per CU, b3k_step<JI> when they do not."""
     import torch
     from puffysics_amd import scenes
     tiles = (count + 63) // 64
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     caps = scenes.SCENES[scene].caps
+    if caps[1] <= 2:                 # one candidate pair: b3k_step<JI, true> at any batch size
+        return "b3k_step<%s, true>" % ("true" if joint_impulses_fit(*caps) else "false")
     if tiles > cus:
         return "b3k_step<%s>" % ("true" if joint_impulses_fit(*caps) else "false")
     masks = 12 <= caps[1] <= 64

@@ -16,10 +16,12 @@
  *                              B3World structs); four waves per tile, each
  *                              copying every fourth 512-word chunk of the
  *                              tile's resetting worlds with all 64 lanes
- *   b3k_step<JI>               optional fused restore, then one b3_step per
+ *   b3k_step<JI, C0>           optional fused restore, then one b3_step per
  *                              selected lane; LDS holds the lane's clip
  *                              polygons, then its body velocities (JI: and
- *                              its joints' accumulated impulses)
+ *                              its joints' accumulated impulses; C0: contact
+ *                              0's row stays in registers, for worlds of at
+ *                              most two shapes)
  *   b3k_step_shared<Masks, JL> the same for batches of at most one tile per
  *                              CU, with the contact writes, preparation,
  *                              contact sweeps and body and joint work split
@@ -109,8 +111,10 @@ __global__ __launch_bounds__(64) void b3k_restore(uint32_t* live, const uint32_t
 
 /* JI: the joints' accumulated impulses stay in LDS past the velocity rows
  * for the whole step (ji_fit; the launch gives ji_lds_rows words per lane),
- * instead of a read and a write of the joint's words in every solve. */
-template <bool JI>
+ * instead of a read and a write of the joint's words in every solve.  C0:
+ * contact 0's row stays in registers for the step (worlds of at most two
+ * shapes, whose only contact it is), instead of a load in every sweep. */
+template <bool JI, bool C0 = false>
 __global__ __launch_bounds__(64) void b3k_step(uint32_t* live, const uint32_t* snap, uint32_t* scratch,
         Geometry g, int count, float dt, int substeps, const unsigned char* step_mask,
         const unsigned char* reset_mask, unsigned int opts) {
@@ -125,7 +129,7 @@ __global__ __launch_bounds__(64) void b3k_step(uint32_t* live, const uint32_t* s
     if (w >= count || (step_mask && !step_mask[w])) return;
     Lane L = lane_view(live, scratch, vel_rows, g, tile, lane, opts);
     if (JI) L.ji = vel_rows + (size_t)ji_word(g) * kLanes + lane;
-    step_world<false, false, JI>(L, dt, substeps);
+    step_world<false, false, JI, C0>(L, dt, substeps);
 }
 
 /* The step with the narrowphase and the contact sweeps shared by
@@ -432,6 +436,8 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
     e->lds_bytes = e->joint_impulses_lds ? (size_t)ji_lds_rows(g) * kLanes * sizeof(float) : lds;
     err = b3i_lds_limit((const void*)b3k_step<false>);
     if (err == hipSuccess) err = b3i_lds_limit((const void*)b3k_step<true>);
+    if (err == hipSuccess) err = b3i_lds_limit((const void*)b3k_step<false, true>);
+    if (err == hipSuccess) err = b3i_lds_limit((const void*)b3k_step<true, true>);
     if (err == hipSuccess) err = b3i_lds_limit((const void*)b3k_step_shared<true, false>);
     if (err == hipSuccess) err = b3i_lds_limit((const void*)b3k_step_shared<false, false>);
     if (err == hipSuccess) err = b3i_lds_limit((const void*)b3k_step_shared<true, true>);
@@ -475,7 +481,11 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
             return err;
         }
         e->tile_parts = 1;
-        if (e->tiles <= cus && shared_lds <= kCuLdsBytes) {
+        /* Worlds of at most two shapes (one candidate pair, at most one
+         * contact) leave the tile's waves nothing to share; their one-wave
+         * step keeps that contact's row in registers (b3k_step<JI, true>):
+         * the hover at 4,096 worlds 0.0398 ms shared, 0.0383 ms one-wave. */
+        if (e->tiles <= cus && shared_lds <= kCuLdsBytes && g.max_s > 2) {
             size_t max_cand = (size_t)g.max_s * (size_t)(g.max_s - 1) / 2;
             size_t stage_words = max_cand * kStageWords;
             if ((size_t)stage_sched_words(g) > stage_words) stage_words = (size_t)stage_sched_words(g);
@@ -621,7 +631,8 @@ hipError_t b3_batch_step_gpu(B3Engine* e, float dt, int substeps, const unsigned
             e->options, e->tile_parts);
         return hipGetLastError();
     }
-    auto one_wave = e->joint_impulses_lds ? b3k_step<true> : b3k_step<false>;
+    auto one_wave = e->g.max_s <= 2 ? (e->joint_impulses_lds ? b3k_step<true, true> : b3k_step<false, true>)
+                                    : (e->joint_impulses_lds ? b3k_step<true> : b3k_step<false>);
     one_wave<<<e->tiles, 64, e->lds_bytes, stream>>>(e->live, e->snap, e->scratch, e->g, e->count, dt, substeps,
         step_mask, reset_mask, e->options);
     return hipGetLastError();

@@ -2405,7 +2405,34 @@ B3D_FN void crow_masses(const Lane& L, int c, CRow* r, Soft cs, Soft ss) {
         r->ib.cy = q3s<S>(rc, R_IB + 3);
         r->ib.cz = v3(qfs<S>(rc, R_IB + 6), qfs<S>(rc, R_IB_ZYZ), qfs<S>(rc, R_IB_ZYZ + 1));
     }
-    r->soft = (r->flags & CF_STATIC) ? ss : cs;
+    /* field by field: a select between the two structs would be one between
+     * their addresses, which keeps a row kept for the step (kept_row) out of
+     * registers */
+    bool st = (r->flags & CF_STATIC) != 0;
+    r->soft.bias_rate = st ? ss.bias_rate : cs.bias_rate;
+    r->soft.mass_scale = st ? ss.mass_scale : cs.mass_scale;
+    r->soft.impulse_scale = st ? ss.impulse_scale : cs.impulse_scale;
+}
+
+/* The delta poses of a row's bodies (a static body's are exactly zero and
+ * the identity for the whole step). */
+B3D_FN void crow_deltas(const Lane& L, CRow* r) {
+    if (r->flags & CF_FIXED_A) {
+        r->dpa = zero3();
+        r->dqa = qid();
+    } else {
+        const uint32_t* da = delta_rec(L, r->a);
+        r->dpa = r3(da, BD_DP);
+        r->dqa = rq4(da, BD_DQ);
+    }
+    if (r->flags & CF_FIXED_B) {
+        r->dpb = zero3();
+        r->dqb = qid();
+    } else {
+        const uint32_t* db = delta_rec(L, r->b);
+        r->dpb = r3(db, BD_DP);
+        r->dqb = rq4(db, BD_DQ);
+    }
 }
 
 /* Normal, points and friction data of a row: loaded one contact ahead.
@@ -2422,22 +2449,7 @@ B3D_FN void crow_load(const Lane& L, int c, CHead h, int relax, CRow* r, const i
     r->twist_mass = h.twist_mass;
     r->n = q3s<S>(rc, R_N);
     r->rolling = qfs<S>(rc, R_ROLLING);
-    if (h.flags & CF_FIXED_A) {
-        r->dpa = zero3();
-        r->dqa = qid();
-    } else {
-        const uint32_t* da = delta_rec(L, h.a);
-        r->dpa = r3(da, BD_DP);
-        r->dqa = rq4(da, BD_DQ);
-    }
-    if (h.flags & CF_FIXED_B) {
-        r->dpb = zero3();
-        r->dqb = qid();
-    } else {
-        const uint32_t* db = delta_rec(L, h.b);
-        r->dpb = r3(db, BD_DP);
-        r->dqb = rq4(db, BD_DQ);
-    }
+    crow_deltas(L, r);
 #pragma unroll
     for (int p = 0; p < kMaxManifold; p++) {
         CPoint& q = r->pt[p];
@@ -2529,6 +2541,7 @@ B3D_FN void crow_solve(const Lane& L, int c, CRow& r, float inv_h, float contact
         float new_t = clampf(r.twist_imp + dtw, -max_t, max_t);
         qsf(rc, R_TWIST, new_t);
         dtw = new_t - r.twist_imp;
+        r.twist_imp = new_t;           /* the row stays current (a row kept for the step) */
         wa = sub(wa, mv(r.ia, scale(n, dtw)));
         wb = add(wb, mv(r.ib, scale(n, dtw)));
 
@@ -2554,6 +2567,7 @@ B3D_FN void crow_solve(const Lane& L, int c, CRow& r, float inv_h, float contact
         df.y = ni.y - r.fi.y;
         qsf(rc, R_FI, ni.x);
         qsf(rc, R_FI + 1, ni.y);
+        r.fi = ni;
         V3 P = add(scale(r.t1, df.x), scale(r.t2, df.y));
         va = msub(va, r.ma, P);
         wa = sub(wa, mv(r.ia, cross(r.ca, P)));
@@ -2578,23 +2592,36 @@ B3D_FN void crow_solve(const Lane& L, int c, CRow& r, float inv_h, float contact
 /* b3_solve_contacts (08:415-437): one Gauss-Seidel sweep in contact order.
  * Rows c+1 and c+2 (masses included) are in flight while row c is solved,
  * and the head of row c+3 while row c+2 loads.  The one-wave step runs
- * large batches, so the rows are streamed (qus). */
-B3D_FN void solve_contacts(const Lane& L, float inv_h, float contact_speed, int use_bias, Soft cs, Soft ss) {
+ * large batches, so the rows are streamed (qus).  With `row0` and `have0`,
+ * contact 0's row is the one the step keeps in registers (kept_row), its
+ * impulses current; `deltas`: its bodies' delta poses have moved since it
+ * was last used (a position update), so they are loaded again.  (A null
+ * row0 is a compile-time constant at every call: the kept row is never
+ * selected through a pointer, which would put it in private memory.) */
+B3D_FN void solve_contacts(const Lane& L, float inv_h, float contact_speed, int use_bias, Soft cs, Soft ss,
+        CRow* row0 = nullptr, int have0 = 0, bool deltas = false) {
     int cc = contact_count_word(L);
     if (cc <= 0) return;
     int relax = !use_bias;
-    CHead h = rhead_load(L, 0);
+    int c0 = 0;
+    if (row0 && have0) {
+        if (deltas) crow_deltas(L, row0);
+        crow_solve(L, 0, *row0, inv_h, contact_speed, use_bias);
+        c0 = 1;
+        if (cc == 1) return;
+    }
+    CHead h = rhead_load(L, c0);
     CRow cur, nxt, nx2;
-    crow_load<true>(L, 0, h, relax, &cur);
-    crow_masses<true>(L, 0, &cur, cs, ss);
-    if (cc > 1) {
-        h = rhead_load(L, 1);
-        crow_load<true>(L, 1, h, relax, &nxt);
-        crow_masses<true>(L, 1, &nxt, cs, ss);
+    crow_load<true>(L, c0, h, relax, &cur);
+    crow_masses<true>(L, c0, &cur, cs, ss);
+    if (cc > c0 + 1) {
+        h = rhead_load(L, c0 + 1);
+        crow_load<true>(L, c0 + 1, h, relax, &nxt);
+        crow_masses<true>(L, c0 + 1, &nxt, cs, ss);
     }
     CHead h2 = h;
-    if (cc > 2) h2 = rhead_load(L, 2);
-    for (int c = 0; c < cc; c++) {
+    if (cc > c0 + 2) h2 = rhead_load(L, c0 + 2);
+    for (int c = c0; c < cc; c++) {
         CHead h3 = h2;
         if (c + 3 < cc) h3 = rhead_load(L, c + 3);
         if (c + 2 < cc) {
@@ -2606,6 +2633,26 @@ B3D_FN void solve_contacts(const Lane& L, float inv_h, float contact_speed, int 
         nxt = nx2;
         h2 = h3;
     }
+}
+
+/* Contact 0's row, loaded once for the whole step (every field, masses
+ * included); 0 when the lane has no contact.  A step whose worlds have at
+ * most two shapes (one candidate pair, so at most one contact) keeps it in
+ * registers: each sweep then loads only its bodies' delta poses, after a
+ * position update. */
+B3D_FN int kept_row(const Lane& L, Soft cs, Soft ss, CRow* row) {
+    if (contact_count_word(L) <= 0) return 0;
+    CHead h = rhead_load(L, 0);
+    crow_load<true>(L, 0, h, 1, row);
+    crow_masses<true>(L, 0, row, cs, ss);
+    return 1;
+}
+/* The kept row's normal impulses after restitution, which writes them. */
+B3D_FN void kept_row_impulses(const Lane& L, CRow* row) {
+    const uint32_t* rc = crec(L, 0, row->slot);
+#pragma unroll
+    for (int p = 0; p < kMaxManifold; p++)
+        if (p < row->pc) row->pt[p].ni = qf(rc, R_NI + 2 * p);
 }
 
 /* One sweep of a shared-narrowphase tile: level by level, each of the
@@ -3790,8 +3837,10 @@ B3D_FN void integrate_velocities_law(const Lane& L, float h, const Law& law) {
  * staged in the velocity rows after contact generation (which uses the
  * same rows for clip polygons) and written back at the end.  JL: the joint
  * rows in LDS (shared tiles); JI: the joint impulses in LDS (one wave per
- * tile, L.ji), staged by the joint warm start and written back at the end. */
-template <bool Masks = false, class Law, bool JL = false, bool JI = false>
+ * tile, L.ji), staged by the joint warm start and written back at the end.
+ * C0: the one-wave step keeps contact 0's row in registers for the step
+ * (kept_row; worlds of at most two shapes, whose only contact it is). */
+template <bool Masks = false, class Law, bool JL = false, bool JI = false, bool C0 = false>
 B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
     static_assert(!(JL && JI), "joint rows and joint impulses are two layouts of the same LDS words");
     if (!(dt > 0.0f)) return;
@@ -3856,6 +3905,9 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
         if (wave_any(L, !warm_done)) warm_start_contacts(L, warm_done);
     }
     if (act) warm_start_joints<JI>(L);
+    CRow row0;
+    int have0 = 0;
+    if constexpr (C0) have0 = kept_row(L, cs, ss, &row0);
     /* a shared tile's waves split the first joint geometry, after the warm
      * start has read the previous step's hinge rows, which it overwrites */
     if (L.staged) B3D_BARRIER();
@@ -3874,7 +3926,7 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
                 integrate_velocities(L, share, stride);
         }
         if (L.staged) solve_contacts_leveled(L, inv_h, contact_speed, 1, cs, ss, nlev);
-        else solve_contacts(L, inv_h, contact_speed, 1, cs, ss);
+        else solve_contacts(L, inv_h, contact_speed, 1, cs, ss, C0 ? &row0 : nullptr, have0);
         if constexpr (JL) solve_joints_leveled(L, h, inv_h, 1, njlev);
         else if (act) solve_joints<JI>(L, h, inv_h, 1);
         if (L.staged) B3D_BARRIER();   /* the joints' velocities */
@@ -3882,11 +3934,14 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
         if (L.staged) B3D_BARRIER();   /* the delta poses */
         if (act) joint_geometry(L, share, stride);
         if (L.staged) solve_contacts_leveled(L, inv_h, contact_speed, 0, cs, ss, nlev);
-        else solve_contacts(L, inv_h, contact_speed, 0, cs, ss);
+        else solve_contacts(L, inv_h, contact_speed, 0, cs, ss, C0 ? &row0 : nullptr, have0, true);
         if constexpr (JL) solve_joints_leveled(L, h, inv_h, 0, njlev);
         if (act) {
             if constexpr (!JL) solve_joints<JI>(L, h, inv_h, 0);
-            if (rest_wave) apply_restitution(L, rest_threshold);
+            if (rest_wave) {
+                apply_restitution(L, rest_threshold);
+                if (have0) kept_row_impulses(L, &row0);
+            }
         }
     }
     /* a shared tile's waves split the write-back, after the last
@@ -3902,10 +3957,11 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
 }
 
 /* b3_step without a hook; JL: the joint rows in LDS (L.jl, shared tiles);
- * JI: the joint impulses in LDS (L.ji, one wave per tile). */
-template <bool Masks = false, bool JL = false, bool JI = false>
+ * JI: the joint impulses in LDS (L.ji, one wave per tile); C0: contact 0's
+ * row kept in registers (one wave per tile). */
+template <bool Masks = false, bool JL = false, bool JI = false, bool C0 = false>
 B3D_FN void step_world(const Lane& L, float dt, int substeps) {
-    step_world<Masks, NoForces, JL, JI>(L, dt, substeps, NoForces());
+    step_world<Masks, NoForces, JL, JI, C0>(L, dt, substeps, NoForces());
 }
 
 /* A helper wave of a shared-narrowphase tile after its narrowphase share:

@@ -544,6 +544,28 @@ def ref_art_lib(caps):
     return _refs[key]
 
 
+def two_shape_worlds(count):
+    """Worlds of the hover's capacities (2 bodies, 2 shapes, 4 contacts, 2
+    joints: at most one candidate pair, so at most one contact) varied for
+    the kept-row step: restitution on every third dynamic shape (with a
+    fast fall, so that bounces happen), rolling resistance on every fourth,
+    friction from 0.2 to 1.0, and every sixth sphere made a box (contacts of
+    up to four points)."""
+    w = clone(scenes.build(1, count))
+    sh, bo = w["shapes"], w["bodies"]
+    k = np.arange(count)
+    sh["restitution"][:, 1] = np.where(k % 3 == 1, np.float32(0.6), np.float32(0.0))
+    sh["rolling"][:, 1] = np.where(k % 4 == 2, np.float32(0.05), np.float32(0.0))
+    sh["friction"][:, 1] = (np.float32(0.2) + np.float32(0.2) * (k % 5)).astype(np.float32)
+    bo["lin_vel"]["y"][:, 1] = np.where(k % 2 == 0, np.float32(-4.0), bo["lin_vel"]["y"][:, 1])
+    box = k % 6 == 5
+    sh["type"][box, 1] = sh["type"][0, 0]                 # the ground's type: box
+    sh["half"]["x"][box, 1] = np.float32(0.3)
+    sh["half"]["y"][box, 1] = np.float32(0.2)
+    sh["half"]["z"][box, 1] = np.float32(0.25)
+    return w
+
+
 def oracle_step_batch(worlds, sig, dt, substeps, active=None):
     """b3_batch_step over a contiguous batch on the oracle."""
     lib = oracle()

@@ -87,6 +87,12 @@ static Lane lane_of(uint32_t* tiles, uint32_t* scratch, float* vel, const Geomet
 static int g_joint_impulses = 0;
 void emu_set_joint_impulses_lds(int mode) { g_joint_impulses = mode; }
 
+/* Contact 0's row kept in registers for emu_step, as b3k_step<JI, true>
+ * keeps it for worlds of at most two shapes: 0 never, 1 for every world
+ * (the lane code handles any contact count). */
+static int g_keep_row0 = 0;
+void emu_set_keep_row0(int mode) { g_keep_row0 = mode; }
+
 void emu_step(uint32_t* tiles, int count, unsigned long long sig, float dt, int substeps,
         const unsigned char* step_mask) {
     Geometry g;
@@ -101,9 +107,11 @@ void emu_step(uint32_t* tiles, int count, unsigned long long sig, float dt, int 
         Lane L = lane_of(tiles, scratch.data(), vel.data(), g, w);
         if (ji) {
             L.ji = vel.data() + (size_t)ji_word(g) * kLanes + w % kLanes;
-            step_world<false, false, true>(L, dt, substeps);
+            if (g_keep_row0) step_world<false, false, true, true>(L, dt, substeps);
+            else step_world<false, false, true>(L, dt, substeps);
         } else {
-            step_world(L, dt, substeps);
+            if (g_keep_row0) step_world<false, false, false, true>(L, dt, substeps);
+            else step_world(L, dt, substeps);
         }
     }
 }

@@ -254,3 +254,97 @@ def test_lane_code_joint_impulses_in_lds_every_feature():
     bad = diff_words(emu.worlds(), ref, CUSTOM_SIG)
     assert len(bad) == 0, bad[:10].tolist()
     assert np.abs(ref["joints"]["angular_impulse"]["x"][:, 0]).max() > 0
+
+
+def _with_kept_row0(fn):
+    """Run fn with emu_step keeping contact 0's row in registers for the
+    step (as b3k_step<JI, true> does), then restore the default."""
+    import ctypes as C
+    from b3test import emu
+    lib = emu()
+    lib.emu_set_keep_row0.argtypes = [C.c_int]
+    lib.emu_set_keep_row0(1)
+    try:
+        return fn()
+    finally:
+        lib.emu_set_keep_row0(0)
+
+
+@pytest.mark.parametrize("scene,count,steps", [(1, 130, 80), (2, 70, 40), (5, 70, 30)])
+def test_lane_code_kept_contact_row(scene, count, steps):
+    """The one-wave step with contact 0's row kept in registers for the step
+    (delta poses reloaded after each position update, impulses updated in
+    place): bit-exact against the oracle.  The hover's worlds have at most
+    one contact, as the device's worlds of two shapes; the stacks and the
+    arm add contacts after the kept one, which the sweep loads as usual."""
+    worlds = scenes.build(scene, count)
+    initial = clone(worlds)
+    e = EmuBatch(scene, worlds)
+    _with_kept_row0(lambda: e.run(0, steps))
+    ref = clone(worlds)
+    oracle_run(scene, ref, initial, 0, steps)
+    bad = diff_words(e.worlds(), ref, scenes.SCENES[scene].sig)
+    assert len(bad) == 0, "first differences (world, word): %s" % bad[:10].tolist()
+    assert (ref["contact_count"] > 0).any()
+
+
+def test_lane_code_kept_contact_row_every_feature():
+    """The kept row on the coverage worlds (restitution, which rewrites the
+    kept row's impulses, rolling, friction, welds and hinges) with a step
+    mask, in the default options (the fused warm start) and with the solver
+    fields kept: every live word but those fields equals the oracle's."""
+    import ctypes as C
+    from b3test import EmuSig, emu, feature_worlds, live_word_mask, oracle_step_batch, solver_field_words, words
+    from puffysics_amd.creation import CUSTOM_SIG
+    lib = emu()
+    lib.emu_set_options.argtypes = [C.c_uint]
+    for opts in (1, 0):
+        worlds = feature_worlds(40)
+        ref = clone(worlds)
+        e = EmuSig(CUSTOM_SIG, worlds)
+        active = (np.arange(40) % 5 != 2).astype(np.uint8)
+
+        def run():
+            for t in range(50):
+                act = active if t % 3 == 0 else None
+                oracle_step_batch(ref, CUSTOM_SIG, 1.0 / 60.0, 4, act)
+                e.step(1.0 / 60.0, 4, act)
+
+        lib.emu_set_options(opts)
+        try:
+            _with_kept_row0(run)
+        finally:
+            lib.emu_set_options(1)
+        got = e.worlds()
+        live = live_word_mask(ref, CUSTOM_SIG) & live_word_mask(got, CUSTOM_SIG)
+        diff = (words(got) != words(ref)) & live
+        if opts:
+            assert not diff.any(), np.argwhere(diff)[:10].tolist()
+        else:
+            assert not (diff & ~solver_field_words(ref)).any()
+    rest = ref["contacts"]["restitution"] > 0
+    assert any(rest[i, :ref["contact_count"][i]].any() for i in range(40))
+
+
+def test_lane_code_kept_contact_row_two_shape_worlds():
+    """The kept row on varied worlds of two shapes (the worlds the device
+    steps with it): restitution bounces, rolling, friction and four-point box
+    contacts, bit-exact against the oracle over 120 steps."""
+    from b3test import EmuSig, oracle_step_batch, two_shape_worlds
+    sig = scenes.SCENES[1].sig
+    worlds = two_shape_worlds(120)
+    ref = clone(worlds)
+    e = EmuSig(sig, worlds)
+    rest_hits = 0
+
+    def run():
+        nonlocal rest_hits
+        for t in range(120):
+            oracle_step_batch(ref, sig, 1.0 / 60.0, 4)
+            e.step(1.0 / 60.0, 4)
+            rest_hits += int(((ref["contacts"]["restitution"][:, 0] > 0) & (ref["contact_count"] > 0)).sum())
+
+    _with_kept_row0(run)
+    bad = diff_words(e.worlds(), ref, sig)
+    assert len(bad) == 0, bad[:10].tolist()
+    assert rest_hits > 0 and (ref["contacts"]["point_count"][:, 0] == 4).any()

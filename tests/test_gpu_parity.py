@@ -348,3 +348,36 @@ def test_default_options_one_wave_scenes(scene, count, steps):
     diff = (wg != wr) & live & ~solver_field_words(ref) & ~both_nan
     assert not diff.any(), describe(np.argwhere(diff), got, ref, worlds)
     assert ref["contact_count"].sum() > 0
+
+
+@pytest.mark.parametrize("keep", [True, False], ids=["keep", "default"])
+def test_two_shape_worlds_kept_row(keep):
+    """Worlds of two shapes step on the one-wave kernel with their contact's
+    row kept in registers (b3k_step<JI, true>) at any batch size: varied
+    hover worlds (restitution bounces, rolling, friction, four-point box
+    contacts) with a step mask on every other step, against the oracle over
+    120 steps; with the solver fields kept every word matches, in the
+    default options every live word but those fields."""
+    from b3test import live_word_mask, oracle_step_batch, solver_field_words, two_shape_worlds, words
+    from puffysics_amd.engine import B3_ENGINE_KEEP_SOLVER_FIELDS, B3Engine
+    sig = scenes.SCENES[1].sig
+    worlds = two_shape_worlds(300)
+    ref = clone(worlds)
+    eng = B3Engine(worlds, sig)
+    eng.set_options(B3_ENGINE_KEEP_SOLVER_FIELDS if keep else 0)
+    active = (np.arange(300) % 7 != 3).astype(np.uint8)
+    d_active = torch.from_numpy(active).cuda()
+    for t in range(120):
+        act = t % 2 == 0
+        oracle_step_batch(ref, sig, 1.0 / 60.0, 4, active if act else None)
+        eng.step(1.0 / 60.0, 4, d_active if act else None)
+    torch.cuda.synchronize()
+    got = eng.download()
+    if keep:
+        bad = diff_words(got, ref, sig)
+        assert len(bad) == 0, describe(bad, got, ref, worlds)
+    else:
+        live = live_word_mask(ref, sig) & live_word_mask(got, sig)
+        diff = (words(got) != words(ref)) & live
+        assert not (diff & ~solver_field_words(ref)).any(), np.argwhere(diff & ~solver_field_words(ref))[:10].tolist()
+    assert (ref["contacts"]["point_count"][:, 0] == 4).any()
