@@ -163,7 +163,7 @@ def joint_impulses_fit(max_b, max_s, max_c, max_j):
 def kernel_name(scene, count):
     """The step kernel a batch launches (b3_engine_create): b3k_step<JI, true>
     for worlds of at most two shapes; else b3k_step_shared<Masks, JL> when
-    the tiles fit one per CU, b3k_step<JI> when they do not."""
+    the tiles fit one per CU, b3k_step<JI, false> when they do not."""
     import torch
     from puffysics_amd import scenes
     tiles = (count + 63) // 64
@@ -172,7 +172,7 @@ def kernel_name(scene, count):
     if caps[1] <= 2:                 # one candidate pair: b3k_step<JI, true> at any batch size
         return "b3k_step<%s, true>" % ("true" if joint_impulses_fit(*caps) else "false")
     if tiles > cus:
-        return "b3k_step<%s>" % ("true" if joint_impulses_fit(*caps) else "false")
+        return "b3k_step<%s, false>" % ("true" if joint_impulses_fit(*caps) else "false")
     masks = 12 <= caps[1] <= 64
     return "b3k_step_shared<%s, %s>" % ("true" if masks else "false", "true" if joint_rows_fit(*caps) else "false")
 
