@@ -135,10 +135,13 @@ hipError_t b3_engine_device_view(const B3Engine* engine, void** tiles, size_t* w
  * disjoint dynamic bodies, level by level, keeping every body's updates in
  * contact order), the velocity and position updates, the joint geometry
  * and, when the joint rows fit in LDS, the joint passes (by joint levels),
- * while wave 0 does the rest.  That allocates at creation a staging buffer of
- * 4 * tiles * 64 * (1 + max(36 * max_shapes * (max_shapes - 1) / 2,
- * 3 * max_contacts)) bytes.  This option launches one wave per tile as for
- * larger batches.  Results are identical either way. */
+ * while wave 0 does the rest; contact-bound worlds split each tile over
+ * `parts` = 2 or 4 such workgroups when the CUs allow.  That allocates at
+ * creation a staging buffer of 4 * tiles * parts * 64 * (1 + max(40 *
+ * max_shapes * (max_shapes - 1) / 2, 2 * max_contacts)) bytes.  Worlds of at
+ * most two shapes (one candidate pair) always step one wave per tile.  This
+ * option launches one wave per tile as for larger batches.  Results are
+ * identical either way. */
 #define B3_ENGINE_ONE_WAVE_PER_TILE 4u
 hipError_t b3_engine_set_options(B3Engine* engine, unsigned int options);
 
