@@ -20,7 +20,7 @@
  *                              selected lane; LDS holds the lane's clip
  *                              polygons, then its body velocities (JI: and
  *                              its joints' accumulated impulses; C0: contact
- *                              0's row stays in registers, for worlds of at
+ *                              0's row kept for the step, for worlds of at
  *                              most two shapes)
  *   b3k_step_shared<Masks, JL> the same for batches of at most one tile per
  *                              CU, with the contact writes, preparation,
@@ -112,8 +112,8 @@ __global__ __launch_bounds__(64) void b3k_restore(uint32_t* live, const uint32_t
 /* JI: the joints' accumulated impulses stay in LDS past the velocity rows
  * for the whole step (ji_fit; the launch gives ji_lds_rows words per lane),
  * instead of a read and a write of the joint's words in every solve.  C0:
- * contact 0's row stays in registers for the step (worlds of at most two
- * shapes, whose only contact it is), instead of a load in every sweep. */
+ * contact 0's row is kept for the step (worlds of at most two shapes, whose
+ * only contact it is), instead of a head and a row load in every sweep. */
 template <bool JI, bool C0 = false>
 __global__ __launch_bounds__(64) void b3k_step(uint32_t* live, const uint32_t* snap, uint32_t* scratch,
         Geometry g, int count, float dt, int substeps, const unsigned char* step_mask,
@@ -483,7 +483,7 @@ hipError_t b3_engine_create(B3Engine** out, B3Batch worlds, unsigned long long c
         e->tile_parts = 1;
         /* Worlds of at most two shapes (one candidate pair, at most one
          * contact) leave the tile's waves nothing to share; their one-wave
-         * step keeps that contact's row in registers (b3k_step<JI, true>):
+         * step keeps that contact's row for the step (b3k_step<JI, true>):
          * the hover at 4,096 worlds 0.0398 ms shared, 0.0383 ms one-wave. */
         if (e->tiles <= cus && shared_lds <= kCuLdsBytes && g.max_s > 2) {
             size_t max_cand = (size_t)g.max_s * (size_t)(g.max_s - 1) / 2;

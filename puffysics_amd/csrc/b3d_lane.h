@@ -2406,8 +2406,8 @@ B3D_FN void crow_masses(const Lane& L, int c, CRow* r, Soft cs, Soft ss) {
         r->ib.cz = v3(qfs<S>(rc, R_IB + 6), qfs<S>(rc, R_IB_ZYZ), qfs<S>(rc, R_IB_ZYZ + 1));
     }
     /* field by field: a select between the two structs would be one between
-     * their addresses, which keeps a row kept for the step (kept_row) out of
-     * registers */
+     * their addresses, which stops the compiler from splitting a row kept
+     * for the step (kept_row) into scalars */
     bool st = (r->flags & CF_STATIC) != 0;
     r->soft.bias_rate = st ? ss.bias_rate : cs.bias_rate;
     r->soft.mass_scale = st ? ss.mass_scale : cs.mass_scale;
@@ -2593,11 +2593,11 @@ B3D_FN void crow_solve(const Lane& L, int c, CRow& r, float inv_h, float contact
  * Rows c+1 and c+2 (masses included) are in flight while row c is solved,
  * and the head of row c+3 while row c+2 loads.  The one-wave step runs
  * large batches, so the rows are streamed (qus).  With `row0` and `have0`,
- * contact 0's row is the one the step keeps in registers (kept_row), its
- * impulses current; `deltas`: its bodies' delta poses have moved since it
- * was last used (a position update), so they are loaded again.  (A null
- * row0 is a compile-time constant at every call: the kept row is never
- * selected through a pointer, which would put it in private memory.) */
+ * contact 0's row is the one the step keeps (kept_row), its impulses
+ * current; `deltas`: its bodies' delta poses have moved since it was last
+ * used (a position update), so they are loaded again.  (A null row0 is a
+ * compile-time constant at every call: the kept row is never selected
+ * through a pointer, which would stop the compiler from splitting it.) */
 B3D_FN void solve_contacts(const Lane& L, float inv_h, float contact_speed, int use_bias, Soft cs, Soft ss,
         CRow* row0 = nullptr, int have0 = 0, bool deltas = false) {
     int cc = contact_count_word(L);
@@ -2637,9 +2637,10 @@ B3D_FN void solve_contacts(const Lane& L, float inv_h, float contact_speed, int 
 
 /* Contact 0's row, loaded once for the whole step (every field, masses
  * included); 0 when the lane has no contact.  A step whose worlds have at
- * most two shapes (one candidate pair, so at most one contact) keeps it in
- * registers: each sweep then loads only its bodies' delta poses, after a
- * position update. */
+ * most two shapes (one candidate pair, so at most one contact) keeps it for
+ * the step, in registers or, where the kernel's registers are full, in the
+ * lane's private memory: each sweep then waits on no head load, and loads
+ * its bodies' delta poses only after a position update. */
 B3D_FN int kept_row(const Lane& L, Soft cs, Soft ss, CRow* row) {
     if (contact_count_word(L) <= 0) return 0;
     CHead h = rhead_load(L, 0);
@@ -3838,8 +3839,8 @@ B3D_FN void integrate_velocities_law(const Lane& L, float h, const Law& law) {
  * same rows for clip polygons) and written back at the end.  JL: the joint
  * rows in LDS (shared tiles); JI: the joint impulses in LDS (one wave per
  * tile, L.ji), staged by the joint warm start and written back at the end.
- * C0: the one-wave step keeps contact 0's row in registers for the step
- * (kept_row; worlds of at most two shapes, whose only contact it is). */
+ * C0: the one-wave step keeps contact 0's row for the step (kept_row;
+ * worlds of at most two shapes, whose only contact it is). */
 template <bool Masks = false, class Law, bool JL = false, bool JI = false, bool C0 = false>
 B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
     static_assert(!(JL && JI), "joint rows and joint impulses are two layouts of the same LDS words");
@@ -3958,7 +3959,7 @@ B3D_FN void step_world(const Lane& L0, float dt, int substeps, const Law& law) {
 
 /* b3_step without a hook; JL: the joint rows in LDS (L.jl, shared tiles);
  * JI: the joint impulses in LDS (L.ji, one wave per tile); C0: contact 0's
- * row kept in registers (one wave per tile). */
+ * row kept for the step (one wave per tile). */
 template <bool Masks = false, bool JL = false, bool JI = false, bool C0 = false>
 B3D_FN void step_world(const Lane& L, float dt, int substeps) {
     step_world<Masks, NoForces, JL, JI, C0>(L, dt, substeps, NoForces());

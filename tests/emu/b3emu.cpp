@@ -87,7 +87,7 @@ static Lane lane_of(uint32_t* tiles, uint32_t* scratch, float* vel, const Geomet
 static int g_joint_impulses = 0;
 void emu_set_joint_impulses_lds(int mode) { g_joint_impulses = mode; }
 
-/* Contact 0's row kept in registers for emu_step, as b3k_step<JI, true>
+/* Contact 0's row kept for the step in emu_step, as b3k_step<JI, true>
  * keeps it for worlds of at most two shapes: 0 never, 1 for every world
  * (the lane code handles any contact count). */
 static int g_keep_row0 = 0;

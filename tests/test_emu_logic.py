@@ -257,7 +257,7 @@ def test_lane_code_joint_impulses_in_lds_every_feature():
 
 
 def _with_kept_row0(fn):
-    """Run fn with emu_step keeping contact 0's row in registers for the
+    """Run fn with emu_step keeping contact 0's row for the
     step (as b3k_step<JI, true> does), then restore the default."""
     import ctypes as C
     from b3test import emu
@@ -272,7 +272,7 @@ def _with_kept_row0(fn):
 
 @pytest.mark.parametrize("scene,count,steps", [(1, 130, 80), (2, 70, 40), (5, 70, 30)])
 def test_lane_code_kept_contact_row(scene, count, steps):
-    """The one-wave step with contact 0's row kept in registers for the step
+    """The one-wave step with contact 0's row kept for the step
     (delta poses reloaded after each position update, impulses updated in
     place): bit-exact against the oracle.  The hover's worlds have at most
     one contact, as the device's worlds of two shapes; the stacks and the

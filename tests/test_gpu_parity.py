@@ -353,7 +353,7 @@ def test_default_options_one_wave_scenes(scene, count, steps):
 @pytest.mark.parametrize("keep", [True, False], ids=["keep", "default"])
 def test_two_shape_worlds_kept_row(keep):
     """Worlds of two shapes step on the one-wave kernel with their contact's
-    row kept in registers (b3k_step<JI, true>) at any batch size: varied
+    row kept for the step (b3k_step<JI, true>) at any batch size: varied
     hover worlds (restitution bounces, rolling, friction, four-point box
     contacts) with a step mask on every other step, against the oracle over
     120 steps; with the solver fields kept every word matches, in the
