@@ -42,6 +42,11 @@ Per workload, all over the same window:
              over the window's first steps, repeated for a bounded time.
 `--profile-commands DIR` / `--profile-summary DIR` (with --scene) give the
 rocprofv3 runs of the same window and reduce them to profiles/.
+
+Two more measurements, each its own JSON line and not the headline:
+`--scene N --art` steps the workload with articulated contacts
+(B3_ENGINE_ART_CONTACTS, the reference's B3_ART_CONTACTS=1 step), and
+`--hover-env N` times the PufferLib hover adapter's vector step on N envs.
 """
 import argparse
 import ctypes as C
@@ -261,7 +266,7 @@ def window_of(scene, steps, warmup):
     return start - w, start, start + steps
 
 
-def run_workload(scene, count, steps, warmup, repeats, event_every, digest, cpu_seconds=None):
+def run_workload(scene, count, steps, warmup, repeats, event_every, digest, cpu_seconds=None, art=False):
     import numpy as np
     import torch
     from puffysics_amd import scenes
@@ -271,6 +276,9 @@ def run_workload(scene, count, steps, warmup, repeats, event_every, digest, cpu_
     log("%s: building %d worlds" % (NAMES[scene], count))
     worlds = scenes.build(scene, count)
     eng = B3Engine(worlds, sc.sig)
+    if art:
+        from puffysics_amd.engine import B3_ENGINE_ART_CONTACTS
+        eng.set_options(B3_ENGINE_ART_CONTACTS)
     tiles = eng.tiles()
     stream = torch.cuda.current_stream()
     settle, start, end = window_of(scene, steps, warmup)
@@ -351,7 +359,7 @@ def run_workload(scene, count, steps, warmup, repeats, event_every, digest, cpu_
     mean_stepped = stepped / steps
     bytes_env = float(bytes_sum) / stepped
     k_ms = kernel_ms[med]
-    kernel = kernel_name(scene, count)
+    kernel = "b3k_step_art<false>" if art else kernel_name(scene, count)
     hbm_gbs = bytes_launch / (k_ms * 1e-3) / 1e9
     flops_env, counted = counted_flops(scene, start, steps)
     tflops = flops_env * mean_stepped / (k_ms * 1e-3) / 1e12
@@ -372,9 +380,12 @@ def run_workload(scene, count, steps, warmup, repeats, event_every, digest, cpu_
                          "frac_nonpacked": round(tflops / FP32_NONPACKED_TFLOPS, 5),
                          "flops_per_env_step": round(flops_env, 1), "counted_steps": counted,
                          "source": "tests/golden/flops.json (oracle fp32 operations counted on the workload)"}}
+    if art:
+        # the counted flops are the independent-body step's: no VALU figure
+        roofline["valu"] = {"note": "tests/golden/flops.json counts the independent-body step, not this one"}
     # the lower of the two ceilings, and the fraction of it reached
     ceil_hbm = HBM_PEAK_GBS * 1e9 / bytes_env
-    ceil_valu = FP32_PEAK_TFLOPS * 1e12 / flops_env
+    ceil_valu = float("inf") if art else FP32_PEAK_TFLOPS * 1e12 / flops_env
     attainable = min(ceil_hbm, ceil_valu)
     roofline["attainable_env_steps_per_s"] = round(attainable, 1)
     roofline["binding"] = "hbm" if ceil_hbm <= ceil_valu else "valu"
@@ -392,6 +403,8 @@ def run_workload(scene, count, steps, warmup, repeats, event_every, digest, cpu_
                   NAMES[scene], count, count, NAMES[scene], sc.dt, sc.substeps, masks),
               "worlds": count, "scene": NAMES[scene], "dt": sc.dt, "substeps": sc.substeps, "repeats": repeats,
               "window": [start, end], "settled_untimed": settle}
+    if art:
+        config["contacts"] = "articulated (B3_ENGINE_ART_CONTACTS: the reference's B3_ART_CONTACTS=1 step)"
     out = {"value": round(rates[med], 1), "unit": "env-steps/s", "steps": steps, "warmup": start - settle,
            "ms_per_step": round(ms[med], 5), "config": config, "roofline": roofline,
            "repeat_values": [round(v, 1) for v in rates]}
@@ -400,6 +413,48 @@ def run_workload(scene, count, steps, warmup, repeats, event_every, digest, cpu_
         out["cpu_baseline"] = cpu_baseline(scene, count, state_at_start, worlds, start, end, cpu_seconds)
         out["gpu_over_cpu"] = round(out["value"] / out["cpu_baseline"]["value"], 1)
     return out
+
+
+def run_hover_env(n, steps, warmup, repeats):
+    """The PufferLib hover environment on the engine (include/b3_hover.h,
+    puffysics_amd/hover.py): env-steps/s of its vector step (actions to
+    forces, the engine step with the previous step's terminals reset, then
+    observations, rewards and terminals), with the trainer's action write
+    (a device copy of pre-drawn actions in [-1, 1]) inside each timed step."""
+    import torch
+    from puffysics_amd.hover import HoverEnvs
+    env = HoverEnvs(n, seed=1)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1)
+    acts = torch.rand((warmup + steps, n), generator=gen, device="cuda") * 2.0 - 1.0
+    stream = torch.cuda.current_stream()
+    rates, ms = [], []
+    for r in range(repeats):
+        env.reset()
+        for i in range(warmup):
+            env.actions.copy_(acts[i])
+            env.step()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for i in range(steps):
+            env.actions.copy_(acts[warmup + i])
+            env.step()
+        b.record(stream)
+        torch.cuda.synchronize()
+        el = a.elapsed_time(b)
+        rates.append(n * steps / (el * 1e-3))
+        ms.append(el / steps)
+        log("  hover env repeat %d: %.4f ms/step, %.4g env-steps/s" % (r, ms[-1], rates[-1]))
+    stats = env.log()
+    env.close()
+    med = sorted(range(repeats), key=lambda i: rates[i])[repeats // 2]
+    return {"metric": "hover env-steps/sec (PufferLib adapter on the engine), 1 MI355X", "value": round(rates[med], 1),
+            "unit": "env-steps/s", "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms[med], 5),
+            "higher_is_better": True, "dtype": "f32", "data": "synthetic (seeded envs, pre-drawn uniform actions)",
+            "config": {"workload": "hover env: %d envs, one vector step = actions, physics step with resets, "
+                                   "observations" % n, "envs": n, "repeats": repeats},
+            "repeat_values": [round(v, 1) for v in rates], "episodes_logged": stats.get("n")}
 
 
 # ---- rocprofv3 summaries of the step kernel over the timed window ----
@@ -655,6 +710,10 @@ def main():
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE) and exit")
     ap.add_argument("--profile-commands", metavar="DIR",
                     help="with --scene: print the rocprofv3 runs whose outputs --profile-summary reads, and exit")
+    ap.add_argument("--art", action="store_true",
+                    help="with --scene: the step with articulated contacts (B3_ENGINE_ART_CONTACTS), no CPU leg")
+    ap.add_argument("--hover-env", type=int, default=0, metavar="N",
+                    help="the PufferLib hover adapter's vector step on N envs, one JSON line, and exit")
     ap.add_argument("--profile-summary", metavar="DIR",
                     help="with --scene: summarise those runs under DIR into profiles/ and exit")
     args = ap.parse_args()
@@ -692,13 +751,19 @@ def main():
     import torch
     from puffysics_amd import scenes
     torch.cuda.set_device(0)
+    if args.hover_env:
+        steps = args.steps if args.steps is not None else 1000
+        print(json.dumps(run_hover_env(args.hover_env, steps, args.warmup, args.repeats)), flush=True)
+        return
+    if args.art and not args.scene:
+        raise SystemExit("--art needs --scene")
     digest = engine_source_digest()
     todo = [args.scene] if args.scene else [1, 2, 3, 4, 5]
     results = {}
     for scene in todo:
         count = (args.worlds if args.scene and args.worlds else scenes.SCENES[scene].worlds)
         res = run_workload(scene, count, steps_of(scene), args.warmup, args.repeats, args.event_every, digest,
-                           None if args.no_cpu else args.cpu_seconds)
+                           None if args.no_cpu or args.art else args.cpu_seconds, art=args.art)
         results["%s%d" % (NAMES[scene], count)] = (scene, count, res)
     head_key = next((k for k, v in results.items() if v[0] == HEADLINE), next(iter(results)))
     head = results[head_key][2]
