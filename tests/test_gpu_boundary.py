@@ -34,9 +34,10 @@ def _vector_step(eng, scene, t, reset, stepm):
     eng.step(sc.dt, sc.substeps, stepm, reset)
 
 
-@pytest.mark.parametrize("scene,count,options", [(5, 4096, 1), (5, 300, 1), (4, 130, 1), (5, 300, 4), (5, 17000, 0)],
+@pytest.mark.parametrize("scene,count,options", [(5, 4096, 1), (5, 300, 1), (4, 130, 1), (5, 300, 4), (5, 17000, 0),
+                                                 (1, 4096, 0)],
                          ids=["arm4096-shared-keep", "arm300-shared-keep", "bin130-shared-keep",
-                              "arm300-one_wave", "arm17000-one_wave-default"])
+                              "arm300-one_wave", "arm17000-one_wave-default", "hover4096-kept_row-default"])
 def test_graph_replay_equals_eager(scene, count, options):
     """Masks, inputs and the fused restore + step of one vector step are
     captured once; each replay is checked against the same calls made
@@ -46,7 +47,8 @@ def test_graph_replay_equals_eager(scene, count, options):
     the one-wave kernel b3k_step runs when forced (option
     B3_ENGINE_ONE_WAVE_PER_TILE = 4) and for 17,000 arm worlds (266 tiles)
     with the default options, the configuration of the 65,536-world
-    benchmark."""
+    benchmark; the hover's worlds (two shapes) take the one-wave kernel that
+    keeps their contact row, b3k_step<JI, true>, at any batch size."""
     sc = scenes.SCENES[scene]
     worlds = scenes.build(scene, count)
     graphed, eager = _engine(worlds, scene, options), _engine(worlds, scene, options)
